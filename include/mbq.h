@@ -1,0 +1,106 @@
+/* mbq — MI355X (gfx950) quantized linear: the C ABI of libmbq.so.
+ *
+ * The drop-in boundary for mashbox's quantized-linear path. mashbox's kernel-package surface
+ * (reference src/mashbox/ops/__init__.py:11-34: TYPES, repack, repack_host, matmul, dequant, plane_bytes, kq_covers,
+ * picks_layer) and its int8 per-channel linear (reference src/mashbox/models/qwen3_8_27b/model.py:72-82) are served by
+ * these entry points; the Python package mashbox_amd binds them with ctypes.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only. "dev" pointers are device (HBM) addresses owned by the caller; "host" pointers are
+ *     host memory. Every device entry point is stream-ordered on `stream` (a hipStream_t; NULL = the default stream)
+ *     and returns before the work finishes; it allocates nothing and holds no host lock.
+ *   - Matrices are row-major. Activations x are bfloat16 bits (uint16) of shape (M, K); results y are (M, N) as
+ *     float32 (out_dtype MBQ_OUT_F32) or bfloat16 bits rounded to nearest even (MBQ_OUT_BF16).
+ *   - Weights have N rows (outputs) and K columns (inputs), as the GGUF reader orders them (reference
+ *     src/mashbox/gguf/reader.py:85-87).
+ *   - Return value: MBQ_OK (0) or a negative MBQ_E* code; mbq_last_error() gives the message of the calling
+ *     thread's last failure. A failure launches nothing.
+ *   - Device pointers must be 16-byte aligned (the kernels issue 128-bit loads and stores).
+ */
+#ifndef MBQ_H
+#define MBQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids on this path (reference src/mashbox/ops/reference.py:22-29); MBQ_INT8 is not a ggml type: it names the
+ * int8 per-output-channel weights of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 */
+#define MBQ_Q8_0 8
+#define MBQ_Q4_K 12
+#define MBQ_INT8 (-8)
+
+#define MBQ_OUT_F32 0
+#define MBQ_OUT_BF16 1
+
+#define MBQ_OK 0
+#define MBQ_E_ARG (-1)      /* bad type, shape, pointer or alignment */
+#define MBQ_E_HIP (-2)      /* a HIP runtime call failed (launch, device query) */
+#define MBQ_E_CAP (-3)      /* the output buffer is smaller than mbq_plane_bytes */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mbq_version(void);
+
+/* Message of the calling thread's last failure ("" if none). The pointer stays valid until the thread's next call. */
+const char* mbq_last_error(void);
+
+/* 1 if type t is a ggml type with kernel planes here (Q8_0, Q4_K), else 0.
+ * Replaces the membership test `t in mod.TYPES` (reference src/mashbox/ops/__init__.py:21,303). */
+int mbq_has_type(int t);
+
+/* Bytes one packed row of `cols` values takes in the file (ggml row bytes), or a negative code if cols is not a
+ * multiple of the type's block. Restates reference src/mashbox/ops/reference.py:390-395. */
+int64_t mbq_row_bytes(int t, int64_t cols);
+
+/* 1 if the kernels run a (rows, cols) weight of type t, else 0 (cols must be a whole number of blocks).
+ * Replaces the optional kq_covers(t, (rows, cols)) (reference src/mashbox/ops/__init__.py:359-363). */
+int mbq_covers(int t, int64_t rows, int64_t cols);
+
+/* Device bytes of one (rows, cols) weight's kernel planes, 256-byte aligned, so that a stack of L weights is
+ * L * mbq_plane_bytes(...) bytes with weight l at byte offset l * mbq_plane_bytes(...).
+ * Replaces plane_bytes(t, shape) (reference src/mashbox/ops/__init__.py:24,374-378). Negative on error. */
+int64_t mbq_plane_bytes(int t, int64_t rows, int64_t cols);
+
+/* Host repack: the file's blocks raw (rows, row_bytes) -> the kernel planes in planes_host (cap bytes, at least
+ * mbq_plane_bytes). A lossless byte permutation (padding bytes are zero); uses up to `threads` host threads
+ * (0 = all cores). Replaces repack_host(t, raw, shape) (reference src/mashbox/ops/__init__.py:22-23,473-474). */
+int mbq_repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes_host, size_t cap,
+                    int threads);
+
+/* Inverse of mbq_repack_host: planes -> the file's blocks (rows, row_bytes). Used to prove the repack lossless. */
+int mbq_unpack_host(int t, const uint8_t* planes_host, int64_t rows, int64_t cols, uint8_t* raw, size_t cap);
+
+/* Device repack: the same permutation as mbq_repack_host, run on the GPU from blocks already in HBM.
+ * Replaces the traced repack(t, raw, shape) on a device array (reference src/mashbox/ops/__init__.py:16,475-485). */
+int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, uint8_t* planes_dev, void* stream);
+
+/* y (M, N) = x (M, K) @ W.T for the planes of one (N, K) weight of ggml type t, float32 accumulation.
+ * planes_dev: a stack of weights laid out as mbq_plane_bytes apart; `layer` picks one of them (0 for a lone weight),
+ * read in place. layer_dev, when not NULL, is a device int32 holding the layer index instead (read by the kernel, so a
+ * captured graph or a device-side layer loop never syncs with the host); nlayers bounds it (an index outside
+ * [0, nlayers) yields zeros... never an out-of-range read).
+ * M = 0 launches nothing. Replaces matmul(x, planes[, layer=]) (reference src/mashbox/ops/__init__.py:17-19,613-616;
+ * call contract src/mashbox/ops/bundle.py:559-598: x as bf16, f32 result). */
+int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+               const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream);
+
+/* W (N, K) float32 from the planes of one weight (layer / layer_dev as in mbq_matmul). Bit for bit the reference
+ * dequantization (NaN where it has NaN). Replaces dequant(planes) (reference src/mashbox/ops/__init__.py:20,691-705). */
+int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
+                int64_t K, float* w_dev, void* stream);
+
+/* int8 per-output-channel linear: y (M, N) = (x (M, K) @ bf16(q).T accumulated in float32) * s, then out_dtype.
+ * q_dev int8 (N, K) row-major, s_dev float32 (N,). Replaces linear(x, {"q", "s"}) (reference
+ * src/mashbox/models/qwen3_8_27b/model.py:72-82); with out_dtype MBQ_OUT_F32 it returns the float32 y*s that the
+ * reference's pj hook receives (model.py:79). */
+int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
+                    void* y_dev, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MBQ_H */

@@ -1,0 +1,62 @@
+"""ctypes binding of libmbq.so (C ABI: include/mbq.h). Loading fails loudly: there is no fallback path here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MBQ_LIB", os.path.join(HERE, "libmbq.so"))
+
+Q8_0, Q4_K, INT8 = 8, 12, -8
+OUT_F32, OUT_BF16 = 0, 1
+
+# every symbol include/mbq.h declares, with its ctypes signature
+_c = ctypes
+_SIGS = {
+    "mbq_version": (_c.c_int, []),
+    "mbq_last_error": (_c.c_char_p, []),
+    "mbq_has_type": (_c.c_int, [_c.c_int]),
+    "mbq_row_bytes": (_c.c_int64, [_c.c_int, _c.c_int64]),
+    "mbq_covers": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64]),
+    "mbq_plane_bytes": (_c.c_int64, [_c.c_int, _c.c_int64, _c.c_int64]),
+    "mbq_repack_host": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_size_t, _c.c_int]),
+    "mbq_unpack_host": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_size_t]),
+    "mbq_repack_dev": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
+    "mbq_matmul": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64,
+                              _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_int, _c.c_void_p]),
+    "mbq_dequant": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                               _c.c_void_p, _c.c_void_p]),
+    "mbq_int8_linear": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
+                                   _c.c_void_p, _c.c_int, _c.c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class MbqError(RuntimeError):
+    """a libmbq.so entry point returned an error code"""
+
+
+def lib() -> ctypes.CDLL:
+    """the loaded libmbq.so; raises OSError when it is missing (build it with mashbox_amd.build)"""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise OSError(f"{LIB_PATH} is missing: build it with `python -m mashbox_amd.build`")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGS.items():
+                    f = getattr(L, name)
+                    f.restype, f.argtypes = res, args
+                _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> int:
+    if rc < 0:
+        msg = lib().mbq_last_error().decode(errors="replace")
+        raise MbqError(f"{what}: {msg} (code {rc})")
+    return rc

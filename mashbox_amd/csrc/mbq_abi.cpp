@@ -1,0 +1,268 @@
+// The C ABI of libmbq.so (declared in include/mbq.h): argument checks, the host repack, and dispatch to the kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/mbq.h"
+#include "mbq_launch.h"
+#include "mbq_layout.h"
+
+namespace mbq {
+
+static thread_local std::string g_error;
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_K; }
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// shape rules shared by every entry point of a ggml type
+static int check_shape(int t, int64_t rows, int64_t cols) {
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12)", t);
+    if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
+    if (cols % block_values(t))
+        return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
+                         block_values(t));
+    if (rows > INT32_MAX || cols > INT32_MAX) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) too large", (long long)rows, (long long)cols);
+    return 0;
+}
+
+// run f(row_begin, row_end) over [0, rows) on up to `threads` host threads
+template <class F>
+static void parallel_rows(int64_t rows, int threads, F f) {
+    int hw = (int)std::thread::hardware_concurrency();
+    if (threads <= 0) threads = hw > 0 ? hw : 1;
+    threads = (int)std::min<int64_t>(threads, std::max<int64_t>(1, rows / 64));
+    if (threads <= 1) {
+        f(0, rows);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const int64_t step = (rows + threads - 1) / threads;
+    for (int i = 0; i < threads; ++i) {
+        const int64_t a = i * step, b = std::min(rows, a + step);
+        if (a >= b) break;
+        pool.emplace_back(f, a, b);
+    }
+    for (auto& th : pool) th.join();
+}
+
+static void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
+    const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
+    for (int64_t n = r0; n < r1; ++n) {
+        const uint8_t* row = raw + n * rb;
+        if (t == T_Q8_0) {
+            uint8_t* q = planes + L.qs_off + n * K;
+            uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                memcpy(d + b * 2, row + b * bb, 2);
+                memcpy(q + b * 32, row + b * bb + 2, 32);
+            }
+        } else {
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(meta + b * 16, src, 16);
+                const uint8_t* qs = src + 16;
+                for (int j = 0; j < 8; ++j) {
+                    uint32_t unit[4] = {0, 0, 0, 0};
+                    for (int i = 0; i < 32; ++i) {
+                        const uint8_t byte = qs[32 * (j >> 1) + i];
+                        const uint32_t v = (j & 1) ? (byte >> 4) : (byte & 15u);
+                        int dw, bit;
+                        q4k_slot(i, &dw, &bit);
+                        unit[dw] |= v << bit;
+                    }
+                    memcpy(q + b * 128 + j * 16, unit, 16);  // little-endian host, as the GPU
+                }
+            }
+        }
+    }
+}
+
+static void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, const Layout& L, int64_t r0, int64_t r1) {
+    const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
+    for (int64_t n = r0; n < r1; ++n) {
+        uint8_t* row = raw + n * rb;
+        if (t == T_Q8_0) {
+            const uint8_t* q = planes + L.qs_off + n * K;
+            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                memcpy(row + b * bb, d + b * 2, 2);
+                memcpy(row + b * bb + 2, q + b * 32, 32);
+            }
+        } else {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, meta + b * 16, 16);
+                uint8_t* qs = dst + 16;
+                memset(qs, 0, 128);
+                for (int j = 0; j < 8; ++j) {
+                    uint32_t unit[4];
+                    memcpy(unit, q + b * 128 + j * 16, 16);
+                    for (int i = 0; i < 32; ++i) {
+                        int dw, bit;
+                        q4k_slot(i, &dw, &bit);
+                        const uint8_t v = (unit[dw] >> bit) & 15u;
+                        qs[32 * (j >> 1) + i] |= (j & 1) ? (uint8_t)(v << 4) : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+static int check_out(int out_dtype) {
+    if (out_dtype != MBQ_OUT_F32 && out_dtype != MBQ_OUT_BF16)
+        return set_error(MBQ_BAD_ARG, "out_dtype %d is neither MBQ_OUT_F32 nor MBQ_OUT_BF16", out_dtype);
+    return 0;
+}
+
+// resolves the planes of one weight of a stack: host layer -> base pointer; device layer -> kernel argument
+static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
+                      int64_t K, Args* a) {
+    if (int rc = check_shape(t, N, K)) return rc;
+    if (!planes || !aligned16(planes)) return set_error(MBQ_BAD_ARG, "planes pointer is NULL or not 16-byte aligned");
+    if (nlayers < 1 || nlayers > INT32_MAX) return set_error(MBQ_BAD_ARG, "nlayers %lld must be >= 1", (long long)nlayers);
+    if (layer_dev == nullptr && (layer < 0 || layer >= nlayers))
+        return set_error(MBQ_BAD_ARG, "layer %lld outside the stack of %lld", (long long)layer, (long long)nlayers);
+    const Layout L = layout(t, N, K);
+    a->stride = L.total;
+    a->base = planes + (layer_dev ? 0 : layer * L.total);
+    a->layer_dev = layer_dev;
+    a->nlayers = (int)nlayers;
+    a->sc_off = L.sc_off;
+    a->srow = nullptr;
+    a->N = N;
+    a->K = K;
+    return 0;
+}
+
+}  // namespace mbq
+
+using namespace mbq;
+
+extern "C" {
+
+int mbq_version(void) { return 100; }
+
+const char* mbq_last_error(void) { return g_error.c_str(); }
+
+int mbq_has_type(int t) { return is_type(t) ? 1 : 0; }
+
+int64_t mbq_row_bytes(int t, int64_t cols) {
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes", t);
+    if (cols < 0 || cols % block_values(t))
+        return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
+                         block_values(t));
+    return cols / block_values(t) * block_bytes(t);
+}
+
+int mbq_covers(int t, int64_t rows, int64_t cols) { return check_shape(t, rows, cols) == 0 ? 1 : 0; }
+
+int64_t mbq_plane_bytes(int t, int64_t rows, int64_t cols) {
+    if (int rc = check_shape(t, rows, cols)) return rc;
+    return layout(t, rows, cols).total;
+}
+
+int mbq_repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes_host, size_t cap, int threads) {
+    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (!raw || !planes_host) return set_error(MBQ_BAD_ARG, "NULL buffer");
+    const Layout L = layout(t, rows, cols);
+    if (cap < (size_t)L.total) return set_error(MBQ_E_CAP, "planes buffer of %zu bytes < %lld", cap, (long long)L.total);
+    memset(planes_host + L.qs_bytes, 0, (size_t)(L.sc_off - L.qs_bytes));
+    memset(planes_host + L.sc_off + L.sc_bytes, 0, (size_t)(L.total - L.sc_off - L.sc_bytes));
+    parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes_host, L, a, b); });
+    return MBQ_OK;
+}
+
+int mbq_unpack_host(int t, const uint8_t* planes_host, int64_t rows, int64_t cols, uint8_t* raw, size_t cap) {
+    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (!raw || !planes_host) return set_error(MBQ_BAD_ARG, "NULL buffer");
+    const int64_t rb = cols / block_values(t) * block_bytes(t);
+    if (cap < (size_t)(rows * rb)) return set_error(MBQ_E_CAP, "raw buffer of %zu bytes < %lld", cap, (long long)(rows * rb));
+    const Layout L = layout(t, rows, cols);
+    parallel_rows(rows, 0, [&](int64_t a, int64_t b) { unpack_rows(t, planes_host, cols, raw, L, a, b); });
+    return MBQ_OK;
+}
+
+int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, uint8_t* planes_dev, void* stream) {
+    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (!raw_dev || !planes_dev || !aligned16(planes_dev)) return set_error(MBQ_BAD_ARG, "NULL or misaligned buffer");
+    const Layout L = layout(t, rows, cols);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // zero the alignment padding, then write every plane byte
+    if (hipMemsetAsync(planes_dev + L.qs_bytes, 0, (size_t)(L.sc_off - L.qs_bytes), s) != hipSuccess ||
+        hipMemsetAsync(planes_dev + L.sc_off + L.sc_bytes, 0, (size_t)(L.total - L.sc_off - L.sc_bytes), s) != hipSuccess)
+        return set_error(MBQ_E_HIP, "hipMemsetAsync failed");
+    return launch_repack(t, raw_dev, rows, cols, planes_dev, L.sc_off, s);
+}
+
+int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+               const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream) {
+    Args a{};
+    if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
+    if (int rc = check_out(out_dtype)) return rc;
+    if (M < 0 || M > INT32_MAX) return set_error(MBQ_BAD_ARG, "M = %lld", (long long)M);
+    if (M == 0) return MBQ_OK;
+    if (!x_dev || !y_dev || !aligned16(x_dev) || !aligned16(y_dev))
+        return set_error(MBQ_BAD_ARG, "x or y is NULL or not 16-byte aligned");
+    a.x = x_dev;
+    a.M = M;
+    a.y = y_dev;
+    a.out_bf16 = out_dtype == MBQ_OUT_BF16;
+    return launch_matmul(t, a, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
+                int64_t K, float* w_dev, void* stream) {
+    Args a{};
+    if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
+    if (!w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "w is NULL or not 16-byte aligned");
+    return launch_dequant(t, a, w_dev, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
+                    void* y_dev, int out_dtype, void* stream) {
+    if (int rc = check_out(out_dtype)) return rc;
+    if (N <= 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX || M < 0 || M > INT32_MAX)
+        return set_error(MBQ_BAD_ARG, "shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    if (K % 16) return set_error(MBQ_BAD_ARG, "int8 K = %lld must be a multiple of 16", (long long)K);
+    if (M == 0) return MBQ_OK;
+    if (!q_dev || !s_dev || !x_dev || !y_dev || !aligned16(q_dev) || !aligned16(x_dev) || !aligned16(y_dev))
+        return set_error(MBQ_BAD_ARG, "q, s, x or y is NULL or q, x, y not 16-byte aligned");
+    Args a{};
+    a.base = reinterpret_cast<const uint8_t*>(q_dev);
+    a.stride = 0;
+    a.layer_dev = nullptr;
+    a.nlayers = 1;
+    a.sc_off = 0;
+    a.srow = s_dev;
+    a.x = x_dev;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.y = y_dev;
+    a.out_bf16 = out_dtype == MBQ_OUT_BF16;
+    return launch_matmul(T_INT8, a, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

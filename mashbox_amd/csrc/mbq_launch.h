@@ -1,0 +1,33 @@
+// Internal interface between the C ABI (mbq_abi.cpp) and the kernel launchers (mbq_kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mbq {
+
+enum : int { MBQ_BAD_ARG = -1, MBQ_LAUNCH_FAIL = -2, MBQ_SMALL_CAP = -3 };
+
+// activation rows up to which the GEMV runs; more rows take the MFMA GEMM
+constexpr int64_t GEMV_MAX_M = 4;
+
+struct Args {
+    const uint8_t* base;       // planes of the weight (layer already applied when the layer is a host value)
+    int64_t stride;            // bytes between stacked weights (layer_dev)
+    const int32_t* layer_dev;  // device layer index, or nullptr
+    int nlayers;
+    int64_t sc_off;            // offset of the scale plane inside one weight's planes
+    const float* srow;         // int8: per-row scales
+    const uint16_t* x;
+    int64_t M, N, K;
+    void* y;
+    int out_bf16;
+};
+
+// records the calling thread's error message; returns code
+int set_error(int code, const char* fmt, ...);
+
+int launch_matmul(int t, const Args& a, hipStream_t s);
+int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
+int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, int64_t sc_off, hipStream_t s);
+
+}  // namespace mbq

@@ -1,0 +1,42 @@
+"""Comparison bars shared by the tests.
+
+- bit equality with NaN == NaN: reference tests/cpu/test_gguf_dequant.py:30-36 (and tests/contracts/test_ops.py:129-134)
+- NMSE = sum (y - ref)^2 / sum ref^2 <= 2e-5 for bfloat16 activations: reference tests/contracts/test_ops.py:28-31,51
+- max |y - ref| / max |ref| <= 1e-2 (bf16 out, fp32 accumulate): the bar BASELINE.json's north star sets
+- a reference that is exactly zero gives exactly zero; every output is finite: tests/contracts/test_ops.py:32,143-147
+"""
+import numpy as np
+
+NMSE_BF16 = 2e-5
+MAX_REL = 1e-2
+
+
+def diff_bits(got, want) -> int:
+    """number of float32 values whose bits differ; NaN must be NaN on both sides"""
+    a = np.ascontiguousarray(np.asarray(got, np.float32))
+    b = np.ascontiguousarray(np.asarray(want, np.float32))
+    assert a.shape == b.shape, (a.shape, b.shape)
+    nan = np.isnan(a) | np.isnan(b)
+    same = np.where(nan, np.isnan(a) & np.isnan(b), a.view(np.uint32) == b.view(np.uint32))
+    return int(np.sum(~same))
+
+
+def product_errors(y, ref):
+    """-> (nmse, max_rel) of y against a float64 reference product"""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert y.shape == ref.shape, (y.shape, ref.shape)
+    assert np.all(np.isfinite(y)), "non-finite output"
+    den = float(np.sum(ref ** 2))
+    if den == 0.0:
+        assert np.all(y == 0.0), "reference is exactly zero, output is not"
+        return 0.0, 0.0
+    nmse = float(np.sum((y - ref) ** 2)) / den
+    max_rel = float(np.max(np.abs(y - ref)) / np.max(np.abs(ref)))
+    return nmse, max_rel
+
+
+def assert_product(y, ref, what=""):
+    nmse, mr = product_errors(y, ref)
+    assert nmse <= NMSE_BF16 and mr <= MAX_REL, f"{what}: NMSE {nmse:.3e} (bar {NMSE_BF16}), max rel {mr:.3e} (bar {MAX_REL})"
+    return nmse, mr

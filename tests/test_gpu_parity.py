@@ -1,0 +1,202 @@
+"""GPU parity: the gfx950 kernels of libmbq.so against the CPU oracle (oracle/ref.py) on the same seeded inputs.
+
+Mirrors the reference's own bars:
+  dequant: bit for bit, NaN where the reference has NaN, on random bytes with all-zero and all-0xFF blocks
+           (reference tests/cpu/test_gguf_dequant.py:17-45; contract rule src/mashbox/ops/__init__.py:691-705)
+  matmul:  NMSE <= 2e-5 against the float64 product of the exact weights (reference tests/contracts/test_ops.py:28-31)
+           and max |y - ref| / max |ref| <= 1e-2; weight rows 1..130, K 1..16 blocks, activation rows 1..130,
+           leading axes, empty batches (reference tests/cpu/test_moe_bundle_dense.py:108-128)
+  int8:    the same product bars for reference src/mashbox/models/qwen3_8_27b/model.py:72-82
+Full-size BASELINE configs: configs 1-3 compared whole; configs 4-5 through a seeded sample of output entries.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gen as G
+from oracle import ref as R
+from tests._check import assert_product, diff_bits
+
+import mashbox_amd.kernels as KQ
+from mashbox_amd import int8 as I8
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [R.Q8_0, R.Q4_K]
+NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K"}
+
+
+def _bf16_tensor(bits: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def _random_blocks(t, rows, kb, rng):
+    bs = R.TYPES[t][1]
+    cols = bs * kb
+    raw = rng.integers(0, 256, size=(rows, R.row_bytes(t, cols)), dtype=np.uint8)
+    raw[0] = 0
+    raw[1] = 0xFF
+    return raw, cols
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+@pytest.mark.parametrize("kb", [1, 2, 16])
+def test_dequant_bit_exact_on_random_bytes(t, kb, cuda):
+    rng = np.random.default_rng(1000 + t + kb)
+    raw, cols = _random_blocks(t, 6, kb, rng)
+    planes = KQ.repack_host(t, raw, (6, cols)).to(cuda)
+    got = KQ.dequant(planes).cpu().numpy()
+    assert diff_bits(got, R.dequant(raw, t, cols)) == 0
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_dequant_leading_axes(t, cuda):
+    """a stack (L, rows, row_bytes) dequantizes as one tensor at a time (test_gguf_dequant.py:48-56)"""
+    rng = np.random.default_rng(2000 + t)
+    raw, cols = _random_blocks(t, 6, 2, rng)
+    st = np.stack([raw, raw[::-1]])
+    planes = KQ.repack_host(t, st, (6, cols)).to(cuda)
+    got = KQ.dequant(planes).cpu().numpy()
+    for i in range(2):
+        assert diff_bits(got[i], R.dequant(st[i], t, cols)) == 0
+        assert diff_bits(KQ.dequant(planes, layer=i).cpu().numpy(), R.dequant(st[i], t, cols)) == 0
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_device_repack_equals_host_repack(t, cuda):
+    rng = np.random.default_rng(3000 + t)
+    raw, cols = _random_blocks(t, 37, 3, rng)
+    host = KQ.repack_host(t, raw, (37, cols))
+    dev = KQ.repack(t, torch.from_numpy(raw).to(cuda), (37, cols))
+    assert torch.equal(host.buf, dev.buf.cpu())
+
+
+MM_SHAPES = [(1, 1), (9, 2), (37, 3), (130, 4)]        # (weight rows N, K in blocks)
+MM_ROWS = [1, 2, 3, 4, 5, 16, 64, 130]
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+@pytest.mark.parametrize("n,kb", MM_SHAPES)
+@pytest.mark.parametrize("m", MM_ROWS)
+def test_matmul_matches_exact_product(t, n, kb, m, cuda):
+    rng = np.random.default_rng([t, n, kb, m])
+    k = R.TYPES[t][1] * kb
+    raw = G.RAW[t](rng, n, k)
+    xb = G.acts(rng, m, k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    x = _bf16_tensor(xb, cuda)
+    y = KQ.matmul(x, planes).cpu().numpy()
+    assert y.dtype == np.float32 and y.shape == (m, n)
+    w = R.dequant(raw, t, k).astype(np.float64)
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ w.T
+    assert_product(y, ref, f"{NAME[t]} m={m} n={n} k={k}")
+    yb = KQ.matmul(x, planes, out_dtype=torch.bfloat16)
+    assert yb.dtype == torch.bfloat16
+    # the bf16 output is the f32 output rounded to nearest even (ops casts the f32 result to x.dtype)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+@pytest.mark.parametrize("lead", [(2, 3), (1, 1, 5), (24,)])
+def test_matmul_leading_axes(t, lead, cuda):
+    rng = np.random.default_rng([t, len(lead)])
+    n, k = 21, R.TYPES[t][1] * 2
+    raw = G.RAW[t](rng, n, k)
+    xb = G.acts(rng, int(np.prod(lead)), k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    y = KQ.matmul(_bf16_tensor(xb, cuda).reshape(lead + (k,)), planes)
+    assert tuple(y.shape) == lead + (n,)
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    assert_product(y.reshape(-1, n).cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("lead", [(0,), (2, 0)])
+def test_empty_batch_gives_an_empty_result(lead, cuda):
+    n, k = 8, 256
+    raw = G.q4_k_raw(np.random.default_rng(0), n, k)
+    planes = KQ.repack_host(R.Q4_K, raw, (n, k)).to(cuda)
+    y = KQ.matmul(torch.zeros(lead + (k,), dtype=torch.bfloat16, device=cuda), planes)
+    assert tuple(y.shape) == lead + (n,) and y.dtype == torch.float32
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+@pytest.mark.parametrize("m", [1, 4, 64])
+def test_layer_reads_one_weight_of_a_stack_in_place(t, m, cuda):
+    rng = np.random.default_rng([t, m, 7])
+    n, k, L = 33, R.TYPES[t][1] * 2, 3
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(L)])
+    xb = G.acts(rng, m, k)
+    planes = KQ.repack_host(t, st, (n, k)).to(cuda)
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    for layer in range(L):
+        ref = xf @ R.dequant(st[layer], t, k).astype(np.float64).T
+        assert_product(KQ.matmul(x, planes, layer=layer).cpu().numpy(), ref, f"host layer {layer}")
+        dl = torch.tensor(layer, dtype=torch.int32, device=cuda)
+        got = KQ.matmul(x, planes, layer=dl).cpu().numpy()
+        assert_product(got, ref, f"device layer {layer}")
+        assert np.array_equal(got, KQ.matmul(x, planes[layer]).cpu().numpy())
+    bad = KQ.matmul(x, planes, layer=torch.tensor(L, dtype=torch.int32, device=cuda)).cpu().numpy()
+    assert np.all(np.isnan(bad)), "a device layer outside the stack must give NaN, never an out-of-range read"
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 64, 130])
+@pytest.mark.parametrize("n,k", [(7, 16), (33, 48), (130, 4096)])
+def test_int8_linear_matches_reference(m, n, k, cuda):
+    rng = np.random.default_rng([m, n, k])
+    xb = G.acts(rng, m, k)
+    q, s = G.int8_weights(rng, n, k)
+    w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+    x = _bf16_tensor(xb, cuda)
+    ref = (R.bf16_to_f32(xb).astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    yf = I8.linear(x, w, pj=lambda v: v).float().cpu().numpy()
+    assert_product(yf, ref, f"int8 m={m} n={n} k={k}")
+    y = I8.linear(x, w)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (m, n)
+    assert_product(y.float().cpu().numpy(), ref)
+    # the oracle's float32 restatement rounds the same way within the bar
+    assert_product(R.int8_linear(R.bf16_to_f32(xb), q, s), ref)
+
+
+# --------------------------------------------------------------------------------- full-size BASELINE configs
+@pytest.mark.parametrize("idx", [1, 2, 3])
+def test_decode_gemv_full_config(idx, cuda):
+    cfg = G.config(idx, seed=0)
+    (_, n, k, wts, xb), = cfg["projections"]
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    if cfg["t"] == "int8":
+        q, s = wts
+        y = I8.linear(x, {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}, pj=lambda v: v)
+        ref = (xf @ q.astype(np.float64).T) * s
+    else:
+        planes = KQ.repack_host(cfg["t"], wts, (n, k)).to(cuda)
+        got_w = KQ.dequant(planes).cpu().numpy()
+        w = R.dequant(wts, cfg["t"], k)
+        assert diff_bits(got_w, w) == 0
+        y = KQ.matmul(x, planes)
+        ref = xf @ w.astype(np.float64).T
+    assert_product(y.float().cpu().numpy(), ref, f"config {idx}")
+
+
+@pytest.mark.parametrize("idx", [4, 5])
+def test_batched_gemm_full_config_sampled(idx, cuda):
+    """full-size configs 4 and 5: every projection runs whole on the GPU; a seeded sample of 24 activation rows x
+    192 weight rows per projection is compared with the exact product"""
+    cfg = G.config(idx, seed=0)
+    rng = np.random.default_rng(idx)
+    for name, n, k, wts, xb in cfg["projections"]:
+        x = _bf16_tensor(xb, cuda)
+        ms = np.sort(rng.choice(xb.shape[0], 24, replace=False))
+        ns = np.sort(rng.choice(n, 192, replace=False))
+        xf = R.bf16_to_f32(xb[ms]).astype(np.float64)
+        if cfg["t"] == "int8":
+            q, s = wts
+            y = I8.linear(x, {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}, pj=lambda v: v)
+            ref = (xf @ q[ns].astype(np.float64).T) * s[ns]
+        else:
+            planes = KQ.repack_host(cfg["t"], wts, (n, k)).to(cuda)
+            y = KQ.matmul(x, planes)
+            ref = xf @ R.dequant(wts[ns], cfg["t"], k).astype(np.float64).T
+        got = y.float().cpu().numpy()[np.ix_(ms, ns)]
+        assert_product(got, ref, f"config {idx} {name}")
