@@ -1,0 +1,241 @@
+#!/usr/bin/env python
+"""bench.py — the quantized-linear hot path on one MI355X against its roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--cpu-seconds S | --no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input of a BASELINE config: one kernel launch for the
+decode GEMV configs 1-3, the 7 projection launches of one 27B-class layer for configs 4-5. The headline (`value`) is
+config 2 (GGUF Q8_0 decode GEMV, x[1,5120] @ W[17408,5120]^T), in GB/s of algorithmic bytes (packed weight bytes +
+scales + x + y, never repack padding) per second, with the weights already in HBM.
+
+Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
+distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
+for K timed launches bracketed by torch.cuda.synchronize() and HIP events on the stream the kernels run on. The kernel's
+average launch duration is the event time / K. The CPU baseline is the oracle's restatement of mashbox's exact path
+(rebuild float32 weights per call, float32 dot) on the host's cores, on a bounded sample of config 2.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s (% MFMA peak)"
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD spec
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, AMD spec (no sparsity)
+HEADLINE = 2
+
+
+def algorithmic_bytes(t, m, n, k):
+    if t == "int8":
+        w = n * k + 4 * n
+    else:
+        bs, ts = {8: (32, 34), 12: (256, 144)}[t]
+        w = n * (k // bs) * ts
+    return w + 2 * m * k + 2 * m * n
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def run_config(idx, steps, warmup, rotate_bytes):
+    import torch
+    from mashbox_amd import synth
+    from mashbox_amd._lib import OUT_BF16, check, lib
+
+    L = lib()
+    dev = torch.device("cuda", 0)
+    t, M, projs = synth.CONFIGS[idx]
+    out = {"projections": {}}
+    total_us = 0.0
+    total_bytes = 0
+    total_flops = 0
+    for pi, (name, N, K) in enumerate(projs):
+        seed = 1000 * idx + pi
+        x = synth.acts(M, K, seed=seed, device=dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if t == "int8":
+            q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
+            wbytes = N * K + 4 * N
+            copies = max(1, math.ceil(rotate_bytes / wbytes))
+            bufs = [(q, s)] + [(q.clone(), s.clone()) for _ in range(copies - 1)]
+
+            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K):
+                qq, ss = bufs[c]
+                return L.mbq_int8_linear(ctypes.c_void_p(qq.data_ptr()), ctypes.c_void_p(ss.data_ptr()),
+                                         ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()),
+                                         OUT_BF16, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        else:
+            raw = (synth.q8_0_raw if t == 8 else synth.q4_k_raw)(N, K, seed=seed + 7, device=dev)
+            pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
+            planes = torch.empty(pb, dtype=torch.uint8, device=dev)
+            check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()),
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "repack")
+            del raw
+            wbytes = pb
+            copies = max(1, math.ceil(rotate_bytes / wbytes))
+            bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
+
+            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K, t=t):
+                return L.mbq_matmul(t, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
+                                    M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        check(launch(0), f"config {idx} {name}")          # eager call: argument errors surface here, not in capture
+        torch.cuda.synchronize()
+
+        def capture(n):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(n):
+                    check(launch(i % copies), "launch")
+            return g
+
+        if warmup > 0:
+            gw = capture(warmup)
+            gw.replay()
+        g = capture(steps)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / steps
+        ab = algorithmic_bytes(t, M, N, K)
+        fl = 2 * M * N * K
+        out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
+                                    "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
+                                    "rotation_MB": round(copies * wbytes / 1e6, 1)}
+        total_us += us
+        total_bytes += ab
+        total_flops += fl
+        del bufs, g
+        torch.cuda.empty_cache()
+    gbs = total_bytes / total_us / 1e3
+    tfl = total_flops / total_us / 1e6
+    out.update({"type": {8: "Q8_0", 12: "Q4_K"}.get(t, t), "M": M, "us_per_step": round(total_us, 3),
+                "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "TFLOPs": round(tfl, 2),
+                "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4), "algorithmic_bytes": total_bytes, "flops": total_flops})
+    log(f"config {idx}: {out['us_per_step']:.2f} us/step  {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% HBM)  "
+        f"{tfl:.1f} TFLOP/s ({100 * tfl / PEAK_BF16_TFLOPS:.1f}% MFMA)")
+    return out
+
+
+def measured_peaks():
+    """the box's achievable HBM rates with plain torch kernels on 2 GiB: read (a float32 sum) and copy (read + write)"""
+    import torch
+    n = (2 << 30) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {}
+    for name, fn, nbytes in (("read_GBps", lambda: a.sum(), 4 * n), ("copy_GBps", lambda: b.copy_(a), 8 * n)):
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(nbytes * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(seconds):
+    """oracle restatement of mashbox's exact path on config 2 (Q8_0 17408 x 5120, M = 1), host cores"""
+    import numpy as np
+    from oracle import gen as G
+    from oracle import ref as R
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(threads, 16))
+    cfg = G.config(HEADLINE, seed=0)
+    (_, n, k, raw, xb), = cfg["projections"]
+    x = R.bf16_to_f32(xb)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        y = R.qmatmul_exact(x, raw, R.Q8_0, (n, k), threads=threads)
+        R.bf16_round(y)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    ab = algorithmic_bytes(8, 1, n, k)
+    try:
+        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
+    except OSError:
+        model = "?"
+    return {"value": round(ab / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 whole (Q8_0 W[17408,5120], x[1,5120]): {len(times)} calls of oracle.ref.qmatmul_exact "
+                      f"(float32 rebuild in 8 row chunks of 2176 + float32 dot, chunks on {threads} threads), "
+                      f"median {med * 1e3:.1f} ms/call; host CPU {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE)")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU: this path is measured on a single MI355X (its kernels shard by weight rows "
+              "with no collective; see DESIGN.md). --gpus must be 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    configs = [int(c) for c in a.configs.split(",") if c]
+    if HEADLINE not in configs:
+        configs.insert(0, HEADLINE)
+    res = {}
+    for c in configs:
+        res[c] = run_config(c, a.steps, a.warmup, a.rotate_mb << 20)
+    head = res[HEADLINE]
+    proj = head["projections"]["w"]
+    traffic = None
+    try:
+        with open(a.traffic) as f:
+            traffic = json.load(f).get("c2", {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        traffic = None
+    line = {
+        "metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(head["us_per_step"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded, BASELINE config value ranges, generated on the GPU)",
+        "config": {"workload": "config 2: GGUF Q8_0 decode GEMV x bf16[1,5120] @ W[17408,5120]^T, fp32 accumulate, "
+                               "bf16 out", "M": 1, "N": 17408, "K": 5120, "weight_type": "Q8_0",
+                   "rotation_MB": proj["rotation_MB"]},
+        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "kernel": "mbq::gemv_kernel<8,1,R>", "kernel_us": proj["us"],
+                     "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
+        "configs": {f"c{c}": {k: v for k, v in r.items() if k != "projections"} | {"projections": r["projections"]}
+                    for c, r in res.items()},
+    }
+    line["measured_peaks"] = measured_peaks()
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "mbq_launch.h"
 #include "mbq_layout.h"
 
@@ -45,6 +47,43 @@ __device__ __forceinline__ uint32_t i8_pair(uint32_t w, int p) {
     return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
 }
 
+// bytes 2p, 2p+1 of w (int8 already offset to unsigned by ^0x80) -> bfloat16 pair (q + 128), exact
+__device__ __forceinline__ uint32_t u8_pair(uint32_t w, int p) {
+    const float f0 = (float)((w >> (16 * p)) & 0xFFu);
+    const float f1 = (float)((w >> (16 * p + 8)) & 0xFFu);
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+// a value the compiler keeps in a VGPR (gfx9 VOP3 instructions take no literal operands, so v_and_or_b32 and v_bfi_b32
+// need their constants in registers)
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Q4_K scale/min extraction parameters of sub-block j (0..7) of a super-block, computed once per lane
+struct Q4kSel {
+    bool hi;                 // j >= 4
+    uint32_t sh_lo, w_lo, sh_lo_m, sh_hi, w_hi;
+};
+__device__ __forceinline__ Q4kSel q4k_sel(int j) {
+    Q4kSel r;
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    r.hi = j >= 4;
+    r.sh_lo = sh;
+    r.w_lo = r.hi ? 4u : 6u;
+    r.sh_lo_m = sh + (r.hi ? 4u : 0u);
+    r.sh_hi = sh + 6u;
+    r.w_hi = r.hi ? 2u : 0u;
+    return r;
+}
+// the same values as q4k_scale_min, without branches
+__device__ __forceinline__ void q4k_scale_min_sel(uint32_t s0, uint32_t s1, uint32_t s2, const Q4kSel& q, uint32_t* sc,
+                                                  uint32_t* mn) {
+    *sc = __builtin_amdgcn_ubfe(q.hi ? s2 : s0, q.sh_lo, q.w_lo) | (__builtin_amdgcn_ubfe(s0, q.sh_hi, q.w_hi) << 4);
+    *mn = __builtin_amdgcn_ubfe(q.hi ? s2 : s1, q.sh_lo_m, q.w_lo) | (__builtin_amdgcn_ubfe(s1, q.sh_hi, q.w_hi) << 4);
+}
+
 // Q4_K: scale and min of sub-block j from the super-block's scale dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11):
 // reference src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
 __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t* sc, uint32_t* mn) {
@@ -79,116 +118,214 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// sum over the 64 lanes of a wave through DPP; the total is returned in every lane (read from lane 63)
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]: every lane holds its quad's sum
+    v += dpp_f<0x114, 0xF>(v);   // row_shr:4
+    v += dpp_f<0x118, 0xF>(v);   // row_shr:8: lane 15 of each row holds the row's sum
+    v += dpp_f<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's sum
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 constexpr uint32_t BF16_ONES = 0x3F803F80u;  // bfloat16 pair (1, 1)
 
 // ---------------------------------------------------------------------------------------------------- decode GEMV
-// One wave owns R consecutive weight rows and the whole K; its 64 lanes stride over the rows' 16-byte units
-// (Q4_K: a 32-quant sub-block; Q8_0 / int8: 16 quants). Every load is a 128-bit vector load and a wave's loads of one
-// row are 1 KiB contiguous. Quants become bfloat16 pairs in registers (exact) and meet x through v_dot2_f32_bf16 with
-// float32 accumulation; block scales are applied once per unit in float32; the lanes' partial sums are reduced across
-// the wave at the end. Up to M = 4 activation rows share each weight load.
-template <int T, int M, int R>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ base, int64_t stride,
-                                                   const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
-                                                   const float* __restrict__ srow, const uint16_t* __restrict__ x,
-                                                   int N, int K, void* __restrict__ y, int out_bf16) {
+// One wave owns one weight row and the whole K; the block's 8 waves own 8 consecutive rows and share x, staged once
+// into LDS as bfloat16. The 64 lanes of a wave stride over the row's 16-byte units (Q4_K: a sub-block of 32 quants;
+// Q8_0 / int8: 16 quants), so each wave-wide load reads 1 KiB of the row contiguously. Loads run in double-buffered
+// stages of CH units per lane: the next stage's loads are in flight while the current stage computes, so several HBM
+// round trips overlap in every wave. Quants become bfloat16 pairs in registers (exact) and meet x through
+// v_dot2_f32_bf16 with float32 accumulation; block scales apply once per unit in float32; the lanes' partial sums are
+// reduced across the wave at the end. Up to M = 4 activation rows share each weight load.
+constexpr int GV_WAVES = 8;
+
+template <int T> struct GvUnit;
+template <> struct GvUnit<T_Q4_K> { u32x4 q, meta; };
+template <> struct GvUnit<T_Q8_0> { u32x4 q; uint32_t d; };
+template <> struct GvUnit<T_INT8> { u32x4 q; };
+
+// unit loads from a row's planes: q and sr are wave-uniform bases (scalar registers), v the lane's unit index
+template <int T>
+__device__ __forceinline__ void gv_load(GvUnit<T>& g, const uint8_t* __restrict__ q, const uint8_t* __restrict__ sr, uint32_t v) {
+    g.q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + v * 16u));
+    if constexpr (T == T_Q4_K) g.meta = ld16(sr + (v >> 3) * 16u);
+    if constexpr (T == T_Q8_0) g.d = *reinterpret_cast<const uint16_t*>(sr + (v >> 1) * 2u);
+}
+
+// 16-byte chunk t of unit u of activation row m. In LDS (XL) the chunks are stored chunk-major, [m][t][u], so the
+// lanes of a wave (consecutive units) read consecutive 16-byte words without bank conflicts; from global memory
+// they are read in place, row-major.
+template <bool XL, int UW>
+__device__ __forceinline__ u32x4 x_chunk(const uint16_t* xs, int K, int U, int m, int t, int u) {
+    if constexpr (XL)
+        return ld16(xs + ((int64_t)(m * (UW / 8) + t) * U + u) * 8);
+    else
+        return ld16(xs + (int64_t)m * K + (int64_t)u * UW + t * 8);
+}
+
+// adds unit u's contribution for the M activation rows to acc (act = false: the lane has no unit here and adds an
+// exact zero: its scale is zeroed, the quants it holds are a valid unit's). xs: the activations (x_chunk); xsum: M rows
+// of the per-unit sums of x (float32), precomputed by the block, which take the +128 offset of the quant pairs back
+// out. The dot2 chains are split in two independent accumulators.
+template <int T, int M, bool XL>
+__device__ __forceinline__ void gv_compute(const GvUnit<T>& g, const uint16_t* xs, const float* xsum, int K, int U, int u,
+                                           bool act, const Q4kSel& sel, uint32_t kmask, uint32_t kmagic, float* acc) {
+    if constexpr (T == T_Q4_K) {
+        uint32_t sc, mn;
+        q4k_scale_min_sel(g.meta[1], g.meta[2], g.meta[3], sel, &sc, &mn);
+        float dsc = f16f(g.meta[0]) * (float)sc;        // exact
+        const float dm = f16f(g.meta[0] >> 16) * (float)mn;    // exact
+        float c = 128.f * dsc + dm;
+        dsc = act ? dsc : 0.f;
+        c = act ? c : 0.f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float P0 = 0.f, P1 = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; t += 2) {
+                const u32x4 xa = x_chunk<XL, 32>(xs, K, U, m, t, u), xb = x_chunk<XL, 32>(xs, K, U, m, t + 1, u);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    P0 = dot2((((g.q[t] >> (4 * p)) & kmask) | kmagic), xa[p], P0);
+                    P1 = dot2((((g.q[t + 1] >> (4 * p)) & kmask) | kmagic), xb[p], P1);
+                }
+            }
+            acc[m] += dsc * (P0 + P1) - c * xsum[m * U + u];
+        }
+    } else {
+        float d = 1.f;
+        if constexpr (T == T_Q8_0) d = f16f(g.d);
+        d = act ? d : 0.f;
+        u32x4 q;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) q[t] = g.q[t] ^ 0x80808080u;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const u32x4 x0 = x_chunk<XL, 16>(xs, K, U, m, 0, u), x1 = x_chunk<XL, 16>(xs, K, U, m, 1, u);
+            float P0 = 0.f, P1 = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    P0 = dot2(u8_pair(q[t], p), x0[(t << 1) + p], P0);
+                    P1 = dot2(u8_pair(q[t + 2], p), x1[(t << 1) + p], P1);
+                }
+            acc[m] += d * ((P0 + P1) - 128.f * xsum[m * U + u]);
+        }
+    }
+}
+
+// Persistent decode GEMV: the grid is exactly the blocks the GPU holds at once, so there is no second round of
+// blocks. Block b owns rows [b*N/P, (b+1)*N/P); each row is cut into S parts of at most 64*CH units, so one part is
+// one wave-wide batch of CH 16-byte loads per lane. The block's waves take the (row, part) items round-robin, with
+// the next item's loads in flight while the current one computes; each item's partial sums are reduced across the
+// wave with DPP into LDS, and the block adds the S parts of each row at the end. Item bookkeeping is wave-uniform
+// (scalar registers); lanes only form 32-bit unit offsets.
+template <int T, int M, int CH, bool XL>
+__global__ __launch_bounds__(64 * GV_WAVES, 2) void gemv_kernel(const uint8_t* __restrict__ base, int64_t stride,
+                                                            const int32_t* __restrict__ layer_dev, int nlayers,
+                                                            int64_t sc_off, const float* __restrict__ srowscale,
+                                                            const uint16_t* __restrict__ x, int N, int K, int S,
+                                                            void* __restrict__ y, int out_bf16) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];   // [x: M x K bf16] [xsum: M x U f32] [parts]
+    constexpr int UW = (T == T_Q4_K) ? 32 : 16;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * 4 + wave) * R;
-    if (n0 >= N) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int P = gridDim.x;
+    const int r0 = (int)((int64_t)blockIdx.x * N / P), r1 = (int)((int64_t)(blockIdx.x + 1) * N / P);
     const int64_t lo = layer_offset(stride, layer_dev, nlayers);
     const bool ok = lo >= 0;
     base += ok ? lo : 0;
-    float acc[R][M];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+    const int U = K / UW;
+    const int PU = (U + S - 1) / S;           // units per part (<= 64 * CH)
+    const int items = (r1 - r0) * S;
+    const int64_t qstride = (int64_t)U * 16;
+    const int64_t sstride = (T == T_Q4_K) ? (int64_t)(K >> 8) * 16 : (int64_t)(K >> 5) * 2;
+    float* xsum = reinterpret_cast<float*>(lds + (XL ? M * K : 0));
+    float* parts = xsum + M * U;              // (r1 - r0) x S x M
 
-    if (ok) {
-        if constexpr (T == T_Q4_K) {
-            const int U = K >> 5;
-            const int64_t rq = K >> 1;
-            const int nsb = K >> 8;
-            const int j = lane & 7;  // sub-block of the super-block: lane-constant since units advance by 64
-            for (int u = lane; u < U; u += 64) {
-                u32x4 xv[M][4];
-                float xs[M];
+    const uint32_t kmask = in_vgpr(0x000F000Fu), kmagic = in_vgpr(0x43004300u);
+    GvUnit<T> A[CH], B[CH];
+    // item it (wave-uniform) -> row, first unit u0, unit count nu
+    auto load = [&](GvUnit<T>* G, int it) {
+        const int row = r0 + it / S, u0 = (it % S) * PU, nu = min(PU, U - u0);
+        const uint8_t* q = base + row * qstride;
+        const uint8_t* sr = base + sc_off + row * sstride;
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) xv[m][i] = ld16(x + (int64_t)m * K + (int64_t)u * 32 + i * 8);
-                    float s = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int p = 0; p < 4; ++p) s = dot2(xv[m][i][p], BF16_ONES, s);
-                    xs[m] = s;
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t n = min(n0 + r, N - 1);
-                    const u32x4 w = ld16(base + n * rq + (int64_t)u * 16);
-                    const u32x4 mt = ld16(base + sc_off + (n * nsb + (u >> 3)) * 16);
-                    uint32_t sc, mn;
-                    q4k_scale_min(mt[1], mt[2], mt[3], j, &sc, &mn);
-                    const float dsc = f16f(mt[0]) * (float)sc;          // exact
-                    const float dm = f16f(mt[0] >> 16) * (float)mn;      // exact
-                    const float c = 128.f * dsc + dm;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        float P = 0.f;
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-#pragma unroll
-                            for (int p = 0; p < 4; ++p) P = dot2(nib_pair(w[t], p), xv[m][t][p], P);
-                        acc[r][m] += dsc * P - c * xs[m];
-                    }
-                }
-            }
-        } else {  // Q8_0 and int8: 16-quant units
-            const int U = K >> 4;
-            for (int u = lane; u < U; u += 64) {
-                u32x4 xv[M][2];
-#pragma unroll
-                for (int m = 0; m < M; ++m)
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) xv[m][i] = ld16(x + (int64_t)m * K + (int64_t)u * 16 + i * 8);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int64_t n = min(n0 + r, N - 1);
-                    const u32x4 w = ld16(base + n * K + (int64_t)u * 16);
-                    float d = 1.f;
-                    if constexpr (T == T_Q8_0)
-                        d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + (n * (K >> 5) + (u >> 1)) * 2));
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        float P = 0.f;
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-#pragma unroll
-                            for (int p = 0; p < 2; ++p) P = dot2(i8_pair(w[t], p), xv[m][t >> 1][((t & 1) << 1) + p], P);
-                        if constexpr (T == T_Q8_0)
-                            acc[r][m] += d * P;
-                        else
-                            acc[r][m] += P;
-                    }
-                }
-            }
+        for (int i = 0; i < CH; ++i) {
+            if (64 * i >= nu) break;           // wave-uniform: no lane has a unit in this slot
+            const int li = (lane + 64 * i < nu) ? lane + 64 * i : 0;
+            gv_load<T>(G[i], q, sr, (uint32_t)(u0 + li));
         }
-    }
+    };
+
+    const bool any = ok && wave < items;
+    if (any) load(A, wave);
+
+    // per-unit sums of x (float32), and in LDS mode the activations themselves, chunk-major [m][t][u]
+    for (int e = threadIdx.x; e < M * U; e += 64 * GV_WAVES) {
+        const int m = e / U, u = e - m * U;
+        const uint16_t* xu = x + (int64_t)m * K + (int64_t)u * UW;
+        float sum = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int n = n0 + r;
-        const float s = (T == T_INT8 && n < N) ? srow[n] : 1.f;
+        for (int t = 0; t < UW / 8; ++t) {
+            const u32x4 v = ld16(xu + t * 8);
+            if constexpr (XL) st16(lds + ((m * (UW / 8) + t) * U + u) * 8, v);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) sum = dot2(v[p], BF16_ONES, sum);
+        }
+        xsum[e] = sum;
+    }
+    __syncthreads();
+    const uint16_t* xa = XL ? lds : x;
+
+    auto finish = [&](const GvUnit<T>* G, int it) {
+        const int rl = it / S, p = it % S, u0 = p * PU, nu = min(PU, U - u0);
+        float acc[CH][M];
+#pragma unroll
+        for (int i = 0; i < CH; ++i)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
+        const Q4kSel sel = q4k_sel((u0 + lane) & 7);   // units advance by 64: the lane's sub-block slot is fixed
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            if (64 * i >= nu) break;           // wave-uniform
+            const bool act = lane + 64 * i < nu;
+            const int u = act ? u0 + lane + 64 * i : u0 + lane;   // inactive: a unit of the same slot, scale zeroed
+            gv_compute<T, M, XL>(G[i], xa, xsum, K, U, u < U ? u : u0, act, sel, kmask, kmagic, acc[i]);
+        }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            float v = wave_sum(acc[r][m]);
-            if (lane == 0 && n < N) {
-                v = ok ? v * s : __builtin_nanf("");
-                store_y(y, (int64_t)m * N + n, v, out_bf16);
-            }
+            float v = 0.f;
+#pragma unroll
+            for (int i = 0; i < CH; ++i) v += acc[i][m];
+            v = wave_sum_dpp(v);
+            if (lane == 0) parts[(rl * S + p) * M + m] = v;
         }
+    };
+    if (any) {
+        for (int it = wave; it < items; it += 2 * GV_WAVES) {
+            const int nx = it + GV_WAVES;
+            if (nx < items) load(B, nx);
+            finish(A, it);
+            if (nx + GV_WAVES < items) load(A, nx + GV_WAVES);
+            if (nx < items) finish(B, nx);
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < (r1 - r0) * M; e += 64 * GV_WAVES) {
+        const int rl = e / M, m = e - rl * M, n = r0 + rl;
+        float v = 0.f;
+        for (int p = 0; p < S; ++p) v += parts[(rl * S + p) * M + m];
+        const float sc = (T == T_INT8) ? srowscale[n] : 1.f;
+        store_y(y, (int64_t)m * N + n, ok ? v * sc : __builtin_nanf(""), out_bf16);
     }
 }
 
@@ -420,24 +557,55 @@ static int check_launch(const char* what) {
     return 0;
 }
 
+// blocks of a GEMV kernel the GPU holds at once (cached per kernel and LDS size)
+template <class K>
+static int resident_blocks(K kernel, size_t lds) {
+    static thread_local struct { const void* k; size_t lds; int n; } cache[32];
+    static thread_local int used = 0;
+    for (int i = 0; i < used; ++i)
+        if (cache[i].k == (const void*)kernel && cache[i].lds == lds) return cache[i].n;
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 64 * GV_WAVES, lds) != hipSuccess || per < 1)
+        return -1;
+    const int n = cus * per;
+    if (used < 32) cache[used++] = {(const void*)kernel, lds, n};
+    return n;
+}
+
 template <int T, int M>
-static void launch_gemv_m(const Args& a, hipStream_t s) {
-    constexpr int R = 2;
-    const dim3 grid((unsigned)((a.N + 4 * R - 1) / (4 * R)));
-    gemv_kernel<T, M, R><<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.srow, a.x, (int)a.N,
-                                              (int)a.K, a.y, a.out_bf16);
+static int launch_gemv_m(const Args& a, hipStream_t s) {
+    constexpr int CH = (T == T_Q4_K) ? (M == 1 ? 4 : 2) : (M <= 2 ? 4 : 2);
+    const int64_t UW = (T == T_Q4_K) ? 32 : 16;
+    const int64_t U = a.K / UW;
+    const int S = (int)((U + 64 * CH - 1) / (64 * CH));
+    const size_t xbytes = (size_t)M * a.K * 2, sums = (size_t)M * U * 4;
+    const bool xl = xbytes + sums <= (size_t)GEMV_MAX_LDS;
+    auto kern = xl ? gemv_kernel<T, M, CH, true> : gemv_kernel<T, M, CH, false>;
+    // parts: rows per block x S x M floats; the block count depends on the LDS, so settle it in two steps
+    size_t lds = (xl ? xbytes : 0) + sums;
+    int P = resident_blocks(kern, lds + 4096);
+    if (P < 1) return set_error(MBQ_LAUNCH_FAIL, "GEMV occupancy query failed");
+    P = (int)std::min<int64_t>(P, a.N);
+    const int64_t rows_max = (a.N + P - 1) / P;
+    lds += (size_t)rows_max * S * M * 4;
+    if (lds > 160 * 1024) return set_error(MBQ_BAD_ARG, "GEMV K = %lld, N = %lld needs too much LDS", (long long)a.K, (long long)a.N);
+    kern<<<dim3((unsigned)P), 64 * GV_WAVES, lds, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.srow, a.x,
+                                                      (int)a.N, (int)a.K, S, a.y, a.out_bf16);
+    return 0;
 }
 
 template <int T>
 static int launch_t(const Args& a, hipStream_t s) {
     if (a.M <= GEMV_MAX_M) {
+        int rc;
         switch (a.M) {
-            case 1: launch_gemv_m<T, 1>(a, s); break;
-            case 2: launch_gemv_m<T, 2>(a, s); break;
-            case 3: launch_gemv_m<T, 3>(a, s); break;
-            default: launch_gemv_m<T, 4>(a, s); break;
+            case 1: rc = launch_gemv_m<T, 1>(a, s); break;
+            case 2: rc = launch_gemv_m<T, 2>(a, s); break;
+            case 3: rc = launch_gemv_m<T, 3>(a, s); break;
+            default: rc = launch_gemv_m<T, 4>(a, s); break;
         }
-        return check_launch("gemv");
+        return rc ? rc : check_launch("gemv");
     }
     const dim3 grid((unsigned)((a.N + GB_N - 1) / GB_N), (unsigned)((a.M + GB_M - 1) / GB_M));
     gemm_kernel<T><<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.srow, a.x, (int)a.M,

@@ -9,6 +9,8 @@ enum : int { MBQ_BAD_ARG = -1, MBQ_LAUNCH_FAIL = -2, MBQ_SMALL_CAP = -3 };
 
 // activation rows up to which the GEMV runs; more rows take the MFMA GEMM
 constexpr int64_t GEMV_MAX_M = 4;
+// activations (M x K bfloat16) up to this many bytes are staged in LDS by the GEMV; larger ones are read from the caches
+constexpr int64_t GEMV_MAX_LDS = 64 * 1024;
 
 struct Args {
     const uint8_t* base;       // planes of the weight (layer already applied when the layer is a host value)

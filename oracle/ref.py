@@ -156,20 +156,31 @@ def exact_chunk_rows(rows: int, cols: int, limit: int | None = None) -> int:
     return best
 
 
-def qmatmul_exact(x: np.ndarray, raw: np.ndarray, t: int, shape, limit: int | None = None) -> np.ndarray:
+def qmatmul_exact(x: np.ndarray, raw: np.ndarray, t: int, shape, limit: int | None = None, threads: int = 1) -> np.ndarray:
     """x (..., cols) float32 values @ W.T -> (..., rows) float32 (NOT yet rounded to x's dtype).
 
     The exact path: the float32 weights are rebuilt from the blocks a chunk of rows at a time and multiplied with a
-    float32 dot (src/mashbox/ops/__init__.py:574-576, 624-632). The caller rounds to the activation dtype (bf16)."""
+    float32 dot (src/mashbox/ops/__init__.py:574-576, 624-632). The caller rounds to the activation dtype (bf16).
+    threads > 1 runs the row chunks concurrently (XLA:CPU runs the reference's program on all host cores)."""
     rows, cols = int(shape[-2]), int(shape[-1])
     rb = row_bytes(t, cols)
     raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(rows, rb)
     x = np.asarray(x, np.float32)
     rc = exact_chunk_rows(rows, cols, limit)
     out = np.empty(x.shape[:-1] + (rows,), np.float32)
-    for a in range(0, rows, rc):
+
+    def chunk(a):
         w = dequant(raw[a:a + rc], t, cols)                   # (rc, cols) f32
         out[..., a:a + rc] = x @ w.T
+
+    starts = range(0, rows, rc)
+    if threads > 1 and len(starts) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(min(threads, len(starts))) as ex:
+            list(ex.map(chunk, starts))
+    else:
+        for a in starts:
+            chunk(a)
     return out
 
 
