@@ -1,0 +1,66 @@
+"""Writes the golden fixtures of tests/golden (run in the build container, where the reference tree is mounted).
+
+    python tests/golden/make_golden.py [/root/reference]
+
+Fixtures (NumPy .npz, no pickles):
+  random_<TYPE>_k<KB>.npz    6 rows x KB blocks of random bytes with an all-zero row and an all-0xFF row (every fp16
+                             scale value: normal, subnormal, inf, NaN), the shape of the reference's own dequant test
+                             (reference tests/cpu/test_gguf_dequant.py:20-27); raw -> w (float32 dequant bits)
+  kquant_<file>_<tensor>.npz real llama-quantize blocks: the first 16 rows of the Q4_K and Q8_0 weights of the
+                             reference's fixture models (reference tests/fixtures/gguf/*-kquant.gguf, Apache-2.0, made by
+                             llama-quantize at llama.cpp a37cc46; the source file's sha256 is stored), with 3 bf16
+                             activation rows x and their float64 product y64
+Expected values come from the oracle (oracle/ref.py), pinned independently by tests/test_oracle.py; the fixtures freeze
+them so that a later change to the oracle or the kernels is checked against the same bytes.
+"""
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from mashbox_amd import gguf  # noqa: E402
+from oracle import gen as G  # noqa: E402
+from oracle import ref as R  # noqa: E402
+
+KQUANT = [("qwen3-kquant", ["blk.0.attn_k.weight", "blk.0.ffn_gate.weight", "blk.0.attn_q.weight", "token_embd.weight"]),
+          ("gemma4-kquant", ["blk.0.ffn_up.weight", "blk.0.ffn_down.weight"])]
+
+
+def main(ref_root):
+    names = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K"}
+    for t in (R.Q8_0, R.Q4_K):
+        for kb in (1, 2, 16):
+            rng = np.random.default_rng(7000 + 10 * t + kb)
+            cols = R.TYPES[t][1] * kb
+            raw = rng.integers(0, 256, size=(6, R.row_bytes(t, cols)), dtype=np.uint8)
+            raw[0], raw[1] = 0, 0xFF
+            np.savez_compressed(os.path.join(HERE, f"random_{names[t]}_k{kb}.npz"), t=t, cols=cols, raw=raw,
+                                w=R.dequant(raw, t, cols))
+    for fname, tensors in KQUANT:
+        path = os.path.join(ref_root, "tests", "fixtures", "gguf", fname + ".gguf")
+        sha = hashlib.sha256(open(path, "rb").read()).hexdigest()
+        with gguf.File(path) as f:
+            for tn in tensors:
+                ten = f.tensors[tn]
+                rows, cols = ten.shape
+                raw = np.array(ten.rows()[:16])
+                w = R.dequant(raw, ten.type, cols)
+                rng = np.random.default_rng(len(tn) + cols)
+                x = G.acts(rng, 3, cols)
+                y64 = R.bf16_to_f32(x).astype(np.float64) @ w.astype(np.float64).T
+                out = os.path.join(HERE, f"kquant_{fname.split('-')[0]}_{tn.replace('.weight', '').replace('.', '_')}.npz")
+                np.savez_compressed(out, t=ten.type, cols=cols, raw=raw, w=w, x=x, y64=y64,
+                                    source=np.array(f"{fname}.gguf sha256 {sha} tensor {tn} {ten.type_name} "
+                                                    f"({rows}, {cols}) rows 0-15"))
+    for n in sorted(os.listdir(HERE)):
+        if n.endswith(".npz"):
+            print(n, os.path.getsize(os.path.join(HERE, n)))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,102 @@
+"""The C ABI of libmbq.so without a GPU: it loads, exports every entry point include/mbq.h declares, and its host-side
+entry points (type table, shapes, plane sizes, the host repack and its inverse, argument checks) behave as declared.
+No entry point that launches a kernel is called with valid arguments here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import gen as G
+from oracle import ref as R
+
+import mashbox_amd._lib as L
+import mashbox_amd.kernels as KQ
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = []
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if h.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", h)).read()
+            src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+            names += re.findall(r"\b(mbq_\w+)\s*\(", src)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    names = _declared()
+    assert len(names) >= 12, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported by libmbq.so"
+    assert set(names) == set(L._SIGS), "ctypes signatures and include/mbq.h disagree"
+
+
+def test_type_table_and_shapes():
+    lib = L.lib()
+    assert lib.mbq_version() >= 100
+    assert lib.mbq_has_type(8) == 1 and lib.mbq_has_type(12) == 1 and lib.mbq_has_type(14) == 0
+    assert lib.mbq_row_bytes(8, 5120) == R.row_bytes(8, 5120) == 5440
+    assert lib.mbq_row_bytes(12, 17408) == R.row_bytes(12, 17408) == 9792
+    assert lib.mbq_row_bytes(12, 100) < 0
+    assert KQ.kq_covers(8, (17408, 5120)) and KQ.kq_covers(12, (5120, 17408))
+    assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(14, (256, 256))
+    for t, (n, k) in [(8, (17408, 5120)), (12, (5120, 17408)), (12, (1, 256)), (8, (3, 32))]:
+        pb = KQ.plane_bytes(t, (n, k))
+        file_bytes = n * R.row_bytes(t, k)
+        assert pb % 256 == 0 and file_bytes <= pb < file_bytes + 512
+
+
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K])
+def test_host_repack_is_lossless(t):
+    rng = np.random.default_rng(40 + t)
+    for n, kb in [(1, 1), (7, 3), (130, 2)]:
+        k = R.TYPES[t][1] * kb
+        raw = rng.integers(0, 256, (n, R.row_bytes(t, k)), dtype=np.uint8)
+        p = KQ.repack_host(t, raw, (n, k), threads=3)
+        back = np.zeros_like(raw)
+        rc = L.lib().mbq_unpack_host(t, ctypes.c_void_p(p.buf.data_ptr()), n, k, back.ctypes.data_as(ctypes.c_void_p),
+                                     back.size)
+        assert rc == 0 and np.array_equal(back, raw)
+
+
+def test_q4_k_unit_layout_yields_bf16_pairs():
+    """a Q4_K plane dword t of a unit holds quants 8t..8t+7 so that ((w >> 4p) & 0x000F000F) | 0x43004300 is the
+    bfloat16 pair (128 + q[8t+2p], 128 + q[8t+2p+1]): checked on the host against the oracle's nibble split"""
+    rng = np.random.default_rng(41)
+    raw = G.q4_k_raw(rng, 2, 256)
+    p = KQ.repack_host(R.Q4_K, raw, (2, 256)).buf.numpy()
+    units = p[:2 * 128].view(np.uint32).reshape(2, 8, 4)            # (row, sub-block, dword)
+    b = raw.reshape(2, 144)
+    q = R.nib(b[:, 16:].reshape(2, 4, 32)).reshape(2, 8, 32)        # oracle's quant order
+    for p_ in range(4):
+        pair = ((units >> np.uint32(4 * p_)) & np.uint32(0x000F000F)) | np.uint32(0x43004300)
+        lo = R.bf16_to_f32((pair & 0xFFFF).astype(np.uint16)) - 128
+        hi = R.bf16_to_f32((pair >> 16).astype(np.uint16)) - 128
+        for t_ in range(4):
+            assert np.array_equal(lo[:, :, t_], q[:, :, 8 * t_ + 2 * p_])
+            assert np.array_equal(hi[:, :, t_], q[:, :, 8 * t_ + 2 * p_ + 1])
+
+
+def test_argument_errors_are_reported_without_a_launch():
+    lib = L.lib()
+    null = ctypes.c_void_p(0)
+    assert lib.mbq_matmul(14, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1
+    assert b"type" in lib.mbq_last_error()
+    assert lib.mbq_matmul(12, null, 0, None, 1, null, 1, 8, 200, null, 0, null) == -1
+    assert b"multiple" in lib.mbq_last_error()
+    assert lib.mbq_matmul(12, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1   # NULL planes
+    assert lib.mbq_matmul(12, ctypes.c_void_p(16), 5, None, 2, null, 1, 8, 256, null, 0, null) == -1
+    assert b"layer" in lib.mbq_last_error()
+    assert lib.mbq_matmul(12, ctypes.c_void_p(16), 0, None, 1, null, 1, 8, 256, null, 7, null) == -1
+    assert lib.mbq_int8_linear(null, null, null, 1, 8, 100, null, 1, null) == -1         # K % 16
+    small = np.zeros(16, np.uint8)
+    raw = np.zeros((1, 144), np.uint8)
+    assert lib.mbq_repack_host(12, raw.ctypes.data_as(ctypes.c_void_p), 1, 256,
+                               small.ctypes.data_as(ctypes.c_void_p), small.size, 1) == -3
+    with pytest.raises(L.MbqError):
+        L.check(-1, "x")

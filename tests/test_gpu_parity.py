@@ -200,3 +200,26 @@ def test_batched_gemm_full_config_sampled(idx, cuda):
             ref = xf @ R.dequant(wts[ns], cfg["t"], k).astype(np.float64).T
         got = y.float().cpu().numpy()[np.ix_(ms, ns)]
         assert_product(got, ref, f"config {idx} {name}")
+
+
+# ------------------------------------------------------------------------------------------------ golden fixtures
+import os  # noqa: E402
+
+_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(_GOLDEN) if f.endswith(".npz")))
+def test_golden_fixture(name, cuda):
+    """committed fixtures (random bytes with zero / 0xFF rows; real llama-quantize blocks of the reference's fixture
+    models): dequant bit for bit, and the product within the bars"""
+    z = np.load(os.path.join(_GOLDEN, name), allow_pickle=False)
+    t, cols, raw = int(z["t"]), int(z["cols"]), z["raw"]
+    rows = raw.shape[0]
+    planes = KQ.repack_host(t, raw, (rows, cols)).to(cuda)
+    assert diff_bits(KQ.dequant(planes).cpu().numpy(), z["w"]) == 0
+    dev_planes = KQ.repack(t, torch.from_numpy(raw).to(cuda), (rows, cols))
+    assert torch.equal(dev_planes.buf, planes.buf)
+    if "x" in z.files:
+        for m in (1, 3):
+            y = KQ.matmul(_bf16_tensor(z["x"][:m], cuda), planes).cpu().numpy()
+            assert_product(y, z["y64"][:m], name)
