@@ -146,6 +146,7 @@ static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t
         return set_error(MBQ_BAD_ARG, "layer %lld outside the stack of %lld", (long long)layer, (long long)nlayers);
     const Layout L = layout(t, N, K);
     a->stride = L.total;
+    a->wbytes = L.total;
     a->base = planes + (layer_dev ? 0 : layer * L.total);
     a->layer_dev = layer_dev;
     a->nlayers = (int)nlayers;
@@ -252,6 +253,7 @@ int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_d
     Args a{};
     a.base = reinterpret_cast<const uint8_t*>(q_dev);
     a.stride = 0;
+    a.wbytes = N * K;
     a.layer_dev = nullptr;
     a.nlayers = 1;
     a.sc_off = 0;

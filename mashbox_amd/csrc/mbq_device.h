@@ -1,0 +1,143 @@
+// Device helpers shared by the gfx950 kernels (vector types, exact conversions, Q4_K scale unpack, wave sums).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mbq {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ----------------------------------------------------------------------------------------------------- helpers
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// fp16 bits -> float32, exact (subnormal, inf and NaN kept): reference src/mashbox/ops/reference.py:49-51
+__device__ __forceinline__ float f16f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu)); }
+
+// float32 -> bfloat16 bits, round to nearest even; NaN stays NaN (quiet)
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Q4_K unit dword -> bfloat16 pair (128 + q[8t+2p], 128 + q[8t+2p+1]); exact (mbq_layout.h)
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int p) { return ((w >> (4 * p)) & 0x000F000Fu) | 0x43004300u; }
+
+// int8 bytes 2p, 2p+1 of w -> bfloat16 pair, exact (every int8 is a bfloat16)
+__device__ __forceinline__ uint32_t i8_pair(uint32_t w, int p) {
+    const float f0 = (float)(int8_t)(w >> (16 * p));
+    const float f1 = (float)(int8_t)(w >> (16 * p + 8));
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+// bytes 2p, 2p+1 of w (int8 already offset to unsigned by ^0x80) -> bfloat16 pair (q + 128), exact
+__device__ __forceinline__ uint32_t u8_pair(uint32_t w, int p) {
+    const float f0 = (float)((w >> (16 * p)) & 0xFFu);
+    const float f1 = (float)((w >> (16 * p + 8)) & 0xFFu);
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+// a value the compiler keeps in a VGPR (gfx9 VOP3 instructions take no literal operands, so v_and_or_b32 and v_bfi_b32
+// need their constants in registers)
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Q4_K scale/min extraction parameters of sub-block j (0..7) of a super-block, computed once per lane
+struct Q4kSel {
+    bool hi;                 // j >= 4
+    uint32_t sh_lo, w_lo, sh_lo_m, sh_hi, w_hi;
+};
+__device__ __forceinline__ Q4kSel q4k_sel(int j) {
+    Q4kSel r;
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    r.hi = j >= 4;
+    r.sh_lo = sh;
+    r.w_lo = r.hi ? 4u : 6u;
+    r.sh_lo_m = sh + (r.hi ? 4u : 0u);
+    r.sh_hi = sh + 6u;
+    r.w_hi = r.hi ? 2u : 0u;
+    return r;
+}
+// the same values as q4k_scale_min, without branches
+__device__ __forceinline__ void q4k_scale_min_sel(uint32_t s0, uint32_t s1, uint32_t s2, const Q4kSel& q, uint32_t* sc,
+                                                  uint32_t* mn) {
+    *sc = __builtin_amdgcn_ubfe(q.hi ? s2 : s0, q.sh_lo, q.w_lo) | (__builtin_amdgcn_ubfe(s0, q.sh_hi, q.w_hi) << 4);
+    *mn = __builtin_amdgcn_ubfe(q.hi ? s2 : s1, q.sh_lo_m, q.w_lo) | (__builtin_amdgcn_ubfe(s1, q.sh_hi, q.w_hi) << 4);
+}
+
+// Q4_K: scale and min of sub-block j from the super-block's scale dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11):
+// reference src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t* sc, uint32_t* mn) {
+    const int sh = 8 * (j & 3);
+    if (j < 4) {
+        *sc = (s0 >> sh) & 63u;
+        *mn = (s1 >> sh) & 63u;
+    } else {
+        *sc = ((s2 >> sh) & 15u) | (((s0 >> (sh + 6)) & 3u) << 4);
+        *mn = ((s2 >> (sh + 4)) & 15u) | (((s1 >> (sh + 6)) & 3u) << 4);
+    }
+}
+
+// byte offset of the layer a kernel reads; -1 when layer_dev names no layer of the stack
+__device__ __forceinline__ int64_t layer_offset(int64_t stride, const int32_t* layer_dev, int nlayers) {
+    if (layer_dev == nullptr) return 0;
+    const int l = *layer_dev;
+    if (l < 0 || l >= nlayers) return -1;
+    return (int64_t)l * stride;
+}
+
+__device__ __forceinline__ void store_y(void* y, int64_t i, float v, int out_bf16) {
+    if (out_bf16)
+        reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)bf16_bits(v);
+    else
+        reinterpret_cast<float*>(y)[i] = v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// sum over the 64 lanes of a wave through DPP; the total is returned in every lane (read from lane 63)
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]: every lane holds its quad's sum
+    v += dpp_f<0x114, 0xF>(v);   // row_shr:4
+    v += dpp_f<0x118, 0xF>(v);   // row_shr:8: lane 15 of each row holds the row's sum
+    v += dpp_f<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's sum
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+constexpr uint32_t BF16_ONES = 0x3F803F80u;  // bfloat16 pair (1, 1)
+
+// a value the compiler treats as unknown, so that it keeps one AND of a two-quant mask instead of splitting it per byte
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// two float32 -> bfloat16 pair (lo, hi), round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    const bf16x2_t p = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, p);
+}
+
+}  // namespace mbq

@@ -1,4 +1,4 @@
-// gfx950 (CDNA4) kernels of the quantized linear: decode GEMV, MFMA GEMM, dequant and device repack.
+// gfx950 (CDNA4) kernels of the quantized linear: decode GEMV, dequant and device repack (the MFMA GEMM: mbq_gemm.hip).
 //
 // Semantics follow reference src/mashbox/ops/__init__.py:594-632 (qmatmul: x @ W.T, float32 accumulation) with the
 // weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K), and the int8 per-channel
@@ -8,133 +8,12 @@
 
 #include <algorithm>
 
+#include "mbq_device.h"
 #include "mbq_launch.h"
 #include "mbq_layout.h"
 
 namespace mbq {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// ----------------------------------------------------------------------------------------------------- helpers
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
-
-// fp16 bits -> float32, exact (subnormal, inf and NaN kept): reference src/mashbox/ops/reference.py:49-51
-__device__ __forceinline__ float f16f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu)); }
-
-// float32 -> bfloat16 bits, round to nearest even; NaN stays NaN (quiet)
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// Q4_K unit dword -> bfloat16 pair (128 + q[8t+2p], 128 + q[8t+2p+1]); exact (mbq_layout.h)
-__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int p) { return ((w >> (4 * p)) & 0x000F000Fu) | 0x43004300u; }
-
-// int8 bytes 2p, 2p+1 of w -> bfloat16 pair, exact (every int8 is a bfloat16)
-__device__ __forceinline__ uint32_t i8_pair(uint32_t w, int p) {
-    const float f0 = (float)(int8_t)(w >> (16 * p));
-    const float f1 = (float)(int8_t)(w >> (16 * p + 8));
-    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-}
-
-// bytes 2p, 2p+1 of w (int8 already offset to unsigned by ^0x80) -> bfloat16 pair (q + 128), exact
-__device__ __forceinline__ uint32_t u8_pair(uint32_t w, int p) {
-    const float f0 = (float)((w >> (16 * p)) & 0xFFu);
-    const float f1 = (float)((w >> (16 * p + 8)) & 0xFFu);
-    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-}
-
-// a value the compiler keeps in a VGPR (gfx9 VOP3 instructions take no literal operands, so v_and_or_b32 and v_bfi_b32
-// need their constants in registers)
-__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-// Q4_K scale/min extraction parameters of sub-block j (0..7) of a super-block, computed once per lane
-struct Q4kSel {
-    bool hi;                 // j >= 4
-    uint32_t sh_lo, w_lo, sh_lo_m, sh_hi, w_hi;
-};
-__device__ __forceinline__ Q4kSel q4k_sel(int j) {
-    Q4kSel r;
-    const uint32_t sh = 8u * (uint32_t)(j & 3);
-    r.hi = j >= 4;
-    r.sh_lo = sh;
-    r.w_lo = r.hi ? 4u : 6u;
-    r.sh_lo_m = sh + (r.hi ? 4u : 0u);
-    r.sh_hi = sh + 6u;
-    r.w_hi = r.hi ? 2u : 0u;
-    return r;
-}
-// the same values as q4k_scale_min, without branches
-__device__ __forceinline__ void q4k_scale_min_sel(uint32_t s0, uint32_t s1, uint32_t s2, const Q4kSel& q, uint32_t* sc,
-                                                  uint32_t* mn) {
-    *sc = __builtin_amdgcn_ubfe(q.hi ? s2 : s0, q.sh_lo, q.w_lo) | (__builtin_amdgcn_ubfe(s0, q.sh_hi, q.w_hi) << 4);
-    *mn = __builtin_amdgcn_ubfe(q.hi ? s2 : s1, q.sh_lo_m, q.w_lo) | (__builtin_amdgcn_ubfe(s1, q.sh_hi, q.w_hi) << 4);
-}
-
-// Q4_K: scale and min of sub-block j from the super-block's scale dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11):
-// reference src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
-__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t* sc, uint32_t* mn) {
-    const int sh = 8 * (j & 3);
-    if (j < 4) {
-        *sc = (s0 >> sh) & 63u;
-        *mn = (s1 >> sh) & 63u;
-    } else {
-        *sc = ((s2 >> sh) & 15u) | (((s0 >> (sh + 6)) & 3u) << 4);
-        *mn = ((s2 >> (sh + 4)) & 15u) | (((s1 >> (sh + 6)) & 3u) << 4);
-    }
-}
-
-// byte offset of the layer a kernel reads; -1 when layer_dev names no layer of the stack
-__device__ __forceinline__ int64_t layer_offset(int64_t stride, const int32_t* layer_dev, int nlayers) {
-    if (layer_dev == nullptr) return 0;
-    const int l = *layer_dev;
-    if (l < 0 || l >= nlayers) return -1;
-    return (int64_t)l * stride;
-}
-
-__device__ __forceinline__ void store_y(void* y, int64_t i, float v, int out_bf16) {
-    if (out_bf16)
-        reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)bf16_bits(v);
-    else
-        reinterpret_cast<float*>(y)[i] = v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
-}
-
-// sum over the 64 lanes of a wave through DPP; the total is returned in every lane (read from lane 63)
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += dpp_f<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]: every lane holds its quad's sum
-    v += dpp_f<0x114, 0xF>(v);   // row_shr:4
-    v += dpp_f<0x118, 0xF>(v);   // row_shr:8: lane 15 of each row holds the row's sum
-    v += dpp_f<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
-    v += dpp_f<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's sum
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-constexpr uint32_t BF16_ONES = 0x3F803F80u;  // bfloat16 pair (1, 1)
 
 // ---------------------------------------------------------------------------------------------------- decode GEMV
 // One wave owns one weight row and the whole K; the block's 8 waves own 8 consecutive rows and share x, staged once
@@ -329,140 +208,6 @@ __global__ __launch_bounds__(64 * GV_WAVES, 2) void gemv_kernel(const uint8_t* _
     }
 }
 
-// ------------------------------------------------------------------------------------------------------ MFMA GEMM
-// Block tile 64 x 64 x 64, 4 waves (2 x 2), each wave 32 x 32 = 2 x 2 tiles of v_mfma_f32_16x16x32_bf16.
-// x tiles are copied to LDS; weight tiles are dequantized into LDS as bfloat16 (int8: exact; Q8_0 / Q4_K: the float32
-// dequantized value rounded to nearest even), then both feed the MFMA with float32 accumulation.
-constexpr int GB_M = 64, GB_N = 64, GB_K = 64, G_LDS = GB_K + 8;
-
-template <int T>
-__device__ __forceinline__ void load_b_tile(uint16_t (*Bs)[G_LDS], const uint8_t* __restrict__ base, int64_t sc_off,
-                                            int n0, int k0, int N, int K, int tid) {
-    const int row = tid >> 2;
-    const int gn = n0 + row;
-    if constexpr (T == T_Q4_K) {
-        const int sub = (tid >> 1) & 1, half = tid & 1;
-        const int sbk = (k0 >> 5) + sub;  // sub-block index within the row
-        uint32_t out[16];
-        if (gn < N) {
-            const u32x2 w = *reinterpret_cast<const u32x2*>(base + (int64_t)gn * (K >> 1) + (int64_t)sbk * 16 + half * 8);
-            const u32x4 mt = ld16(base + sc_off + ((int64_t)gn * (K >> 8) + (sbk >> 3)) * 16);
-            uint32_t sc, mn;
-            q4k_scale_min(mt[1], mt[2], mt[3], sbk & 7, &sc, &mn);
-            const float dsc = f16f(mt[0]) * (float)sc;
-            const float dm = f16f(mt[0] >> 16) * (float)mn;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const int p = e >> 1;
-                    const float q0 = (float)((w[tt] >> (4 * p)) & 15u);
-                    const float q1 = (float)((w[tt] >> (16 + 4 * p)) & 15u);
-                    const float v0 = dsc * q0 - dm, v1 = dsc * q1 - dm;
-                    out[tt * 4 + p] = bf16_bits(v0) | (bf16_bits(v1) << 16);
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) out[i] = 0u;
-        }
-        uint16_t* dst = &Bs[row][sub * 32 + half * 16];
-        st16(dst, u32x4{out[0], out[1], out[2], out[3]});
-        st16(dst + 8, u32x4{out[4], out[5], out[6], out[7]});
-    } else {
-        const int c = tid & 3;
-        const int gk = k0 + c * 16;
-        uint32_t out[8];
-        if (gn < N && gk < K) {
-            const u32x4 w = ld16(base + (int64_t)gn * K + gk);
-            if constexpr (T == T_Q8_0) {
-                const float d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + ((int64_t)gn * (K >> 5) + (gk >> 5)) * 2));
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int p = 0; p < 2; ++p) {
-                        const float v0 = (float)(int8_t)(w[t] >> (16 * p)) * d;
-                        const float v1 = (float)(int8_t)(w[t] >> (16 * p + 8)) * d;
-                        out[t * 2 + p] = bf16_bits(v0) | (bf16_bits(v1) << 16);
-                    }
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int p = 0; p < 2; ++p) out[t * 2 + p] = i8_pair(w[t], p);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) out[i] = 0u;
-        }
-        uint16_t* dst = &Bs[row][c * 16];
-        st16(dst, u32x4{out[0], out[1], out[2], out[3]});
-        st16(dst + 8, u32x4{out[4], out[5], out[6], out[7]});
-    }
-}
-
-template <int T>
-__global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ base, int64_t stride,
-                                                   const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
-                                                   const float* __restrict__ srow, const uint16_t* __restrict__ x,
-                                                   int M, int N, int K, void* __restrict__ y, int out_bf16) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[GB_M][G_LDS];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[GB_N][G_LDS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
-    const int64_t lo = layer_offset(stride, layer_dev, nlayers);
-    const bool ok = lo >= 0;
-    base += ok ? lo : 0;
-    const int wm = wave >> 1, wn = wave & 1;
-    f32x4_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int jn = 0; jn < 2; ++jn) acc[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    if (ok) {
-        for (int k0 = 0; k0 < K; k0 += GB_K) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int e = tid + 256 * i, row = e >> 3, ch = e & 7;
-                const int gm = m0 + row, gk = k0 + ch * 8;
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (gm < M && gk < K) v = ld16(x + (int64_t)gm * K + gk);
-                st16(&As[row][ch * 8], v);
-            }
-            load_b_tile<T>(Bs, base, sc_off, n0, k0, N, K, tid);
-            __syncthreads();
-#pragma unroll
-            for (int ks = 0; ks < GB_K / 32; ++ks) {
-                bf16x8_t a[2], b[2];
-                const int kk = ks * 32 + (lane >> 4) * 8;
-#pragma unroll
-                for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const bf16x8_t*>(&As[wm * 32 + i * 16 + (lane & 15)][kk]);
-#pragma unroll
-                for (int jn = 0; jn < 2; ++jn) b[jn] = *reinterpret_cast<const bf16x8_t*>(&Bs[wn * 32 + jn * 16 + (lane & 15)][kk]);
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int jn = 0; jn < 2; ++jn)
-                        acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[jn], acc[i][jn], 0, 0, 0);
-            }
-            __syncthreads();
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int jn = 0; jn < 2; ++jn) {
-            const int n = n0 + wn * 32 + jn * 16 + (lane & 15);
-            if (n >= N) continue;
-            const float s = (T == T_INT8) ? srow[n] : 1.f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * 32 + i * 16 + (lane >> 4) * 4 + r;
-                if (m < M) store_y(y, (int64_t)m * N + n, ok ? acc[i][jn][r] * s : __builtin_nanf(""), out_bf16);
-            }
-        }
-}
-
 // ------------------------------------------------------------------------------------------------------- dequant
 // One thread per 16-byte unit (Q4_K: a sub-block of 32 values; Q8_0: half a block, 16 values). Bit for bit the
 // reference dequantization: Q8_0 v = f32(q) * d and Q4_K v = (d*sc)*q - dmin*m, whose products are exact in float32.
@@ -607,10 +352,7 @@ static int launch_t(const Args& a, hipStream_t s) {
         }
         return rc ? rc : check_launch("gemv");
     }
-    const dim3 grid((unsigned)((a.N + GB_N - 1) / GB_N), (unsigned)((a.M + GB_M - 1) / GB_M));
-    gemm_kernel<T><<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.srow, a.x, (int)a.M,
-                                        (int)a.N, (int)a.K, a.y, a.out_bf16);
-    return check_launch("gemm");
+    return launch_gemm(T, a, s);
 }
 
 int launch_matmul(int t, const Args& a, hipStream_t s) {

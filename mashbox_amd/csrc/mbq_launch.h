@@ -18,6 +18,7 @@ struct Args {
     const int32_t* layer_dev;  // device layer index, or nullptr
     int nlayers;
     int64_t sc_off;            // offset of the scale plane inside one weight's planes
+    int64_t wbytes;            // bytes of one weight's planes (int8: the N x K quants)
     const float* srow;         // int8: per-row scales
     const uint16_t* x;
     int64_t M, N, K;
@@ -29,6 +30,7 @@ struct Args {
 int set_error(int code, const char* fmt, ...);
 
 int launch_matmul(int t, const Args& a, hipStream_t s);
+int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, int64_t sc_off, hipStream_t s);
 
