@@ -8,7 +8,8 @@
  * Conventions
  *   - Plain pointers and sizes only. "dev" pointers are device (HBM) addresses owned by the caller; "host" pointers are
  *     host memory. Every device entry point is stream-ordered on `stream` (a hipStream_t; NULL = the default stream)
- *     and returns before the work finishes; it allocates nothing and holds no host lock.
+ *     and returns before the work finishes; none allocates, except the GEMM's one-time split-K workspace (see
+ *     mbq_gemm_plan), and none holds a host lock.
  *   - Matrices are row-major. Activations x are bfloat16 bits (uint16) of shape (M, K); results y are (M, N) as
  *     float32 (out_dtype MBQ_OUT_F32) or bfloat16 bits rounded to nearest even (MBQ_OUT_BF16).
  *   - Weights have N rows (outputs) and K columns (inputs), as the GGUF reader orders them (reference
@@ -98,6 +99,18 @@ int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* 
  * reference's pj hook receives (model.py:79). */
 int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
                     void* y_dev, int out_dtype, void* stream);
+
+/* Tuning and introspection (no counterpart in the reference, whose kernels are closed). For an activation batch of M
+ * rows, mbq_gemm_plan reports how mbq_matmul / mbq_int8_linear would run a (N, K) weight of type t (MBQ_INT8 for the
+ * int8 linear): *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses the per-device workspace
+ * below); bm = bn = splits = 0 means the decode GEMV (M <= 4). mbq_force_gemm_plan makes every later GEMM call in the
+ * process use tiles bm x bn and `splits` K ranges (bm = 0: automatic again); shapes: 256x{256,192,128},
+ * 128x{256,192,128,64}, 64x{256,192,128,64}.
+ * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
+ * counters), allocated by the first such call on a device and kept until the process ends; GEMM calls on one device
+ * that overlap in time must not both split K. */
+int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* bm, int* bn, int* splits);
+int mbq_force_gemm_plan(int bm, int bn, int splits);
 
 #ifdef __cplusplus
 }

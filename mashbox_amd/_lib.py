@@ -29,7 +29,22 @@ _SIGS = {
                                _c.c_void_p, _c.c_void_p]),
     "mbq_int8_linear": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                    _c.c_void_p, _c.c_int, _c.c_void_p]),
+    "mbq_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64, _c.c_int64, _c.POINTER(_c.c_int),
+                                 _c.POINTER(_c.c_int), _c.POINTER(_c.c_int)]),
+    "mbq_force_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int]),
 }
+
+
+def gemm_plan(t: int, m: int, n: int, k: int):
+    """-> (tile rows, tile cols, K splits) the library would use; (0, 0, 0) = decode GEMV"""
+    bm, bn, sp = _c.c_int(), _c.c_int(), _c.c_int()
+    check(lib().mbq_gemm_plan(int(t), int(m), int(n), int(k), _c.byref(bm), _c.byref(bn), _c.byref(sp)), "gemm_plan")
+    return bm.value, bn.value, sp.value
+
+
+def force_gemm_plan(bm: int = 0, bn: int = 0, splits: int = 0):
+    """force every later GEMM of the process to bm x bn tiles and `splits` K ranges; force_gemm_plan() = automatic"""
+    check(lib().mbq_force_gemm_plan(int(bm), int(bn), int(splits)), "force_gemm_plan")
 
 _lock = threading.Lock()
 _lib = None

@@ -23,6 +23,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <atomic>
+#include <mutex>
+#include <type_traits>
+
 #include "mbq_device.h"
 #include "mbq_launch.h"
 #include "mbq_layout.h"
@@ -117,13 +122,19 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
     return s;
 }
 
+// element i (0..3) of a vector, by selects (an index that varies across lanes must not send the vector to scratch)
+__device__ __forceinline__ uint32_t sel4(const u32x4& v, int i) {
+    const uint32_t lo = (i & 1) ? v[1] : v[0], hi = (i & 1) ? v[3] : v[2];
+    return (i & 2) ? hi : lo;
+}
+
 // chunk t (0..3: values 8t .. 8t+7) of a unit, as 8 bfloat16
 template <int T>
 __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int t) {
     u32x4 o;
     if constexpr (T == T_Q4_K) {
         // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h)
-        const uint32_t w = b.q[t];
+        const uint32_t w = sel4(b.q, t);
         const uint32_t m0 = opaque(w & 0x000F000Fu), m1 = opaque(w & 0x00F000F0u);
         const uint32_t m2 = opaque(w & 0x0F000F00u), m3 = opaque(w & 0xF000F000u);
         o[0] = pack_bf16(__builtin_fmaf((float)(m0 & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((m0 >> 16) & 0xFFu), s.a, -s.b));
@@ -131,42 +142,74 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         o[2] = pack_bf16(__builtin_fmaf((float)((m2 >> 8) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(m2 >> 24), s.a, -s.b));
         o[3] = pack_bf16(__builtin_fmaf((float)((m3 >> 8) & 0xFFu), s.c, -s.b), __builtin_fmaf((float)(m3 >> 24), s.c, -s.b));
     } else {
-        const u32x4 q = t < 2 ? b.q0 : b.q1;
-        const int h = (t & 1) * 2;
+        // dwords 2t, 2t+1 of the unit's 8 (q0: 0..3, q1: 4..7)
+        const uint32_t w0 = (t & 2) ? ((t & 1) ? b.q1[2] : b.q1[0]) : ((t & 1) ? b.q0[2] : b.q0[0]);
+        const uint32_t w1 = (t & 2) ? ((t & 1) ? b.q1[3] : b.q1[1]) : ((t & 1) ? b.q0[3] : b.q0[1]);
         uint32_t r[4];
-        i8x4<T == T_Q8_0>(q[h], s.a, s.b, &r[0]);
-        i8x4<T == T_Q8_0>(q[h + 1], s.a, s.b, &r[2]);
+        i8x4<T == T_Q8_0>(w0, s.a, s.b, &r[0]);
+        i8x4<T == T_Q8_0>(w1, s.a, s.b, &r[2]);
         o = u32x4{r[0], r[1], r[2], r[3]};
     }
     return o;
 }
 
-template <int T, int BM, int BN, bool KFULL>
-__global__ __launch_bounds__(GT, 1) void gemm_kernel(const uint8_t* __restrict__ base, int64_t stride,
-                                                     const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
-                                                     int64_t wbytes, const float* __restrict__ srow,
-                                                     const uint16_t* __restrict__ x, int M, int N, int K,
-                                                     void* __restrict__ y, int out_bf16) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t gemm_lds[];   // [A stage 0][A stage 1][B stage 0][B stage 1]
-    uint16_t* const B0 = gemm_lds + 2 * BM * GK;
+// rows of one LDS weight stage: the tile's rows, plus 16 private rows of a 192-row tile's spare threads
+constexpr int b_rows(int bn) { return (GT % (2 * bn) == 0) ? bn : bn + 16; }
+
+// kernel arguments
+struct GemmArgs {
+    const uint8_t* base;        // planes of the weight (host layer applied)
+    int64_t stride;             // bytes between stacked weights (layer_dev)
+    const int32_t* layer_dev;   // device layer index, or nullptr
+    int nlayers;
+    int64_t sc_off, wbytes;     // scale plane offset and bytes of one weight's planes
+    const float* srow;          // int8: per-row scales
+    const uint16_t* x;
+    int M, N, K;
+    void* y;
+    int out_bf16;
+    int S, kts;                 // K splits and K steps per split
+    float* ws;                  // S > 1: partial tiles, BM x BN floats per (tile, split)
+    int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
+};
+
+// Pipeline of depth P (1 or 3): x is DMA'd P steps ahead into P + 1 LDS stages, weight units are loaded into P + 1
+// register buffers P + 1 steps ahead, and the unit of step l + 1 is dequantized into one of 2 LDS weight stages during
+// step l. With split-K (S > 1) the blocks of one tile each run a contiguous range of K steps; each writes its float32
+// partial tile to the workspace, and the block that arrives last (an atomic counter per tile, reset by that block) adds
+// the S partials in split order, so the result does not depend on which block finishes last.
+template <int T, int BM, int BN, int P, bool KFULL>
+__global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kernel(const GemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t gemm_lds[];   // [A stage 0 .. P][B stage 0][B stage 1]
+    constexpr int NA = P + 1;
+    constexpr int BROWS = b_rows(BN);                   // weight stage rows (a 192-row tile adds 16 private rows)
+    uint16_t* const B0 = gemm_lds + NA * BM * GK;
     constexpr int TI = BM / 32, TJ = BN / 64;           // MFMA tiles per wave
     constexpr int XD = BM / 64;                         // x DMA instructions per wave per step (8 rows each)
     constexpr int NB = b_loads<T>();
+    static_assert(P == 1 || P == 3, "the weight stage of a step must follow from its register buffer");
+    const int M = g.M, N = g.N, K = g.K;
 
-    // XCD-aware tile order: block b runs on XCD b % 8; XCD x takes a contiguous range of tiles, N fastest, so the
-    // blocks running at once on one XCD share one x row-panel (BM x K) in that XCD's L2
-    const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN, T_ = MT * NT;
-    const int b = blockIdx.x, xcd = b & 7, q = T_ >> 3, rem = T_ & 7;
-    const int tile = xcd * q + min(xcd, rem) + (b >> 3);
+    // XCD-aware order: block b runs on XCD b % 8; XCD x takes a contiguous range of (tile, split) items, splits
+    // fastest, then tiles N fastest, so the blocks running at once on one XCD share one x row-panel in its L2
+    const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN, TB = MT * NT * g.S;
+    const int b = blockIdx.x, xcd = b & 7, q = TB >> 3, rem = TB & 7;
+    const int item = xcd * q + min(xcd, rem) + (b >> 3);
+    const int tile = item / g.S, kz = item - tile * g.S;
     const int m0 = (tile / NT) * BM, n0 = (tile % NT) * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
-    const int64_t lo = layer_offset(stride, layer_dev, nlayers);
+    const int64_t lo = layer_offset(g.stride, g.layer_dev, g.nlayers);
     const bool ok = lo >= 0;
-    base += ok ? lo : 0;
-    const rsrc_t wr = make_rsrc(base, (uint32_t)wbytes);
-    const rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)M * K * 2));
+    const uint8_t* base = g.base + (ok ? lo : 0);
+    const rsrc_t wr = make_rsrc(base, (uint32_t)g.wbytes);
+    const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
+
+    // this block's K steps [ks0, ks0 + n)
+    const int KT = (K + GK - 1) / GK;
+    const int ks0 = kz * g.kts, n = ok ? min(KT - ks0, g.kts) : 0;
+    auto k0 = [&](int l) { return (ks0 + min(l, n - 1)) * GK; };      // K offset of local step l (clamped)
 
     // x tile by DMA: instruction i of wave w fills tile rows 8 (w + 8 i) .. +7; lane l writes LDS slot l & 7 of row
     // l >> 3, which holds chunk (l & 7) ^ (l >> 3) of that row (the swizzle of lds_off). Rows past M read zero.
@@ -178,21 +221,31 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const uint8_t* __restrict__
         xvo[i] = (uint32_t)(((int64_t)(m0 + r) * K + c * 8) * 2);
         xk[i] = c * 8;
     }
-    auto dma_x = [&](int s, int k0) {
+    auto dma_x = [&](int s, int kk) {
 #pragma unroll
         for (int i = 0; i < XD; ++i) {
             uint32_t v = xvo[i];
-            if constexpr (!KFULL) v = (k0 + xk[i] < K) ? v : 0x7FFFFFF0u;     // past K: out of range, reads zero
-            dma16(xr, gemm_lds + s * BM * GK + 8 * (wave + 8 * i) * GK, v, (uint32_t)k0 * 2);
+            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : 0x7FFFFFF0u;     // past K: out of range, reads zero
+            dma16(xr, gemm_lds + s * BM * GK + 8 * (wave + 8 * i) * GK, v, (uint32_t)kk * 2);
         }
     };
 
-    // this thread's weight unit: row br (clamped to N-1: rows past N only feed outputs that are never stored), unit bu;
-    // the tile has 2 BN units, so with BN < 256 the threads from 2 BN on dequantize nothing
-    constexpr bool ALL_OWN = 2 * BN >= GT;
-    const int br = ALL_OWN ? tid >> 1 : min(tid >> 1, BN - 1), bu = tid & 1;
-    const bool bown = ALL_OWN || tid < 2 * BN;
-    const BOff bo = b_off<T>(sc_off, min(n0 + br, N - 1), K, bu);
+    // Dequant work: the tile's 2 BN weight units (row br, unit bu; rows clamped to N - 1, since rows past N only feed
+    // outputs that are never stored), LPU threads per unit, each dequantizing CPT of its 4 chunks. A tile of 192 rows
+    // has 384 units for 512 threads: the last 128 threads repeat a unit and store it to private rows past the tile, so
+    // every step stays free of branches and no two lanes store to one LDS address.
+    constexpr int LPU = (GT % (2 * BN) == 0) ? GT / (2 * BN) : 1, CPT = 4 / LPU, OWN = 2 * BN * LPU;
+    const int unit = min(tid / LPU, 2 * BN - 1), br = unit >> 1, bu = unit & 1, t0 = (tid % LPU) * CPT;
+    const BOff bo = b_off<T>(g.sc_off, min(n0 + br, N - 1), K, bu);
+    int boff[CPT];                                       // LDS element offset of each of this thread's chunks
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int d = tid - OWN;
+        boff[c] = (OWN >= GT || d < 0) ? br * GK + (((4 * bu + t0 + c) ^ (br & 7)) << 3) : (BN + d / 8) * GK + ((d % 8) << 3);
+    }
+    auto put_chunk = [&](uint16_t* Bst, const BUnit<T>& u, const BScale& sc, int c) {
+        st16(Bst + boff[c], b_chunk<T>(u, sc, t0 + c));
+    };
 
     f32x4_t acc[TI][TJ];
 #pragma unroll
@@ -200,20 +253,21 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const uint8_t* __restrict__
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int KT = ok ? (K + GK - 1) / GK : 0;
+    BUnit<T> R[NA];
 
-    // one pipeline step: MFMAs on stage kt & 1; meanwhile x of step kt + 1 streams into the other stage by DMA, the
-    // weight unit of step kt + 1 (`dq`, loaded a step ago) is dequantized into it in slices between the MFMAs, and the
-    // weight unit of step kt + 2 is loaded into `nl`
-    auto step = [&](int kt, BUnit<T>& nl, const BUnit<T>& dq) {
-        const int cur = kt & 1, nxt = cur ^ 1, kn = (kt + 1) * GK;
-        dma_x(nxt, min(kt + 1, KT - 1) * GK);
+    // local step l (l % NA == U): MFMAs on A stage U and B stage U & 1; x of step l + P streams into A stage
+    // (U + P) % NA, the unit of step l + 1 (register buffer U + 1) is dequantized into B stage (U + 1) & 1 between the
+    // MFMAs, and buffer U (dequantized a step ago) is refilled with the unit of step l + P + 1
+    auto step = [&](auto U_, int l) {
+        constexpr int U = decltype(U_)::value;
+        dma_x((U + P) % NA, k0(l + P));
         __builtin_amdgcn_sched_barrier(0);             // the DMA stays ahead of the weight loads (vmcnt order below)
-        b_load<T, KFULL>(nl, wr, bo, K, min(kt + 2, KT - 1) * GK, bu);
-        const uint16_t* Ac = gemm_lds + cur * BM * GK;
-        const uint16_t* Bc = B0 + cur * BN * GK;
-        uint16_t* Bn = B0 + nxt * BN * GK + br * GK;
-        const BScale sc = b_scale<T>(dq, ((kn >> 5) + bu) & 7);
+        b_load<T, KFULL>(R[U], wr, bo, K, k0(l + P + 1), bu);
+        const BUnit<T>& dq = R[(U + 1) % NA];
+        const uint16_t* Ac = gemm_lds + U * BM * GK;
+        const uint16_t* Bc = B0 + (U & 1) * BROWS * GK;
+        uint16_t* Bn = B0 + ((U + 1) & 1) * BROWS * GK;
+        const BScale sc = b_scale<T>(dq, ((k0(l + 1) >> 5) + bu) & 7);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int c = ks * 4 + (lane >> 4);
@@ -228,75 +282,148 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const uint8_t* __restrict__
                 for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb[j], acc[i][j], 0, 0, 0);
                 // one 16-byte chunk of the next stage's weight tile after every few activation-row tiles
                 constexpr int EVERY = TI / 2;
-                if (i % EVERY == EVERY - 1) {
-                    const int t = ks * 2 + i / EVERY;
-                    if (bown) st16(Bn + (((4 * bu + t) ^ (br & 7)) << 3), b_chunk<T>(dq, sc, t));
-                }
+                if (i % EVERY == EVERY - 1 && ks * 2 + i / EVERY < CPT) put_chunk(Bn, dq, sc, ks * 2 + i / EVERY);
             }
         }
-        // the x DMA of step kt + 1 has landed once at most the NB weight loads issued after it are in flight
-        __builtin_amdgcn_s_waitcnt(0x0F70 | NB);
+        // the x DMA of step l + 1 (issued P steps ago) has landed once at most the loads issued after it are in flight:
+        // its own step's NB weight loads and P - 1 later steps' XD + NB
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (NB + (P - 1) * (XD + NB)));
         __syncthreads();
     };
 
-    BUnit<T> r0, r1;
-    if (KT > 0) {
-        dma_x(0, 0);
-        b_load<T, KFULL>(r0, wr, bo, K, 0, bu);
-        b_load<T, KFULL>(r1, wr, bo, K, min(1, KT - 1) * GK, bu);
-        const BScale sc = b_scale<T>(r0, bu);
-        if (bown)
+    if (n > 0) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) st16(B0 + br * GK + (((4 * bu + t) ^ (br & 7)) << 3), b_chunk<T>(r0, sc, t));
-        __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0): the first x tile has landed
+        for (int p = 0; p < P; ++p) dma_x(p, k0(p));
+#pragma unroll
+        for (int r = 0; r < NA; ++r) b_load<T, KFULL>(R[r], wr, bo, K, k0(r), bu);
+        const BScale sc = b_scale<T>(R[0], ((k0(0) >> 5) + bu) & 7);
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) put_chunk(B0, R[0], sc, c);
+        __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0): the first x tiles have landed
     }
     __syncthreads();
-    // both steps of a pair unconditional, so that no load is sunk into a conditional block (its latency must overlap
-    // the step before its use); an odd step count ends with one more step
-    int kt = 0;
-    for (; kt + 1 < KT; kt += 2) {
-        step(kt, r0, r1);
-        step(kt + 1, r1, r0);
+    // the NA steps of a round are unconditional, so that no load is sunk into a conditional block (its latency must
+    // overlap the steps before its use); the last n % NA steps run one by one
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    int l = 0;
+    for (; l + NA <= n; l += NA) {
+        step(I0{}, l);
+        step(I1{}, l + 1);
+        if constexpr (NA == 4) {
+            step(I2{}, l + 2);
+            step(I3{}, l + 3);
+        }
     }
-    if (kt < KT) step(kt, r0, r1);
+    if (l < n) step(I0{}, l);
+    if constexpr (NA == 4) {
+        if (l + 1 < n) step(I1{}, l + 1);
+        if (l + 2 < n) step(I2{}, l + 2);
+    }
 
     // epilogue: lane holds column n = lane & 15 and rows 4 * (lane >> 4) + r of each 16 x 16 tile
+    if (g.S > 1) {
+        // this split's partial tile, in the lanes' own layout
+        f32x4_t* slot = reinterpret_cast<f32x4_t*>(g.ws) + (int64_t)(tile * g.S + kz) * (BM * BN / 4);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) slot[((wave * TI + i) * TJ + j) * 64 + lane] = acc[i][j];
+        __threadfence();
+        __syncthreads();
+        int* flag = reinterpret_cast<int*>(gemm_lds);
+        if (tid == 0) {
+            const int old = atomicAdd(g.cnt + tile, 1);
+            *flag = old == g.S - 1;
+            if (old == g.S - 1) g.cnt[tile] = 0;         // every split has arrived: ready for the next launch
+        }
+        __syncthreads();
+        if (!*flag) return;
+        __threadfence();
+        const f32x4_t* first = reinterpret_cast<const f32x4_t*>(g.ws) + (int64_t)tile * g.S * (BM * BN / 4);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int e = ((wave * TI + i) * TJ + j) * 64 + lane;
+                f32x4_t v = first[e];
+                for (int z = 1; z < g.S; ++z) v += first[(int64_t)z * (BM * BN / 4) + e];
+                acc[i][j] = v;
+            }
+    }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
-        const int n = n0 + wn * (BN / 4) + j * 16 + (lane & 15);
-        if (n >= N) continue;
-        const float s = (T == T_INT8) ? srow[n] : 1.f;
+        const int nn = n0 + wn * (BN / 4) + j * 16 + (lane & 15);
+        if (nn >= N) continue;
+        const float s = (T == T_INT8) ? g.srow[nn] : 1.f;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * (BM / 2) + i * 16 + (lane >> 4) * 4 + r;
-                if (m < M) store_y(y, (int64_t)m * N + n, ok ? acc[i][j][r] * s : __builtin_nanf(""), out_bf16);
+                if (m < M) store_y(g.y, (int64_t)m * N + nn, ok ? acc[i][j][r] * s : __builtin_nanf(""), g.out_bf16);
             }
     }
 }
 
-template <int T, int BM, int BN, bool KFULL>
-static int launch_tile(const Args& a, hipStream_t s) {
-    auto kern = gemm_kernel<T, BM, BN, KFULL>;
-    const size_t lds = (size_t)(2 * BM * GK + 2 * BN * GK) * sizeof(uint16_t);
+// ------------------------------------------------------------------------------------------------- workspace
+// Split-K partials and arrival counters, one set per device, allocated (and the counters cleared) by the first GEMM
+// call that splits K on that device and kept until the process ends. GEMM calls on one device that overlap in time
+// (two streams) must not both split K; the dispatcher sizes splits to fit the fixed size.
+constexpr size_t WS_BYTES = (size_t)64 << 20;
+constexpr int WS_TILES = 1 << 16;
+
+struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
+
+static int workspace(Workspace* out) {
+    static Workspace per_dev[64];
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MBQ_LAUNCH_FAIL, "GEMM: no device");
+    std::lock_guard<std::mutex> lk(mu);
+    Workspace& w = per_dev[dev];
+    if (!w.ws) {
+        void *p = nullptr, *c = nullptr;
+        if (hipMalloc(&p, WS_BYTES) != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
+        if (hipMalloc(&c, WS_TILES * sizeof(int)) != hipSuccess || hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess) {
+            (void)hipFree(p);
+            return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K counter allocation failed");
+        }
+        w.ws = static_cast<float*>(p);
+        w.cnt = static_cast<int*>(c);
+    }
+    *out = w;
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------------------- launchers
+template <int T, int BM, int BN, int P>
+static size_t lds_bytes() { return (size_t)((P + 1) * BM * GK + 2 * b_rows(BN) * GK) * sizeof(uint16_t); }
+
+template <int T, int BM, int BN, int P, bool KFULL>
+static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
+    auto kern = gemm_kernel<T, BM, BN, P, KFULL>;
+    const size_t lds = lds_bytes<T, BM, BN, P>();
     static bool attr_set = false;
     if (!attr_set) {
         if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
         attr_set = true;
     }
+    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
+               a.y, a.out_bf16, S, kts, w.ws, w.cnt};
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    kern<<<dim3((unsigned)tiles), GT, lds, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x,
-                                                (int)a.M, (int)a.N, (int)a.K, a.y, a.out_bf16);
+    kern<<<dim3((unsigned)(tiles * S)), GT, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM launch: %s", hipGetErrorString(e));
     return 0;
 }
 
-template <int T, int BM, int BN>
-static int launch_k(const Args& a, hipStream_t s) {
-    return (a.K % GK == 0) ? launch_tile<T, BM, BN, true>(a, s) : launch_tile<T, BM, BN, false>(a, s);
+template <int T, int BM, int BN, int P>
+static int launch_k(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
+    return (a.K % GK == 0) ? launch_tile<T, BM, BN, P, true>(a, S, kts, w, s) : launch_tile<T, BM, BN, P, false>(a, S, kts, w, s);
 }
 
 // compute units of the current device (cached per device)
@@ -312,39 +439,133 @@ static int cu_count() {
     return cache[dev];
 }
 
-// Tile shape for an (M, N) problem: the one with the least modelled time, where time = rounds of tiles over the CUs
-// (one block per CU: the LDS stages take most of a CU's 160 KB) x the tile's work x a per-tile overhead that shrinks
-// with the tile's size (operand traffic per flop ~ 1/BM + 1/BN).
+struct Plan { int idx, S, kts; };
+
+
+// blocks of one tile shape resident per CU (LDS and registers), queried once per process
+template <int T, int BM, int BN, int P>
+static int occupancy() {
+    static int v = 0;
+    if (v == 0) {
+        auto kern = gemm_kernel<T, BM, BN, P, true>;
+        int n = 0;
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes<T, BM, BN, P>()) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, GT, lds_bytes<T, BM, BN, P>()) != hipSuccess || n < 1)
+            n = 1;
+        v = n;
+    }
+    return v;
+}
+
+template <int T>
+struct Cand {
+    int bm, bn;
+    int (*occ)();
+    int (*launch)(const Args&, int, int, const Workspace&, hipStream_t);
+};
+
+template <int T, int BM, int BN, int P>
+static constexpr Cand<T> cand() { return Cand<T>{BM, BN, occupancy<T, BM, BN, P>, launch_k<T, BM, BN, P>}; }
+
+template <int T>
+static const Cand<T> CANDS[] = {cand<T, 256, 256, 1>(), cand<T, 256, 192, 1>(), cand<T, 256, 128, 1>(),
+                                cand<T, 128, 256, 1>(), cand<T, 128, 192, 1>(), cand<T, 128, 128, 3>(),
+                                cand<T, 128, 64, 3>(),  cand<T, 64, 256, 3>(),  cand<T, 64, 192, 3>(),
+                                cand<T, 64, 128, 3>(),  cand<T, 64, 64, 3>()};
+
+// Tile shape and K split for an (M, N, K) problem: the candidate with the least modelled time. A block's K step costs
+// about 0.1 us + 3.5e-5 us per output of its tile (fitted to MI355X timings of these kernels at 2048 and 64 activation
+// rows); blocks run in rounds over the CUs x the blocks of that shape a CU holds (LDS, registers). K is split only for
+// batches of at most 64 rows (then the weight stream, not the matrix work, bounds the time): into at most 4 ranges of
+// at least 4 steps, until the tiles x splits reach 128 blocks; larger batches fill the GPU with tiles, and a split's
+// partial tiles would cost more than the rounds they save.
+template <int T>
+static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
+    const int64_t KT = (K + GK - 1) / GK;
+    Plan best{(int)(sizeof CANDS<T> / sizeof CANDS<T>[0]) - 1, 1, (int)KT};
+    double best_t = 1e300;
+    for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i) {
+        const int bm = CANDS<T>[i].bm, bn = CANDS<T>[i].bn;
+        if (bm > 64 && M <= bm / 2) continue;                // more than half the tile's rows would be padding
+        if (M <= 64 && bn != 128) continue;
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        const int occ = CANDS<T>[i].occ();
+        int64_t S = 1;
+        if (M <= 64 && tiles < 128 && tiles <= WS_TILES) {
+            S = std::min<int64_t>({(128 + tiles - 1) / tiles, 4, std::max<int64_t>(1, KT / 4)});
+            S = std::max<int64_t>(1, std::min<int64_t>(S, (int64_t)(WS_BYTES / ((size_t)tiles * bm * bn * 4))));
+        }
+        const int64_t kts = (KT + S - 1) / S;
+        S = (KT + kts - 1) / kts;                            // no empty split
+        const int64_t rounds = (tiles * S + (int64_t)cus * occ - 1) / ((int64_t)cus * occ);
+        const double t = (double)rounds * occ * (0.1 + 3.46e-5 * bm * bn) * kts;
+        if (t < best_t) best_t = t, best = Plan{i, (int)S, (int)kts};
+    }
+    return best;
+}
+
+// forced plan (tests, tuning): tile rows, tile columns, splits; 0 = automatic
+static std::atomic<int> g_force_bm{0}, g_force_bn{0}, g_force_s{0};
+
+template <int T>
+static int find_cand(int bm, int bn) {
+    for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i)
+        if (CANDS<T>[i].bm == bm && CANDS<T>[i].bn == bn) return i;
+    return -1;
+}
+
+template <int T>
+static int pick(const Args& a, Plan* p) {
+    *p = plan_gemm<T>(a.M, a.N, a.K, cu_count());
+    const int fbm = g_force_bm.load(), fbn = g_force_bn.load(), fs = g_force_s.load();
+    if (fbm > 0) {
+        const int i = find_cand<T>(fbm, fbn);
+        if (i < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", fbm, fbn);
+        const int64_t KT = (a.K + GK - 1) / GK, tiles = ((a.M + fbm - 1) / fbm) * ((a.N + fbn - 1) / fbn);
+        int64_t S = std::max(1, fs), kts = (KT + S - 1) / S;
+        S = (KT + kts - 1) / kts;
+        if (S > 1 && (tiles > WS_TILES || (size_t)tiles * S * fbm * fbn * 4 > WS_BYTES))
+            return set_error(MBQ_BAD_ARG, "forced split of %lld tiles x %lld does not fit the workspace", (long long)tiles, (long long)S);
+        *p = Plan{i, (int)S, (int)kts};
+    }
+    return 0;
+}
+
 template <int T>
 static int launch_gemm_t(const Args& a, hipStream_t s) {
     // buffer resources address one weight's planes and the whole x with 32-bit offsets
     if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
         return set_error(MBQ_BAD_ARG, "GEMM operands over 2 GiB (weight %lld bytes, x %lld x %lld)", (long long)a.wbytes,
                          (long long)a.M, (long long)a.K);
-    const int cus = cu_count();
-    static const int shapes[][2] = {{256, 256}, {256, 192}, {256, 128}, {128, 256}, {128, 192}, {128, 128}, {128, 64}, {64, 256}, {64, 128}, {64, 64}};
-    int best = 0;
-    double best_t = 1e300;
-    for (int i = 0; i < (int)(sizeof shapes / sizeof shapes[0]); ++i) {
-        const int bm = shapes[i][0], bn = shapes[i][1];
-        if (bm > 64 && a.M <= bm / 2) continue;            // more than half the tile's rows would be padding
-        const int64_t tiles = ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
-        const int64_t rounds = (tiles + cus - 1) / cus;
-        const double t = (double)rounds * bm * bn * (1.0 + 64.0 / bm + 64.0 / bn);
-        if (t < best_t) best_t = t, best = i;
+    Plan p;
+    if (int rc = pick<T>(a, &p)) return rc;
+    Workspace w;
+    if (p.S > 1)
+        if (int rc = workspace(&w)) return rc;
+    return CANDS<T>[p.idx].launch(a, p.S, p.kts, w, s);
+}
+
+int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits) {
+    Plan p;
+    int rc;
+    switch (t) {
+        case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
+        case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
+        case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
+        default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
-    switch (best) {
-        case 0: return launch_k<T, 256, 256>(a, s);
-        case 1: return launch_k<T, 256, 192>(a, s);
-        case 2: return launch_k<T, 256, 128>(a, s);
-        case 3: return launch_k<T, 128, 256>(a, s);
-        case 4: return launch_k<T, 128, 192>(a, s);
-        case 5: return launch_k<T, 128, 128>(a, s);
-        case 6: return launch_k<T, 128, 64>(a, s);
-        case 7: return launch_k<T, 64, 256>(a, s);
-        case 8: return launch_k<T, 64, 128>(a, s);
-        default: return launch_k<T, 64, 64>(a, s);
-    }
+    if (rc) return rc;
+    *splits = p.S;
+    return 0;
+}
+
+int force_gemm_plan(int bm, int bn, int splits) {
+    if (bm != 0 && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", bm, bn);
+    if (splits < 0) return set_error(MBQ_BAD_ARG, "splits %d", splits);
+    g_force_bm = bm;
+    g_force_bn = bn;
+    g_force_s = splits;
+    return 0;
 }
 
 int launch_gemm(int t, const Args& a, hipStream_t s) {

@@ -223,3 +223,81 @@ def test_golden_fixture(name, cuda):
         for m in (1, 3):
             y = KQ.matmul(_bf16_tensor(z["x"][:m], cuda), planes).cpu().numpy()
             assert_product(y, z["y64"][:m], name)
+
+
+# ------------------------------------------------------------------------------------ every GEMM tile shape, split-K
+from mashbox_amd import _lib as LIB  # noqa: E402
+
+GEMM_TILES = [(256, 256), (256, 192), (256, 128), (128, 256), (128, 192), (128, 128), (128, 64), (64, 256), (64, 192),
+              (64, 128), (64, 64)]
+
+
+def _int8_f32(x, w):
+    """the float32 y * s that the int8 linear hands its pj hook, before the rounding to x's dtype"""
+    got = []
+    I8.linear(x, w, pj=lambda v: got.append(v.clone()) or v)
+    return got[0].cpu().numpy()
+
+
+@pytest.fixture
+def forced_plan():
+    yield LIB.force_gemm_plan
+    LIB.force_gemm_plan()
+
+
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("bm,bn", GEMM_TILES)
+def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cuda):
+    """partial tiles on both edges, K over several steps (a Q8_0 / int8 K that is not a multiple of the 64-value step
+    included), split-K into 3 ranges against 1"""
+    rng = np.random.default_rng([bm, bn, 0 if t == "int8" else t])
+    m, n = bm + bm // 2 - 3, bn + 17
+    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, "int8": 16 * 25}[t]
+    xb = G.acts(rng, m, k)
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    if t == "int8":
+        q, s = G.int8_weights(rng, n, k)
+        w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+        run = lambda: _int8_f32(x, w)
+        ref = (xf @ q.astype(np.float64).T) * s
+    else:
+        raw = G.RAW[t](rng, n, k)
+        planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+        run = lambda: KQ.matmul(x, planes).cpu().numpy()
+        ref = xf @ R.dequant(raw, t, k).astype(np.float64).T
+    outs = []
+    for splits in (1, 3):
+        forced_plan(bm, bn, splits)
+        assert LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)[:2] == (bm, bn)
+        y = run()
+        assert_product(y, ref, f"{t} tile {bm}x{bn} splits {splits}")
+        outs.append(y)
+    # a split sums float32 partials in another order: close to, not bitwise equal to, one range
+    assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("t", [R.Q4_K, "int8"], ids=["Q4_K", "int8"])
+def test_split_k_repeats_bit_for_bit(t, cuda):
+    """the automatic plan for a skinny batch splits K; repeated calls (the arrival counters reset themselves) give the
+    same bits, whichever split arrives last"""
+    rng = np.random.default_rng(77)
+    m, n, k = 64, 1024, 5120
+    xb = G.acts(rng, m, k)
+    x = _bf16_tensor(xb, cuda)
+    tt = -8 if t == "int8" else t
+    assert LIB.gemm_plan(tt, m, n, k)[2] > 1
+    if t == "int8":
+        q, s = G.int8_weights(rng, n, k)
+        w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+        run = lambda: _int8_f32(x, w)
+        ref = (R.bf16_to_f32(xb).astype(np.float64) @ q.astype(np.float64).T) * s
+    else:
+        raw = G.RAW[t](rng, n, k)
+        planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+        run = lambda: KQ.matmul(x, planes).cpu().numpy()
+        ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    first = run()
+    assert_product(first, ref)
+    for _ in range(4):
+        assert np.array_equal(run().view(np.uint32), first.view(np.uint32))
