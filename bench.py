@@ -48,6 +48,7 @@ def log(*a):
 def run_config(idx, steps, warmup, rotate_bytes):
     import torch
     from mashbox_amd import synth
+    from mashbox_amd import _lib as LIB
     from mashbox_amd._lib import OUT_BF16, check, lib
 
     L = lib()
@@ -114,7 +115,8 @@ def run_config(idx, steps, warmup, rotate_bytes):
         fl = 2 * M * N * K
         out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
                                     "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
-                                    "rotation_MB": round(copies * wbytes / 1e6, 1)}
+                                    "rotation_MB": round(copies * wbytes / 1e6, 1),
+                                    "plan": "gemv" if M <= 4 else "%dx%d/%d" % LIB.gemm_plan(-8 if t == "int8" else t, M, N, K)}
         total_us += us
         total_bytes += ab
         total_flops += fl
@@ -182,6 +184,87 @@ def cpu_baseline(seconds):
                       f"median {med * 1e3:.1f} ms/call; host CPU {model}"}
 
 
+def pmc_probe(launches=24, copy_mib=1024):
+    """the headline kernel alone, eagerly, for rocprofv3 --pmc: `launches` config-2 GEMV launches over rotating weight
+    copies, then a plain device copy of copy_mib MiB (read and written once) to calibrate the counters"""
+    import torch
+    from mashbox_amd import synth
+    from mashbox_amd._lib import OUT_BF16, check, lib
+
+    L = lib()
+    dev = torch.device("cuda", 0)
+    t, M, ((_, N, K),) = synth.CONFIGS[HEADLINE]
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    x = synth.acts(M, K, seed=1000 * HEADLINE, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    raw = synth.q8_0_raw(N, K, seed=1000 * HEADLINE + 7, device=dev)
+    pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
+    planes = torch.empty(pb, dtype=torch.uint8, device=dev)
+    check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st), "repack")
+    copies = [planes] + [planes.clone() for _ in range(11)]
+    for i in range(launches):
+        check(L.mbq_matmul(t, ctypes.c_void_p(copies[i % len(copies)].data_ptr()), 0, None, 1,
+                           ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st), "matmul")
+    src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": {"launches": launches, "copy_bytes": copy_mib << 20,
+                                    "algorithmic_bytes": algorithmic_bytes(t, M, N, K)}}), flush=True)
+
+
+def _counter_rows(d):
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    return rows
+
+
+def summarize_pmc(fetch_dir, write_dir, out, copy_mib=1024):
+    """profiles/traffic.json from the two rocprofv3 --pmc runs of --pmc-probe (FETCH_SIZE, then WRITE_SIZE): HBM bytes
+    per headline-kernel launch, each counter scaled by what it reads for the calibration copy"""
+    def per(rows, counter):
+        # headline-kernel dispatches, and the calibration copies: the probe's last 4 dispatches
+        rows = [r for r in rows if r["Counter_Name"] == counter]
+        last = sorted(int(r["Dispatch_Id"]) for r in rows)[-4:]
+        k = [float(r["Counter_Value"]) for r in rows if "gemv_kernel<8, 1," in r["Kernel_Name"]]
+        c = [float(r["Counter_Value"]) for r in rows if int(r["Dispatch_Id"]) in last]
+        return k, c
+    fk, fc = per(_counter_rows(fetch_dir), "FETCH_SIZE")
+    wk, wc = per(_counter_rows(write_dir), "WRITE_SIZE")
+    if not (fk and fc and wk and wc):
+        raise SystemExit(f"missing dispatches: gemv fetch {len(fk)} copy fetch {len(fc)} gemv write {len(wk)} copy write {len(wc)}")
+    import statistics as stt
+    known_kib = (copy_mib << 20) / 1024.0
+    ff, fw = known_kib / stt.median(fc), known_kib / stt.median(wc)
+    fetch_b = stt.median(fk[1:] or fk) * ff * 1024.0       # the first launch also faults in code and tables
+    write_b = stt.median(wk[1:] or wk) * fw * 1024.0
+    rec = {"c2": {"hbm_bytes_per_launch": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+                  "fetch_kib_raw": stt.median(fk), "write_kib_raw": stt.median(wk), "copy_fetch_kib_raw": stt.median(fc),
+                  "copy_write_kib_raw": stt.median(wc), "copy_kib": known_kib, "fetch_scale": round(ff, 4),
+                  "write_scale": round(fw, 4), "launches": len(fk),
+                  "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -f csv -- python3 bench.py --pmc-probe"}}
+    with open(out, "w") as f:
+        json.dump(rec, f, indent=1)
+    print(json.dumps(rec), flush=True)
+
+
+def summarize_stats(csv_path, top=12):
+    """markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv"""
+    import csv
+    rows = list(csv.DictReader(open(csv_path)))
+    key = lambda r: float(r.get("TotalDurationNs", 0) or 0)
+    print("| kernel | calls | avg us | min us | max us | % time |\n|---|---:|---:|---:|---:|---:|")
+    for r in sorted(rows, key=key, reverse=True)[:top]:
+        name = r["Name"]
+        name = name[:90] + ("..." if len(name) > 90 else "")
+        print(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+              f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,7 +276,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE)")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the headline kernel + a calibration copy (for --pmc)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write --traffic from the two --pmc runs of --pmc-probe")
+    ap.add_argument("--summarize-stats", metavar="KERNEL_STATS_CSV", help="print a rocprofv3 --stats CSV as markdown")
     a = ap.parse_args()
+    if a.summarize_pmc:
+        return summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.traffic)
+    if a.summarize_stats:
+        return summarize_stats(a.summarize_stats)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU: this path is measured on a single MI355X (its kernels shard by weight rows "
               "with no collective; see DESIGN.md). --gpus must be 1.", file=sys.stderr)
@@ -202,6 +293,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if a.pmc_probe:
+        return pmc_probe()
     configs = [int(c) for c in a.configs.split(",") if c]
     if HEADLINE not in configs:
         configs.insert(0, HEADLINE)
@@ -226,7 +319,7 @@ def main():
                    "rotation_MB": proj["rotation_MB"]},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "mbq::gemv_kernel<8,1,R>", "kernel_us": proj["us"],
+                     "kernel": "mbq::gemv_kernel<8, 1, 4, true>", "kernel_us": proj["us"],
                      "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
         "configs": {f"c{c}": {k: v for k, v in r.items() if k != "projections"} | {"projections": r["projections"]}
                     for c, r in res.items()},
