@@ -93,6 +93,11 @@ int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* l
 int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
                 int64_t K, float* w_dev, void* stream);
 
+/* W (rows, cols) float32 straight from the file's blocks raw_dev (rows, row_bytes) in HBM, no planes: the exact path's
+ * rebuild, bit for bit the reference dequantization (NaN where it has NaN). Replaces dequant(raw, t, cols) of
+ * reference src/mashbox/ops/reference.py:398-409 as the exact path calls it (src/mashbox/ops/__init__.py:574-576). */
+int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream);
+
 /* int8 per-output-channel linear: y (M, N) = (x (M, K) @ bf16(q).T accumulated in float32) * s, then out_dtype.
  * q_dev int8 (N, K) row-major, s_dev float32 (N,). Replaces linear(x, {"q", "s"}) (reference
  * src/mashbox/models/qwen3_8_27b/model.py:72-82); with out_dtype MBQ_OUT_F32 it returns the float32 y*s that the

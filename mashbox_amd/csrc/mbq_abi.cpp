@@ -241,6 +241,12 @@ int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* 
     return launch_dequant(t, a, w_dev, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream) {
+    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (!raw_dev || !w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "raw is NULL or w is NULL / not 16-byte aligned");
+    return launch_dequant_raw(t, raw_dev, rows, cols, w_dev, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
                     void* y_dev, int out_dtype, void* stream) {
     if (int rc = check_out(out_dtype)) return rc;

@@ -259,6 +259,49 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     }
 }
 
+// ------------------------------------------------------------------------------------------------- raw dequant
+static int check_launch(const char* what);
+// The file's blocks (rows, row_bytes) -> float32 (rows, cols), without planes: reference src/mashbox/ops/reference.py
+// :398-409 (dequant) with :101-103 (Q8_0) and :132-149 (Q4_K), the rebuild of the exact path. One thread per 32 values
+// (a Q8_0 block, a Q4_K sub-block); the blocks are 34 / 144 bytes apart, so bytes are read one at a time.
+template <int T>
+__global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
+                                                          float* __restrict__ w) {
+    const int64_t units = rows * (K / 32);
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= units) return;
+    const int64_t n = g / (K / 32), u = g % (K / 32);
+    float* out = w + n * K + u * 32;
+    if constexpr (T == T_Q8_0) {
+        const uint8_t* b = raw + (n * (K / 32) + u) * 34;
+        const float d = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+        for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)b[2 + i] * d;
+    } else {
+        const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 144;
+        const int j = (int)(u & 7);
+        const uint32_t s0 = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+        const uint32_t s1 = b[8] | (b[9] << 8) | (b[10] << 16) | ((uint32_t)b[11] << 24);
+        const uint32_t s2 = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
+        uint32_t sc, mn;
+        q4k_scale_min(s0, s1, s2, j, &sc, &mn);
+        const float dsc = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8)) * (float)sc;      // exact
+        const float dm = f16f((uint32_t)b[2] | ((uint32_t)b[3] << 8)) * (float)mn;       // exact
+        const uint8_t* q = b + 16 + 32 * (j >> 1);                   // sub-block 2g: low nibbles, 2g+1: high nibbles
+        const int sh = (j & 1) * 4;
+        for (int i = 0; i < 32; ++i) out[i] = dsc * (float)((q[i] >> sh) & 15u) - dm;
+    }
+}
+
+int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s) {
+    const int64_t units = rows * (K / 32);
+    const dim3 grid((unsigned)((units + 255) / 256));
+    if (t == T_Q4_K)
+        dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    else
+        dequant_raw_kernel<T_Q8_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    return check_launch("dequant_raw");
+}
+
 // ------------------------------------------------------------------------------------------------ device repack
 // One thread per block: the file's bytes (unaligned, 34 or 144 bytes apart) into the planes of mbq_layout.h.
 template <int T>

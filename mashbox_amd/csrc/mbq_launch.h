@@ -34,6 +34,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
 int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits);
 int force_gemm_plan(int bm, int bn, int splits);
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
+int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s);
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, int64_t sc_off, hipStream_t s);
 
 }  // namespace mbq
