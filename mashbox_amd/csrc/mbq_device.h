@@ -126,6 +126,34 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// buffer resources: loads carry a 32-bit per-lane offset and a scalar offset, and read zero past num_records
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt not waited (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | 0x0F70 | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the memory fence of __syncthreads, which waits for every load in flight (LDS DMA
+// included) and so empties a load pipeline at each step. The caller has waited (vmcnt) for the loads whose LDS writes
+// the other waves read after the barrier; the empty asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void barrier_nofence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 constexpr uint32_t BF16_ONES = 0x3F803F80u;  // bfloat16 pair (1, 1)
 
 // a value the compiler treats as unknown, so that it keeps one AND of a two-quant mask instead of splitting it per byte

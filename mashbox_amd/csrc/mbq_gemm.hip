@@ -39,17 +39,6 @@ constexpr int GK = 64, GT = 512;
 // element offset of chunk c (8 bfloat16) of row r in an LDS tile of 64-value rows
 __device__ __forceinline__ int lds_off(int r, int c) { return r * GK + ((c ^ (r & 7)) << 3); }
 
-// buffer resources: loads carry a 32-bit per-lane offset and a scalar offset, and read zero past num_records
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-}
 // 16 bytes per lane from global memory straight into LDS: lane l writes lds_wave + 16 l (lds_wave wave-uniform)
 __device__ __forceinline__ void dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
@@ -372,12 +361,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 // Split-K partials and arrival counters, one set per device, allocated (and the counters cleared) by the first GEMM
 // call that splits K on that device and kept until the process ends. GEMM calls on one device that overlap in time
 // (two streams) must not both split K; the dispatcher sizes splits to fit the fixed size.
-constexpr size_t WS_BYTES = (size_t)64 << 20;
-constexpr int WS_TILES = 1 << 16;
-
-struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
-
-static int workspace(Workspace* out) {
+int workspace(Workspace* out) {
     static Workspace per_dev[64];
     static std::mutex mu;
     int dev = 0;
@@ -531,12 +515,30 @@ static int pick(const Args& a, Plan* p) {
     return 0;
 }
 
+// the weight-stream kernel (mbq_wsgemm.hip) runs a batch of at most WS_MAX_M rows, unless a plan forces an LDS tile;
+// a forced plan with 16-row tiles forces the weight-stream kernel (bn rows per block, `splits` K ranges)
+static bool use_ws(int64_t M, int* nr, int* S) {
+    const int fbm = g_force_bm.load();
+    if (fbm == 16) {
+        *nr = g_force_bn.load();
+        *S = std::max(1, g_force_s.load());
+        return M > GEMV_MAX_M && M <= WS_MAX_M;
+    }
+    return fbm == 0 && M > GEMV_MAX_M && M <= WS_MAX_M;
+}
+
 template <int T>
 static int launch_gemm_t(const Args& a, hipStream_t s) {
     // buffer resources address one weight's planes and the whole x with 32-bit offsets
     if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
         return set_error(MBQ_BAD_ARG, "GEMM operands over 2 GiB (weight %lld bytes, x %lld x %lld)", (long long)a.wbytes,
                          (long long)a.M, (long long)a.K);
+    int nr = 0, S = 1;
+    if (use_ws(a.M, &nr, &S)) {
+        if (g_force_bm.load() != 16) wsgemm_plan(T, a, &nr, &S);
+        return launch_wsgemm(T, a, nr, S, s);
+    }
+    if (g_force_bm.load() == 16) return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs %lld < M <= %lld", (long long)GEMV_MAX_M, (long long)WS_MAX_M);
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
@@ -548,6 +550,15 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
 int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits) {
     Plan p;
     int rc;
+    int nr = 0, S = 1;
+    if (use_ws(a.M, &nr, &S)) {
+        if (g_force_bm.load() != 16) wsgemm_plan(t, a, &nr, &S);
+        wsgemm_effective(t, a, &nr, &S);
+        *bm = 16;
+        *bn = nr;
+        *splits = S;
+        return 0;
+    }
     switch (t) {
         case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
         case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
@@ -560,7 +571,8 @@ int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits) {
 }
 
 int force_gemm_plan(int bm, int bn, int splits) {
-    if (bm != 0 && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", bm, bn);
+    if (bm == 16 && bn != 64 && bn != 128) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM takes 64 or 128 rows per block, not %d", bn);
+    if (bm != 0 && bm != 16 && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", bm, bn);
     if (splits < 0) return set_error(MBQ_BAD_ARG, "splits %d", splits);
     g_force_bm = bm;
     g_force_bn = bn;

@@ -26,11 +26,24 @@ struct Args {
     int out_bf16;
 };
 
+// Split-K partials and arrival counters of the GEMM kernels, one set per device (mbq_gemm.hip): WS_BYTES of float32
+// partial tiles and WS_TILES int counters, allocated (counters cleared) by the first call that needs them on a device
+// and kept until the process ends. Every kernel that uses them leaves the counters it touched at zero.
+constexpr size_t WS_BYTES = (size_t)64 << 20;
+constexpr int WS_TILES = 1 << 16;
+struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
+int workspace(Workspace* out);
+
 // records the calling thread's error message; returns code
 int set_error(int code, const char* fmt, ...);
 
 int launch_matmul(int t, const Args& a, hipStream_t s);
 int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
+// weight-stream GEMM (mbq_wsgemm.hip) for GEMV_MAX_M < M <= WS_MAX_M: rows_per_block 32 or 64, splits >= 1
+constexpr int64_t WS_MAX_M = 64;
+int launch_wsgemm(int t, const Args& a, int rows_per_block, int splits, hipStream_t s);
+int wsgemm_plan(int t, const Args& a, int* rows_per_block, int* splits);
+void wsgemm_effective(int t, const Args& a, int* rows_per_block, int* splits);   // what a launch with these runs
 int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits);
 int force_gemm_plan(int bm, int bn, int splits);
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s);

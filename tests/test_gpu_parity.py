@@ -277,16 +277,53 @@ def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cu
     assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
 
 
-@pytest.mark.parametrize("t", [R.Q4_K, "int8"], ids=["Q4_K", "int8"])
-def test_split_k_repeats_bit_for_bit(t, cuda):
-    """the automatic plan for a skinny batch splits K; repeated calls (the arrival counters reset themselves) give the
-    same bits, whichever split arrives last"""
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("m", [5, 17, 40, 64])
+@pytest.mark.parametrize("rows", [64, 128])
+@pytest.mark.parametrize("kfull", [False, True], ids=["k_ragged", "k_full"])
+def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
+    """the weight-stream kernel (4 < M <= 64): 1-4 tiles of 16 activation rows, 64 and 128 weight rows per block,
+    ragged weight rows, a K that is or is not a multiple of the kernel's iteration (64 values; 128 for Q4_K, whose K
+    is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
+    rng = np.random.default_rng([m, rows, int(kfull), 0 if t == "int8" else t])
+    n = 3 * rows + 17
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
+    xb = G.acts(rng, m, k)
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    if t == "int8":
+        q, s = G.int8_weights(rng, n, k)
+        w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+        run = lambda: _int8_f32(x, w)
+        ref = (xf @ q.astype(np.float64).T) * s
+    else:
+        raw = G.RAW[t](rng, n, k)
+        planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+        run = lambda: KQ.matmul(x, planes).cpu().numpy()
+        ref = xf @ R.dequant(raw, t, k).astype(np.float64).T
+    outs = []
+    for splits in (1, 3):
+        forced_plan(16, rows, splits)
+        bm, bn, sp = LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)
+        assert (bm, bn) == (16, rows) and 1 <= sp <= splits
+        y = run()
+        assert_product(y, ref, f"{t} m={m} rows {rows} k={k} splits {splits}")
+        outs.append(y)
+    assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("m,plan", [(64, (16, 64, 4)), (130, (64, 128, 3))], ids=["weight_stream", "lds_tiles"])
+def test_split_k_repeats_bit_for_bit(t, m, plan, forced_plan, cuda):
+    """a K split into ranges repeats bit for bit over calls (the arrival counters reset themselves), whichever split
+    arrives last: both GEMM kernels"""
     rng = np.random.default_rng(77)
-    m, n, k = 64, 1024, 5120
+    n, k = 1024, 5120
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
     tt = -8 if t == "int8" else t
-    assert LIB.gemm_plan(tt, m, n, k)[2] > 1
+    forced_plan(*plan)
+    assert LIB.gemm_plan(tt, m, n, k) == plan
     if t == "int8":
         q, s = G.int8_weights(rng, n, k)
         w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
