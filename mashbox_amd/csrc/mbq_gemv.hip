@@ -1,0 +1,335 @@
+// gfx950 decode GEMV of the quantized linear (M <= GEMV_MAX_M activation rows).
+//
+// y (M, N) = x (M, K) @ W.T with float32 accumulation: reference src/mashbox/ops/__init__.py:594-632 (qmatmul) on the
+// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K), and the int8 per-channel
+// linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (dot, then * s). Plane layouts: mbq_layout.h.
+//
+// HBM-bound: every weight byte is read once, 16 bytes per lane, each wave-wide load 1 KiB of one row (non-temporal).
+//
+// Work split. A persistent grid; block b owns rows [b N / P, (b + 1) N / P). A row's U units (a unit: 16 bytes of quants
+// = 16 int8 values, or a Q4_K sub-block of 32) are cut into S parts of PU units, at most 64 CH: one part of one row is
+// an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
+// block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
+// multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
+// the inner loop). The next item's loads (DEPTH - 1 items) are in flight while an item computes; every load is unconditional (chunks
+// past a part's end and items past a wave's last reload data already fetched, cache hits), so the compiler's vmcnt
+// waits count exactly the next item's loads. An item's sums are reduced across the wave with DPP; with S > 1 the block
+// adds a row's parts through LDS at the end.
+//
+// Arithmetic, float32 accumulation with v_dot2_f32_bf16:
+//   int8 / Q8_0   a signed byte convert (one SDWA op per value) and a pack give exact bfloat16 pairs; Q8_0 scales the
+//                 unit's sum by d.
+//   Q4_K          ((w >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair (128 + q, 128 + q'); per unit
+//                 y += (d sc) * sum(x (128 + q)) - (128 d sc + dmin m) * sum(x); the per-unit sums of x are computed
+//                 once per wave from its x registers.
+// A lane that holds no unit of a part (the part's last chunk) reads a valid unit and has its scale zeroed.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "mbq_device.h"
+#include "mbq_launch.h"
+#include "mbq_layout.h"
+
+namespace mbq {
+
+constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
+constexpr int GV_BLOCKS_PER_CU = 1;   // grid: one block per CU (more, shorter-lived waves measured slower on MI355X)
+constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
+
+template <int T> constexpr int gv_uw() { return T == T_Q4_K ? 32 : 16; }      // values per 16-byte unit
+template <int T> constexpr int gv_tpu() { return gv_uw<T>() / 8; }            // 16-byte x chunks per unit
+// chunks per item that the registers hold (x of M rows for CH chunks, and two items' loads in flight)
+template <int T> constexpr int gv_chmax(int M) {
+    return T == T_Q4_K ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
+}
+
+struct GvArgs {
+    const uint8_t* base;        // planes (host layer applied)
+    int64_t stride;             // bytes between stacked weights (layer_dev)
+    const int32_t* layer_dev;
+    int nlayers;
+    int64_t sc_off;             // scale plane offset
+    int64_t wbytes;             // bytes of one weight's planes (int8: N x K)
+    const float* srow;          // int8 per-row scales
+    const uint16_t* x;
+    int N, K, S, PU;            // rows, columns, parts per row (divides 8), units per part
+    void* y;
+    int out_bf16;
+};
+
+// 4 int8 quants (one dword) -> 2 bfloat16 pairs, exact
+__device__ __forceinline__ void gv_i8x4(uint32_t w, uint32_t* lo, uint32_t* hi) {
+    *lo = pack_bf16((float)(int8_t)(w & 0xFFu), (float)(int8_t)((w >> 8) & 0xFFu));
+    *hi = pack_bf16((float)(int8_t)((w >> 16) & 0xFFu), (float)(int8_t)(w >> 24));
+}
+
+template <int T, int M, int CH, int DEPTH = 2>
+__global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
+    extern __shared__ float parts[];                                  // S > 1: (r1 - r0) x S x M
+    constexpr int UW = gv_uw<T>(), TPU = gv_tpu<T>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = g.N, K = g.K, S = g.S, PU = g.PU;
+    const int P = gridDim.x;
+    const int r0 = (int)((int64_t)blockIdx.x * N / P), r1 = (int)((int64_t)(blockIdx.x + 1) * N / P);
+    const int64_t lo = layer_offset(g.stride, g.layer_dev, g.nlayers);
+    const bool ok = lo >= 0;
+    const rsrc_t wr = make_rsrc(g.base + (ok ? lo : 0), (uint32_t)g.wbytes);
+    const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
+    const int U = K / UW;
+    const uint32_t qstride = (uint32_t)U * 16u;
+    const uint32_t sstride = (T == T_Q4_K) ? (uint32_t)(K >> 8) * 16u : (uint32_t)(K >> 5) * 2u;
+
+    // this wave's part and its units
+    const int part = wave % S, rstep = GV_WAVES / S;
+    const int u0 = part * PU, nu = max(0, min(PU, U - u0));
+    const int lastc = max(0, (nu - 1) >> 6);                         // last chunk with a unit of the part
+    const int nrows = r1 - r0, first = wave / S;
+    const int nit = first < nrows ? (nrows - 1 - first) / rstep + 1 : 0;   // rows this wave takes
+    const bool any = ok && nit > 0 && nu > 0;
+
+    struct Raw { u32x4 q[CH]; u32x4 meta[CH]; uint32_t d[CH]; };
+    auto load = [&](Raw& R, int k) {                                  // the k-th row of the wave (clamped)
+        const int row = r0 + first + min(k, nit - 1) * rstep;
+        const uint32_t qs = (uint32_t)row * qstride + (uint32_t)u0 * 16u;
+        const uint32_t ss = (uint32_t)g.sc_off + (uint32_t)row * sstride;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const uint32_t c = (uint32_t)min(i, lastc);               // wave-uniform
+            R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)lane * 16u, qs + 1024u * c, 2));
+            if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, (uint32_t)(lane >> 1) * 2u, ss + (uint32_t)u0 + 64u * c);
+            if constexpr (T == T_Q4_K) R.meta[i] = bload16(wr, (uint32_t)(lane >> 3) * 16u, ss + (uint32_t)u0 * 2u + 128u * c);
+        }
+    };
+
+    Raw A, B, C;
+    if (any) {
+        load(A, 0);
+        if constexpr (DEPTH == 3) load(B, 1);
+    }
+
+    // x of the lane's units (clamped to the row), per activation row, and for Q4_K the per-unit sums of x
+    u32x4 xv[CH][M][TPU];
+    float xs[CH][M];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int u = min(u0 + lane + 64 * i, U - 1);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float sum = 0.f;
+#pragma unroll
+            for (int t = 0; t < TPU; ++t) {
+                xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
+                if constexpr (T == T_Q4_K) {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) sum = dot2(xv[i][m][t][p], BF16_ONES, sum);
+                }
+            }
+            xs[i][m] = sum;
+        }
+    }
+    const Q4kSel sel = q4k_sel((u0 + lane) & 7);                     // units advance by 64: the lane's slot is fixed
+    const uint32_t kmask = in_vgpr(0x000F000Fu), kmagic = in_vgpr(0x43004300u);
+
+    auto finish = [&](const Raw& R, int k) {
+        const int rl = first + k * rstep;
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.f;
+        // chunk i; FULL: every lane holds a unit of the part (no zeroed scale)
+        auto chunk = [&](auto FULL_, int i) {
+            constexpr bool FULL = decltype(FULL_)::value;
+            const bool act = FULL || lane + 64 * i < nu;
+            if constexpr (T == T_Q4_K) {
+                uint32_t sc, mn;
+                q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
+                float dsc = f16f(R.meta[i][0]) * (float)sc;             // exact
+                const float dm = f16f(R.meta[i][0] >> 16) * (float)mn;  // exact
+                float c = 128.f * dsc + dm;
+                if constexpr (!FULL) {
+                    dsc = act ? dsc : 0.f;
+                    c = act ? c : 0.f;
+                }
+                float P0[M], P1[M];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp) {
+                        const uint32_t pr = ((R.q[i][t] >> (4 * pp)) & kmask) | kmagic;
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
+                            float& Pm = (pp & 1) ? P1[m] : P0[m];
+                            Pm = dot2(pr, xv[i][m][t][pp], (t == 0 && pp < 2) ? 0.f : Pm);
+                        }
+                    }
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(dsc, P0[m] + P1[m], __builtin_fmaf(-c, xs[i][m], acc[m]));
+            } else {
+                float d = 1.f;
+                if constexpr (T == T_Q8_0) d = f16f(R.d[i]);
+                if constexpr (!FULL) d = act ? d : 0.f;
+                float P0[M], P1[M];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    uint32_t b0, b1;
+                    gv_i8x4(R.q[i][t], &b0, &b1);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float& Pm = (t & 1) ? P1[m] : P0[m];
+                        Pm = dot2(b0, xv[i][m][t >> 1][2 * (t & 1)], t < 2 ? 0.f : Pm);
+                        Pm = dot2(b1, xv[i][m][t >> 1][2 * (t & 1) + 1], Pm);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(d, P0[m] + P1[m], acc[m]);
+            }
+        };
+        using Full = std::integral_constant<bool, true>;
+        using Part = std::integral_constant<bool, false>;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            if (64 * (i + 1) <= nu) chunk(Full{}, i);                  // wave-uniform
+            else if (64 * i < nu) chunk(Part{}, i);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float v = wave_sum_dpp(acc[m]);
+            if (lane == 0) {
+                if (S == 1) {
+                    const int n = r0 + rl;
+                    const float sc = (T == T_INT8) ? g.srow[n] : 1.f;
+                    store_y(g.y, (int64_t)m * N + n, v * sc, g.out_bf16);
+                } else {
+                    parts[(rl * S + part) * M + m] = v;
+                }
+            }
+        }
+    };
+    if (any) {
+        if constexpr (DEPTH == 3) {
+            // while item k computes, items k + 1 and k + 2 load
+            for (int k = 0; k < nit; k += 3) {
+                load(C, k + 2);
+                finish(A, k);
+                load(A, k + 3);
+                if (k + 1 < nit) finish(B, k + 1);
+                load(B, k + 4);
+                if (k + 2 < nit) finish(C, k + 2);
+            }
+        } else {
+            // while item k computes, item k + 1 loads
+            for (int k = 0; k < nit; k += 2) {
+                load(B, k + 1);
+                finish(A, k);
+                load(A, k + 2);
+                if (k + 1 < nit) finish(B, k + 1);
+            }
+        }
+    }
+    if (S > 1 || !ok) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < nrows * M; e += GV_THREADS) {
+            const int rl = e / M, m = e - rl * M, n = r0 + rl;
+            float v = 0.f;
+            if (S > 1)
+                for (int p = 0; p < S; ++p) v += parts[(rl * S + p) * M + m];
+            const float sc = (T == T_INT8) ? g.srow[n] : 1.f;
+            store_y(g.y, (int64_t)m * N + n, ok ? v * sc : __builtin_nanf(""), g.out_bf16);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------ launchers
+// blocks of a GEMV kernel the GPU holds at once (cached per kernel and LDS size)
+template <class Kern>
+static int resident_blocks(Kern kernel, size_t lds) {
+    static thread_local struct { const void* k; size_t lds; int n; } cache[64];
+    static thread_local int used = 0;
+    for (int i = 0; i < used; ++i)
+        if (cache[i].k == (const void*)kernel && cache[i].lds == lds) return cache[i].n;
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GV_THREADS, lds) != hipSuccess || per < 1)
+        return -1;
+    const int n = cus * per;
+    if (used < 64) cache[used++] = {(const void*)kernel, lds, n};
+    return n;
+}
+
+// Parts per row: the fewest S in {1, 2, 4, 8} whose parts take at most GV_ITEM_CHUNKS chunks and fit the registers
+// (at M = 1: K <= 24576 int8 / Q8_0, 49152 Q4_K); PU rounded to the scale granularity (Q8_0 scales cover 2 units, Q4_K
+// meta 8). Returns the chunks the parts need, or -1.
+template <int T, int M>
+static int gv_parts(int64_t U, int* S, int* PU) {
+    const int64_t gran = T == T_Q4_K ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
+    for (int s = 1; s <= GV_WAVES; s *= 2) {
+        const int64_t pu = ((U + s - 1) / s + gran - 1) / gran * gran;
+        if (pu <= cap) {
+            *S = s;
+            *PU = (int)pu;
+            return (int)((pu + 63) / 64);
+        }
+    }
+    return -1;
+}
+
+template <int T, int M, int CH>
+static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
+    auto kern = gemv_kernel<T, M, CH>;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    int P = resident_blocks(kern, 4096);
+    if (P < 1) return set_error(MBQ_LAUNCH_FAIL, "GEMV occupancy query failed");
+    P = (int)std::min<int64_t>({(int64_t)P, (int64_t)cus * GV_BLOCKS_PER_CU, a.N});
+    const int64_t rows_max = (a.N + P - 1) / P;
+    const size_t lds = S > 1 ? (size_t)rows_max * S * M * 4 : 0;
+    if (lds > 64 * 1024) return set_error(MBQ_BAD_ARG, "GEMV N = %lld needs too much LDS", (long long)a.N);
+    GvArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.N, (int)a.K, S, PU, a.y, a.out_bf16};
+    kern<<<dim3((unsigned)P), GV_THREADS, lds, s>>>(g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "gemv: %s", hipGetErrorString(e));
+    return 0;
+}
+
+template <int T, int M>
+static int launch_gemv_m(const Args& a, hipStream_t s) {
+    if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
+        return set_error(MBQ_BAD_ARG, "GEMV operands over 2 GiB");
+    int S = 1, PU = 0;
+    const int ch = gv_parts<T, M>(a.K / gv_uw<T>(), &S, &PU);
+    if (ch < 1) return set_error(MBQ_BAD_ARG, "GEMV K = %lld is too long for %d activation rows", (long long)a.K, M);
+    constexpr int C = gv_chmax<T>(M);
+    switch (ch) {
+        case 1: return launch_gemv_ch<T, M, 1>(a, S, PU, s);
+        case 2: if constexpr (C >= 2) return launch_gemv_ch<T, M, 2>(a, S, PU, s); break;
+        case 3: if constexpr (C >= 3) return launch_gemv_ch<T, M, 3>(a, S, PU, s); break;
+        case 4: if constexpr (C >= 4) return launch_gemv_ch<T, M, 4>(a, S, PU, s); break;
+        case 5: if constexpr (C >= 5) return launch_gemv_ch<T, M, 5>(a, S, PU, s); break;
+        case 6: if constexpr (C >= 6) return launch_gemv_ch<T, M, 6>(a, S, PU, s); break;
+    }
+    return set_error(MBQ_BAD_ARG, "GEMV: no kernel for %d chunks", ch);
+}
+
+template <int T>
+static int launch_gemv_t(const Args& a, hipStream_t s) {
+    switch (a.M) {
+        case 1: return launch_gemv_m<T, 1>(a, s);
+        case 2: return launch_gemv_m<T, 2>(a, s);
+        case 3: return launch_gemv_m<T, 3>(a, s);
+        default: return launch_gemv_m<T, 4>(a, s);
+    }
+}
+
+int launch_gemv(int t, const Args& a, hipStream_t s) {
+    switch (t) {
+        case T_Q8_0: return launch_gemv_t<T_Q8_0>(a, s);
+        case T_Q4_K: return launch_gemv_t<T_Q4_K>(a, s);
+        case T_INT8: return launch_gemv_t<T_INT8>(a, s);
+    }
+    return set_error(MBQ_BAD_ARG, "no GEMV for type %d", t);
+}
+
+}  // namespace mbq

@@ -38,6 +38,7 @@ int workspace(Workspace* out);
 int set_error(int code, const char* fmt, ...);
 
 int launch_matmul(int t, const Args& a, hipStream_t s);
+int launch_gemv(int t, const Args& a, hipStream_t s);   // M <= GEMV_MAX_M (mbq_gemv.hip)
 int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
 // weight-stream GEMM (mbq_wsgemm.hip) for GEMV_MAX_M < M <= WS_MAX_M: rows_per_block 32 or 64, splits >= 1
 constexpr int64_t WS_MAX_M = 64;
