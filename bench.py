@@ -116,7 +116,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
         out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
                                     "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
                                     "rotation_MB": round(copies * wbytes / 1e6, 1),
-                                    "plan": "gemv" if M <= 4 else "%dx%d/%d" % LIB.gemm_plan(-8 if t == "int8" else t, M, N, K)}
+                                    "plan": LIB.plan_str(-8 if t == "int8" else t, M, N, K)}
         total_us += us
         total_bytes += ab
         total_flops += fl
@@ -319,7 +319,7 @@ def main():
                    "rotation_MB": proj["rotation_MB"]},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "mbq::gemv_kernel<8, 1, 4, true>", "kernel_us": proj["us"],
+                     "kernel": "mbq::gemv_kernel (Q8_0, 1 activation row)", "kernel_us": proj["us"],
                      "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
         "configs": {f"c{c}": {k: v for k, v in r.items() if k != "projections"} | {"projections": r["projections"]}
                     for c, r in res.items()},

@@ -107,16 +107,25 @@ int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_d
 
 /* Tuning and introspection (no counterpart in the reference, whose kernels are closed). For an activation batch of M
  * rows, mbq_gemm_plan reports how mbq_matmul / mbq_int8_linear would run a (N, K) weight of type t (MBQ_INT8 for the
- * int8 linear): *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses the per-device workspace
- * below); bm = bn = splits = 0 means the decode GEMV (M <= 4); bm = 16 means the weight-stream kernel of batches of
- * 5..64 rows, with *bn weight rows per block (64 or 128). mbq_force_gemm_plan makes every later GEMM call in the
- * process use tiles bm x bn and `splits` K ranges (bm = 0: automatic again); shapes of the LDS-tile kernel:
- * 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}; of the weight-stream kernel (5..64 rows): 16x64, 16x128.
+ * int8 linear): the kernel (MBQ_KERNEL_*), *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses
+ * the per-device workspace below).
+ *   MBQ_KERNEL_GEMV    M <= 4, bm = bn = splits = 0.
+ *   MBQ_KERNEL_STREAM  weight-stream kernel, 5 <= M <= 64: bm = 16, bn = weight rows per block (64 or 128).
+ *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
+ *   MBQ_KERNEL_DIRECT  weight-direct kernel of large batches: 256x{256,192,128}, 128x{320,256,128}; splits = 1.
+ * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
+ * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES or MBQ_KERNEL_DIRECT: that kernel with
+ * its own tile choice).
  * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
  * counters), allocated by the first such call on a device and kept until the process ends; GEMM calls on one device
  * that overlap in time must not both split K. */
-int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* bm, int* bn, int* splits);
-int mbq_force_gemm_plan(int bm, int bn, int splits);
+#define MBQ_KERNEL_AUTO 0
+#define MBQ_KERNEL_GEMV 0
+#define MBQ_KERNEL_STREAM 1
+#define MBQ_KERNEL_TILES 2
+#define MBQ_KERNEL_DIRECT 3
+int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits);
+int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits);
 
 #ifdef __cplusplus
 }

@@ -31,21 +31,35 @@ _SIGS = {
     "mbq_int8_linear": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                    _c.c_void_p, _c.c_int, _c.c_void_p]),
     "mbq_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64, _c.c_int64, _c.POINTER(_c.c_int),
-                                 _c.POINTER(_c.c_int), _c.POINTER(_c.c_int)]),
-    "mbq_force_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int]),
+                                 _c.POINTER(_c.c_int), _c.POINTER(_c.c_int), _c.POINTER(_c.c_int)]),
+    "mbq_force_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
 }
 
 
+# GEMM kernels of gemm_plan / force_gemm_plan (MBQ_KERNEL_* of include/mbq.h)
+KERNEL_AUTO = KERNEL_GEMV = 0
+KERNEL_STREAM, KERNEL_TILES, KERNEL_DIRECT = 1, 2, 3
+KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_STREAM: "stream", KERNEL_TILES: "tiles", KERNEL_DIRECT: "direct"}
+
+
 def gemm_plan(t: int, m: int, n: int, k: int):
-    """-> (tile rows, tile cols, K splits) the library would use; (0, 0, 0) = decode GEMV"""
-    bm, bn, sp = _c.c_int(), _c.c_int(), _c.c_int()
-    check(lib().mbq_gemm_plan(int(t), int(m), int(n), int(k), _c.byref(bm), _c.byref(bn), _c.byref(sp)), "gemm_plan")
-    return bm.value, bn.value, sp.value
+    """-> (kernel, tile rows, tile cols, K splits) the library would use; (0, 0, 0, 0) = decode GEMV"""
+    kn, bm, bn, sp = _c.c_int(), _c.c_int(), _c.c_int(), _c.c_int()
+    check(lib().mbq_gemm_plan(int(t), int(m), int(n), int(k), _c.byref(kn), _c.byref(bm), _c.byref(bn), _c.byref(sp)),
+          "gemm_plan")
+    return kn.value, bm.value, bn.value, sp.value
 
 
-def force_gemm_plan(bm: int = 0, bn: int = 0, splits: int = 0):
-    """force every later GEMM of the process to bm x bn tiles and `splits` K ranges; force_gemm_plan() = automatic"""
-    check(lib().mbq_force_gemm_plan(int(bm), int(bn), int(splits)), "force_gemm_plan")
+def force_gemm_plan(kernel: int = KERNEL_AUTO, bm: int = 0, bn: int = 0, splits: int = 0):
+    """force every later GEMM (M > 4) of the process to one kernel, bm x bn tiles and `splits` K ranges;
+    force_gemm_plan() = automatic"""
+    check(lib().mbq_force_gemm_plan(int(kernel), int(bm), int(bn), int(splits)), "force_gemm_plan")
+
+
+def plan_str(t: int, m: int, n: int, k: int) -> str:
+    """the plan as text, e.g. 'direct 256x192/1'"""
+    kn, bm, bn, sp = gemm_plan(t, m, n, k)
+    return "gemv" if kn == KERNEL_GEMV else f"{KERNEL_NAMES[kn]} {bm}x{bn}/{sp}"
 
 _lock = threading.Lock()
 _lib = None

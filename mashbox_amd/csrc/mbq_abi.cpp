@@ -273,8 +273,8 @@ int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_d
     return launch_matmul(T_INT8, a, reinterpret_cast<hipStream_t>(stream));
 }
 
-int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* bm, int* bn, int* splits) {
-    if (!bm || !bn || !splits) return set_error(MBQ_BAD_ARG, "NULL output");
+int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits) {
+    if (!kernel || !bm || !bn || !splits) return set_error(MBQ_BAD_ARG, "NULL output");
     if (t == T_INT8) {
         if (N <= 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX || K % 16) return set_error(MBQ_BAD_ARG, "int8 shape (%lld, %lld)", (long long)N, (long long)K);
     } else if (int rc = check_shape(t, N, K)) {
@@ -282,16 +282,16 @@ int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* bm, int* bn, int*
     }
     if (M < 0 || M > INT32_MAX) return set_error(MBQ_BAD_ARG, "M = %lld", (long long)M);
     if (M <= GEMV_MAX_M) {
-        *bm = *bn = *splits = 0;
+        *kernel = *bm = *bn = *splits = 0;
         return MBQ_OK;
     }
     Args a{};
     a.M = M;
     a.N = N;
     a.K = K;
-    return gemm_plan(t, a, bm, bn, splits);
+    return gemm_plan(t, a, kernel, bm, bn, splits);
 }
 
-int mbq_force_gemm_plan(int bm, int bn, int splits) { return force_gemm_plan(bm, bn, splits); }
+int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits) { return force_gemm_plan(kernel, bm, bn, splits); }
 
 }  // extern "C"

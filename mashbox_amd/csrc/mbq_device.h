@@ -162,6 +162,13 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+// v as a register value the compiler cannot look through (so byte extracts stay register ops on it), without the
+// ordering constraints of a volatile asm
+__device__ __forceinline__ uint32_t hide(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // two float32 -> bfloat16 pair (lo, hi), round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     const bf16x2_t p = {(__bf16)lo, (__bf16)hi};

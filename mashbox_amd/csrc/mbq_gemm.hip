@@ -488,8 +488,8 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
     return best;
 }
 
-// forced plan (tests, tuning): tile rows, tile columns, splits; 0 = automatic
-static std::atomic<int> g_force_bm{0}, g_force_bn{0}, g_force_s{0};
+// forced plan (tests, tuning): kernel, tile rows, tile columns, splits; kernel 0 = automatic
+static std::atomic<int> g_force_kind{0}, g_force_bm{0}, g_force_bn{0}, g_force_s{0};
 
 template <int T>
 static int find_cand(int bm, int bn) {
@@ -501,8 +501,8 @@ static int find_cand(int bm, int bn) {
 template <int T>
 static int pick(const Args& a, Plan* p) {
     *p = plan_gemm<T>(a.M, a.N, a.K, cu_count());
-    const int fbm = g_force_bm.load(), fbn = g_force_bn.load(), fs = g_force_s.load();
-    if (fbm > 0) {
+    if (g_force_kind.load() == K_TILES && g_force_bm.load() > 0) {
+        const int fbm = g_force_bm.load(), fbn = g_force_bn.load(), fs = g_force_s.load();
         const int i = find_cand<T>(fbm, fbn);
         if (i < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", fbm, fbn);
         const int64_t KT = (a.K + GK - 1) / GK, tiles = ((a.M + fbm - 1) / fbm) * ((a.N + fbn - 1) / fbn);
@@ -515,16 +515,40 @@ static int pick(const Args& a, Plan* p) {
     return 0;
 }
 
-// the weight-stream kernel (mbq_wsgemm.hip) runs a batch of at most WS_MAX_M rows, unless a plan forces an LDS tile;
-// a forced plan with 16-row tiles forces the weight-stream kernel (bn rows per block, `splits` K ranges)
-static bool use_ws(int64_t M, int* nr, int* S) {
-    const int fbm = g_force_bm.load();
-    if (fbm == 16) {
-        *nr = g_force_bn.load();
-        *S = std::max(1, g_force_s.load());
-        return M > GEMV_MAX_M && M <= WS_MAX_M;
+// The kernel of a batch of M > GEMV_MAX_M rows: the weight-stream kernel (mbq_wsgemm.hip) up to WS_MAX_M rows, else the
+// LDS-tile kernel; a forced plan overrides it (and is the only way to the weight-direct kernel, mbq_pgemm.hip).
+struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block; K_DIRECT: bm = 16 mt, bn = 64 nt
+
+static int choose(int t, const Args& a, Choice* c) {
+    const int fk = g_force_kind.load();
+    if (fk == K_STREAM) {
+        if (a.M <= GEMV_MAX_M || a.M > WS_MAX_M)
+            return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs %lld < M <= %lld", (long long)GEMV_MAX_M, (long long)WS_MAX_M);
+        *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
+        return 0;
     }
-    return fbm == 0 && M > GEMV_MAX_M && M <= WS_MAX_M;
+    if (fk == K_DIRECT) {
+        int bm = g_force_bm.load(), bn = g_force_bn.load();
+        if (bm == 0) {                                       // the kernel's own tile choice
+            int mt = 0, nt = 0;
+            pgemm_shape(a.M, a.N, a.K, &mt, &nt);
+            bm = 16 * mt, bn = 64 * nt;
+        }
+        *c = Choice{K_DIRECT, bm, bn, 1};
+        return 0;
+    }
+    if (fk == K_TILES) {
+        *c = Choice{K_TILES, g_force_bm.load(), g_force_bn.load(), std::max(1, g_force_s.load())};
+        return 0;
+    }
+    if (a.M <= WS_MAX_M) {
+        int nr = 0, S = 1;
+        wsgemm_plan(t, a, &nr, &S);
+        *c = Choice{K_STREAM, 16, nr, S};
+    } else {
+        *c = Choice{K_TILES, 0, 0, 0};
+    }
+    return 0;
 }
 
 template <int T>
@@ -533,12 +557,10 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
         return set_error(MBQ_BAD_ARG, "GEMM operands over 2 GiB (weight %lld bytes, x %lld x %lld)", (long long)a.wbytes,
                          (long long)a.M, (long long)a.K);
-    int nr = 0, S = 1;
-    if (use_ws(a.M, &nr, &S)) {
-        if (g_force_bm.load() != 16) wsgemm_plan(T, a, &nr, &S);
-        return launch_wsgemm(T, a, nr, S, s);
-    }
-    if (g_force_bm.load() == 16) return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs %lld < M <= %lld", (long long)GEMV_MAX_M, (long long)WS_MAX_M);
+    Choice c;
+    if (int rc = choose(T, a, &c)) return rc;
+    if (c.kind == K_STREAM) return launch_wsgemm(T, a, c.bn, c.S, s);
+    if (c.kind == K_DIRECT) return launch_pgemm(T, a, c.bm / 16, c.bn / 64, s);
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
@@ -547,18 +569,26 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     return CANDS<T>[p.idx].launch(a, p.S, p.kts, w, s);
 }
 
-int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits) {
-    Plan p;
-    int rc;
-    int nr = 0, S = 1;
-    if (use_ws(a.M, &nr, &S)) {
-        if (g_force_bm.load() != 16) wsgemm_plan(t, a, &nr, &S);
+int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) {
+    Choice c;
+    if (int rc = choose(t, a, &c)) return rc;
+    *kernel = c.kind;
+    if (c.kind == K_STREAM) {
+        int nr = c.bn, S = c.S;
         wsgemm_effective(t, a, &nr, &S);
         *bm = 16;
         *bn = nr;
         *splits = S;
         return 0;
     }
+    if (c.kind == K_DIRECT) {
+        *bm = c.bm;
+        *bn = c.bn;
+        *splits = 1;
+        return 0;
+    }
+    Plan p;
+    int rc;
     switch (t) {
         case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
         case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
@@ -570,13 +600,26 @@ int gemm_plan(int t, const Args& a, int* bm, int* bn, int* splits) {
     return 0;
 }
 
-int force_gemm_plan(int bm, int bn, int splits) {
-    if (bm == 16 && bn != 64 && bn != 128) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM takes 64 or 128 rows per block, not %d", bn);
-    if (bm != 0 && bm != 16 && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no GEMM tile %d x %d", bm, bn);
+int force_gemm_plan(int kernel, int bm, int bn, int splits) {
     if (splits < 0) return set_error(MBQ_BAD_ARG, "splits %d", splits);
-    g_force_bm = bm;
-    g_force_bn = bn;
-    g_force_s = splits;
+    switch (kernel) {
+        case K_AUTO: break;
+        case K_STREAM:
+            if (bm != 16 || (bn != 64 && bn != 128)) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM runs 16 x 64 or 16 x 128, not %d x %d", bm, bn);
+            break;
+        case K_TILES:
+            if ((bm || bn) && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no LDS GEMM tile %d x %d", bm, bn);
+            break;
+        case K_DIRECT:
+            if ((bm || bn) && (bm % 16 || bn % 64 || splits > 1 || !pgemm_shape_known(bm / 16, bn / 64)))
+                return set_error(MBQ_BAD_ARG, "no weight-direct GEMM tile %d x %d (splits %d)", bm, bn, splits);
+            break;
+        default: return set_error(MBQ_BAD_ARG, "no GEMM kernel %d", kernel);
+    }
+    g_force_kind = kernel;
+    g_force_bm = kernel ? bm : 0;
+    g_force_bn = kernel ? bn : 0;
+    g_force_s = kernel ? splits : 0;
     return 0;
 }
 

@@ -1,0 +1,92 @@
+// Weight-direct MFMA operands, shared by the GEMMs that take their weights from HBM straight into registers
+// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_K), 64 contiguous
+// bytes of each row of the quant plane. Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
+// (g = l >> 4, the lane group). The MFMA sums over K, so any K order works when x follows it: in K step s of an
+// iteration, lane group g holds the 8 values K = k0 + g KI/4 + 8 s + e (e = 0..7) for both operands.
+//   int8   16 quants = 2 K steps; bf16(q) is exact; the per-row scale multiplies the float32 sum in the epilogue.
+//   Q8_0   16 quants of block (k0 + 16 g) / 32; the B operand is q * d (exact in float32) rounded to nearest even
+//          bfloat16, the value the LDS GEMM stores.
+//   Q4_K   one 16-byte unit = the 32 quants of sub-block k0/32 + g = 4 K steps; the B operand is (d sc) q - dmin m
+//          (exact in float32) rounded to nearest even bfloat16.
+// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K); plane layouts: mbq_layout.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mbq_device.h"
+#include "mbq_layout.h"
+
+namespace mbq {
+
+template <int T> constexpr int ws_ki() { return T == T_Q4_K ? 128 : 64; }
+inline int ws_ki_of(int t) { return t == T_Q4_K ? 128 : 64; }
+
+// raw bytes of one iteration of one 16-row tile, as one lane holds them
+template <int T> struct WsRaw;
+template <> struct WsRaw<T_INT8> { u32x4 q; };
+template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
+template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
+template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : 2; }   // buffer loads per tile per iteration
+
+// per-lane dequant constants of one tile's unit
+struct WsScale { float a, b, c; };   // Q8_0: d; Q4_K: d*sc, dmin*m, d*sc/16
+
+template <int T>
+__device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
+    WsScale s{1.f, 0.f, 0.f};
+    if constexpr (T == T_Q8_0) {
+        s.a = f16f(w.d);
+    } else if constexpr (T == T_Q4_K) {
+        uint32_t sc, mn;
+        q4k_scale_min_sel(w.meta[1], w.meta[2], w.meta[3], q4k_sel(j), &sc, &mn);
+        s.a = f16f(w.meta[0]) * (float)sc;          // exact
+        s.b = f16f(w.meta[0] >> 16) * (float)mn;    // exact
+        s.c = s.a * 0.0625f;                        // exact: a power-of-two scale
+    }
+    return s;
+}
+
+// dword p (0..3) of the B operand of K step s: bfloat16 values 2p, 2p + 1 of the lane's 8 (s, p constants once the
+// caller's loops are unrolled); each dword is independent of the others, so a caller can spread them between MFMAs
+template <int T>
+__device__ __forceinline__ uint32_t ws_bpair(const WsRaw<T>& w, const WsScale& sc, int s, int p) {
+    if constexpr (T == T_Q4_K) {
+        // dword s of the unit: quant 8s+2p in bits 4p..4p+3, quant 8s+2p+1 in bits 16+4p.. (mbq_layout.h); the odd
+        // nibble positions come out 16 times too large and take the scale d*sc/16
+        const uint32_t v = w.q[s];
+        if (p == 0) {
+            const uint32_t m = opaque(v & 0x000F000Fu);
+            return pack_bf16(__builtin_fmaf((float)(m & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)((m >> 16) & 0xFFu), sc.a, -sc.b));
+        } else if (p == 1) {
+            const uint32_t m = opaque(v & 0x00F000F0u);
+            return pack_bf16(__builtin_fmaf((float)(m & 0xFFu), sc.c, -sc.b), __builtin_fmaf((float)((m >> 16) & 0xFFu), sc.c, -sc.b));
+        } else if (p == 2) {
+            const uint32_t m = opaque(v & 0x0F000F00u);
+            return pack_bf16(__builtin_fmaf((float)((m >> 8) & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)(m >> 24), sc.a, -sc.b));
+        } else {
+            const uint32_t m = opaque(v & 0xF000F000u);
+            return pack_bf16(__builtin_fmaf((float)((m >> 8) & 0xFFu), sc.c, -sc.b), __builtin_fmaf((float)(m >> 24), sc.c, -sc.b));
+        }
+    } else {
+        // 16 quants = dwords 2s, 2s + 1 of K step s; q * d is exact in float32 (at most 19 significant bits)
+        const uint32_t v = hide(w.q[2 * s + (p >> 1)]);
+        const int sh = (p & 1) * 16;
+        float f0 = (float)(int8_t)((v >> sh) & 0xFFu), f1 = (float)(int8_t)((v >> (sh + 8)) & 0xFFu);
+        if constexpr (T == T_Q8_0) f0 *= sc.a, f1 *= sc.a;
+        return pack_bf16(f0, f1);
+    }
+}
+
+// B operand of K step s: the 8 values of the lane's row, as bfloat16
+template <int T>
+__device__ __forceinline__ bf16x8_t ws_bop(const WsRaw<T>& w, const WsScale& sc, int s) {
+    const u32x4 o{ws_bpair<T>(w, sc, s, 0), ws_bpair<T>(w, sc, s, 1), ws_bpair<T>(w, sc, s, 2), ws_bpair<T>(w, sc, s, 3)};
+    return __builtin_bit_cast(bf16x8_t, o);
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l writes lds_wave + 16 l (lds_wave wave-uniform)
+__device__ __forceinline__ void ws_dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
+}
+
+}  // namespace mbq

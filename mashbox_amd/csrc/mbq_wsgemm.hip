@@ -16,15 +16,7 @@
 // (l - 1) % D is no longer read), DMA x of iteration l + D - 1 into stage (l - 1) % D, convert and multiply, then load
 // the weights of iteration l + D into the buffer just used.
 //
-// Iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_K): 64 contiguous bytes of each row of the quant
-// plane. Lane l reads 16 bytes of row (l & 15) of its tile at byte 16 g (g = l >> 4, the lane group). The MFMA sums over
-// K, so any K order works when x follows it: in K step s of an iteration, lane group g holds the 8 values
-// K = k0 + g KI/4 + 8 s + e (e = 0..7) for both operands.
-//   int8   16 quants = 2 K steps; bf16(q) is exact; the per-row scale multiplies the float32 sum in the epilogue.
-//   Q8_0   16 quants of block (k0 + 16 g) / 32; the B operand is q * d (exact in float32) rounded to nearest even
-//          bfloat16, the value the LDS GEMM stores.
-//   Q4_K   one 16-byte unit = the 32 quants of sub-block k0/32 + g = 4 K steps; the B operand is (d sc) q - dmin m
-//          (exact in float32) rounded to nearest even bfloat16.
+// Iterations, lane layout and the B operand of each type: mbq_wdirect.h.
 // x stage layout: ROWS rows of KI bfloat16 in 16-byte chunks, chunk c of row r at slot c ^ (r & (CH - 1)), so that
 // the A-operand reads (16 rows, one chunk each per lane group) hit distinct banks; the DMA applies the swizzle through
 // each lane's source address. x rows past M and chunks past K read zero through the buffer range check. Weight rows
@@ -44,24 +36,16 @@
 #include "mbq_device.h"
 #include "mbq_launch.h"
 #include "mbq_layout.h"
+#include "mbq_wdirect.h"
 
 namespace mbq {
 
 constexpr int WS_THREADS = 256;    // 4 waves
 
-template <int T> constexpr int ws_ki() { return T == T_Q4_K ? 128 : 64; }
-static int ws_ki_of(int t) { return t == T_Q4_K ? 128 : 64; }
 // iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_K) at 64 activation rows
 template <int T> constexpr int ws_depth() { return T == T_Q4_K ? 4 : 8; }
 // x rows staged: 16 MT, rounded so that every wave issues the same number of 1 KiB DMA instructions per stage
 template <int T, int MT> constexpr int ws_rows() { return T == T_Q4_K ? 16 * MT : (MT <= 2 ? 32 : 64); }
-
-// raw bytes of one iteration of one 16-row tile, as one lane holds them
-template <int T> struct WsRaw;
-template <> struct WsRaw<T_INT8> { u32x4 q; };
-template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
-template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
-template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : 2; }   // buffer loads per tile per iteration
 
 struct WsArgs {
     const uint8_t* base;        // planes of the weight (host layer applied)
@@ -78,61 +62,6 @@ struct WsArgs {
     float* ws;                  // S > 1: partial tiles, one block's outputs per (tile, split)
     int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
 };
-
-// per-lane dequant constants of one tile's unit
-struct WsScale { float a, b, c; };   // Q8_0: d; Q4_K: d*sc, dmin*m, d*sc/16
-
-template <int T>
-__device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
-    WsScale s{1.f, 0.f, 0.f};
-    if constexpr (T == T_Q8_0) {
-        s.a = f16f(w.d);
-    } else if constexpr (T == T_Q4_K) {
-        uint32_t sc, mn;
-        q4k_scale_min_sel(w.meta[1], w.meta[2], w.meta[3], q4k_sel(j), &sc, &mn);
-        s.a = f16f(w.meta[0]) * (float)sc;          // exact
-        s.b = f16f(w.meta[0] >> 16) * (float)mn;    // exact
-        s.c = s.a * 0.0625f;                        // exact: a power-of-two scale
-    }
-    return s;
-}
-
-// 4 int8 quants (one dword) -> 2 bfloat16 pairs of q * d; with SCALED false, of q (exact)
-template <bool SCALED>
-__device__ __forceinline__ void ws_i8x4(uint32_t w, float d, uint32_t* o) {
-    float f0 = (float)(int8_t)(w & 0xFFu), f1 = (float)(int8_t)((w >> 8) & 0xFFu);
-    float f2 = (float)(int8_t)((w >> 16) & 0xFFu), f3 = (float)(int8_t)(w >> 24);
-    if constexpr (SCALED) f0 *= d, f1 *= d, f2 *= d, f3 *= d;     // exact: at most 19 significant bits
-    o[0] = pack_bf16(f0, f1);
-    o[1] = pack_bf16(f2, f3);
-}
-
-// B operand of K step s (a constant once the caller's loop is unrolled): the 8 values of the lane's row, as bfloat16
-template <int T>
-__device__ __forceinline__ bf16x8_t ws_bop(const WsRaw<T>& w, const WsScale& sc, int s) {
-    u32x4 o;
-    if constexpr (T == T_Q4_K) {
-        // dword s of the unit: quant 8s+2p in bits 4p..4p+3, quant 8s+2p+1 in bits 16+4p.. (mbq_layout.h)
-        const uint32_t v = w.q[s];
-        const uint32_t m0 = opaque(v & 0x000F000Fu), m1 = opaque(v & 0x00F000F0u);
-        const uint32_t m2 = opaque(v & 0x0F000F00u), m3 = opaque(v & 0xF000F000u);
-        o[0] = pack_bf16(__builtin_fmaf((float)(m0 & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)((m0 >> 16) & 0xFFu), sc.a, -sc.b));
-        o[1] = pack_bf16(__builtin_fmaf((float)(m1 & 0xFFu), sc.c, -sc.b), __builtin_fmaf((float)((m1 >> 16) & 0xFFu), sc.c, -sc.b));
-        o[2] = pack_bf16(__builtin_fmaf((float)((m2 >> 8) & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)(m2 >> 24), sc.a, -sc.b));
-        o[3] = pack_bf16(__builtin_fmaf((float)((m3 >> 8) & 0xFFu), sc.c, -sc.b), __builtin_fmaf((float)(m3 >> 24), sc.c, -sc.b));
-    } else {
-        uint32_t r[4];
-        ws_i8x4<T == T_Q8_0>(w.q[2 * s], sc.a, &r[0]);
-        ws_i8x4<T == T_Q8_0>(w.q[2 * s + 1], sc.a, &r[2]);
-        o = u32x4{r[0], r[1], r[2], r[3]};
-    }
-    return __builtin_bit_cast(bf16x8_t, o);
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l writes lds_wave + 16 l (lds_wave wave-uniform)
-__device__ __forceinline__ void ws_dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
-}
 
 template <int T, int MT, int NT, bool KFULL>
 __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {

@@ -268,13 +268,67 @@ def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cu
         ref = xf @ R.dequant(raw, t, k).astype(np.float64).T
     outs = []
     for splits in (1, 3):
-        forced_plan(bm, bn, splits)
-        assert LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)[:2] == (bm, bn)
+        forced_plan(LIB.KERNEL_TILES, bm, bn, splits)
+        assert LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)[:3] == (LIB.KERNEL_TILES, bm, bn)
         y = run()
         assert_product(y, ref, f"{t} tile {bm}x{bn} splits {splits}")
         outs.append(y)
     # a split sums float32 partials in another order: close to, not bitwise equal to, one range
     assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
+
+
+def _direct_case(t, m, n, k, rng, cuda):
+    xb = G.acts(rng, m, k)
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    if t == "int8":
+        q, s = G.int8_weights(rng, n, k)
+        w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+        return (lambda: _int8_f32(x, w)), (xf @ q.astype(np.float64).T) * s
+    raw = G.RAW[t](rng, n, k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    return (lambda: KQ.matmul(x, planes).cpu().numpy()), xf @ R.dequant(raw, t, k).astype(np.float64).T
+
+
+DIRECT_SHAPES = [(16, 4), (16, 3), (16, 2), (8, 5), (8, 4), (8, 2)]
+
+
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("mt,nt", DIRECT_SHAPES)
+@pytest.mark.parametrize("kfull", [False, True], ids=["k_ragged", "k_full"])
+def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
+    """the weight-direct kernel of large batches: every tile shape, a batch of exactly one activation tile and one of
+    2 tiles + a ragged rest (the last tile shifted back over the one before), ragged weight rows, a K that is or is not
+    a multiple of the kernel's iteration (64 values; 128 for Q4_K, whose K is always whole)"""
+    if t == R.Q4_K and not kfull:
+        pytest.skip("a Q4_K K is a whole number of 256-value super-blocks")
+    bm, bn = 16 * mt, 64 * nt
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
+    for m, n in ((bm, bn + 17), (2 * bm + 37, 2 * bn + 17)):
+        rng = np.random.default_rng([m, n, int(kfull), 0 if t == "int8" else t])
+        run, ref = _direct_case(t, m, n, k, rng, cuda)
+        forced_plan(LIB.KERNEL_DIRECT, bm, bn, 1)
+        assert LIB.gemm_plan(-8 if t == "int8" else t, m, n, k) == (LIB.KERNEL_DIRECT, bm, bn, 1)
+        assert_product(run(), ref, f"{t} direct {bm}x{bn} m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+def test_kernel_choice_by_batch_and_forced_auto_shapes(t, forced_plan, cuda):
+    """automatic plans: GEMV to 4 rows, weight-stream to 64, LDS tiles beyond; a forced kernel with bm = bn = 0 takes
+    that kernel's own tile choice, and both prefill kernels give the right product"""
+    n, k = 1000, 1024
+    tt = -8 if t == "int8" else t
+    assert LIB.gemm_plan(tt, 4, n, k)[0] == LIB.KERNEL_GEMV
+    assert LIB.gemm_plan(tt, 64, n, k)[0] == LIB.KERNEL_STREAM
+    assert LIB.gemm_plan(tt, 65, n, k)[0] == LIB.KERNEL_TILES
+    assert LIB.gemm_plan(tt, 2048, n, k)[0] == LIB.KERNEL_TILES
+    m = 300
+    run, ref = _direct_case(t, m, n, k, np.random.default_rng(5), cuda)
+    for kind in (LIB.KERNEL_TILES, LIB.KERNEL_DIRECT):
+        forced_plan(kind, 0, 0, 0)
+        kn, bm, bn, _ = LIB.gemm_plan(tt, m, n, k)
+        assert kn == kind and bm > 0 and bn > 0
+        assert_product(run(), ref, f"{t} kernel {kind} {bm}x{bn}")
 
 
 @pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
@@ -303,9 +357,9 @@ def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
         ref = xf @ R.dequant(raw, t, k).astype(np.float64).T
     outs = []
     for splits in (1, 3):
-        forced_plan(16, rows, splits)
-        bm, bn, sp = LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)
-        assert (bm, bn) == (16, rows) and 1 <= sp <= splits
+        forced_plan(LIB.KERNEL_STREAM, 16, rows, splits)
+        kn, bm, bn, sp = LIB.gemm_plan(-8 if t == "int8" else t, m, n, k)
+        assert (kn, bm, bn) == (LIB.KERNEL_STREAM, 16, rows) and 1 <= sp <= splits
         y = run()
         assert_product(y, ref, f"{t} m={m} rows {rows} k={k} splits {splits}")
         outs.append(y)
@@ -313,7 +367,7 @@ def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
 
 
 @pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
-@pytest.mark.parametrize("m,plan", [(64, (16, 64, 4)), (130, (64, 128, 3))], ids=["weight_stream", "lds_tiles"])
+@pytest.mark.parametrize("m,plan", [(64, (1, 16, 64, 4)), (130, (2, 64, 128, 3))], ids=["weight_stream", "lds_tiles"])
 def test_split_k_repeats_bit_for_bit(t, m, plan, forced_plan, cuda):
     """a K split into ranges repeats bit for bit over calls (the arrival counters reset themselves), whichever split
     arrives last: both GEMM kernels"""
