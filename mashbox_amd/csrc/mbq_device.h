@@ -128,6 +128,9 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 
 // buffer resources: loads carry a 32-bit per-lane offset and a scalar offset, and read zero past num_records
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// A buffer-load offset beyond every buffer this library addresses (their byte ranges are at most BUF_MAX_BYTES, checked
+// by each launcher): the load returns zero without touching memory. With a scalar offset below 2^31 the sum cannot wrap.
+constexpr uint32_t OOB_VOFF = 0x7FFFFFF0u;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }

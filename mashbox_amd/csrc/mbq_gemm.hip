@@ -214,7 +214,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 #pragma unroll
         for (int i = 0; i < XD; ++i) {
             uint32_t v = xvo[i];
-            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : 0x7FFFFFF0u;     // past K: out of range, reads zero
+            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : OOB_VOFF;     // past K: out of range, reads zero
             dma16(xr, gemm_lds + s * BM * GK + 8 * (wave + 8 * i) * GK, v, (uint32_t)kk * 2);
         }
     };
@@ -554,7 +554,7 @@ static int choose(int t, const Args& a, Choice* c) {
 template <int T>
 static int launch_gemm_t(const Args& a, hipStream_t s) {
     // buffer resources address one weight's planes and the whole x with 32-bit offsets
-    if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "GEMM operands over 2 GiB (weight %lld bytes, x %lld x %lld)", (long long)a.wbytes,
                          (long long)a.M, (long long)a.K);
     Choice c;

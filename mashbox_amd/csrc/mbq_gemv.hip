@@ -11,9 +11,9 @@
 // an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
 // block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
 // multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
-// the inner loop). The next item's loads (DEPTH - 1 items) are in flight while an item computes; every load is unconditional (chunks
-// past a part's end and items past a wave's last reload data already fetched, cache hits), so the compiler's vmcnt
-// waits count exactly the next item's loads. An item's sums are reduced across the wave with DPP; with S > 1 the block
+// the inner loop). The next item's loads (DEPTH - 1 items) are in flight while an item computes; every load is
+// unconditional (lanes past a part's end, chunks past it and items past a wave's last row read out of the buffer's
+// range: zero, and no memory traffic), so the compiler's vmcnt waits count exactly the next item's loads. An item's sums are reduced across the wave with DPP; with S > 1 the block
 // adds a row's parts through LDS at the end.
 //
 // Arithmetic, float32 accumulation with v_dot2_f32_bf16:
@@ -22,7 +22,7 @@
 //   Q4_K          ((w >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair (128 + q, 128 + q'); per unit
 //                 y += (d sc) * sum(x (128 + q)) - (128 d sc + dmin m) * sum(x); the per-unit sums of x are computed
 //                 once per wave from its x registers.
-// A lane that holds no unit of a part (the part's last chunk) reads a valid unit and has its scale zeroed.
+// A lane that holds no unit of a part (the part's last chunk) reads zero and has its scale zeroed.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -92,16 +92,25 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const bool any = ok && nit > 0 && nu > 0;
 
     struct Raw { u32x4 q[CH]; u32x4 meta[CH]; uint32_t d[CH]; };
+    // Lane offsets of a load. The lanes past the part's last unit (in its last chunk), the chunks past that one and the
+    // items past the wave's last row take an offset beyond the buffer's range: such a load returns zero without
+    // touching memory, so no byte is fetched twice, and the load stays unconditional.
+    const bool lane_in = 64 * lastc + lane < nu;                       // the lane's unit of the last chunk exists
+    const uint32_t vq = (uint32_t)lane * 16u, vq_last = lane_in ? vq : OOB_VOFF;
+    const uint32_t vd = (uint32_t)(lane >> 1) * 2u, vd_last = lane_in ? vd : OOB_VOFF;
+    const uint32_t vm = (uint32_t)(lane >> 3) * 16u, vm_last = lane_in ? vm : OOB_VOFF;
     auto load = [&](Raw& R, int k) {                                  // the k-th row of the wave (clamped)
+        const bool live = k < nit;                                    // wave-uniform
         const int row = r0 + first + min(k, nit - 1) * rstep;
         const uint32_t qs = (uint32_t)row * qstride + (uint32_t)u0 * 16u;
         const uint32_t ss = (uint32_t)g.sc_off + (uint32_t)row * sstride;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const uint32_t c = (uint32_t)min(i, lastc);               // wave-uniform
-            R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)lane * 16u, qs + 1024u * c, 2));
-            if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, (uint32_t)(lane >> 1) * 2u, ss + (uint32_t)u0 + 64u * c);
-            if constexpr (T == T_Q4_K) R.meta[i] = bload16(wr, (uint32_t)(lane >> 3) * 16u, ss + (uint32_t)u0 * 2u + 128u * c);
+            auto off = [&](uint32_t full, uint32_t last) { return (!live || i > lastc) ? OOB_VOFF : (i < lastc ? full : last); };
+            R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
+            if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
+            if constexpr (T == T_Q4_K) R.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
         }
     };
 
@@ -296,7 +305,7 @@ static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
 
 template <int T, int M>
 static int launch_gemv_m(const Args& a, hipStream_t s) {
-    if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "GEMV operands over 2 GiB");
     int S = 1, PU = 0;
     const int ch = gv_parts<T, M>(a.K / gv_uw<T>(), &S, &PU);

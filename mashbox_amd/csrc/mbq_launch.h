@@ -34,6 +34,10 @@ constexpr int WS_TILES = 1 << 16;
 struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
 int workspace(Workspace* out);
 
+// largest weight plane or activation range a kernel addresses through a buffer resource (32-bit offsets; below the
+// out-of-range offset OOB_VOFF of mbq_device.h)
+constexpr int64_t BUF_MAX_BYTES = 0x7FFFFF00;
+
 // records the calling thread's error message; returns code
 int set_error(int code, const char* fmt, ...);
 

@@ -117,8 +117,8 @@ __global__ __launch_bounds__(PG_THREADS, 1) void pgemm_kernel(const PgArgs g) {
     // x of iteration `it` into stage st; iterations past the last one read zero (the loop runs whole rounds of 4)
     auto dma_x = [&](int st, int it) {
         const int kk = k0(it);
-        uint32_t v = it < n ? xv : 0x7FFFFFF0u;
-        if constexpr (!KFULL) v = (kk + 8 * xc < K) ? v : 0x7FFFFFF0u;        // past K: out of range, reads zero
+        uint32_t v = it < n ? xv : OOB_VOFF;
+        if constexpr (!KFULL) v = (kk + 8 * xc < K) ? v : OOB_VOFF;        // past K: out of range, reads zero
 #pragma unroll
         for (int i = 0; i < NDW; ++i)
             ws_dma16(xr, pg_x + st * STAGE + RPI * (wave + 4 * i) * KI, v, (uint32_t)(kk * 2 + i * 4 * RPI * K * 2));
@@ -356,7 +356,7 @@ bool pgemm_shape_known(int mt, int nt) { return pg_index(mt, nt) >= 0; }
 int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s) {
     const int idx = pg_index(mt, nt);
     if (idx < 0) return set_error(MBQ_BAD_ARG, "weight-direct GEMM: no tile of %d x %d activation x weight row tiles", mt, nt);
-    if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "weight-direct GEMM operands over 2 GiB");
     if (a.M < 16 * mt) return set_error(MBQ_BAD_ARG, "weight-direct GEMM: %lld activation rows, fewer than a tile's %d", (long long)a.M, 16 * mt);
     switch (t) {

@@ -104,14 +104,14 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
 #pragma unroll
     for (int i = 0; i < NDW; ++i) {
         const int r = RPI * (wave + 4 * i) + lane / CH, c = (lane % CH) ^ (r & (CH - 1));
-        xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + c * 8) * 2) : 0x7FFFFFF0u;
+        xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + c * 8) * 2) : OOB_VOFF;
         xk[i] = c * 8;
     }
     auto dma_x = [&](int st, int kk) {
 #pragma unroll
         for (int i = 0; i < NDW; ++i) {
             uint32_t v = xvo[i];
-            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : 0x7FFFFFF0u;      // past K: out of range, reads zero
+            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : OOB_VOFF;      // past K: out of range, reads zero
             ws_dma16(xr, ws_x + st * STAGE + RPI * (wave + 4 * i) * KI, v, (uint32_t)kk * 2u);
         }
     };
@@ -353,7 +353,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
     if (a.M <= GEMV_MAX_M || a.M > WS_MAX_M) return set_error(MBQ_BAD_ARG, "weight-stream GEMM: M = %lld", (long long)a.M);
     if (nr != 64 && nr != 128) return set_error(MBQ_BAD_ARG, "weight-stream GEMM: %d rows per block (64 or 128)", nr);
     wsgemm_effective(t, a, &nr, &S);
-    if (a.wbytes >= ((int64_t)1 << 31) || a.M * a.K * 2 >= ((int64_t)1 << 31))
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "weight-stream GEMM operands over 2 GiB");
     const int64_t KT = (a.K + ws_ki_of(t) - 1) / ws_ki_of(t);
     const int64_t kts = (KT + S - 1) / S;
