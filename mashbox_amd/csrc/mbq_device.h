@@ -8,6 +8,7 @@ namespace mbq {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -163,6 +164,40 @@ constexpr uint32_t BF16_ONES = 0x3F803F80u;  // bfloat16 pair (1, 1)
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     asm volatile("" : "+v"(v));
     return v;
+}
+
+// v_mfma_f32_16x16x32_bf16 on an accumulator pinned to accumulation registers and updated in place. For kernels whose
+// accumulators fill the accumulation registers: the compiler's own MFMA there writes its result to other registers
+// than its accumulator input and copies the accumulators back every iteration. The compiler sees an opaque
+// instruction, so the asm pads on entry the hazard such kernels meet (2 wait states after a VALU write of an A or B
+// operand register), and a kernel must wait out the last MFMA (mfma_drain) before its VALU instructions read the
+// accumulators, and must not leave conditional blocks between these MFMAs (the compiler may move accumulators between
+// registers at block boundaries, right after an MFMA that is still writing them).
+__device__ __forceinline__ void mfma_acc(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// the same with the accumulator in (arch) vector registers, for kernels whose accumulators exceed the accumulation
+// registers of their occupancy (the compiler splits a wave's registers evenly between the two files)
+__device__ __forceinline__ void mfma_accv(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+// v_mfma_f32_32x32x16_bf16, the same two forms. Lane l: A row l % 32, B column l % 32, both K values 8 (l / 32) .. +7;
+// accumulator element 4 i + r is row 8 i + 4 (l / 32) + r, column l % 32 (checked on MI355X).
+__device__ __forceinline__ void mfma32_acc(f32x16_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma32_accv(f32x16_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+// 24 wait states: the last mfma_acc / mfma32_acc (16 passes) has written its accumulator before the next instruction
+// reads it
+__device__ __forceinline__ void mfma_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // v as a register value the compiler cannot look through (so byte extracts stay register ops on it), without the

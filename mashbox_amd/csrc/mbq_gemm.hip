@@ -357,6 +357,214 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
     }
 }
 
+// ----------------------------------------------------------------------------------------- specialized waves
+// Block tile 256 x 192 with specialized waves. On gfx950 a wave's VALU instructions do not overlap its own MFMAs, but
+// another wave's VALU instructions issue while the matrix core runs. So waves 0-3 (one per SIMD) only multiply: each
+// owns a 128 x 96 quarter of the tile as 4 x 3 tiles of v_mfma_f32_32x32x16_bf16 (accumulators pinned by mfma32_acc /
+// mfma32_accv: 128 accumulation registers and 64 vector registers, the even split of 256 at two waves per SIMD; the
+// 32 x 32 shape needs half the operand registers of 16 x 16 per K, so a whole K substep is read ahead) and reads its
+// A and B operands from LDS. Waves 4-7 (the other wave of each SIMD) only produce: x tiles by DMA into a ring of 3 LDS stages (issued
+// two steps ahead), weight units from HBM into a ring of 3 register sets (three steps ahead), dequantized into a ring of
+// 2 bf16 LDS stages one step ahead. One barrier per step: the step-l barrier says stage l is complete, and that the
+// stages of step l - 1 are no longer read.
+//
+// Step l, producers (after barrier l): DMA x(l + 2) into A stage (l + 2) % 3 (spread between the next item's chunks),
+// load weights (l + 3), dequantize weights (l + 1) into B stage (l + 1) % 2, wait for x(l + 1), barrier l + 1. Consumers: barrier l, then the 48 MFMAs of step l
+// from A stage l % 3 and B stage l % 2, each K substep's operands read during the one before. Both roles pass n
+// barriers in the same order.
+constexpr int SG_BM = 256, SG_BN = 192;
+constexpr size_t SG_LDS = (size_t)(3 * SG_BM + 2 * SG_BN) * GK * sizeof(uint16_t);   // 144 KiB
+
+template <int T, bool KFULL>
+__global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t sg_lds[];   // A[3][256][64], B[2][192][64] bfloat16
+    uint16_t* const A0 = sg_lds;
+    uint16_t* const B0 = sg_lds + 3 * SG_BM * GK;
+    const int M = g.M, N = g.N, K = g.K;
+
+    // XCD-aware order, as gemm_kernel
+    const int MT = (M + SG_BM - 1) / SG_BM, NT = (N + SG_BN - 1) / SG_BN, TB = MT * NT;
+    const int b = blockIdx.x, xcd = b & 7, q = TB >> 3, rem = TB & 7;
+    const int tile = xcd * q + min(xcd, rem) + (b >> 3);
+    const int m0 = (tile / NT) * SG_BM, n0 = (tile % NT) * SG_BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t lo = layer_offset(g.stride, g.layer_dev, g.nlayers);
+    const bool ok = lo >= 0;
+    const int KT = (K + GK - 1) / GK, n = ok ? KT : 0;
+    auto k0 = [&](int l) { return min(l, n - 1) * GK; };
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+
+    if (wave < 4) {
+        // ---------------------------------------------------------------------------------------------- consumer
+        // 4 x 3 tiles of v_mfma_f32_32x32x16_bf16; a K step is 4 substeps of 16 values, and the 7 operands of substep
+        // s + 1 (4 A row tiles, 3 B column tiles) are read while the 12 MFMAs of substep s run
+        const int cm = wave >> 1, cn = wave & 1;
+        f32x16_t acc[4][3];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[i][j] = f32x16_t{};
+        const int ar = cm * 128 + (lane & 31), br = cn * 96 + (lane & 31), lh = lane >> 5;
+        for (int l = 0; l < n; ++l) {
+            barrier_nofence();                                     // stage l is complete
+            fence();
+            const uint16_t* As = A0 + (l % 3) * SG_BM * GK;
+            const uint16_t* Bs = B0 + (l & 1) * SG_BN * GK;
+            // operand o of substep s: o < 4 A row tile o, else B column tile o - 4; chunk 2 s + (lane >> 5)
+            auto rd = [&](int s, int o) {
+                const uint16_t* base = o < 4 ? As + lds_off(ar + 32 * o, 2 * s + lh) : Bs + lds_off(br + 32 * (o - 4), 2 * s + lh);
+                return *reinterpret_cast<const bf16x8_t*>(base);
+            };
+            bf16x8_t op[2][7];
+#pragma unroll
+            for (int o = 0; o < 7; ++o) op[0][o] = rd(0, o);
+            fence();
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) {
+                        const int k = 3 * i + j;
+                        if (s + 1 < 4 && k < 7) op[(s + 1) & 1][k] = rd(s + 1, k);
+                        // 128 of the 192 accumulator registers fit the accumulation registers at two waves per SIMD
+                        if (j < 2) mfma32_acc(acc[i][j], op[s & 1][i], op[s & 1][4 + j]);
+                        else mfma32_accv(acc[i][j], op[s & 1][i], op[s & 1][4 + j]);
+                        fence();
+                    }
+            }
+            // the compiler may copy accumulators at the loop's back edge or exit (the join with the path that skips the
+            // loop): no such copy may follow an MFMA that is still writing
+            mfma_drain();
+        }
+        // lane holds weight row n0 + 96 cn + 32 j + (lane & 31) and activation rows m0 + 128 cm + 32 i + 8 e + 4 (lane >> 5) + r
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int nn = n0 + br + 32 * j;
+            if (nn >= N) continue;
+            const float sc = (T == T_INT8) ? g.srow[nn] : 1.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int m = m0 + cm * 128 + 32 * i + 8 * e + 4 * lh + r;
+                        if (m < M) store_y(g.y, (int64_t)m * N + nn, ok ? acc[i][j][4 * e + r] * sc : __builtin_nanf(""), g.out_bf16);
+                    }
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------------------------------------------- producer
+    const int pt = tid - 4 * 64, pw = wave - 4;                     // producer thread 0..255, producer wave 0..3
+    const uint8_t* base = g.base + (ok ? lo : 0);
+    const rsrc_t wr = make_rsrc(base, (uint32_t)g.wbytes);
+    const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
+    // x DMA: instruction i of producer wave w fills tile rows 8 (w + 4 i) .. +7 (8 instructions x 4 waves x 8 rows);
+    // lane l writes LDS slot l & 7 of row l >> 3, holding chunk (l & 7) ^ (row & 7) (the swizzle of lds_off)
+    constexpr int XD = SG_BM * GK * 2 / (4 * 64 * 16);              // 8
+    static_assert(XD == 4 * 2, "the producer step interleaves one DMA instruction per dequantized chunk of 2 units");
+    uint32_t xvo[XD];
+    int xk[XD];
+#pragma unroll
+    for (int i = 0; i < XD; ++i) {
+        const int r = 8 * (pw + 4 * i) + (lane >> 3), c = (lane & 7) ^ (lane >> 3);
+        xvo[i] = m0 + r < M ? (uint32_t)(((int64_t)(m0 + r) * K + c * 8) * 2) : OOB_VOFF;     // rows past M: zero
+        xk[i] = c * 8;
+    }
+    auto dma_x = [&](int l) {                                        // x of step l into A stage l % 3
+        const int kk = k0(l);
+        uint16_t* st = A0 + (l % 3) * SG_BM * GK;
+#pragma unroll
+        for (int i = 0; i < XD; ++i) {
+            uint32_t v = xvo[i];
+            if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : OOB_VOFF;      // past K: zero
+            dma16(xr, st + 8 * (pw + 4 * i) * GK, v, (uint32_t)kk * 2);
+        }
+    };
+    // weight units of a step: 2 per row (32 values each) = 384; producer thread t takes unit t and, for t < 128, unit
+    // t + 256 (row u >> 1, unit u & 1 of the step); rows past N are clamped (their outputs are never stored)
+    constexpr int UPT = 2;                                          // units per producer thread (the second for t < 128)
+    const bool two = pt < 2 * SG_BN - 256;
+    BOff bo[UPT];
+    int bu[UPT], brow[UPT];
+#pragma unroll
+    for (int v = 0; v < UPT; ++v) {
+        const int u = v == 0 ? pt : pt + 256;
+        brow[v] = u >> 1;
+        bu[v] = u & 1;
+        bo[v] = b_off<T>(g.sc_off, min(n0 + brow[v], N - 1), K, bu[v]);
+    }
+    if (!two) bo[1] = BOff{OOB_VOFF, OOB_VOFF};                      // no second unit: its loads read zero, no traffic
+    BUnit<T> R[3][UPT];
+    auto load_w = [&](BUnit<T>* Rr, int l) {
+#pragma unroll
+        for (int v = 0; v < UPT; ++v) b_load<T, KFULL>(Rr[v], wr, bo[v], K, k0(l), bu[v]);
+    };
+    auto dequant = [&](const BUnit<T>* Rr, int l) {                   // weights of step l into B stage l % 2
+        uint16_t* st = B0 + (l & 1) * SG_BN * GK;
+#pragma unroll
+        for (int v = 0; v < UPT; ++v) {
+            if (v == 1 && !two) break;                                // wave-uniform: waves 4-5 take two units
+            const BScale sc = b_scale<T>(Rr[v], ((k0(l) >> 5) + bu[v]) & 7);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) st16(st + lds_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc, c));
+        }
+    };
+    constexpr int NDW = XD, NWL = UPT * b_loads<T>();
+    if (n > 0) {
+        dma_x(0);
+        dma_x(1);
+        load_w(R[0], 0);
+        load_w(R[1], 1);
+        load_w(R[2], 2);
+        dequant(R[0], 0);
+        wait_vm<NDW + 3 * NWL>();                                     // x(0) has landed
+        barrier_nofence();                                            // barrier 0
+        // step l (l = 0 .. n - 2): x(l + 2), weights (l + 3), dequantize (l + 1), wait x(l + 1), barrier l + 1. The x
+        // DMA's 8 instructions are spread between the dequantized chunks (a burst of them slows the consumers' reads).
+        auto pstep = [&](auto U_, int l) {
+            constexpr int U = decltype(U_)::value;                    // l % 3
+            const int kk = k0(l + 2);
+            uint16_t* ast = A0 + ((l + 2) % 3) * SG_BM * GK;
+            auto dma_i = [&](int i) {
+                uint32_t v = xvo[i];
+                if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : OOB_VOFF;
+                dma16(xr, ast + 8 * (pw + 4 * i) * GK, v, (uint32_t)kk * 2);
+            };
+            const BUnit<T>* Rr = R[(U + 1) % 3];                      // weights of step l + 1
+            uint16_t* bst = B0 + ((l + 1) & 1) * SG_BN * GK;
+            BScale sc[UPT];
+#pragma unroll
+            for (int v = 0; v < UPT; ++v) sc[v] = b_scale<T>(Rr[v], ((k0(l + 1) >> 5) + bu[v]) & 7);
+            dma_i(0);
+            load_w(R[U], l + 3);                                      // the set of step l, dequantized a step ago
+#pragma unroll
+            for (int i = 0; i < XD; ++i) {
+                if (i > 0) dma_i(i);
+                const int v = i >> 2, c = i & 3;                      // chunk c of unit v
+                if (v == 0 || two) st16(bst + lds_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
+            }
+            wait_vm<NDW + NWL>();                                     // x(l + 1) has landed (loads complete in order)
+            barrier_nofence();
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        int l = 0;
+        for (; l + 3 <= n - 1; l += 3) {
+            pstep(I0{}, l);
+            pstep(I1{}, l + 1);
+            pstep(I2{}, l + 2);
+        }
+        if (l < n - 1) pstep(I0{}, l);
+        if (l + 1 < n - 1) pstep(I1{}, l + 1);
+        wait_vm<0>();                                                 // no DMA may land after the block ends
+    }
+}
+
 // ------------------------------------------------------------------------------------------------- workspace
 // Split-K partials and arrival counters, one set per device, allocated (and the counters cleared) by the first GEMM
 // call that splits K on that device and kept until the process ends. GEMM calls on one device that overlap in time
@@ -405,8 +613,28 @@ static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStr
     return 0;
 }
 
+template <int T, bool KFULL>
+static int launch_sg(const Args& a, hipStream_t s) {
+    auto kern = sgemm_kernel<T, KFULL>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)SG_LDS) != hipSuccess)
+            return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", SG_LDS);
+        attr_set = true;
+    }
+    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
+               a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr};
+    const int64_t tiles = ((a.M + SG_BM - 1) / SG_BM) * ((a.N + SG_BN - 1) / SG_BN);
+    kern<<<dim3((unsigned)tiles), GT, SG_LDS, s>>>(g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
+// the 256 x 192 tile without a K split runs the specialized-wave kernel
 template <int T, int BM, int BN, int P>
 static int launch_k(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
+    if (BM == SG_BM && BN == SG_BN && S == 1) return (a.K % GK == 0) ? launch_sg<T, true>(a, s) : launch_sg<T, false>(a, s);
     return (a.K % GK == 0) ? launch_tile<T, BM, BN, P, true>(a, S, kts, w, s) : launch_tile<T, BM, BN, P, false>(a, S, kts, w, s);
 }
 

@@ -67,14 +67,6 @@ struct PgArgs {
     int mtiles, tiles;          // activation tiles, all tiles
 };
 
-// v_mfma_f32_16x16x32_bf16 on an accumulator pinned to accumulation registers and updated in place (the compiler's own
-// MFMA writes its result to other registers than its accumulator input in this kernel, and then copies the
-// accumulators back every iteration). The compiler sees an opaque instruction, so the asm pads the hazard it can meet
-// here on entry: 2 wait states after a VALU write of an A or B operand register.
-__device__ __forceinline__ void mfma_acc(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
-    asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-
 template <int T, int MT, int NT, bool KFULL>
 __global__ __launch_bounds__(PG_THREADS, 1) void pgemm_kernel(const PgArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint16_t pg_x[];   // D stages of 16 MT x KI bfloat16
@@ -236,13 +228,10 @@ __global__ __launch_bounds__(PG_THREADS, 1) void pgemm_kernel(const PgArgs g) {
             step(I1{}, l + 1);
             step(I2{}, l + 2);
             step(I3{}, l + 3);
+            mfma_drain();                                             // before any accumulator copy at the back edge or exit
         }
         wait_vm<0>();                                                 // no DMA may land after the block ends
     }
-    // the accumulators are read below by VALU instructions: wait out the last MFMAs (at most 18 wait states)
-    fence();
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-    fence();
 
     // epilogue: lane holds weight row n0 + 16 j + (lane & 15) and activation rows m0 + 16 i + 4 (lane >> 4) + r; the rows
     // before mfirst belong to the tile before
