@@ -48,6 +48,19 @@ def q4_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
     return np.concatenate([d, dmin, R.pack_scale_min_k4(sc, mn), qs], axis=-1).reshape(n, nb * 144)
 
 
+def q6_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
+    """(n, row_bytes) uint8 Q6_K super-blocks: d fp16 ~ U(lo, hi) / 64; 16 int8 scales uniform in [-127, 127]; 6-bit
+    quants uniform in [0, 63], packed as the Q6_K layout holds them (src/mashbox/ops/reference.py:164-173)"""
+    nb = k // 256
+    q = rng.integers(0, 64, (n, nb, 2, 4, 32), dtype=np.uint8)        # value 128g + 32r + i
+    # ql[64g + 32j + i]: low nibble = q(g, j, i) & 15, high nibble = q(g, 2 + j, i) & 15
+    ql = np.concatenate([(q[:, :, :, j] & 15) | ((q[:, :, :, 2 + j] & 15) << 4) for j in range(2)], -1)
+    qh = sum(((q[:, :, :, r] >> 4) << (2 * r)) for r in range(4)).astype(np.uint8)
+    sc = rng.integers(-127, 128, (n, nb, 16), dtype=np.int8).view(np.uint8)
+    d = (rng.uniform(lo, hi, (n, nb)) / 64).astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    return np.concatenate([ql.reshape(n, nb, 128), qh.reshape(n, nb, 64), sc, d], axis=-1).reshape(n, nb * 210)
+
+
 def int8_weights(rng, n: int, k: int, lo=1e-3, hi=1e-2):
     """int8 per-output-channel: q (n, k) uniform in [-127, 127], s (n,) float32 ~ U(lo, hi)"""
     q = rng.integers(-127, 128, (n, k), dtype=np.int8)
@@ -55,7 +68,7 @@ def int8_weights(rng, n: int, k: int, lo=1e-3, hi=1e-2):
     return q, s
 
 
-RAW = {R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw}
+RAW = {R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw, R.Q6_K: q6_k_raw}
 
 
 def config(idx: int, seed: int = 0, scale: float = 1.0):

@@ -12,6 +12,7 @@ It restates, from scratch in NumPy, what the reference computes (reference = /ro
   Q8_0 block                        src/mashbox/ops/reference.py:101-103 (_q8_0)
   6-bit scale/min unpack            src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
   Q4_K super-block                  src/mashbox/ops/reference.py:142-149 (_q4_k)
+  Q6_K super-block                  src/mashbox/ops/reference.py:164-173 (_q6_k)
   dequant(raw, t, cols)             src/mashbox/ops/reference.py:398-409
   exact-path row chunking           src/mashbox/ops/__init__.py:555-571  (EXACT_CHUNK, exact_chunk_rows)
   exact-path product                src/mashbox/ops/__init__.py:574-576, 624-632 (_exact, qmatmul's Raw branch)
@@ -31,6 +32,10 @@ How each function is pinned (tests/test_oracle.py):
                   (sc, m) values per slot; the nibble order is pinned by real llama-quantize blocks from the reference's
                   fixture file tests/fixtures/gguf/qwen3-kquant.gguf, whose dequantized rows must be smooth
                   weight-like values (see tests/golden).
+  dequant Q6_K    closed form: v = (d*sc)*(q - 32) is exact in float32 (at most 11 + 7 + 5 significant bits), checked
+                  against `fractions` on a grid; the bit layout against a per-index restatement of llama.cpp's scalar
+                  loop (ggml-quants.c dequantize_row_q6_K, the algorithm gguf-py restates) on random blocks and on the
+                  real llama-quantize blocks of the reference's fixture files; all-zero / all-0xFF blocks.
   qmatmul_exact   against a float64 product (reference bars: tests/contracts/test_ops.py:22-31), and chunked == whole.
   int8_linear     per element closed form: every bf16(x)*bf16(q) product is exact in float32; checked against a float64
                   product of the same values.
@@ -40,9 +45,9 @@ from __future__ import annotations
 import numpy as np
 
 # ggml type id -> (name, values per block, bytes per block) for the types on this path
-# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these two)
-TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144)}
-Q8_0, Q4_K = 8, 12
+# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these three)
+TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 14: ("Q6_K", 256, 210)}
+Q8_0, Q4_K, Q6_K = 8, 12, 14
 QK_K = 256
 EXACT_CHUNK = 1 << 24          # src/mashbox/ops/__init__.py:555
 
@@ -127,7 +132,24 @@ def q4_k_blocks(b: np.ndarray) -> np.ndarray:
         return (ds * q - dm).reshape(n, QK_K)
 
 
-BLOCKS = {Q8_0: q8_0_blocks, Q4_K: q4_k_blocks}
+def q6_k_blocks(b: np.ndarray) -> np.ndarray:
+    """(N, 210) super-blocks -> (N, 256) float32: (d*sc_j)*(q - 32) over 16 sub-blocks of 16 values
+    (src/mashbox/ops/reference.py:164-173). Bytes: ql 0-127 (low nibbles), qh 128-191 (2-bit highs), sc 192-207 (int8),
+    d 208-209 (fp16). Value 128g + 32r + i (g < 2, r < 4, i < 32): low = nibble r // 2 of ql[64g + 32 (r % 2) + i],
+    high = bits 2r, 2r + 1 of qh[32g + i]."""
+    n = b.shape[0]
+    ql, qh = b[:, :128], b[:, 128:192]
+    sc = b[:, 192:208].view(np.int8).astype(np.float32)
+    d = f16_to_f32(b[:, 208:210])                              # (N, 1)
+    ds = (d * sc).reshape(n, 16, 1)
+    lo = nib(ql.reshape(n, 2, 64)).reshape(n, 8, 32)
+    hi = ((qh.reshape(n, 2, 1, 32) >> np.array([0, 2, 4, 6], np.uint8).reshape(1, 1, 4, 1)) & np.uint8(3)).reshape(n, 8, 32)
+    q = ((lo | (hi << np.uint8(4))).astype(np.int16) - 32).astype(np.float32).reshape(n, 16, 16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (ds * q).reshape(n, QK_K)
+
+
+BLOCKS = {Q8_0: q8_0_blocks, Q4_K: q4_k_blocks, Q6_K: q6_k_blocks}
 
 
 def dequant(raw: np.ndarray, t: int, cols: int) -> np.ndarray:

@@ -9,6 +9,9 @@ Each check compares the oracle with something independent of its own formula, ch
     ggml-quants.c (get_scale_min_k4, dequantize_row_q4_K; the published algorithm gguf-py 0.19.0 restates in vector
     form and reference src/mashbox/ops/reference.py:132-149 follows) on random bytes (a nibble order, a sub-block
     grouping or a scale/min swap fails);
+  - Q6_K: the scalar loop of llama.cpp's dequantize_row_q6_K per index, in exact rationals rounded once (a swapped
+    nibble, a wrong 2-bit shift, a scale index off by a sub-block or a missing -32 fails), random blocks, edge blocks
+    and every real llama-quantize Q6_K block of the golden fixtures;
   - the 6-bit packer: round trip over all 64 x 64 (scale, min) pairs in all 8 slots;
   - bf16 rounding: torch's own float32 -> bfloat16 cast on ties, NaN, inf, subnormals and random values;
   - exact product: the float64 product and the reference's float32 bars (reference tests/contracts/test_ops.py:19-35:
@@ -202,6 +205,70 @@ def test_q4_k_edge_blocks():
     assert np.array_equal(v[2], want.astype(np.float32))
 
 
+# ------------------------------------------------------------------------------------------------------------- Q6_K
+def ggml_q6_k_row(block: bytes):
+    """llama.cpp dequantize_row_q6_K for one super-block (ql[128], qh[64], int8 scales[16], fp16 d), per index, in exact
+    rationals rounded once per value; an exact zero takes the sign float32 (d * sc) * q gives it"""
+    d = f16_from_definition(block[208] | block[209] << 8)
+    ql, qh = block[0:128], block[128:192]
+    sc = np.frombuffer(block[192:208], np.int8)
+    y = [None] * 256
+    for h in range(2):                                   # n = 0, 128
+        for l in range(32):
+            is_ = l // 16
+            q = [(ql[64 * h + l] & 0xF) | (((qh[32 * h + l] >> 0) & 3) << 4),
+                 (ql[64 * h + l + 32] & 0xF) | (((qh[32 * h + l] >> 2) & 3) << 4),
+                 (ql[64 * h + l] >> 4) | (((qh[32 * h + l] >> 4) & 3) << 4),
+                 (ql[64 * h + l + 32] >> 4) | (((qh[32 * h + l] >> 6) & 3) << 4)]
+            for r in range(4):
+                s = int(sc[8 * h + is_ + 2 * r])
+                qv = q[r] - 32
+                with np.errstate(all="ignore"):
+                    zero = (np.float32(d) * np.float32(s)) * np.float32(qv)
+                y[128 * h + 32 * r + l] = f32_round(Fraction(d) * s * qv, zero)
+    return np.array(y, np.float32)
+
+
+def test_q6_k_matches_the_scalar_loop_on_random_blocks():
+    """random blocks with finite d (subnormal to the fp16 maximum, both signs): every code, scale and zero sign"""
+    rng = np.random.default_rng(13)
+    raw = rng.integers(0, 256, (24, 210), dtype=np.uint8)
+    d = rng.choice(np.array([2.0 ** -24, 3e-5, 1e-3, 0.5, 7.0, 65504.0, -2.5, 0.0], np.float16), 24)
+    raw[:, 208:210] = d.view(np.uint8).reshape(24, 2)
+    raw[3, 192:208] = 0                                   # sc = 0: signed zeros
+    got = R.dequant(raw, R.Q6_K, 256)
+    for i in range(raw.shape[0]):
+        assert diff_bits(got[i], ggml_q6_k_row(bytes(raw[i]))) == 0, i
+
+
+def test_q6_k_closed_form_is_exact():
+    """(d * sc) * (q - 32) has at most 11 + 7 + 5 significant bits: the float32 value is the exact product for every
+    finite fp16 d, int8 sc and 6-bit q (brute force over sc and q at several d)"""
+    for dv in (np.float16(65504.0), np.float16(-1.0009765625), np.float16(2.0 ** -24), np.float16(0.0999)):
+        for s in range(-128, 128, 5):
+            for q in range(64):
+                exact = Fraction(float(dv)) * s * (q - 32)
+                got = (np.float32(dv) * np.float32(s)) * np.float32(q - 32)
+                assert Fraction(float(got)) == exact, (dv, s, q)
+
+
+def test_q6_k_edge_blocks():
+    raw = np.zeros((3, 210), np.uint8)
+    raw[1] = 0xFF                                          # d = NaN
+    raw[2, 208:210] = f16_bytes([np.float16(0.5)])
+    raw[2, 192:208] = np.arange(-8, 8, dtype=np.int8).view(np.uint8)
+    raw[2, 0:128] = 0x21                                   # every low nibble 1 or 2
+    raw[2, 128:192] = 0b11100100                           # 2-bit highs 0, 1, 2, 3 for r = 0..3
+    v = R.dequant(raw, R.Q6_K, 256)
+    assert np.all(v[0] == 0) and np.all(np.signbit(v[0]))  # (0 * 0) * -32 = -0
+    assert np.all(np.isnan(v[1]))
+    idx = np.arange(256)
+    r = (idx % 128) // 32
+    low = np.where(r < 2, 1, 2)
+    want = 0.5 * np.arange(-8, 8)[idx // 16] * (low + 16 * r - 32)
+    assert np.array_equal(v[2], want.astype(np.float32))
+
+
 def test_generators_make_blocks_of_the_stated_ranges():
     rng = np.random.default_rng(3)
     raw = G.q4_k_raw(rng, 16, 512)
@@ -213,6 +280,12 @@ def test_generators_make_blocks_of_the_stated_ranges():
     q8 = G.q8_0_raw(rng, 16, 512).reshape(-1, 34)
     qs = q8[:, 2:].view(np.int8)
     assert qs.min() >= -127 and qs.max() <= 127
+    q6 = G.q6_k_raw(rng, 16, 512).reshape(-1, 210)
+    d6, sc6 = R.f16_to_f32(q6[:, 208:210]), q6[:, 192:208].view(np.int8)
+    assert np.all((d6 >= 9.9e-4 / 64) & (d6 <= 1.001e-2 / 64)) and sc6.min() >= -127 and sc6.max() <= 127
+    ds6 = d6.repeat(16, 0) * sc6.reshape(-1, 1)
+    w6 = R.dequant(q6, R.Q6_K, 256).reshape(-1, 16)[ds6[:, 0] != 0] / ds6[ds6[:, 0] != 0]
+    assert w6.min() == -32 and w6.max() == 31 and np.array_equal(w6, np.round(w6))
 
 
 # ------------------------------------------------------------------------------------------------- exact product
@@ -230,7 +303,7 @@ def test_exact_chunk_rows_is_the_largest_fitting_divisor():
         assert R.exact_chunk_rows(r, c) == want
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K])
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q6_K])
 def test_exact_product_meets_the_float32_bars(t):
     """reference tests/contracts/test_ops.py:19-35: NMSE <= 1e-8 and |y - ref| <= gamma_K (|x| @ |W|.T)"""
     rng = np.random.default_rng(20 + t)
@@ -299,8 +372,8 @@ def test_golden_fixtures_are_present():
 
 
 def test_real_llama_quantize_blocks_match_the_scalar_forms():
-    """real Q4_K / Q8_0 blocks from the reference's fixture models (via tests/golden): the oracle equals llama.cpp's
-    scalar dequant loop (Q4_K) and the exact product (Q8_0) on every block"""
+    """real Q4_K / Q6_K / Q8_0 blocks from the reference's fixture models (via tests/golden): the oracle equals
+    llama.cpp's scalar dequant loops (Q4_K, Q6_K) and the exact product (Q8_0) on every third block"""
     seen = set()
     for name in _golden():
         if not name.startswith("kquant_"):
@@ -315,10 +388,12 @@ def test_real_llama_quantize_blocks_match_the_scalar_forms():
             b = bytes(blocks[i])
             if t == R.Q4_K:
                 want = ggml_q4_k_row(b)
+            elif t == R.Q6_K:
+                want = ggml_q6_k_row(b)
             else:
                 d = Fraction(f16_from_definition(b[0] | b[1] << 8))
                 want = np.array([f32_round(Fraction(int(c)) * d, np.float32(int(c)) * np.float32(float(d)))
                              for c in np.frombuffer(b[2:], np.int8)], np.float32)
             assert diff_bits(vals[i], want) == 0, (name, i)
         seen.add(t)
-    assert seen == {R.Q8_0, R.Q4_K}
+    assert seen == {R.Q8_0, R.Q4_K, R.Q6_K}
