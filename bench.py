@@ -1,12 +1,14 @@
 #!/usr/bin/env python
 """bench.py — the quantized-linear hot path on one MI355X against its roofline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--cpu-seconds S | --no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,q6k_head] [--cpu-seconds S | --no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input of a BASELINE config: one kernel launch for the
 decode GEMV configs 1-3, the 7 projection launches of one 27B-class layer for configs 4-5. The headline (`value`) is
 config 2 (GGUF Q8_0 decode GEMV, x[1,5120] @ W[17408,5120]^T), in GB/s of algorithmic bytes (packed weight bytes +
-scales + x + y, never repack padding) per second, with the weights already in HBM.
+scales + x + y, never repack padding) per second, with the weights already in HBM. `q6k_head` is not a BASELINE
+config: it is the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one
+activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs.
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
 distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
@@ -36,7 +38,7 @@ def algorithmic_bytes(t, m, n, k):
     if t == "int8":
         w = n * k + 4 * n
     else:
-        bs, ts = {8: (32, 34), 12: (256, 144)}[t]
+        bs, ts = {8: (32, 34), 12: (256, 144), 14: (256, 210)}[t]
         w = n * (k // bs) * ts
     return w + 2 * m * k + 2 * m * n
 
@@ -53,13 +55,13 @@ def run_config(idx, steps, warmup, rotate_bytes):
 
     L = lib()
     dev = torch.device("cuda", 0)
-    t, M, projs = synth.CONFIGS[idx]
+    t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
     out = {"projections": {}}
     total_us = 0.0
     total_bytes = 0
     total_flops = 0
     for pi, (name, N, K) in enumerate(projs):
-        seed = 1000 * idx + pi
+        seed = (1000 * idx if isinstance(idx, int) else 9000) + pi
         x = synth.acts(M, K, seed=seed, device=dev)
         y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         if t == "int8":
@@ -74,7 +76,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
                                          ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()),
                                          OUT_BF16, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         else:
-            raw = (synth.q8_0_raw if t == 8 else synth.q4_k_raw)(N, K, seed=seed + 7, device=dev)
+            raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
             pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
             planes = torch.empty(pb, dtype=torch.uint8, device=dev)
             check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()),
@@ -124,9 +126,12 @@ def run_config(idx, steps, warmup, rotate_bytes):
         torch.cuda.empty_cache()
     gbs = total_bytes / total_us / 1e3
     tfl = total_flops / total_us / 1e6
-    out.update({"type": {8: "Q8_0", 12: "Q4_K"}.get(t, t), "M": M, "us_per_step": round(total_us, 3),
+    out.update({"type": {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}.get(t, t), "M": M, "us_per_step": round(total_us, 3),
                 "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "TFLOPs": round(tfl, 2),
                 "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4), "algorithmic_bytes": total_bytes, "flops": total_flops})
+    if idx in synth.REF_TPU_US:
+        out["reference_tpu_v6e_us"] = synth.REF_TPU_US[idx]
+        out["speedup_vs_reference_tpu_v6e"] = round(synth.REF_TPU_US[idx] / total_us, 2)
     log(f"config {idx}: {out['us_per_step']:.2f} us/step  {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% HBM)  "
         f"{tfl:.1f} TFLOP/s ({100 * tfl / PEAK_BF16_TFLOPS:.1f}% MFMA)")
     return out
@@ -270,7 +275,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -295,7 +300,7 @@ def main():
         sys.exit(2)
     if a.pmc_probe:
         return pmc_probe()
-    configs = [int(c) for c in a.configs.split(",") if c]
+    configs = [int(c) if c.isdigit() else c for c in a.configs.split(",") if c]
     if HEADLINE not in configs:
         configs.insert(0, HEADLINE)
     res = {}
@@ -321,8 +326,8 @@ def main():
                      "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "kernel": "mbq::gemv_kernel (Q8_0, 1 activation row)", "kernel_us": proj["us"],
                      "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
-        "configs": {f"c{c}": {k: v for k, v in r.items() if k != "projections"} | {"projections": r["projections"]}
-                    for c, r in res.items()},
+        "configs": {(f"c{c}" if isinstance(c, int) else c): {k: v for k, v in r.items() if k != "projections"}
+                    | {"projections": r["projections"]} for c, r in res.items()},
     }
     line["measured_peaks"] = measured_peaks()
     if not a.no_cpu:

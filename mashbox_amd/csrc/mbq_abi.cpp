@@ -27,13 +27,13 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
-static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_K; }
+static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // shape rules shared by every entry point of a ggml type
 static int check_shape(int t, int64_t rows, int64_t cols) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12)", t);
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", t);
     if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
     if (cols % block_values(t))
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
@@ -62,11 +62,44 @@ static void parallel_rows(int64_t rows, int threads, F f) {
     for (auto& th : pool) th.join();
 }
 
+// Q6_K: the 6-bit quant i (0..31) of unit j (0..7) of a super-block, from the file's ql / qh bytes
+// (reference src/mashbox/ops/reference.py:164-173: value 128g + 32r + i takes nibble r / 2 of ql[64g + 32 (r % 2) + i]
+// and bits 2r, 2r + 1 of qh[32g + i])
+static inline uint32_t q6k_file_quant(const uint8_t* blk, int j, int i) {
+    const int g = j >> 2, r = j & 3;
+    const uint32_t lo = (blk[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15u;
+    const uint32_t hi = (blk[128 + 32 * g + i] >> (2 * r)) & 3u;
+    return lo | (hi << 4);
+}
+
 static void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         const uint8_t* row = raw + n * rb;
-        if (t == T_Q8_0) {
+        if (t == T_Q6_K) {
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* h = planes + L.hi_off + n * (K / 4);
+            uint8_t* sc = planes + L.sc_off + n * (K / 16);
+            uint8_t* d = planes + L.d_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(sc + b * 16, src + 192, 16);
+                memcpy(d + b * 2, src + 208, 2);
+                for (int j = 0; j < 8; ++j) {
+                    uint8_t* qu = q + b * 128 + j * 16;
+                    uint8_t* hu = h + b * 64 + j * 8;
+                    memset(qu, 0, 16);
+                    memset(hu, 0, 8);
+                    for (int i = 0; i < 32; ++i) {
+                        const uint32_t v = q6k_file_quant(src, j, i);
+                        int lb, lbit, hb, hbit;
+                        q6k_slot(i, &lb, &lbit, &hb, &hbit);
+                        qu[lb] |= (uint8_t)((v & 15u) << lbit);
+                        hu[hb] |= (uint8_t)((v >> 4) << hbit);
+                    }
+                }
+            }
+        } else if (t == T_Q8_0) {
             uint8_t* q = planes + L.qs_off + n * K;
             uint8_t* d = planes + L.sc_off + n * nb * 2;
             for (int64_t b = 0; b < nb; ++b) {
@@ -100,7 +133,30 @@ static void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         uint8_t* row = raw + n * rb;
-        if (t == T_Q8_0) {
+        if (t == T_Q6_K) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* h = planes + L.hi_off + n * (K / 4);
+            const uint8_t* sc = planes + L.sc_off + n * (K / 16);
+            const uint8_t* d = planes + L.d_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memset(dst, 0, 192);
+                memcpy(dst + 192, sc + b * 16, 16);
+                memcpy(dst + 208, d + b * 2, 2);
+                for (int j = 0; j < 8; ++j) {
+                    const uint8_t* qu = q + b * 128 + j * 16;
+                    const uint8_t* hu = h + b * 64 + j * 8;
+                    const int g = j >> 2, r = j & 3;
+                    for (int i = 0; i < 32; ++i) {
+                        int lb, lbit, hb, hbit;
+                        q6k_slot(i, &lb, &lbit, &hb, &hbit);
+                        const uint8_t lo = (qu[lb] >> lbit) & 15u, hi = (hu[hb] >> hbit) & 3u;
+                        dst[64 * g + 32 * (r & 1) + i] |= (uint8_t)(lo << (4 * (r >> 1)));
+                        dst[128 + 32 * g + i] |= (uint8_t)(hi << (2 * r));
+                    }
+                }
+            }
+        } else if (t == T_Q8_0) {
             const uint8_t* q = planes + L.qs_off + n * K;
             const uint8_t* d = planes + L.sc_off + n * nb * 2;
             for (int64_t b = 0; b < nb; ++b) {
@@ -130,6 +186,16 @@ static void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
     }
 }
 
+// calls f(offset, bytes) on every run of alignment padding between and after the planes; false if f fails
+template <class F>
+static bool for_each_gap(const Layout& L, F f) {
+    const int64_t ends[4][2] = {{L.qs_off + L.qs_bytes, L.hi_off}, {L.hi_off + L.hi_bytes, L.sc_off},
+                                {L.sc_off + L.sc_bytes, L.d_off}, {L.d_off + L.d_bytes, L.total}};
+    for (const auto& e : ends)
+        if (e[1] > e[0] && !f(e[0], e[1] - e[0])) return false;
+    return true;
+}
+
 static int check_out(int out_dtype) {
     if (out_dtype != MBQ_OUT_F32 && out_dtype != MBQ_OUT_BF16)
         return set_error(MBQ_BAD_ARG, "out_dtype %d is neither MBQ_OUT_F32 nor MBQ_OUT_BF16", out_dtype);
@@ -151,6 +217,8 @@ static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t
     a->layer_dev = layer_dev;
     a->nlayers = (int)nlayers;
     a->sc_off = L.sc_off;
+    a->hi_off = L.hi_off;
+    a->d_off = L.d_off;
     a->srow = nullptr;
     a->N = N;
     a->K = K;
@@ -189,8 +257,7 @@ int mbq_repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8
     if (!raw || !planes_host) return set_error(MBQ_BAD_ARG, "NULL buffer");
     const Layout L = layout(t, rows, cols);
     if (cap < (size_t)L.total) return set_error(MBQ_E_CAP, "planes buffer of %zu bytes < %lld", cap, (long long)L.total);
-    memset(planes_host + L.qs_bytes, 0, (size_t)(L.sc_off - L.qs_bytes));
-    memset(planes_host + L.sc_off + L.sc_bytes, 0, (size_t)(L.total - L.sc_off - L.sc_bytes));
+    for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes_host + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes_host, L, a, b); });
     return MBQ_OK;
 }
@@ -211,10 +278,9 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
     const Layout L = layout(t, rows, cols);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     // zero the alignment padding, then write every plane byte
-    if (hipMemsetAsync(planes_dev + L.qs_bytes, 0, (size_t)(L.sc_off - L.qs_bytes), s) != hipSuccess ||
-        hipMemsetAsync(planes_dev + L.sc_off + L.sc_bytes, 0, (size_t)(L.total - L.sc_off - L.sc_bytes), s) != hipSuccess)
+    if (!for_each_gap(L, [&](int64_t off, int64_t n) { return hipMemsetAsync(planes_dev + off, 0, (size_t)n, s) == hipSuccess; }))
         return set_error(MBQ_E_HIP, "hipMemsetAsync failed");
-    return launch_repack(t, raw_dev, rows, cols, planes_dev, L.sc_off, s);
+    return launch_repack(t, raw_dev, rows, cols, planes_dev, L, s);
 }
 
 int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,

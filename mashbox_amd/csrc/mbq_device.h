@@ -33,6 +33,22 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // Q4_K unit dword -> bfloat16 pair (128 + q[8t+2p], 128 + q[8t+2p+1]); exact (mbq_layout.h)
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w, int p) { return ((w >> (4 * p)) & 0x000F000Fu) | 0x43004300u; }
 
+// Q6_K unit (mbq_layout.h): the 6-bit quants of values 8t .. 8t+3 (*lo) and 8t+4 .. 8t+7 (*hi) as the bytes of two
+// dwords, from dword t of the low-nibble plane (ql) and dword t / 2 of the high-bit plane (qh)
+__device__ __forceinline__ void q6k_bytes(uint32_t ql, uint32_t qh, int t, uint32_t* lo, uint32_t* hi) {
+    const uint32_t m = 0x30303030u;
+    const uint32_t h0 = (t & 1) ? (qh & m) : ((qh << 4) & m);
+    const uint32_t h1 = (t & 1) ? ((qh >> 2) & m) : ((qh << 2) & m);
+    *lo = (ql & 0x0F0F0F0Fu) | h0;
+    *hi = ((ql >> 4) & 0x0F0F0F0Fu) | h1;
+}
+
+// bytes 2p, 2p+1 (each < 128) of w -> bfloat16 pair (128 + byte, 128 + byte'), exact: one byte permute against the
+// exponent byte 0x43 held in every byte of c43
+__device__ __forceinline__ uint32_t b128_pair(uint32_t w, uint32_t c43, int p) {
+    return __builtin_amdgcn_perm(c43, w, p ? 0x04030402u : 0x04010400u);
+}
+
 // int8 bytes 2p, 2p+1 of w -> bfloat16 pair, exact (every int8 is a bfloat16)
 __device__ __forceinline__ uint32_t i8_pair(uint32_t w, int p) {
     const float f0 = (float)(int8_t)(w >> (16 * p));

@@ -1,7 +1,8 @@
 // gfx950 MFMA GEMM of the quantized linear for the prefill / batched-decode regime (many activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K),
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
+// :164-173 (Q6_K),
 // and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // Block tile BM x 256 (activation rows x weight rows), K step 64, 512 threads = 8 waves in a 2 x 4 grid; each wave owns a
@@ -9,8 +10,9 @@
 // Per K step every thread
 //   - copies ACH 16-byte chunks of the x tile (bfloat16) into LDS,
 //   - dequantizes one 32-value weight unit into LDS as bfloat16 (Q4_K: a sub-block, 16 bytes of nibbles + the
-//     super-block's scales; Q8_0 / int8: 32 bytes of quants); each value is the float32 dequantization (d*sc)*q - dmin*m
-//     resp. q*d rounded to nearest even (int8 values are exact),
+//     super-block's scales; Q6_K: 16 bytes of low nibbles, 8 of high bits, 2 sub-block scales and the super-block
+//     scale; Q8_0 / int8: 32 bytes of quants); each value is the float32 dequantization (d*sc)*q - dmin*m,
+//     (d*sc)*(q - 32) resp. q*d rounded to nearest even (int8 values are exact),
 //   - runs 2 K-substeps of MFMAs on the tiles of the step before, from the other LDS stage.
 // Pipeline: the raw bytes of step k+2 are loaded into registers at the top of step k, the raw bytes of step k+1 (loaded
 // one step earlier) are dequantized into LDS stage (k+1)&1 in slices placed between the MFMAs of step k, so global
@@ -49,22 +51,31 @@ template <int T> struct BUnit;
 template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
-template <int T> constexpr int b_loads() { return T == T_Q8_0 ? 3 : 2; }   // buffer loads per unit
+template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
+template <int T> constexpr int b_loads() { return T == T_Q6_K ? 4 : T == T_Q8_0 ? 3 : 2; }   // buffer loads per unit
 
-// per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset)
-struct BOff { uint32_t q, s; };
+// per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h and d: Q6_K
+struct BOff { uint32_t q, s, h, d; };
 
 template <int T>
-__device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t bn, int K, int u) {
-    if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16)};
-    else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u)};
+__device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_off, int64_t bn, int K, int u) {
+    if constexpr (T == T_Q6_K)
+        return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 4) + 2 * u),
+                    (uint32_t)(hi_off + bn * (K >> 2) + 8 * u), (uint32_t)(d_off + bn * (K >> 7))};
+    else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
+    else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
 }
 
 // loads unit u of the K step at k0; with KFULL false, a Q8_0 unit past K gets scale 0 (its quants may be any bytes;
 // the x they meet is zero)
 template <int T, bool KFULL>
 __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int K, int k0, int u) {
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q6_K) {
+        b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
+        b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, (uint32_t)k0 >> 2, 0));
+        b.s = bload2(r, o.s, (uint32_t)k0 >> 4);
+        b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 2);
+    } else if constexpr (T == T_Q4_K) {
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
     } else {
@@ -93,12 +104,18 @@ __device__ __forceinline__ void i8x4(uint32_t w, float d, float d128, uint32_t* 
 }
 
 // per-unit dequant constants
-struct BScale { float a, b, c; };   // Q4_K: d*sc, dmin*m, d*sc/16; Q8_0: d, 128 d
+struct BScale { float a, b, c, e; };   // Q4_K: d*sc, dmin*m, d*sc/16; Q8_0: d, 128 d; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
 
 template <int T>
 __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
-    BScale s{1.f, 128.f, 0.f};
-    if constexpr (T == T_Q4_K) {
+    BScale s{1.f, 128.f, 0.f, 0.f};
+    if constexpr (T == T_Q6_K) {
+        const float d = f16f(b.d);
+        s.a = d * (float)(int8_t)(b.s & 0xFFu);           // exact
+        s.b = 32.f * s.a;
+        s.c = d * (float)(int8_t)((b.s >> 8) & 0xFFu);
+        s.e = 32.f * s.c;
+    } else if constexpr (T == T_Q4_K) {
         uint32_t sc, mn;
         q4k_scale_min_sel(b.meta[1], b.meta[2], b.meta[3], q4k_sel(j), &sc, &mn);
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
@@ -121,7 +138,16 @@ __device__ __forceinline__ uint32_t sel4(const u32x4& v, int i) {
 template <int T>
 __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int t) {
     u32x4 o;
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q6_K) {
+        // the quants of values 8t .. 8t+3 and 8t+4 .. 8t+7 as bytes; (q - 32) * (d sc) is one exact FMA
+        uint32_t lo, hi;
+        q6k_bytes(sel4(b.q, t), (t & 2) ? b.h[1] : b.h[0], t, &lo, &hi);
+        const float ds = (t & 2) ? s.c : s.a, m = (t & 2) ? s.e : s.b;
+        o[0] = pack_bf16(__builtin_fmaf((float)(lo & 0xFFu), ds, -m), __builtin_fmaf((float)((lo >> 8) & 0xFFu), ds, -m));
+        o[1] = pack_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(lo >> 24), ds, -m));
+        o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), ds, -m), __builtin_fmaf((float)((hi >> 8) & 0xFFu), ds, -m));
+        o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(hi >> 24), ds, -m));
+    } else if constexpr (T == T_Q4_K) {
         // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h)
         const uint32_t w = sel4(b.q, t);
         const uint32_t m0 = opaque(w & 0x000F000Fu), m1 = opaque(w & 0x00F000F0u);
@@ -152,6 +178,7 @@ struct GemmArgs {
     const int32_t* layer_dev;   // device layer index, or nullptr
     int nlayers;
     int64_t sc_off, wbytes;     // scale plane offset and bytes of one weight's planes
+    int64_t hi_off, d_off;      // Q6_K high-bit and super-block scale planes
     const float* srow;          // int8: per-row scales
     const uint16_t* x;
     int M, N, K;
@@ -225,7 +252,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
     // every step stays free of branches and no two lanes store to one LDS address.
     constexpr int LPU = (GT % (2 * BN) == 0) ? GT / (2 * BN) : 1, CPT = 4 / LPU, OWN = 2 * BN * LPU;
     const int unit = min(tid / LPU, 2 * BN - 1), br = unit >> 1, bu = unit & 1, t0 = (tid % LPU) * CPT;
-    const BOff bo = b_off<T>(g.sc_off, min(n0 + br, N - 1), K, bu);
+    const BOff bo = b_off<T>(g.sc_off, g.hi_off, g.d_off, min(n0 + br, N - 1), K, bu);
     int boff[CPT];                                       // LDS element offset of each of this thread's chunks
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
@@ -276,7 +303,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
         }
         // the x DMA of step l + 1 (issued P steps ago) has landed once at most the loads issued after it are in flight:
         // its own step's NB weight loads and P - 1 later steps' XD + NB
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (NB + (P - 1) * (XD + NB)));
+        wait_vm<NB + (P - 1) * (XD + NB)>();
         __syncthreads();
     };
 
@@ -495,9 +522,9 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         const int u = v == 0 ? pt : pt + 256;
         brow[v] = u >> 1;
         bu[v] = u & 1;
-        bo[v] = b_off<T>(g.sc_off, min(n0 + brow[v], N - 1), K, bu[v]);
+        bo[v] = b_off<T>(g.sc_off, g.hi_off, g.d_off, min(n0 + brow[v], N - 1), K, bu[v]);
     }
-    if (!two) bo[1] = BOff{OOB_VOFF, OOB_VOFF};                      // no second unit: its loads read zero, no traffic
+    if (!two) bo[1] = BOff{OOB_VOFF, OOB_VOFF, OOB_VOFF, OOB_VOFF};                      // no second unit: its loads read zero, no traffic
     BUnit<T> R[3][UPT];
     auto load_w = [&](BUnit<T>* Rr, int l) {
 #pragma unroll
@@ -604,8 +631,8 @@ static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStr
             return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
         attr_set = true;
     }
-    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
-               a.y, a.out_bf16, S, kts, w.ws, w.cnt};
+    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
+               (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt};
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     kern<<<dim3((unsigned)(tiles * S)), GT, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -622,8 +649,8 @@ static int launch_sg(const Args& a, hipStream_t s) {
             return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", SG_LDS);
         attr_set = true;
     }
-    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
-               a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr};
+    GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
+               (int)a.N, (int)a.K, a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr};
     const int64_t tiles = ((a.M + SG_BM - 1) / SG_BM) * ((a.N + SG_BN - 1) / SG_BN);
     kern<<<dim3((unsigned)tiles), GT, SG_LDS, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -631,11 +658,17 @@ static int launch_sg(const Args& a, hipStream_t s) {
     return 0;
 }
 
-// the 256 x 192 tile without a K split runs the specialized-wave kernel
+// the 256 x 192 tile without a K split runs the specialized-wave kernel; K-quant rows (multiples of 256 values) always
+// fill whole K steps
 template <int T, int BM, int BN, int P>
 static int launch_k(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
-    if (BM == SG_BM && BN == SG_BN && S == 1) return (a.K % GK == 0) ? launch_sg<T, true>(a, s) : launch_sg<T, false>(a, s);
-    return (a.K % GK == 0) ? launch_tile<T, BM, BN, P, true>(a, S, kts, w, s) : launch_tile<T, BM, BN, P, false>(a, S, kts, w, s);
+    if constexpr (T == T_Q4_K || T == T_Q6_K) {
+        if (BM == SG_BM && BN == SG_BN && S == 1) return launch_sg<T, true>(a, s);
+        return launch_tile<T, BM, BN, P, true>(a, S, kts, w, s);
+    } else {
+        if (BM == SG_BM && BN == SG_BN && S == 1) return (a.K % GK == 0) ? launch_sg<T, true>(a, s) : launch_sg<T, false>(a, s);
+        return (a.K % GK == 0) ? launch_tile<T, BM, BN, P, true>(a, S, kts, w, s) : launch_tile<T, BM, BN, P, false>(a, S, kts, w, s);
+    }
 }
 
 // compute units of the current device (cached per device)
@@ -759,7 +792,7 @@ static int choose(int t, const Args& a, Choice* c) {
         int bm = g_force_bm.load(), bn = g_force_bn.load();
         if (bm == 0) {                                       // the kernel's own tile choice
             int mt = 0, nt = 0;
-            pgemm_shape(a.M, a.N, a.K, &mt, &nt);
+            pgemm_shape(t, a.M, a.N, a.K, &mt, &nt);
             bm = 16 * mt, bn = 64 * nt;
         }
         *c = Choice{K_DIRECT, bm, bn, 1};
@@ -820,6 +853,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
     switch (t) {
         case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
         case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
+        case T_Q6_K: rc = pick<T_Q6_K>(a, &p); if (!rc) *bm = CANDS<T_Q6_K>[p.idx].bm, *bn = CANDS<T_Q6_K>[p.idx].bn; break;
         case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
@@ -855,6 +889,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_gemm_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemm_t<T_Q4_K>(a, s);
+        case T_Q6_K: return launch_gemm_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemm_t<T_INT8>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);

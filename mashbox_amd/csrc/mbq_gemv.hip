@@ -1,13 +1,13 @@
 // gfx950 decode GEMV of the quantized linear (M <= GEMV_MAX_M activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with float32 accumulation: reference src/mashbox/ops/__init__.py:594-632 (qmatmul) on the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K), and the int8 per-channel
+// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), and the int8 per-channel
 // linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (dot, then * s). Plane layouts: mbq_layout.h.
 //
 // HBM-bound: every weight byte is read once, 16 bytes per lane, each wave-wide load 1 KiB of one row (non-temporal).
 //
 // Work split. A persistent grid; block b owns rows [b N / P, (b + 1) N / P). A row's U units (a unit: 16 bytes of quants
-// = 16 int8 values, or a Q4_K sub-block of 32) are cut into S parts of PU units, at most 64 CH: one part of one row is
+// = 16 int8 values, or 32 Q4_K / Q6_K values) are cut into S parts of PU units, at most 64 CH: one part of one row is
 // an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
 // block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
 // multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
@@ -22,6 +22,9 @@
 //   Q4_K          ((w >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair (128 + q, 128 + q'); per unit
 //                 y += (d sc) * sum(x (128 + q)) - (128 d sc + dmin m) * sum(x); the per-unit sums of x are computed
 //                 once per wave from its x registers.
+//   Q6_K          an AND, an AND-OR and at most one shift per four values leave the 6-bit quants as bytes
+//                 (q6k_bytes), and one byte permute per pair makes the bfloat16 pair (128 + q, 128 + q'); per half unit
+//                 (16 values, one scale) y += (d sc) * sum(x (128 + q)) - 160 (d sc) * sum(x).
 // A lane that holds no unit of a part (the part's last chunk) reads zero and has its scale zeroed.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -39,11 +42,11 @@ constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_BLOCKS_PER_CU = 1;   // grid: one block per CU (more, shorter-lived waves measured slower on MI355X)
 constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
 
-template <int T> constexpr int gv_uw() { return T == T_Q4_K ? 32 : 16; }      // values per 16-byte unit
+template <int T> constexpr int gv_uw() { return (T == T_Q4_K || T == T_Q6_K) ? 32 : 16; }   // values per 16-byte unit
 template <int T> constexpr int gv_tpu() { return gv_uw<T>() / 8; }            // 16-byte x chunks per unit
 // chunks per item that the registers hold (x of M rows for CH chunks, and two items' loads in flight)
 template <int T> constexpr int gv_chmax(int M) {
-    return T == T_Q4_K ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
+    return (T == T_Q4_K || T == T_Q6_K) ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
 }
 
 struct GvArgs {
@@ -52,6 +55,7 @@ struct GvArgs {
     const int32_t* layer_dev;
     int nlayers;
     int64_t sc_off;             // scale plane offset
+    int64_t hi_off, d_off;      // Q6_K high-bit and super-block scale planes
     int64_t wbytes;             // bytes of one weight's planes (int8: N x K)
     const float* srow;          // int8 per-row scales
     const uint16_t* x;
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
     const int U = K / UW;
     const uint32_t qstride = (uint32_t)U * 16u;
-    const uint32_t sstride = (T == T_Q4_K) ? (uint32_t)(K >> 8) * 16u : (uint32_t)(K >> 5) * 2u;
+    const uint32_t sstride = (T == T_Q4_K) ? (uint32_t)(K >> 8) * 16u : (T == T_Q6_K) ? (uint32_t)(K >> 4) : (uint32_t)(K >> 5) * 2u;
 
     // this wave's part and its units
     const int part = wave % S, rstep = GV_WAVES / S;
@@ -91,7 +95,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const int nit = first < nrows ? (nrows - 1 - first) / rstep + 1 : 0;   // rows this wave takes
     const bool any = ok && nit > 0 && nu > 0;
 
-    struct Raw { u32x4 q[CH]; u32x4 meta[CH]; uint32_t d[CH]; };
+    struct Raw { u32x4 q[CH]; u32x4 meta[CH]; uint32_t d[CH]; u32x2 h[CH]; uint32_t s[CH]; };
     // Lane offsets of a load. The lanes past the part's last unit (in its last chunk), the chunks past that one and the
     // items past the wave's last row take an offset beyond the buffer's range: such a load returns zero without
     // touching memory, so no byte is fetched twice, and the load stays unconditional.
@@ -99,6 +103,9 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t vq = (uint32_t)lane * 16u, vq_last = lane_in ? vq : OOB_VOFF;
     const uint32_t vd = (uint32_t)(lane >> 1) * 2u, vd_last = lane_in ? vd : OOB_VOFF;
     const uint32_t vm = (uint32_t)(lane >> 3) * 16u, vm_last = lane_in ? vm : OOB_VOFF;
+    const uint32_t vh = (uint32_t)lane * 8u, vh_last = lane_in ? vh : OOB_VOFF;          // Q6_K high bits
+    const uint32_t vs = (uint32_t)lane * 2u, vs_last = lane_in ? vs : OOB_VOFF;          // Q6_K scale pairs
+    const uint32_t vd6 = (uint32_t)(lane >> 3) * 2u, vd6_last = lane_in ? vd6 : OOB_VOFF;  // Q6_K super-block scales
     auto load = [&](Raw& R, int k) {                                  // the k-th row of the wave (clamped)
         const bool live = k < nit;                                    // wave-uniform
         const int row = r0 + first + min(k, nit - 1) * rstep;
@@ -111,6 +118,12 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
             R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
             if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
             if constexpr (T == T_Q4_K) R.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
+            if constexpr (T == T_Q6_K) {
+                R.h[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                    wr, off(vh, vh_last), (uint32_t)g.hi_off + (uint32_t)row * (qstride >> 1) + (uint32_t)u0 * 8u + 512u * c, 2));
+                R.s[i] = bload2(wr, off(vs, vs_last), ss + (uint32_t)u0 * 2u + 128u * c);
+                R.d[i] = bload2(wr, off(vd6, vd6_last), (uint32_t)g.d_off + (uint32_t)row * (uint32_t)(K >> 7) + ((uint32_t)u0 >> 2) + 16u * c);
+            }
         }
     };
 
@@ -122,26 +135,31 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 
     // x of the lane's units (clamped to the row), per activation row, and for Q4_K the per-unit sums of x
     u32x4 xv[CH][M][TPU];
-    float xs[CH][M];
+    float xs[CH][M], xs2[CH][M];                                      // Q6_K: sums of x over each half unit
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
         const int u = min(u0 + lane + 64 * i, U - 1);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            float sum = 0.f;
+            float sum = 0.f, sum2 = 0.f;
 #pragma unroll
             for (int t = 0; t < TPU; ++t) {
                 xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
-                if constexpr (T == T_Q4_K) {
+                if constexpr (T == T_Q4_K || T == T_Q6_K) {
 #pragma unroll
-                    for (int p = 0; p < 4; ++p) sum = dot2(xv[i][m][t][p], BF16_ONES, sum);
+                    for (int p = 0; p < 4; ++p) {
+                        if (T == T_Q6_K && t >= 2) sum2 = dot2(xv[i][m][t][p], BF16_ONES, sum2);
+                        else sum = dot2(xv[i][m][t][p], BF16_ONES, sum);
+                    }
                 }
             }
             xs[i][m] = sum;
+            xs2[i][m] = sum2;
         }
     }
     const Q4kSel sel = q4k_sel((u0 + lane) & 7);                     // units advance by 64: the lane's slot is fixed
     const uint32_t kmask = in_vgpr(0x000F000Fu), kmagic = in_vgpr(0x43004300u);
+    const uint32_t c43 = in_vgpr(0x43434343u);
 
     auto finish = [&](const Raw& R, int k) {
         const int rl = first + k * rstep;
@@ -152,7 +170,34 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
         auto chunk = [&](auto FULL_, int i) {
             constexpr bool FULL = decltype(FULL_)::value;
             const bool act = FULL || lane + 64 * i < nu;
-            if constexpr (T == T_Q4_K) {
+            if constexpr (T == T_Q6_K) {
+                const float d = f16f(R.d[i]);
+                float ds0 = d * (float)(int8_t)(R.s[i] & 0xFFu), ds1 = d * (float)(int8_t)((R.s[i] >> 8) & 0xFFu);   // exact
+                if constexpr (!FULL) {
+                    ds0 = act ? ds0 : 0.f;
+                    ds1 = act ? ds1 : 0.f;
+                }
+                float A0[M], B0[M], A1[M], B1[M];                         // halves 0 / 1, quant bytes lo / hi
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    uint32_t lo, hi;
+                    q6k_bytes(R.q[i][t], R.h[i][t >> 1], t, &lo, &hi);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float& A = t < 2 ? A0[m] : A1[m];
+                        float& B = t < 2 ? B0[m] : B1[m];
+                        A = dot2(b128_pair(lo, c43, 0), xv[i][m][t][0], (t & 1) ? A : 0.f);
+                        A = dot2(b128_pair(lo, c43, 1), xv[i][m][t][1], A);
+                        B = dot2(b128_pair(hi, c43, 0), xv[i][m][t][2], (t & 1) ? B : 0.f);
+                        B = dot2(b128_pair(hi, c43, 1), xv[i][m][t][3], B);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    acc[m] = __builtin_fmaf(ds0, A0[m] + B0[m], __builtin_fmaf(-160.f * ds0, xs[i][m], acc[m]));
+                    acc[m] = __builtin_fmaf(ds1, A1[m] + B1[m], __builtin_fmaf(-160.f * ds1, xs2[i][m], acc[m]));
+                }
+            } else if constexpr (T == T_Q4_K) {
                 uint32_t sc, mn;
                 q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
                 float dsc = f16f(R.meta[i][0]) * (float)sc;             // exact
@@ -273,7 +318,7 @@ static int resident_blocks(Kern kernel, size_t lds) {
 // meta 8). Returns the chunks the parts need, or -1.
 template <int T, int M>
 static int gv_parts(int64_t U, int* S, int* PU) {
-    const int64_t gran = T == T_Q4_K ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
+    const int64_t gran = (T == T_Q4_K || T == T_Q6_K) ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
     for (int s = 1; s <= GV_WAVES; s *= 2) {
         const int64_t pu = ((U + s - 1) / s + gran - 1) / gran * gran;
         if (pu <= cap) {
@@ -296,7 +341,7 @@ static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
     const int64_t rows_max = (a.N + P - 1) / P;
     const size_t lds = S > 1 ? (size_t)rows_max * S * M * 4 : 0;
     if (lds > 64 * 1024) return set_error(MBQ_BAD_ARG, "GEMV N = %lld needs too much LDS", (long long)a.N);
-    GvArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.N, (int)a.K, S, PU, a.y, a.out_bf16};
+    GvArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, a.wbytes, a.srow, a.x, (int)a.N, (int)a.K, S, PU, a.y, a.out_bf16};
     kern<<<dim3((unsigned)P), GV_THREADS, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "gemv: %s", hipGetErrorString(e));
@@ -336,6 +381,7 @@ int launch_gemv(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_gemv_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemv_t<T_Q4_K>(a, s);
+        case T_Q6_K: return launch_gemv_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemv_t<T_INT8>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMV for type %d", t);

@@ -2,7 +2,7 @@
 // mbq_gemv.hip; weight-stream GEMM: mbq_wsgemm.hip; LDS-tile MFMA GEMM: mbq_gemm.hip).
 //
 // Semantics follow reference src/mashbox/ops/__init__.py:594-632 (qmatmul: x @ W.T, float32 accumulation) with the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K), and the int8 per-channel
+// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), and the int8 per-channel
 // linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82. Plane layouts: mbq_layout.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,13 +17,14 @@ namespace mbq {
 
 
 // ------------------------------------------------------------------------------------------------------- dequant
-// One thread per 16-byte unit (Q4_K: a sub-block of 32 values; Q8_0: half a block, 16 values). Bit for bit the
-// reference dequantization: Q8_0 v = f32(q) * d and Q4_K v = (d*sc)*q - dmin*m, whose products are exact in float32.
+// One thread per 16-byte unit (Q4_K, Q6_K: 32 values; Q8_0: half a block, 16 values). Bit for bit the reference
+// dequantization: Q8_0 v = f32(q) * d, Q4_K v = (d*sc)*q - dmin*m and Q6_K v = (d*sc)*(q - 32), whose products are
+// exact in float32 (Q6_K keeps the reference's order of the two products, which fixes the sign of a zero).
 template <int T>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base, int64_t stride,
                                                       const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
-                                                      int N, int K, float* __restrict__ w) {
-    const int64_t uw = (T == T_Q4_K) ? 32 : 16;
+                                                      int64_t hi_off, int64_t d_off, int N, int K, float* __restrict__ w) {
+    const int64_t uw = (T == T_Q8_0) ? 16 : 32;
     const int64_t units = (int64_t)N * (K / uw);
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= units) return;
@@ -36,7 +37,27 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         for (int i = 0; i < uw; ++i) out[i] = __builtin_nanf("");
         return;
     }
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q6_K) {
+        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
+        const u32x2 h = *reinterpret_cast<const u32x2*>(base + hi_off + n * (K >> 2) + u * 8);
+        const uint16_t scp = *reinterpret_cast<const uint16_t*>(base + sc_off + n * (K >> 4) + u * 2);
+        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + d_off + (n * (K >> 8) + (u >> 3)) * 2));
+        const float ds0 = d * (float)(int8_t)(scp & 0xFFu), ds1 = d * (float)(int8_t)(scp >> 8);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t lo, hi;
+            q6k_bytes(q[t], h[t >> 1], t, &lo, &hi);
+            const float ds = t < 2 ? ds0 : ds1;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = ds * (float)((int)((lo >> (8 * e)) & 0xFFu) - 32);
+                v[4 + e] = ds * (float)((int)((hi >> (8 * e)) & 0xFFu) - 32);
+            }
+            st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+            st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
+        }
+    } else if constexpr (T == T_Q4_K) {
         const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
         const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
         uint32_t sc, mn;
@@ -70,8 +91,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // ------------------------------------------------------------------------------------------------- raw dequant
 static int check_launch(const char* what);
 // The file's blocks (rows, row_bytes) -> float32 (rows, cols), without planes: reference src/mashbox/ops/reference.py
-// :398-409 (dequant) with :101-103 (Q8_0) and :132-149 (Q4_K), the rebuild of the exact path. One thread per 32 values
-// (a Q8_0 block, a Q4_K sub-block); the blocks are 34 / 144 bytes apart, so bytes are read one at a time.
+// :398-409 (dequant) with :101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), the rebuild of the exact path. One
+// thread per 32 values (a Q8_0 block, a Q4_K sub-block, two Q6_K sub-blocks); the blocks are 34 / 144 / 210 bytes
+// apart, so bytes are read one at a time.
 template <int T>
 __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
                                                           float* __restrict__ w) {
@@ -84,6 +106,17 @@ __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restr
         const uint8_t* b = raw + (n * (K / 32) + u) * 34;
         const float d = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
         for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)b[2 + i] * d;
+    } else if constexpr (T == T_Q6_K) {
+        // value 32j + i of the super-block (j = 4g + r): nibble r / 2 of ql[64g + 32 (r % 2) + i], bits 2r, 2r + 1 of
+        // qh[32g + i], sub-block scale sc[2j + i / 16]
+        const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 210;
+        const int j = (int)(u & 7), g = j >> 2, r = j & 3;
+        const float d = f16f((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+        const float ds0 = d * (float)(int8_t)b[192 + 2 * j], ds1 = d * (float)(int8_t)b[193 + 2 * j];
+        for (int i = 0; i < 32; ++i) {
+            const int q = ((b[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15) | (((b[128 + 32 * g + i] >> (2 * r)) & 3) << 4);
+            out[i] = (i < 16 ? ds0 : ds1) * (float)(q - 32);
+        }
     } else {
         const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 144;
         const int j = (int)(u & 7);
@@ -105,17 +138,19 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
     const dim3 grid((unsigned)((units + 255) / 256));
     if (t == T_Q4_K)
         dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    else if (t == T_Q6_K)
+        dequant_raw_kernel<T_Q6_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
     else
         dequant_raw_kernel<T_Q8_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
     return check_launch("dequant_raw");
 }
 
 // ------------------------------------------------------------------------------------------------ device repack
-// One thread per block: the file's bytes (unaligned, 34 or 144 bytes apart) into the planes of mbq_layout.h.
+// One thread per block: the file's bytes (unaligned, 34, 144 or 210 bytes apart) into the planes of mbq_layout.h.
 template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
-                                                     int64_t sc_off) {
-    const int bv = (T == T_Q4_K) ? 256 : 32, bb = (T == T_Q4_K) ? 144 : 34;
+                                                     int64_t sc_off, int64_t hi_off, int64_t d_off) {
+    const int bv = (T == T_Q8_0) ? 32 : 256, bb = (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (int64_t)N * nb) return;
@@ -127,6 +162,29 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         uint8_t* d = planes + sc_off + (n * nb + b) * 2;
         d[0] = src[0];
         d[1] = src[1];
+    } else if constexpr (T == T_Q6_K) {
+        uint8_t* sc = planes + sc_off + n * (K >> 4) + b * 16;
+        for (int i = 0; i < 16; ++i) sc[i] = src[192 + i];
+        uint8_t* d = planes + d_off + (n * nb + b) * 2;
+        d[0] = src[208];
+        d[1] = src[209];
+        uint32_t* qd = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 128);
+        uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + n * (K >> 2) + b * 64);
+        for (int j = 0; j < 8; ++j) {
+            const int g = j >> 2, r = j & 3;
+            uint32_t qw[4] = {0, 0, 0, 0}, hw[2] = {0, 0};
+            for (int i = 0; i < 32; ++i) {
+                const uint32_t lo = (src[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15u;
+                const uint32_t hi = (src[128 + 32 * g + i] >> (2 * r)) & 3u;
+                // slots of mbq_layout.h: low nibble dword i/8, byte i%4, bits 4 ((i/4)%2); high bits dword i/16,
+                // byte i%4, bits 2 ((i/4)%4)
+                qw[i >> 3] |= lo << (8 * (i & 3) + 4 * ((i >> 2) & 1));
+                hw[i >> 4] |= hi << (8 * (i & 3) + 2 * ((i >> 2) & 3));
+            }
+            for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
+            hd[j * 2] = hw[0];
+            hd[j * 2 + 1] = hw[1];
+        }
     } else {
         uint8_t* meta = planes + sc_off + (n * nb + b) * 16;
         for (int i = 0; i < 16; ++i) meta[i] = src[i];
@@ -162,29 +220,32 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_t<T_Q4_K>(a, s);
+        case T_Q6_K: return launch_t<T_Q6_K>(a, s);
         case T_INT8: return launch_t<T_INT8>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
 
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s) {
-    const int64_t uw = (t == T_Q4_K) ? 32 : 16;
+    const int64_t uw = (t == T_Q8_0) ? 16 : 32;
     const int64_t units = a.N * (a.K / uw);
     const dim3 grid((unsigned)((units + 255) / 256));
-    if (t == T_Q4_K)
-        dequant_kernel<T_Q4_K><<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, (int)a.N, (int)a.K, w);
-    else
-        dequant_kernel<T_Q8_0><<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, (int)a.N, (int)a.K, w);
+    auto run = [&](auto kern) {
+        kern<<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, (int)a.N, (int)a.K, w);
+    };
+    if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
+    else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
+    else run(dequant_kernel<T_Q8_0>);
     return check_launch("dequant");
 }
 
-int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, int64_t sc_off, hipStream_t s) {
+int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
     const int64_t blocks = N * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
-    if (t == T_Q4_K)
-        repack_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, sc_off);
-    else
-        repack_kernel<T_Q8_0><<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, sc_off);
+    auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
+    if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
+    else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
+    else run(repack_kernel<T_Q8_0>);
     return check_launch("repack");
 }
 

@@ -18,6 +18,7 @@ struct Args {
     const int32_t* layer_dev;  // device layer index, or nullptr
     int nlayers;
     int64_t sc_off;            // offset of the scale plane inside one weight's planes
+    int64_t hi_off, d_off;     // Q6_K: offsets of the high-bit plane and of the super-block scale plane
     int64_t wbytes;            // bytes of one weight's planes (int8: the N x K quants)
     const float* srow;         // int8: per-row scales
     const uint16_t* x;
@@ -52,7 +53,7 @@ void wsgemm_effective(int t, const Args& a, int* rows_per_block, int* splits);  
 // weight-direct GEMM (mbq_pgemm.hip) of large batches, run by a forced plan (the LDS-tile kernel is faster on MI355X at
 // every batch measured, 256..2048 rows): tiles of 16 mt activation rows x 64 nt weight rows
 int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s);
-int pgemm_shape(int64_t M, int64_t N, int64_t K, int* mt, int* nt);
+int pgemm_shape(int t, int64_t M, int64_t N, int64_t K, int* mt, int* nt);
 bool pgemm_shape_known(int mt, int nt);
 // GEMM kernels (the values of MBQ_KERNEL_* in mbq.h)
 enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2, K_DIRECT = 3 };
@@ -60,6 +61,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits);
 int force_gemm_plan(int kernel, int bm, int bn, int splits);
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s);
-int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, int64_t sc_off, hipStream_t s);
+struct Layout;
+int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s);
 
 }  // namespace mbq

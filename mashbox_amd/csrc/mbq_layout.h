@@ -11,38 +11,67 @@
 //                                  so ((dword >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair
 //                                  (128 + q[8t+2p], 128 + q[8t+2p+1]) in one AND-OR
 //     meta (N, K/256, 16 B)        the super-block's first 16 bytes as stored: d fp16, dmin fp16, 12 scale bytes
+//   Q6_K (ggml 14, 256 values / 210 B per super-block; reference src/mashbox/ops/reference.py:164-173)
+//     qs   (N, K/32, 16 B)         low 4 bits of the 6-bit quants q of 32 values; dword t, byte j: bits 0-3 = q[8t+j],
+//                                  bits 4-7 = q[8t+4+j] (values counted inside the unit of 32)
+//     qh   (N, K/32, 8 B)          high 2 bits of the same 32 quants; dword h, byte j: bits 2r, 2r+1 = q[16h+4r+j]
+//                                  (r = 0..3), so one AND and at most one shift move the high bits of four values to
+//                                  bits 4-5 of their bytes, and an AND-OR with the low nibbles leaves q[8t..8t+3] and
+//                                  q[8t+4..8t+7] as bytes (q6k_bytes in mbq_device.h)
+//     sc   (N, K/16)   int8        the sub-block scales, in file order
+//     d    (N, K/256)  fp16        the super-block scales
+//   value = (d * sc) * (q - 32), exact in float32
 //
-// Both planes start 256-byte aligned and the whole is rounded up to 256 bytes, so a stack of weights is a plain array
-// of these records (mbq_plane_bytes apart). The byte count is the file's plus at most 511 bytes of zero padding.
+// Every plane starts 256-byte aligned and the whole is rounded up to 256 bytes, so a stack of weights is a plain array
+// of these records (mbq_plane_bytes apart). The byte count is the file's plus at most 256 bytes of zero padding per
+// plane.
 #pragma once
 #include <stdint.h>
 
 namespace mbq {
 
-enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_INT8 = -8 };
+enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_INT8 = -8 };
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
+// plane offsets and sizes in bytes; hi (the Q6_K high bits) and d (the Q6_K super-block scales) are empty for the
+// other types
 struct Layout {
-    int64_t qs_off, qs_bytes, sc_off, sc_bytes, total;
+    int64_t qs_off, qs_bytes, hi_off, hi_bytes, sc_off, sc_bytes, d_off, d_bytes, total;
 };
 
-inline int block_values(int t) { return t == T_Q8_0 ? 32 : t == T_Q4_K ? 256 : 0; }
-inline int block_bytes(int t) { return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : 0; }
+inline int block_values(int t) { return t == T_Q8_0 ? 32 : (t == T_Q4_K || t == T_Q6_K) ? 256 : 0; }
+inline int block_bytes(int t) { return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : 0; }
 
 inline Layout layout(int t, int64_t n, int64_t k) {
     Layout L{};
     if (t == T_Q8_0) {
         L.qs_bytes = n * k;
         L.sc_bytes = n * (k / 32) * 2;
-    } else {  // T_Q4_K
+    } else if (t == T_Q4_K) {
         L.qs_bytes = n * (k / 2);
         L.sc_bytes = n * (k / 256) * 16;
+    } else {  // T_Q6_K
+        L.qs_bytes = n * (k / 2);
+        L.hi_bytes = n * (k / 4);
+        L.sc_bytes = n * (k / 16);
+        L.d_bytes = n * (k / 256) * 2;
     }
     L.qs_off = 0;
-    L.sc_off = align256(L.qs_bytes);
-    L.total = align256(L.sc_off + L.sc_bytes);
+    L.hi_off = align256(L.qs_bytes);
+    L.sc_off = align256(L.hi_off + L.hi_bytes);
+    L.d_off = align256(L.sc_off + L.sc_bytes);
+    L.total = align256(L.d_off + L.d_bytes);
     return L;
+}
+
+// Q6_K: where quant i (0..31) of a unit sits: low nibble in qs dword i/8, byte i%4, bits 4 ((i/4)%2) ..; high bits in
+// qh dword i/16, byte i%4, bits 2 ((i/4)%4) ..
+inline void q6k_slot(int i, int* lo_byte, int* lo_bit, int* hi_byte, int* hi_bit) {
+    *lo_byte = 4 * (i >> 3) + (i & 3);
+    *lo_bit = 4 * ((i >> 2) & 1);
+    *hi_byte = 4 * (i >> 4) + (i & 3);
+    *hi_bit = 2 * ((i >> 2) & 3);
 }
 
 // Q4_K: position of quant i (0..31) of a sub-block inside its 16-byte unit: (dword index, bit offset)

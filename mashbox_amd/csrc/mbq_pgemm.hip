@@ -2,7 +2,8 @@
 // weights from HBM straight into MFMA operands, activations shared through LDS.
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K),
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
+// :164-173 (Q6_K),
 // and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // Block = 4 waves, one per SIMD (one block per CU: the float32 accumulators of a 16 MT x 16 NT wave tile live in the
@@ -47,8 +48,9 @@
 namespace mbq {
 
 constexpr int PG_THREADS = 256;    // 4 waves
-// x stages in LDS: 2 for Q4_K's 64 KiB stages of 256 rows x 128 values, else 4 (at most 128 KiB)
-template <int T, int MT> constexpr int pg_stages() { return (T == T_Q4_K && MT > 8) ? 2 : 4; }
+// x stages in LDS: 2 for Q4_K's 64 KiB stages of 256 rows x 128 values, else 4 (at most 128 KiB); Q6_K, with 4 weight
+// loads per row tile, always 2 (the loads in flight stay within the 63 that vmcnt counts)
+template <int T, int MT> constexpr int pg_stages() { return (T == T_Q6_K || (T == T_Q4_K && MT > 8)) ? 2 : 4; }
 // weight iterations in flight per wave
 template <int T, int MT, int NT> constexpr int pg_wdepth() { return 4; }
 template <int T, int MT> constexpr size_t pg_lds_bytes() { return (size_t)pg_stages<T, MT>() * 16 * MT * ws_ki<T>() * 2; }
@@ -59,6 +61,7 @@ struct PgArgs {
     const int32_t* layer_dev;   // device layer index, or nullptr
     int nlayers;
     int64_t sc_off, wbytes;     // scale plane offset and bytes of one weight's planes (int8: N x K)
+    int64_t hi_off, d_off;      // Q6_K high-bit and super-block scale planes
     const float* srow;          // int8: per-row scales
     const uint16_t* x;
     int M, N, K;
@@ -94,14 +97,9 @@ __global__ __launch_bounds__(PG_THREADS, 1) void pgemm_kernel(const PgArgs g) {
     const int n = ok ? KT : 0;
     auto k0 = [&](int l) { return min(l, n - 1) * KI; };            // K offset of iteration l (clamped)
 
-    uint32_t vq[NT], vs[NT];
+    WsOff wo[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const uint32_t row = (uint32_t)min(n0 + 16 * j + r16, N - 1);
-        vq[j] = row * (uint32_t)(T == T_Q4_K ? K / 2 : K) + 16u * lg;
-        if constexpr (T == T_Q8_0) vs[j] = (uint32_t)g.sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
-        if constexpr (T == T_Q4_K) vs[j] = (uint32_t)g.sc_off + row * (uint32_t)(K / 256) * 16u;
-    }
+    for (int j = 0; j < NT; ++j) wo[j] = ws_off<T>((uint32_t)min(n0 + 16 * j + r16, N - 1), K, lg, g.sc_off, g.hi_off, g.d_off);
     // x DMA: instruction i of wave w fills rows RPI (w + 4 i) ..; lane l writes slot l % CH of row l / CH, which holds
     // chunk (l % CH) ^ (row & (CH - 1)) (4 RPI is a multiple of CH, so the chunk is the same for every instruction)
     const int xr0 = RPI * wave + lane / CH, xc = (lane % CH) ^ (xr0 & (CH - 1));
@@ -117,14 +115,7 @@ __global__ __launch_bounds__(PG_THREADS, 1) void pgemm_kernel(const PgArgs g) {
     };
     auto load_w = [&](WsRaw<T>* W, int kk) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            W[j].q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, vq[j], (uint32_t)(T == T_Q4_K ? kk / 2 : kk), 2));
-            if constexpr (T == T_Q8_0) {
-                W[j].d = bload2(wr, vs[j], (uint32_t)(kk / 32) * 2u);
-                if constexpr (!KFULL) W[j].d = (kk + 16 * lg < K) ? W[j].d : 0u;
-            }
-            if constexpr (T == T_Q4_K) W[j].meta = bload16(wr, vs[j], (uint32_t)(kk / 256) * 16u);
-        }
+        for (int j = 0; j < NT; ++j) ws_load<T, KFULL>(W[j], wr, wo[j], kk, K, lg);
     };
     // A operand of K step s, row tile i: chunk lg KS + s (8 bfloat16) of x row 16 i + (lane & 15) of stage st, where
     // (16 i + r16) & (CH - 1) = r16 & (CH - 1)
@@ -262,7 +253,7 @@ static int pg_launch(const Args& a, hipStream_t s) {
         attr_set = true;
     }
     const int64_t mtiles = (a.M + 16 * MT - 1) / (16 * MT), ntiles = (a.N + 64 * NT - 1) / (64 * NT);
-    PgArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
+    PgArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
              a.y, a.out_bf16, (int)mtiles, (int)(mtiles * ntiles)};
     kern<<<dim3((unsigned)(mtiles * ntiles)), PG_THREADS, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -272,7 +263,8 @@ static int pg_launch(const Args& a, hipStream_t s) {
 
 template <int T, int MT, int NT>
 static int pg_launch_k(const Args& a, hipStream_t s) {
-    return a.K % ws_ki<T>() == 0 ? pg_launch<T, MT, NT, true>(a, s) : pg_launch<T, MT, NT, false>(a, s);
+    if constexpr (T == T_Q4_K || T == T_Q6_K) return pg_launch<T, MT, NT, true>(a, s);   // rows of whole 256-value blocks
+    else return a.K % ws_ki<T>() == 0 ? pg_launch<T, MT, NT, true>(a, s) : pg_launch<T, MT, NT, false>(a, s);
 }
 
 // tile shapes: activation row tiles MT x weight row tiles NT per wave
@@ -283,14 +275,14 @@ constexpr int PG_NSHAPES = (int)(sizeof PG_SHAPES / sizeof PG_SHAPES[0]);
 template <int T>
 static int pg_dispatch(const Args& a, int idx, hipStream_t s) {
     switch (idx) {
-        case 0: return pg_launch_k<T, 16, 4>(a, s);
+        case 0: if constexpr (T != T_Q6_K) return pg_launch_k<T, 16, 4>(a, s); break;
         case 1: return pg_launch_k<T, 16, 3>(a, s);
         case 2: return pg_launch_k<T, 16, 2>(a, s);
-        case 3: return pg_launch_k<T, 8, 5>(a, s);
+        case 3: if constexpr (T != T_Q6_K) return pg_launch_k<T, 8, 5>(a, s); break;
         case 4: return pg_launch_k<T, 8, 4>(a, s);
         case 5: return pg_launch_k<T, 8, 2>(a, s);
     }
-    return set_error(MBQ_BAD_ARG, "weight-direct GEMM: no tile shape %d", idx);
+    return set_error(MBQ_BAD_ARG, "weight-direct GEMM: no tile shape %d for ggml type %d", idx, T);
 }
 
 static int pg_cus() {
@@ -315,20 +307,23 @@ static double pg_model(int64_t M, int64_t N, int64_t K, int cus, const PgShape& 
     return (double)rounds * sh.mt * sh.nt * (double)K / eff;
 }
 
-static int pg_best(int64_t M, int64_t N, int64_t K) {
+// Q6_K's weight buffers (4 loads per row tile) leave no registers for the 16 x 4 and 8 x 5 tiles
+static bool pg_type_has(int t, int i) { return t != T_Q6_K || (i != 0 && i != 3); }
+
+static int pg_best(int t, int64_t M, int64_t N, int64_t K) {
     const int cus = pg_cus();
-    int best = 0;
+    int best = t == T_Q6_K ? 1 : 0;
     double bt = 1e300;
     for (int i = 0; i < PG_NSHAPES; ++i) {
-        if (16 * PG_SHAPES[i].mt > M) continue;
+        if (16 * PG_SHAPES[i].mt > M || !pg_type_has(t, i)) continue;
         const double t = pg_model(M, N, K, cus, PG_SHAPES[i]);
         if (t < bt) bt = t, best = i;
     }
     return best;
 }
 
-int pgemm_shape(int64_t M, int64_t N, int64_t K, int* mt, int* nt) {
-    const int i = pg_best(M, N, K);
+int pgemm_shape(int t, int64_t M, int64_t N, int64_t K, int* mt, int* nt) {
+    const int i = pg_best(t, M, N, K);
     *mt = PG_SHAPES[i].mt;
     *nt = PG_SHAPES[i].nt;
     return 0;
@@ -352,6 +347,7 @@ int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s) {
         case T_INT8: return pg_dispatch<T_INT8>(a, idx, s);
         case T_Q8_0: return pg_dispatch<T_Q8_0>(a, idx, s);
         case T_Q4_K: return pg_dispatch<T_Q4_K>(a, idx, s);
+        case T_Q6_K: return pg_dispatch<T_Q6_K>(a, idx, s);
     }
     return set_error(MBQ_BAD_ARG, "weight-direct GEMM: no kernel for type %d", t);
 }

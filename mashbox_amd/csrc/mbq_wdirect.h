@@ -1,6 +1,6 @@
 // Weight-direct MFMA operands, shared by the GEMMs that take their weights from HBM straight into registers
-// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_K), 64 contiguous
-// bytes of each row of the quant plane. Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
+// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_K and Q6_K), 64
+// contiguous bytes of each row of the quant plane. Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
 // (g = l >> 4, the lane group). The MFMA sums over K, so any K order works when x follows it: in K step s of an
 // iteration, lane group g holds the 8 values K = k0 + g KI/4 + 8 s + e (e = 0..7) for both operands.
 //   int8   16 quants = 2 K steps; bf16(q) is exact; the per-row scale multiplies the float32 sum in the epilogue.
@@ -8,7 +8,10 @@
 //          bfloat16, the value the LDS GEMM stores.
 //   Q4_K   one 16-byte unit = the 32 quants of sub-block k0/32 + g = 4 K steps; the B operand is (d sc) q - dmin m
 //          (exact in float32) rounded to nearest even bfloat16.
-// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K); plane layouts: mbq_layout.h.
+//   Q6_K   the same 32 values: 16 bytes of low nibbles, 8 bytes of high bits, the two 16-value scales and the
+//          super-block scale; the B operand is (d sc) (q - 32) (exact in float32) rounded to nearest even bfloat16.
+// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :164-173 (Q6_K); plane layouts:
+// mbq_layout.h.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -18,23 +21,62 @@
 
 namespace mbq {
 
-template <int T> constexpr int ws_ki() { return T == T_Q4_K ? 128 : 64; }
-inline int ws_ki_of(int t) { return t == T_Q4_K ? 128 : 64; }
+template <int T> constexpr int ws_ki() { return (T == T_Q4_K || T == T_Q6_K) ? 128 : 64; }
+inline int ws_ki_of(int t) { return (t == T_Q4_K || t == T_Q6_K) ? 128 : 64; }
 
 // raw bytes of one iteration of one 16-row tile, as one lane holds them
 template <int T> struct WsRaw;
 template <> struct WsRaw<T_INT8> { u32x4 q; };
 template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
-template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : 2; }   // buffer loads per tile per iteration
+template <> struct WsRaw<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
+template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_K ? 4 : 2; }   // buffer loads per tile per iteration
+
+// per-lane byte offsets of one weight row's planes (the iteration's part goes in the scalar offset)
+struct WsOff { uint32_t q, s, h, d; };
+template <int T>
+__device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_off, int64_t hi_off, int64_t d_off) {
+    WsOff o{row * (uint32_t)((T == T_Q4_K || T == T_Q6_K) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
+    if constexpr (T == T_Q8_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
+    if constexpr (T == T_Q4_K) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 256) * 16u;
+    if constexpr (T == T_Q6_K) {
+        o.s = (uint32_t)sc_off + row * (uint32_t)(K / 16) + 2u * lg;
+        o.h = (uint32_t)hi_off + row * (uint32_t)(K / 4) + 8u * lg;
+        o.d = (uint32_t)d_off + row * (uint32_t)(K / 256) * 2u;
+    }
+    return o;
+}
+
+// the lane's bytes of the iteration at K offset kk (non-temporal quant loads); with KFULL false a Q8_0 block past K
+// gets scale 0 (the x it meets is zero, its quants may be any bytes)
+template <int T, bool KFULL>
+__device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, int kk, int K, int lg) {
+    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)((T == T_Q4_K || T == T_Q6_K) ? kk / 2 : kk), 2));
+    if constexpr (T == T_Q8_0) {
+        w.d = bload2(wr, o.s, (uint32_t)(kk / 32) * 2u);
+        if constexpr (!KFULL) w.d = (kk + 16 * lg < K) ? w.d : 0u;
+    }
+    if constexpr (T == T_Q4_K) w.meta = bload16(wr, o.s, (uint32_t)(kk / 256) * 16u);
+    if constexpr (T == T_Q6_K) {
+        w.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, o.h, (uint32_t)(kk / 4), 2));
+        w.s = bload2(wr, o.s, (uint32_t)(kk / 16));
+        w.d = bload2(wr, o.d, (uint32_t)(kk / 256) * 2u);
+    }
+}
 
 // per-lane dequant constants of one tile's unit
-struct WsScale { float a, b, c; };   // Q8_0: d; Q4_K: d*sc, dmin*m, d*sc/16
+struct WsScale { float a, b, c, e; };   // Q8_0: d; Q4_K: d*sc, dmin*m, d*sc/16; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
 
 template <int T>
 __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
-    WsScale s{1.f, 0.f, 0.f};
-    if constexpr (T == T_Q8_0) {
+    WsScale s{1.f, 0.f, 0.f, 0.f};
+    if constexpr (T == T_Q6_K) {
+        const float d = f16f(w.d);
+        s.a = d * (float)(int8_t)(w.s & 0xFFu);           // exact
+        s.b = 32.f * s.a;
+        s.c = d * (float)(int8_t)((w.s >> 8) & 0xFFu);
+        s.e = 32.f * s.c;
+    } else if constexpr (T == T_Q8_0) {
         s.a = f16f(w.d);
     } else if constexpr (T == T_Q4_K) {
         uint32_t sc, mn;
@@ -50,7 +92,15 @@ __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
 // caller's loops are unrolled); each dword is independent of the others, so a caller can spread them between MFMAs
 template <int T>
 __device__ __forceinline__ uint32_t ws_bpair(const WsRaw<T>& w, const WsScale& sc, int s, int p) {
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q6_K) {
+        // values 8s .. 8s+3 (p = 0, 1) and 8s+4 .. 8s+7 (p = 2, 3) of the unit as bytes; (q - 32) (d sc) is one exact FMA
+        uint32_t lo, hi;
+        q6k_bytes(w.q[s], w.h[s >> 1], s, &lo, &hi);
+        const uint32_t v = p < 2 ? lo : hi;
+        const int sh = (p & 1) * 16;
+        const float ds = s < 2 ? sc.a : sc.c, m = s < 2 ? sc.b : sc.e;
+        return pack_bf16(__builtin_fmaf((float)((v >> sh) & 0xFFu), ds, -m), __builtin_fmaf((float)((v >> (sh + 8)) & 0xFFu), ds, -m));
+    } else if constexpr (T == T_Q4_K) {
         // dword s of the unit: quant 8s+2p in bits 4p..4p+3, quant 8s+2p+1 in bits 16+4p.. (mbq_layout.h); the odd
         // nibble positions come out 16 times too large and take the scale d*sc/16
         const uint32_t v = w.q[s];

@@ -2,7 +2,8 @@
 // batched-decode regime.
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0) and :132-149 (Q4_K),
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
+// :164-173 (Q6_K),
 // and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // With at most 64 activation rows the weight stream bounds the time, so every weight byte goes from HBM (non-temporal
@@ -42,10 +43,10 @@ namespace mbq {
 
 constexpr int WS_THREADS = 256;    // 4 waves
 
-// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_K) at 64 activation rows
-template <int T> constexpr int ws_depth() { return T == T_Q4_K ? 4 : 8; }
+// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_K, Q6_K) at 64 activation rows
+template <int T> constexpr int ws_depth() { return (T == T_Q4_K || T == T_Q6_K) ? 4 : 8; }
 // x rows staged: 16 MT, rounded so that every wave issues the same number of 1 KiB DMA instructions per stage
-template <int T, int MT> constexpr int ws_rows() { return T == T_Q4_K ? 16 * MT : (MT <= 2 ? 32 : 64); }
+template <int T, int MT> constexpr int ws_rows() { return (T == T_Q4_K || T == T_Q6_K) ? 16 * MT : (MT <= 2 ? 32 : 64); }
 
 struct WsArgs {
     const uint8_t* base;        // planes of the weight (host layer applied)
@@ -53,6 +54,7 @@ struct WsArgs {
     const int32_t* layer_dev;   // device layer index, or nullptr
     int nlayers;
     int64_t sc_off, wbytes;     // scale plane offset and bytes of one weight's planes (int8: N x K)
+    int64_t hi_off, d_off;      // Q6_K high-bit and super-block scale planes
     const float* srow;          // int8: per-row scales
     const uint16_t* x;
     int M, N, K;
@@ -89,14 +91,9 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
     auto k0 = [&](int l) { return (kb + min(l, n - 1)) * KI; };          // K offset of local iteration l (clamped)
 
     // weight offsets: row (clamped) x row bytes + the lane group's 16 bytes
-    uint32_t vq[NT], vs[NT];
+    WsOff wo[NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const uint32_t row = (uint32_t)min(n0 + 16 * j + r16, N - 1);
-        vq[j] = row * (uint32_t)(T == T_Q4_K ? K / 2 : K) + 16u * lg;
-        if constexpr (T == T_Q8_0) vs[j] = (uint32_t)g.sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
-        if constexpr (T == T_Q4_K) vs[j] = (uint32_t)g.sc_off + row * (uint32_t)(K / 256) * 16u;
-    }
+    for (int j = 0; j < NT; ++j) wo[j] = ws_off<T>((uint32_t)min(n0 + 16 * j + r16, N - 1), K, lg, g.sc_off, g.hi_off, g.d_off);
     // x DMA: instruction i of wave w fills rows RPI (w + 4 i) ..; lane l writes slot l % CH of row l / CH, which holds
     // chunk (l % CH) ^ (row & (CH - 1)); rows past M are out of the buffer's range and read zero
     uint32_t xvo[NDW];
@@ -117,14 +114,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
     };
     auto load_w = [&](WsRaw<T>* W, int kk) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            W[j].q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, vq[j], (uint32_t)(T == T_Q4_K ? kk / 2 : kk), 2));
-            if constexpr (T == T_Q8_0) {
-                W[j].d = bload2(wr, vs[j], (uint32_t)(kk / 32) * 2u);
-                if constexpr (!KFULL) W[j].d = (kk + 16 * lg < K) ? W[j].d : 0u;
-            }
-            if constexpr (T == T_Q4_K) W[j].meta = bload16(wr, vs[j], (uint32_t)(kk / 256) * 16u);
-        }
+        for (int j = 0; j < NT; ++j) ws_load<T, KFULL>(W[j], wr, wo[j], kk, K, lg);
     };
     // A operand: chunk c (8 bfloat16) of x row 16 i + (lane & 15) from stage st
     auto a_op = [&](int st, int i, int c) {
@@ -282,7 +272,7 @@ static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStrea
             return set_error(MBQ_LAUNCH_FAIL, "weight-stream GEMM: %zu bytes of LDS refused", lds);
         attr_set = true;
     }
-    WsArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
+    WsArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
              a.y, a.out_bf16, S, kts, w.ws, w.cnt};
     const int64_t tiles = (a.N + 64 * NT - 1) / (64 * NT);
     kern<<<dim3((unsigned)(tiles * S)), WS_THREADS, lds, s>>>(g);
@@ -294,11 +284,20 @@ static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStrea
 template <int T, int NT>
 static int ws_launch_m(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
     const bool kfull = a.K % ws_ki<T>() == 0;
-    switch ((a.M + 15) / 16) {
-        case 1: return kfull ? ws_launch<T, 1, NT, true>(a, S, kts, w, s) : ws_launch<T, 1, NT, false>(a, S, kts, w, s);
-        case 2: return kfull ? ws_launch<T, 2, NT, true>(a, S, kts, w, s) : ws_launch<T, 2, NT, false>(a, S, kts, w, s);
-        case 3: return kfull ? ws_launch<T, 3, NT, true>(a, S, kts, w, s) : ws_launch<T, 3, NT, false>(a, S, kts, w, s);
-        default: return kfull ? ws_launch<T, 4, NT, true>(a, S, kts, w, s) : ws_launch<T, 4, NT, false>(a, S, kts, w, s);
+    if constexpr (T == T_Q4_K || T == T_Q6_K) {                       // rows of whole 256-value blocks
+        switch ((a.M + 15) / 16) {
+            case 1: return ws_launch<T, 1, NT, true>(a, S, kts, w, s);
+            case 2: return ws_launch<T, 2, NT, true>(a, S, kts, w, s);
+            case 3: return ws_launch<T, 3, NT, true>(a, S, kts, w, s);
+            default: return ws_launch<T, 4, NT, true>(a, S, kts, w, s);
+        }
+    } else {
+        switch ((a.M + 15) / 16) {
+            case 1: return kfull ? ws_launch<T, 1, NT, true>(a, S, kts, w, s) : ws_launch<T, 1, NT, false>(a, S, kts, w, s);
+            case 2: return kfull ? ws_launch<T, 2, NT, true>(a, S, kts, w, s) : ws_launch<T, 2, NT, false>(a, S, kts, w, s);
+            case 3: return kfull ? ws_launch<T, 3, NT, true>(a, S, kts, w, s) : ws_launch<T, 3, NT, false>(a, S, kts, w, s);
+            default: return kfull ? ws_launch<T, 4, NT, true>(a, S, kts, w, s) : ws_launch<T, 4, NT, false>(a, S, kts, w, s);
+        }
     }
 }
 
@@ -323,7 +322,7 @@ static size_t ws_partial_bytes(int64_t M, int nr) { return (size_t)((M + 15) / 1
 // the partial tiles within the workspace.
 static void ws_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int* nr, int* S) {
     const int64_t KT = (K + ws_ki_of(t) - 1) / ws_ki_of(t);
-    const int depth = t == T_Q4_K ? 4 : 8;
+    const int depth = (t == T_Q4_K || t == T_Q6_K) ? 4 : 8;
     const int64_t tiles64 = (N + 63) / 64;
     if (tiles64 >= cus) {
         *nr = 128;
@@ -368,6 +367,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);
         case T_Q8_0: return nr == 64 ? ws_launch_m<T_Q8_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q8_0, 2>(a, S, (int)kts, w, s);
         case T_Q4_K: return nr == 64 ? ws_launch_m<T_Q4_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_K, 2>(a, S, (int)kts, w, s);
+        case T_Q6_K: return nr == 64 ? ws_launch_m<T_Q6_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q6_K, 2>(a, S, (int)kts, w, s);
     }
     return set_error(MBQ_BAD_ARG, "weight-stream GEMM: no kernel for type %d", t);
 }

@@ -3,8 +3,10 @@
 Value ranges are those of the five BASELINE configs: fp16 block scales d (and Q4_K dmin) ~ U(1e-3, 1e-2), Q8_0 / int8
 quants uniform in [-127, 127], Q4_K six-bit scales and mins uniform in [0, 63] packed as the Q4_K scale bytes hold
 them (reference src/mashbox/ops/reference.py:132-139), four-bit quants uniform in [0, 15], int8 per-row scales
-~ U(1e-3, 1e-2), activations ~ N(0, 1) rounded to bfloat16. The bytes are the file's block layout (Q8_0 34 B per 32
-values, Q4_K 144 B per 256), ready for repack.
+~ U(1e-3, 1e-2), activations ~ N(0, 1) rounded to bfloat16; Q6_K (the reference's Q6_K output-head shape, not a
+BASELINE config): d ~ U(1e-3, 1e-2) / 64, int8 sub-block scales uniform in [-127, 127], six-bit quants uniform in
+[0, 63]. The bytes are the file's block layout (Q8_0 34 B per 32 values, Q4_K 144 B and Q6_K 210 B per 256), ready
+for repack.
 """
 from __future__ import annotations
 
@@ -53,6 +55,22 @@ def q4_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> 
     return torch.cat([d, dmin, s.to(torch.uint8), qs.to(torch.uint8)], dim=-1).reshape(n, nb * 144)
 
 
+def q6_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:
+    """(n, k/256*210) uint8 Q6_K super-blocks: ql (low nibbles), qh (2-bit highs), 16 int8 scales, fp16 d
+    (reference src/mashbox/ops/reference.py:164-173: value 128g + 32r + i takes nibble r // 2 of ql[64g + 32 (r % 2) + i]
+    and bits 2r, 2r + 1 of qh[32g + i])"""
+    g = _gen(seed, device)
+    nb = k // 256
+    q = torch.randint(0, 64, (n, nb, 2, 4, 32), generator=g, device=device, dtype=torch.int32)
+    ql = torch.cat([(q[:, :, :, j] & 15) | ((q[:, :, :, 2 + j] & 15) << 4) for j in range(2)], dim=-1)   # (n, nb, 2, 64)
+    qh = sum((q[:, :, :, r] >> 4) << (2 * r) for r in range(4))                                         # (n, nb, 2, 32)
+    del q
+    sc = torch.randint(-127, 128, (n, nb, 16), generator=g, device=device, dtype=torch.int8).view(torch.uint8)
+    d = _uniform_f16_bytes(g, (n, nb, 1), lo / 64, hi / 64, device)
+    return torch.cat([ql.reshape(n, nb, 128).to(torch.uint8), qh.reshape(n, nb, 64).to(torch.uint8), sc, d],
+                     dim=-1).reshape(n, nb * 210)
+
+
 def int8_weights(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2):
     g = _gen(seed, device)
     q = torch.randint(-127, 128, (n, k), generator=g, device=device, dtype=torch.int8)
@@ -70,3 +88,7 @@ CONFIGS = {
     4: ("int8", 64, LAYER_27B),
     5: (12, 2048, LAYER_27B),
 }
+# the reference's largest published per-call number: a Q6_K output head, 151936 x 2560, one activation row
+# (reference CORE-CHANGES.md:73, 369.8 us on TPU v6e-1)
+EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)])}
+REF_TPU_US = {"q6k_head": 369.8}

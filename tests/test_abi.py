@@ -39,19 +39,24 @@ def test_library_exports_every_declared_symbol():
 def test_type_table_and_shapes():
     lib = L.lib()
     assert lib.mbq_version() >= 100
-    assert lib.mbq_has_type(8) == 1 and lib.mbq_has_type(12) == 1 and lib.mbq_has_type(14) == 0
+    assert lib.mbq_has_type(8) == 1 and lib.mbq_has_type(12) == 1 and lib.mbq_has_type(14) == 1
+    assert lib.mbq_has_type(13) == 0 and lib.mbq_has_type(2) == 0
+    assert lib.mbq_row_bytes(14, 2560) == R.row_bytes(14, 2560) == 2100
     assert lib.mbq_row_bytes(8, 5120) == R.row_bytes(8, 5120) == 5440
     assert lib.mbq_row_bytes(12, 17408) == R.row_bytes(12, 17408) == 9792
     assert lib.mbq_row_bytes(12, 100) < 0
     assert KQ.kq_covers(8, (17408, 5120)) and KQ.kq_covers(12, (5120, 17408))
-    assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(14, (256, 256))
-    for t, (n, k) in [(8, (17408, 5120)), (12, (5120, 17408)), (12, (1, 256)), (8, (3, 32))]:
+    assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(13, (256, 256))
+    assert KQ.kq_covers(14, (151936, 2560)) and not KQ.kq_covers(14, (8, 128))
+    for t, (n, k) in [(8, (17408, 5120)), (12, (5120, 17408)), (12, (1, 256)), (8, (3, 32)), (14, (151936, 2560)),
+                      (14, (1, 256)), (14, (3, 512))]:
         pb = KQ.plane_bytes(t, (n, k))
         file_bytes = n * R.row_bytes(t, k)
-        assert pb % 256 == 0 and file_bytes <= pb < file_bytes + 512
+        planes = 4 if t == 14 else 2                                  # each plane pads to 256 bytes
+        assert pb % 256 == 0 and file_bytes <= pb < file_bytes + 256 * planes
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K])
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q6_K])
 def test_host_repack_is_lossless(t):
     rng = np.random.default_rng(40 + t)
     for n, kb in [(1, 1), (7, 3), (130, 2)]:
@@ -82,10 +87,38 @@ def test_q4_k_unit_layout_yields_bf16_pairs():
             assert np.array_equal(hi[:, :, t_], q[:, :, 8 * t_ + 2 * p_ + 1])
 
 
+def test_q6_k_unit_layout_yields_quant_bytes():
+    """a Q6_K unit: low nibbles of dword t and the high bits of dword t / 2, masked and shifted as the kernels do
+    (q6k_bytes: (ql & 0x0F0F0F0F) | (qh << 4 or qh) & 0x30303030, ((ql >> 4) & 0x0F0F0F0F) | (qh << 2 or qh >> 2) &
+    0x30303030), are the 6-bit quants of values 8t..8t+3 and 8t+4..8t+7 as bytes: checked on the host against the
+    oracle's dequant of blocks with d = 1 and every scale 1 (its values are then q - 32)"""
+    rng = np.random.default_rng(42)
+    raw = G.q6_k_raw(rng, 3, 512).reshape(6, 210)
+    raw[:, 192:208] = 1
+    raw[:, 208:210] = np.array([1.0], np.float16).view(np.uint8)
+    raw = raw.reshape(3, 420)
+    q = (R.dequant(raw, R.Q6_K, 512) + 32).astype(np.uint32).reshape(3, 16, 32)   # (row, unit, value)
+    p = KQ.repack_host(R.Q6_K, raw, (3, 512)).buf.numpy()
+    L_ = 3 * 256
+    ql = p[:L_].view(np.uint32).reshape(3, 16, 4)
+    hi_off = (L_ + 255) // 256 * 256
+    qh = p[hi_off:hi_off + 3 * 128].view(np.uint32).reshape(3, 16, 2)
+    m3, m0f = np.uint32(0x30303030), np.uint32(0x0F0F0F0F)
+    for t_ in range(4):
+        h = qh[:, :, t_ >> 1]
+        h0 = (h & m3) if t_ & 1 else ((h << np.uint32(4)) & m3)
+        h1 = ((h >> np.uint32(2)) & m3) if t_ & 1 else ((h << np.uint32(2)) & m3)
+        lo = (ql[:, :, t_] & m0f) | h0
+        hi = ((ql[:, :, t_] >> np.uint32(4)) & m0f) | h1
+        for j in range(4):
+            assert np.array_equal((lo >> np.uint32(8 * j)) & np.uint32(0xFF), q[:, :, 8 * t_ + j])
+            assert np.array_equal((hi >> np.uint32(8 * j)) & np.uint32(0xFF), q[:, :, 8 * t_ + 4 + j])
+
+
 def test_argument_errors_are_reported_without_a_launch():
     lib = L.lib()
     null = ctypes.c_void_p(0)
-    assert lib.mbq_matmul(14, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1
+    assert lib.mbq_matmul(13, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1
     assert b"type" in lib.mbq_last_error()
     assert lib.mbq_matmul(12, null, 0, None, 1, null, 1, 8, 200, null, 0, null) == -1
     assert b"multiple" in lib.mbq_last_error()

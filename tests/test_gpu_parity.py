@@ -22,8 +22,11 @@ from mashbox_amd import int8 as I8
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [R.Q8_0, R.Q4_K]
-NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K"}
+TYPES = [R.Q8_0, R.Q4_K, R.Q6_K]
+NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q6_K: "Q6_K"}
+GEMM_TYPES = [R.Q8_0, R.Q4_K, R.Q6_K, "int8"]
+GEMM_IDS = ["Q8_0", "Q4_K", "Q6_K", "int8"]
+KQUANT = (R.Q4_K, R.Q6_K)                             # rows of whole 256-value super-blocks
 
 
 def _bf16_tensor(bits: np.ndarray, dev) -> torch.Tensor:
@@ -202,6 +205,24 @@ def test_batched_gemm_full_config_sampled(idx, cuda):
         assert_product(got, ref, f"config {idx} {name}")
 
 
+def test_q6_k_output_head_full_size_sampled(cuda):
+    """the reference's published Q6_K shape (an output head of 151936 x 2560, one activation row; reference
+    CORE-CHANGES.md:73): repacked on the GPU from the file's blocks, run whole by the decode GEMV, and a seeded sample of
+    2048 rows compared with the exact product; two and four activation rows the same way"""
+    n, k = 151936, 2560
+    rng = np.random.default_rng(14)
+    raw = G.q6_k_raw(rng, n, k)
+    planes = KQ.repack(R.Q6_K, torch.from_numpy(raw).to(cuda), (n, k))
+    ns = np.sort(rng.choice(n, 2048, replace=False))
+    w = R.dequant(raw[ns], R.Q6_K, k).astype(np.float64)
+    assert diff_bits(KQ.dequant(planes).cpu().numpy()[ns], w.astype(np.float32)) == 0
+    for m in (1, 2, 4):
+        xb = G.acts(rng, m, k)
+        y = KQ.matmul(_bf16_tensor(xb, cuda), planes).cpu().numpy()
+        assert np.all(np.isfinite(y))
+        assert_product(y[:, ns], R.bf16_to_f32(xb).astype(np.float64) @ w.T, f"Q6_K head m={m}")
+
+
 # ------------------------------------------------------------------------------------------------ golden fixtures
 import os  # noqa: E402
 
@@ -245,14 +266,14 @@ def forced_plan():
     LIB.force_gemm_plan()
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
 @pytest.mark.parametrize("bm,bn", GEMM_TILES)
 def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cuda):
     """partial tiles on both edges, K over several steps (a Q8_0 / int8 K that is not a multiple of the 64-value step
     included), split-K into 3 ranges against 1"""
     rng = np.random.default_rng([bm, bn, 0 if t == "int8" else t])
     m, n = bm + bm // 2 - 3, bn + 17
-    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, "int8": 16 * 25}[t]
+    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, R.Q6_K: 256 * 3, "int8": 16 * 25}[t]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
     xf = R.bf16_to_f32(xb).astype(np.float64)
@@ -293,17 +314,20 @@ def _direct_case(t, m, n, k, rng, cuda):
 DIRECT_SHAPES = [(16, 4), (16, 3), (16, 2), (8, 5), (8, 4), (8, 2)]
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
 @pytest.mark.parametrize("mt,nt", DIRECT_SHAPES)
 @pytest.mark.parametrize("kfull", [False, True], ids=["k_ragged", "k_full"])
 def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
     """the weight-direct kernel of large batches: every tile shape, a batch of exactly one activation tile and one of
     2 tiles + a ragged rest (the last tile shifted back over the one before), ragged weight rows, a K that is or is not
-    a multiple of the kernel's iteration (64 values; 128 for Q4_K, whose K is always whole)"""
-    if t == R.Q4_K and not kfull:
-        pytest.skip("a Q4_K K is a whole number of 256-value super-blocks")
+    a multiple of the kernel's iteration (64 values; 128 for Q4_K and Q6_K, whose K is always whole)"""
+    if t in KQUANT and not kfull:
+        pytest.skip("a K-quant K is a whole number of 256-value super-blocks")
+    if t == R.Q6_K and (mt, nt) in ((16, 4), (8, 5)):
+        pytest.skip("no Q6_K weight-direct kernel of this shape (test_weight_direct_q6_k_refuses_the_widest_shapes)")
     bm, bn = 16 * mt, 64 * nt
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), R.Q6_K: (256 * 5, 256 * 5),
+         "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     for m, n in ((bm, bn + 17), (2 * bm + 37, 2 * bn + 17)):
         rng = np.random.default_rng([m, n, int(kfull), 0 if t == "int8" else t])
         run, ref = _direct_case(t, m, n, k, rng, cuda)
@@ -312,7 +336,23 @@ def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
         assert_product(run(), ref, f"{t} direct {bm}x{bn} m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+def test_weight_direct_q6_k_refuses_the_widest_shapes(forced_plan, cuda):
+    """the 16 x 4 and 8 x 5 row-tile shapes have no Q6_K kernel: a forced plan of them raises, launching nothing, and
+    the kernel's own shape choice avoids them"""
+    rng = np.random.default_rng(9)
+    m, n, k = 256, 640, 512
+    run, ref = _direct_case(R.Q6_K, m, n, k, rng, cuda)
+    for bm, bn in ((256, 256), (128, 320)):
+        forced_plan(LIB.KERNEL_DIRECT, bm, bn, 1)
+        with pytest.raises(RuntimeError, match="no tile shape"):
+            run()
+    forced_plan(LIB.KERNEL_DIRECT, 0, 0, 0)
+    _, bm, bn, _ = LIB.gemm_plan(R.Q6_K, 4096, 8192, 4096)
+    assert (bm, bn) not in ((256, 256), (128, 320))
+    assert_product(run(), ref)
+
+
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
 def test_kernel_choice_by_batch_and_forced_auto_shapes(t, forced_plan, cuda):
     """automatic plans: GEMV to 4 rows, weight-stream to 64, LDS tiles beyond; a forced kernel with bm = bn = 0 takes
     that kernel's own tile choice, and both prefill kernels give the right product"""
@@ -331,17 +371,18 @@ def test_kernel_choice_by_batch_and_forced_auto_shapes(t, forced_plan, cuda):
         assert_product(run(), ref, f"{t} kernel {kind} {bm}x{bn}")
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
 @pytest.mark.parametrize("m", [5, 17, 40, 64])
 @pytest.mark.parametrize("rows", [64, 128])
 @pytest.mark.parametrize("kfull", [False, True], ids=["k_ragged", "k_full"])
 def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
     """the weight-stream kernel (4 < M <= 64): 1-4 tiles of 16 activation rows, 64 and 128 weight rows per block,
-    ragged weight rows, a K that is or is not a multiple of the kernel's iteration (64 values; 128 for Q4_K, whose K
-    is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
+    ragged weight rows, a K that is or is not a multiple of the kernel's iteration (64 values; 128 for Q4_K and Q6_K,
+    whose K is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
     rng = np.random.default_rng([m, rows, int(kfull), 0 if t == "int8" else t])
     n = 3 * rows + 17
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), R.Q6_K: (256 * 5, 256 * 6),
+         "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
     xf = R.bf16_to_f32(xb).astype(np.float64)
@@ -366,7 +407,7 @@ def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
     assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, "int8"], ids=["Q8_0", "Q4_K", "int8"])
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
 @pytest.mark.parametrize("m,plan", [(64, (1, 16, 64, 4)), (130, (2, 64, 128, 3))], ids=["weight_stream", "lds_tiles"])
 def test_split_k_repeats_bit_for_bit(t, m, plan, forced_plan, cuda):
     """a K split into ranges repeats bit for bit over calls (the arrival counters reset themselves), whichever split
