@@ -39,7 +39,10 @@
 namespace mbq {
 
 constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
-constexpr int GV_BLOCKS_PER_CU = 1;   // grid: one block per CU (more, shorter-lived waves measured slower on MI355X)
+// grid: one block per CU, two when every wave still gets at least GV_ROWS_2BPC rows (part rows) of a tall weight
+// (measured on MI355X: a 151936-row output head runs 10-14 % faster with two blocks per CU; weights of 5120-17408 rows
+// run slower, their waves then have only a few rows each)
+constexpr int GV_ROWS_2BPC = 16;
 constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
 
 template <int T> constexpr int gv_uw() { return (T == T_Q4_K || T == T_Q6_K) ? 32 : 16; }   // values per 16-byte unit
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
             const int rl = e / M, m = e - rl * M, n = r0 + rl;
             float v = 0.f;
             if (S > 1)
-                for (int p = 0; p < S; ++p) v += parts[(rl * S + p) * M + m];
+                for (int p = 0; p < S && p * PU < U; ++p) v += parts[(rl * S + p) * M + m];   // parts past K hold nothing
             const float sc = (T == T_INT8) ? g.srow[n] : 1.f;
             store_y(g.y, (int64_t)m * N + n, ok ? v * sc : __builtin_nanf(""), g.out_bf16);
         }
@@ -337,7 +340,8 @@ static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
     int P = resident_blocks(kern, 4096);
     if (P < 1) return set_error(MBQ_LAUNCH_FAIL, "GEMV occupancy query failed");
-    P = (int)std::min<int64_t>({(int64_t)P, (int64_t)cus * GV_BLOCKS_PER_CU, a.N});
+    const int bpc = a.N * S >= (int64_t)cus * 2 * GV_WAVES * GV_ROWS_2BPC ? 2 : 1;
+    P = (int)std::min<int64_t>({(int64_t)P, (int64_t)cus * bpc, a.N});
     const int64_t rows_max = (a.N + P - 1) / P;
     const size_t lds = S > 1 ? (size_t)rows_max * S * M * 4 : 0;
     if (lds > 64 * 1024) return set_error(MBQ_BAD_ARG, "GEMV N = %lld needs too much LDS", (long long)a.N);

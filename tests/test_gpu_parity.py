@@ -205,6 +205,21 @@ def test_batched_gemm_full_config_sampled(idx, cuda):
         assert_product(got, ref, f"config {idx} {name}")
 
 
+@pytest.mark.parametrize("t", KQUANT, ids=NAME.get)
+@pytest.mark.parametrize("m", [3, 4])
+def test_gemv_row_parts_past_the_row_end(t, m, cuda):
+    """K = 8448 (264 units of 32 values) at 3-4 activation rows: the GEMV cuts a row into 8 parts of 40 units, so the
+    last part starts past the row's end and holds nothing; the block's sum over the parts must leave it out"""
+    rng = np.random.default_rng([t, m, 8448])
+    n, k = 70, 8448
+    raw = G.RAW[t](rng, n, k)
+    xb = G.acts(rng, m, k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    y = KQ.matmul(_bf16_tensor(xb, cuda), planes).cpu().numpy()
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    assert_product(y, ref, f"{NAME[t]} m={m} k={k}")
+
+
 def test_q6_k_output_head_full_size_sampled(cuda):
     """the reference's published Q6_K shape (an output head of 151936 x 2560, one activation row; reference
     CORE-CHANGES.md:73): repacked on the GPU from the file's blocks, run whole by the decode GEMV, and a seeded sample of
