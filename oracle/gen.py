@@ -48,6 +48,21 @@ def q4_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
     return np.concatenate([d, dmin, R.pack_scale_min_k4(sc, mn), qs], axis=-1).reshape(n, nb * 144)
 
 
+def q5_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
+    """(n, row_bytes) uint8 Q5_K super-blocks: d, dmin fp16 ~ U(lo, hi) / 2; 8 six-bit scales and mins uniform in
+    [0, 63]; 5-bit quants uniform in [0, 31], packed as the Q5_K layout holds them (src/mashbox/ops/reference.py:150-159)"""
+    nb = k // 256
+    d = (rng.uniform(lo, hi, (n, nb)) / 2).astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    dmin = (rng.uniform(lo, hi, (n, nb)) / 2).astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    sc = rng.integers(0, 64, (n, nb, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, (n, nb, 8), dtype=np.uint8)
+    q = rng.integers(0, 32, (n, nb, 8, 32), dtype=np.uint8)           # value 32j + i
+    # qs[32g + i]: low nibble = q(2g, i) & 15, high nibble = q(2g + 1, i) & 15; qh[i] bit j = q(j, i) >> 4
+    qs = ((q[:, :, 0::2] & 15) | ((q[:, :, 1::2] & 15) << 4)).reshape(n, nb, 128)
+    qh = sum(((q[:, :, j] >> 4) << j) for j in range(8)).astype(np.uint8)
+    return np.concatenate([d, dmin, R.pack_scale_min_k4(sc, mn), qh, qs], axis=-1).reshape(n, nb * 176)
+
+
 def q6_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
     """(n, row_bytes) uint8 Q6_K super-blocks: d fp16 ~ U(lo, hi) / 64; 16 int8 scales uniform in [-127, 127]; 6-bit
     quants uniform in [0, 63], packed as the Q6_K layout holds them (src/mashbox/ops/reference.py:164-173)"""
@@ -68,7 +83,7 @@ def int8_weights(rng, n: int, k: int, lo=1e-3, hi=1e-2):
     return q, s
 
 
-RAW = {R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw, R.Q6_K: q6_k_raw}
+RAW = {R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw, R.Q5_K: q5_k_raw, R.Q6_K: q6_k_raw}
 
 
 def config(idx: int, seed: int = 0, scale: float = 1.0):

@@ -12,6 +12,7 @@ It restates, from scratch in NumPy, what the reference computes (reference = /ro
   Q8_0 block                        src/mashbox/ops/reference.py:101-103 (_q8_0)
   6-bit scale/min unpack            src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
   Q4_K super-block                  src/mashbox/ops/reference.py:142-149 (_q4_k)
+  Q5_K super-block                  src/mashbox/ops/reference.py:150-159 (_q5_k)
   Q6_K super-block                  src/mashbox/ops/reference.py:164-173 (_q6_k)
   dequant(raw, t, cols)             src/mashbox/ops/reference.py:398-409
   exact-path row chunking           src/mashbox/ops/__init__.py:555-571  (EXACT_CHUNK, exact_chunk_rows)
@@ -32,6 +33,10 @@ How each function is pinned (tests/test_oracle.py):
                   (sc, m) values per slot; the nibble order is pinned by real llama-quantize blocks from the reference's
                   fixture file tests/fixtures/gguf/qwen3-kquant.gguf, whose dequantized rows must be smooth
                   weight-like values (see tests/golden).
+  dequant Q5_K    closed form: v = RN_f32(d*sc*q - dmin*m) with a single rounding (q < 32: at most 11 + 6 + 5 bits in
+                  the product), checked against exact `fractions` arithmetic rounded once; the bit layout against a
+                  per-index restatement of llama.cpp's scalar loop (dequantize_row_q5_K) on random blocks and on the real
+                  llama-quantize blocks of the reference's fixture files; all-zero / all-0xFF blocks.
   dequant Q6_K    closed form: v = (d*sc)*(q - 32) is exact in float32 (at most 11 + 7 + 5 significant bits), checked
                   against `fractions` on a grid; the bit layout against a per-index restatement of llama.cpp's scalar
                   loop (ggml-quants.c dequantize_row_q6_K, the algorithm gguf-py restates) on random blocks and on the
@@ -45,9 +50,9 @@ from __future__ import annotations
 import numpy as np
 
 # ggml type id -> (name, values per block, bytes per block) for the types on this path
-# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these three)
-TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 14: ("Q6_K", 256, 210)}
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these four)
+TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 QK_K = 256
 EXACT_CHUNK = 1 << 24          # src/mashbox/ops/__init__.py:555
 
@@ -132,6 +137,22 @@ def q4_k_blocks(b: np.ndarray) -> np.ndarray:
         return (ds * q - dm).reshape(n, QK_K)
 
 
+def q5_k_blocks(b: np.ndarray) -> np.ndarray:
+    """(N, 176) super-blocks -> (N, 256) float32: (d*sc_j)*q - dmin*m_j over 8 sub-blocks of 32, q = low | high << 4
+    (src/mashbox/ops/reference.py:150-159). Bytes: d, dmin fp16 0-3, 12 scale bytes 4-15 (as Q4_K), qh 16-47, qs 48-175.
+    Value 32j + i: low = nibble j % 2 of qs[32 (j // 2) + i], high = bit j of qh[i]."""
+    n = b.shape[0]
+    d, dmin = f16_to_f32(b[:, 0:2]), f16_to_f32(b[:, 2:4])    # (N, 1) each
+    sc, mn = scale_min_k4(b[:, 4:16])
+    ds = (d * sc.astype(np.float32)).reshape(n, 8, 1)
+    dm = (dmin * mn.astype(np.float32)).reshape(n, 8, 1)
+    lo = nib(b[:, 48:].reshape(n, 4, 32)).reshape(n, 8, 32)
+    hi = ((b[:, 16:48].reshape(n, 1, 32) >> np.arange(8, dtype=np.uint8).reshape(1, 8, 1)) & np.uint8(1))
+    q = (lo | (hi << np.uint8(4))).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (ds * q - dm).reshape(n, QK_K)
+
+
 def q6_k_blocks(b: np.ndarray) -> np.ndarray:
     """(N, 210) super-blocks -> (N, 256) float32: (d*sc_j)*(q - 32) over 16 sub-blocks of 16 values
     (src/mashbox/ops/reference.py:164-173). Bytes: ql 0-127 (low nibbles), qh 128-191 (2-bit highs), sc 192-207 (int8),
@@ -149,7 +170,7 @@ def q6_k_blocks(b: np.ndarray) -> np.ndarray:
         return (ds * q).reshape(n, QK_K)
 
 
-BLOCKS = {Q8_0: q8_0_blocks, Q4_K: q4_k_blocks, Q6_K: q6_k_blocks}
+BLOCKS = {Q8_0: q8_0_blocks, Q4_K: q4_k_blocks, Q5_K: q5_k_blocks, Q6_K: q6_k_blocks}
 
 
 def dequant(raw: np.ndarray, t: int, cols: int) -> np.ndarray:

@@ -6,7 +6,7 @@ Fixtures (NumPy .npz, no pickles):
   random_<TYPE>_k<KB>.npz    6 rows x KB blocks of random bytes with an all-zero row and an all-0xFF row (every fp16
                              scale value: normal, subnormal, inf, NaN), the shape of the reference's own dequant test
                              (reference tests/cpu/test_gguf_dequant.py:20-27); raw -> w (float32 dequant bits)
-  kquant_<file>_<tensor>.npz real llama-quantize blocks: the first 16 rows of Q4_K, Q6_K and Q8_0 weights of the
+  kquant_<file>_<tensor>.npz real llama-quantize blocks: the first 16 rows of Q4_K, Q5_K, Q6_K and Q8_0 weights of the
                              reference's fixture models (reference tests/fixtures/gguf/*-kquant.gguf, Apache-2.0, made by
                              llama-quantize at llama.cpp a37cc46; the source file's sha256 is stored), with 3 bf16
                              activation rows x and their float64 product y64
@@ -28,14 +28,15 @@ from oracle import gen as G  # noqa: E402
 from oracle import ref as R  # noqa: E402
 
 KQUANT = [("qwen3-kquant", ["blk.0.attn_k.weight", "blk.0.ffn_gate.weight", "blk.0.attn_q.weight", "token_embd.weight",
-                            "blk.0.ffn_down.weight", "output.weight"]),
-          ("gemma4-kquant", ["blk.0.ffn_up.weight", "blk.0.ffn_down.weight", "blk.0.attn_v.weight"]),
-          ("qwen35-kquant", ["blk.0.attn_qkv.weight"])]
+                            "blk.0.ffn_down.weight", "output.weight", "blk.0.ffn_up.weight"]),
+          ("gemma4-kquant", ["blk.0.ffn_up.weight", "blk.0.ffn_down.weight", "blk.0.attn_v.weight",
+                             "blk.2.attn_output.weight"]),
+          ("qwen35-kquant", ["blk.0.attn_qkv.weight", "blk.0.ffn_down.weight"])]
 
 
 def main(ref_root):
-    names = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q6_K: "Q6_K"}
-    for t in (R.Q8_0, R.Q4_K, R.Q6_K):
+    names = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
+    for t in (R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K):
         for kb in (1, 2, 16):
             rng = np.random.default_rng(7000 + 10 * t + kb)
             cols = R.TYPES[t][1] * kb

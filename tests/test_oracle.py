@@ -9,6 +9,8 @@ Each check compares the oracle with something independent of its own formula, ch
     ggml-quants.c (get_scale_min_k4, dequantize_row_q4_K; the published algorithm gguf-py 0.19.0 restates in vector
     form and reference src/mashbox/ops/reference.py:132-149 follows) on random bytes (a nibble order, a sub-block
     grouping or a scale/min swap fails);
+  - Q5_K: the scalar loop of llama.cpp's dequantize_row_q5_K per index, in exact rationals rounded once (a high bit
+    taken from the wrong qh bit or nibble half fails), random and edge blocks, real llama-quantize Q5_K blocks;
   - Q6_K: the scalar loop of llama.cpp's dequantize_row_q6_K per index, in exact rationals rounded once (a swapped
     nibble, a wrong 2-bit shift, a scale index off by a sub-block or a missing -32 fails), random blocks, edge blocks
     and every real llama-quantize Q6_K block of the golden fixtures;
@@ -205,6 +207,58 @@ def test_q4_k_edge_blocks():
     assert np.array_equal(v[2], want.astype(np.float32))
 
 
+# ------------------------------------------------------------------------------------------------------------- Q5_K
+def ggml_q5_k_row(block: bytes):
+    """llama.cpp dequantize_row_q5_K for one super-block (d, dmin, scales[12], qh[32], qs[128]), per index, in exact
+    rationals rounded once per value"""
+    d = Fraction(f16_from_definition(block[0] | block[1] << 8))
+    mn = Fraction(f16_from_definition(block[2] | block[3] << 8))
+    scales, qh, ql = block[4:16], block[16:48], block[48:176]
+    out, is_, qo, u1, u2 = [], 0, 0, 1, 2
+    for _ in range(0, 256, 64):
+        sc, m = ggml_scale_min_k4(is_, scales)
+        d1, m1 = d * sc, mn * m
+        sc, m = ggml_scale_min_k4(is_ + 1, scales)
+        d2, m2 = d * sc, mn * m
+        for l in range(32):
+            q = (ql[qo + l] & 0xF) + (16 if qh[l] & u1 else 0)
+            out.append(f32_round(d1 * q - m1, _zero(d1, q, m1)))
+        for l in range(32):
+            q = (ql[qo + l] >> 4) + (16 if qh[l] & u2 else 0)
+            out.append(f32_round(d2 * q - m2, _zero(d2, q, m2)))
+        qo += 32
+        is_ += 2
+        u1 <<= 2
+        u2 <<= 2
+    return np.array(out, np.float32)
+
+
+def test_q5_k_matches_the_scalar_loop_on_random_blocks():
+    """random finite blocks: every scale, min, code, high bit and subnormal scale; one rounding per value"""
+    rng = np.random.default_rng(15)
+    raw = rng.integers(0, 256, (24, 176), dtype=np.uint8)
+    d = rng.choice(np.array([2.0 ** -24, 3e-5, 1e-3, 0.5, 7.0, 65504.0, -2.5, 0.0], np.float16), (24, 2))
+    raw[:, 0:4] = d.view(np.uint8).reshape(24, 4)
+    got = R.dequant(raw, R.Q5_K, 256)
+    for i in range(raw.shape[0]):
+        assert diff_bits(got[i], ggml_q5_k_row(bytes(raw[i]))) == 0, i
+
+
+def test_q5_k_edge_blocks():
+    raw = np.zeros((3, 176), np.uint8)
+    raw[1] = 0xFF                                          # d = dmin = NaN
+    raw[2, 0:2] = f16_bytes([np.float16(0.5)])             # d = 0.5, dmin = 0
+    raw[2, 4:16] = R.pack_scale_min_k4(np.arange(1, 9, dtype=np.uint8)[None], np.zeros((1, 8), np.uint8))[0]
+    raw[2, 16:48] = 0b10100101                             # high bits of sub-blocks 0, 2, 5, 7
+    raw[2, 48:176] = 0x73                                  # low nibbles 3 (even sub-blocks) and 7 (odd)
+    v = R.dequant(raw, R.Q5_K, 256)
+    assert np.all(v[0] == 0)
+    assert np.all(np.isnan(v[1]))
+    j = np.arange(256) // 32
+    q = np.where(j % 2 == 0, 3, 7) + 16 * ((0b10100101 >> j) & 1)
+    assert np.array_equal(v[2], (0.5 * (j + 1) * q).astype(np.float32))
+
+
 # ------------------------------------------------------------------------------------------------------------- Q6_K
 def ggml_q6_k_row(block: bytes):
     """llama.cpp dequantize_row_q6_K for one super-block (ql[128], qh[64], int8 scales[16], fp16 d), per index, in exact
@@ -286,6 +340,15 @@ def test_generators_make_blocks_of_the_stated_ranges():
     ds6 = d6.repeat(16, 0) * sc6.reshape(-1, 1)
     w6 = R.dequant(q6, R.Q6_K, 256).reshape(-1, 16)[ds6[:, 0] != 0] / ds6[ds6[:, 0] != 0]
     assert w6.min() == -32 and w6.max() == 31 and np.array_equal(w6, np.round(w6))
+    q5 = G.q5_k_raw(rng, 16, 512).reshape(-1, 176)
+    d5 = R.f16_to_f32(q5[:, 0:2])
+    assert np.all((d5 >= 9.9e-4 / 2) & (d5 <= 1.001e-2 / 2))
+    sc5, mn5 = R.scale_min_k4(q5[:, 4:16])
+    ok = (sc5 > 0).reshape(-1)
+    w5 = (R.dequant(q5, R.Q5_K, 256).reshape(-1, 32) + (R.f16_to_f32(q5[:, 2:4]) * mn5).reshape(-1, 1))[ok] / \
+        (d5 * sc5).reshape(-1, 1)[ok]
+    w5 = np.round(w5)
+    assert w5.min() == 0 and w5.max() == 31
 
 
 # ------------------------------------------------------------------------------------------------- exact product
@@ -303,7 +366,7 @@ def test_exact_chunk_rows_is_the_largest_fitting_divisor():
         assert R.exact_chunk_rows(r, c) == want
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_exact_product_meets_the_float32_bars(t):
     """reference tests/contracts/test_ops.py:19-35: NMSE <= 1e-8 and |y - ref| <= gamma_K (|x| @ |W|.T)"""
     rng = np.random.default_rng(20 + t)
@@ -372,8 +435,8 @@ def test_golden_fixtures_are_present():
 
 
 def test_real_llama_quantize_blocks_match_the_scalar_forms():
-    """real Q4_K / Q6_K / Q8_0 blocks from the reference's fixture models (via tests/golden): the oracle equals
-    llama.cpp's scalar dequant loops (Q4_K, Q6_K) and the exact product (Q8_0) on every third block"""
+    """real Q4_K / Q5_K / Q6_K / Q8_0 blocks from the reference's fixture models (via tests/golden): the oracle equals
+    llama.cpp's scalar dequant loops (Q4_K, Q5_K, Q6_K) and the exact product (Q8_0) on every third block"""
     seen = set()
     for name in _golden():
         if not name.startswith("kquant_"):
@@ -390,10 +453,12 @@ def test_real_llama_quantize_blocks_match_the_scalar_forms():
                 want = ggml_q4_k_row(b)
             elif t == R.Q6_K:
                 want = ggml_q6_k_row(b)
+            elif t == R.Q5_K:
+                want = ggml_q5_k_row(b)
             else:
                 d = Fraction(f16_from_definition(b[0] | b[1] << 8))
                 want = np.array([f32_round(Fraction(int(c)) * d, np.float32(int(c)) * np.float32(float(d)))
                              for c in np.frombuffer(b[2:], np.int8)], np.float32)
             assert diff_bits(vals[i], want) == 0, (name, i)
         seen.add(t)
-    assert seen == {R.Q8_0, R.Q4_K, R.Q6_K}
+    assert seen == {R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K}
