@@ -32,6 +32,7 @@ extern "C" {
  * int8 per-output-channel weights of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 */
 #define MBQ_Q8_0 8
 #define MBQ_Q4_K 12
+#define MBQ_Q5_K 13
 #define MBQ_Q6_K 14
 #define MBQ_INT8 (-8)
 
@@ -49,7 +50,7 @@ int mbq_version(void);
 /* Message of the calling thread's last failure ("" if none). The pointer stays valid until the thread's next call. */
 const char* mbq_last_error(void);
 
-/* 1 if type t is a ggml type with kernel planes here (Q8_0, Q4_K, Q6_K), else 0.
+/* 1 if type t is a ggml type with kernel planes here (Q8_0, Q4_K, Q5_K, Q6_K), else 0.
  * Replaces the membership test `t in mod.TYPES` (reference src/mashbox/ops/__init__.py:21,303). */
 int mbq_has_type(int t);
 

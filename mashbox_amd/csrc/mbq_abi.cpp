@@ -27,13 +27,13 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
-static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
+static bool is_type(int t) { return t == T_Q8_0 || kquant(t); }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // shape rules shared by every entry point of a ggml type
 static int check_shape(int t, int64_t rows, int64_t cols) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12, Q6_K = 14)", t);
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14)", t);
     if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
     if (cols % block_values(t))
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
@@ -76,7 +76,31 @@ static void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         const uint8_t* row = raw + n * rb;
-        if (t == T_Q6_K) {
+        if (t == T_Q5_K) {
+            // reference src/mashbox/ops/reference.py:150-159: value 32j + i takes nibble j % 2 of qs[32 (j / 2) + i]
+            // (qs at byte 48) and bit j of qh[i] (qh at byte 16)
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* h = planes + L.hi_off + n * (K / 8);
+            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(meta + b * 16, src, 16);
+                for (int j = 0; j < 8; ++j) {
+                    uint8_t* qu = q + b * 128 + j * 16;
+                    uint8_t* hu = h + b * 32 + j * 4;
+                    memset(qu, 0, 16);
+                    memset(hu, 0, 4);
+                    for (int i = 0; i < 32; ++i) {
+                        const uint32_t lo = (src[48 + 32 * (j >> 1) + i] >> (4 * (j & 1))) & 15u;
+                        const uint32_t hi = (src[16 + i] >> j) & 1u;
+                        int lb, lbit, hb, hbit;
+                        q5k_slot(i, &lb, &lbit, &hb, &hbit);
+                        qu[lb] |= (uint8_t)(lo << lbit);
+                        hu[hb] |= (uint8_t)(hi << hbit);
+                    }
+                }
+            }
+        } else if (t == T_Q6_K) {
             uint8_t* q = planes + L.qs_off + n * (K / 2);
             uint8_t* h = planes + L.hi_off + n * (K / 4);
             uint8_t* sc = planes + L.sc_off + n * (K / 16);
@@ -133,7 +157,27 @@ static void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         uint8_t* row = raw + n * rb;
-        if (t == T_Q6_K) {
+        if (t == T_Q5_K) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* h = planes + L.hi_off + n * (K / 8);
+            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, meta + b * 16, 16);
+                memset(dst + 16, 0, 160);
+                for (int j = 0; j < 8; ++j) {
+                    const uint8_t* qu = q + b * 128 + j * 16;
+                    const uint8_t* hu = h + b * 32 + j * 4;
+                    for (int i = 0; i < 32; ++i) {
+                        int lb, lbit, hb, hbit;
+                        q5k_slot(i, &lb, &lbit, &hb, &hbit);
+                        const uint8_t lo = (qu[lb] >> lbit) & 15u, hi = (hu[hb] >> hbit) & 1u;
+                        dst[48 + 32 * (j >> 1) + i] |= (uint8_t)(lo << (4 * (j & 1)));
+                        dst[16 + i] |= (uint8_t)(hi << j);
+                    }
+                }
+            }
+        } else if (t == T_Q6_K) {
             const uint8_t* q = planes + L.qs_off + n * (K / 2);
             const uint8_t* h = planes + L.hi_off + n * (K / 4);
             const uint8_t* sc = planes + L.sc_off + n * (K / 16);

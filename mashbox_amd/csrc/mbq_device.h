@@ -43,6 +43,17 @@ __device__ __forceinline__ void q6k_bytes(uint32_t ql, uint32_t qh, int t, uint3
     *hi = ((ql >> 4) & 0x0F0F0F0Fu) | h1;
 }
 
+// Q5_K unit (mbq_layout.h): the 5-bit quants of values 8t .. 8t+3 (*lo) and 8t+4 .. 8t+7 (*hi) as the bytes of two
+// dwords, from dword t of the low-nibble plane (ql) and the unit's high-bit dword (qh): a rotate brings bit 2t (2t + 1)
+// of every qh byte to bit 4, and a bit-field insert joins it to the low nibbles
+__device__ __forceinline__ void q5k_bytes(uint32_t ql, uint32_t qh, int t, uint32_t* lo, uint32_t* hi) {
+    const uint32_t m = 0x10101010u;
+    const uint32_t a = __builtin_amdgcn_alignbit(qh, qh, (uint32_t)(2 * t + 28) & 31u);
+    const uint32_t b = __builtin_amdgcn_alignbit(qh, qh, (uint32_t)(2 * t + 29) & 31u);
+    *lo = (a & m) | (ql & 0x0F0F0F0Fu);
+    *hi = (b & m) | ((ql >> 4) & 0x0F0F0F0Fu);
+}
+
 // bytes 2p, 2p+1 (each < 128) of w -> bfloat16 pair (128 + byte, 128 + byte'), exact: one byte permute against the
 // exponent byte 0x43 held in every byte of c43
 __device__ __forceinline__ uint32_t b128_pair(uint32_t w, uint32_t c43, int p) {

@@ -1,8 +1,8 @@
 // gfx950 MFMA GEMM of the quantized linear for the prefill / batched-decode regime (many activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
-// :164-173 (Q6_K),
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K),
+// :150-159 (Q5_K) and :164-173 (Q6_K),
 // and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // Block tile BM x 256 (activation rows x weight rows), K step 64, 512 threads = 8 waves in a 2 x 4 grid; each wave owns a
@@ -52,9 +52,10 @@ template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
-template <int T> constexpr int b_loads() { return T == T_Q6_K ? 4 : T == T_Q8_0 ? 3 : 2; }   // buffer loads per unit
+template <> struct BUnit<T_Q5_K> { u32x4 q, meta; uint32_t h; };
+template <int T> constexpr int b_loads() { return T == T_Q6_K ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
 
-// per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h and d: Q6_K
+// per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h: Q5_K, Q6_K; d: Q6_K
 struct BOff { uint32_t q, s, h, d; };
 
 template <int T>
@@ -62,6 +63,8 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     if constexpr (T == T_Q6_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 4) + 2 * u),
                     (uint32_t)(hi_off + bn * (K >> 2) + 8 * u), (uint32_t)(d_off + bn * (K >> 7))};
+    else if constexpr (T == T_Q5_K)
+        return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
     else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
 }
@@ -75,9 +78,10 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, (uint32_t)k0 >> 2, 0));
         b.s = bload2(r, o.s, (uint32_t)k0 >> 4);
         b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 2);
-    } else if constexpr (T == T_Q4_K) {
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
+        if constexpr (T == T_Q5_K) b.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, o.h, (uint32_t)k0 >> 3, 0);
     } else {
         b.q0 = bload16(r, o.q, (uint32_t)k0);
         b.q1 = bload16(r, o.q + 16, (uint32_t)k0);
@@ -104,7 +108,7 @@ __device__ __forceinline__ void i8x4(uint32_t w, float d, float d128, uint32_t* 
 }
 
 // per-unit dequant constants
-struct BScale { float a, b, c, e; };   // Q4_K: d*sc, dmin*m, d*sc/16; Q8_0: d, 128 d; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+struct BScale { float a, b, c, e; };   // Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q8_0: d, 128 d; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
 
 template <int T>
 __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
@@ -115,7 +119,7 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.b = 32.f * s.a;
         s.c = d * (float)(int8_t)((b.s >> 8) & 0xFFu);
         s.e = 32.f * s.c;
-    } else if constexpr (T == T_Q4_K) {
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         uint32_t sc, mn;
         q4k_scale_min_sel(b.meta[1], b.meta[2], b.meta[3], q4k_sel(j), &sc, &mn);
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
@@ -147,6 +151,14 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         o[1] = pack_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(lo >> 24), ds, -m));
         o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), ds, -m), __builtin_fmaf((float)((hi >> 8) & 0xFFu), ds, -m));
         o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(hi >> 24), ds, -m));
+    } else if constexpr (T == T_Q5_K) {
+        // the quants of values 8t .. 8t+3 and 8t+4 .. 8t+7 as bytes; (d sc) q - dmin m is one FMA with one rounding
+        uint32_t lo, hi;
+        q5k_bytes(sel4(b.q, t), b.h, t, &lo, &hi);
+        o[0] = pack_bf16(__builtin_fmaf((float)(lo & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((lo >> 8) & 0xFFu), s.a, -s.b));
+        o[1] = pack_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(lo >> 24), s.a, -s.b));
+        o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((hi >> 8) & 0xFFu), s.a, -s.b));
+        o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(hi >> 24), s.a, -s.b));
     } else if constexpr (T == T_Q4_K) {
         // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h)
         const uint32_t w = sel4(b.q, t);
@@ -662,7 +674,7 @@ static int launch_sg(const Args& a, hipStream_t s) {
 // fill whole K steps
 template <int T, int BM, int BN, int P>
 static int launch_k(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
-    if constexpr (T == T_Q4_K || T == T_Q6_K) {
+    if constexpr (kquant(T)) {
         if (BM == SG_BM && BN == SG_BN && S == 1) return launch_sg<T, true>(a, s);
         return launch_tile<T, BM, BN, P, true>(a, S, kts, w, s);
     } else {
@@ -853,6 +865,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
     switch (t) {
         case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
         case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
+        case T_Q5_K: rc = pick<T_Q5_K>(a, &p); if (!rc) *bm = CANDS<T_Q5_K>[p.idx].bm, *bn = CANDS<T_Q5_K>[p.idx].bn; break;
         case T_Q6_K: rc = pick<T_Q6_K>(a, &p); if (!rc) *bm = CANDS<T_Q6_K>[p.idx].bm, *bn = CANDS<T_Q6_K>[p.idx].bn; break;
         case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
@@ -889,6 +902,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_gemm_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemm_t<T_Q4_K>(a, s);
+        case T_Q5_K: return launch_gemm_t<T_Q5_K>(a, s);
         case T_Q6_K: return launch_gemm_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemm_t<T_INT8>(a, s);
     }

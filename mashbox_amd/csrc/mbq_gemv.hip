@@ -1,13 +1,14 @@
 // gfx950 decode GEMV of the quantized linear (M <= GEMV_MAX_M activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with float32 accumulation: reference src/mashbox/ops/__init__.py:594-632 (qmatmul) on the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), and the int8 per-channel
+// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), and
+// the int8 per-channel
 // linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (dot, then * s). Plane layouts: mbq_layout.h.
 //
 // HBM-bound: every weight byte is read once, 16 bytes per lane, each wave-wide load 1 KiB of one row (non-temporal).
 //
 // Work split. A persistent grid; block b owns rows [b N / P, (b + 1) N / P). A row's U units (a unit: 16 bytes of quants
-// = 16 int8 values, or 32 Q4_K / Q6_K values) are cut into S parts of PU units, at most 64 CH: one part of one row is
+// = 16 int8 values, or 32 K-quant values) are cut into S parts of PU units, at most 64 CH: one part of one row is
 // an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
 // block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
 // multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
@@ -22,6 +23,8 @@
 //   Q4_K          ((w >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair (128 + q, 128 + q'); per unit
 //                 y += (d sc) * sum(x (128 + q)) - (128 d sc + dmin m) * sum(x); the per-unit sums of x are computed
 //                 once per wave from its x registers.
+//   Q5_K          q5k_bytes (a rotate and a bit-field insert per four values) then one byte permute per pair make
+//                 (128 + q, 128 + q'); per unit the Q4_K sum.
 //   Q6_K          an AND, an AND-OR and at most one shift per four values leave the 6-bit quants as bytes
 //                 (q6k_bytes), and one byte permute per pair makes the bfloat16 pair (128 + q, 128 + q'); per half unit
 //                 (16 values, one scale) y += (d sc) * sum(x (128 + q)) - 160 (d sc) * sum(x).
@@ -45,11 +48,11 @@ constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_ROWS_2BPC = 16;
 constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
 
-template <int T> constexpr int gv_uw() { return (T == T_Q4_K || T == T_Q6_K) ? 32 : 16; }   // values per 16-byte unit
+template <int T> constexpr int gv_uw() { return kquant(T) ? 32 : 16; }   // values per 16-byte unit
 template <int T> constexpr int gv_tpu() { return gv_uw<T>() / 8; }            // 16-byte x chunks per unit
 // chunks per item that the registers hold (x of M rows for CH chunks, and two items' loads in flight)
 template <int T> constexpr int gv_chmax(int M) {
-    return (T == T_Q4_K || T == T_Q6_K) ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
+    return kquant(T) ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
 }
 
 struct GvArgs {
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
     const int U = K / UW;
     const uint32_t qstride = (uint32_t)U * 16u;
-    const uint32_t sstride = (T == T_Q4_K) ? (uint32_t)(K >> 8) * 16u : (T == T_Q6_K) ? (uint32_t)(K >> 4) : (uint32_t)(K >> 5) * 2u;
+    const uint32_t sstride = (T == T_Q4_K || T == T_Q5_K) ? (uint32_t)(K >> 8) * 16u : (T == T_Q6_K) ? (uint32_t)(K >> 4) : (uint32_t)(K >> 5) * 2u;
 
     // this wave's part and its units
     const int part = wave % S, rstep = GV_WAVES / S;
@@ -109,6 +112,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t vh = (uint32_t)lane * 8u, vh_last = lane_in ? vh : OOB_VOFF;          // Q6_K high bits
     const uint32_t vs = (uint32_t)lane * 2u, vs_last = lane_in ? vs : OOB_VOFF;          // Q6_K scale pairs
     const uint32_t vd6 = (uint32_t)(lane >> 3) * 2u, vd6_last = lane_in ? vd6 : OOB_VOFF;  // Q6_K super-block scales
+    const uint32_t vh5 = (uint32_t)lane * 4u, vh5_last = lane_in ? vh5 : OOB_VOFF;        // Q5_K high bits
     auto load = [&](Raw& R, int k) {                                  // the k-th row of the wave (clamped)
         const bool live = k < nit;                                    // wave-uniform
         const int row = r0 + first + min(k, nit - 1) * rstep;
@@ -120,7 +124,10 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
             auto off = [&](uint32_t full, uint32_t last) { return (!live || i > lastc) ? OOB_VOFF : (i < lastc ? full : last); };
             R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
             if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
-            if constexpr (T == T_Q4_K) R.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
+            if constexpr (T == T_Q4_K || T == T_Q5_K) R.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
+            if constexpr (T == T_Q5_K)
+                R.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    wr, off(vh5, vh5_last), (uint32_t)g.hi_off + (uint32_t)row * (qstride >> 2) + (uint32_t)u0 * 4u + 256u * c, 2);
             if constexpr (T == T_Q6_K) {
                 R.h[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                     wr, off(vh, vh_last), (uint32_t)g.hi_off + (uint32_t)row * (qstride >> 1) + (uint32_t)u0 * 8u + 512u * c, 2));
@@ -148,7 +155,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 #pragma unroll
             for (int t = 0; t < TPU; ++t) {
                 xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
-                if constexpr (T == T_Q4_K || T == T_Q6_K) {
+                if constexpr (kquant(T)) {
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         if (T == T_Q6_K && t >= 2) sum2 = dot2(xv[i][m][t][p], BF16_ONES, sum2);
@@ -200,6 +207,31 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                     acc[m] = __builtin_fmaf(ds0, A0[m] + B0[m], __builtin_fmaf(-160.f * ds0, xs[i][m], acc[m]));
                     acc[m] = __builtin_fmaf(ds1, A1[m] + B1[m], __builtin_fmaf(-160.f * ds1, xs2[i][m], acc[m]));
                 }
+            } else if constexpr (T == T_Q5_K) {
+                uint32_t sc, mn;
+                q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
+                float dsc = f16f(R.meta[i][0]) * (float)sc;             // exact
+                const float dm = f16f(R.meta[i][0] >> 16) * (float)mn;  // exact
+                float c = 128.f * dsc + dm;
+                if constexpr (!FULL) {
+                    dsc = act ? dsc : 0.f;
+                    c = act ? c : 0.f;
+                }
+                float P0[M], P1[M];                                       // quant bytes lo / hi
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    uint32_t lo, hi;
+                    q5k_bytes(R.q[i][t], R.s[i], t, &lo, &hi);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        P0[m] = dot2(b128_pair(lo, c43, 0), xv[i][m][t][0], t ? P0[m] : 0.f);
+                        P0[m] = dot2(b128_pair(lo, c43, 1), xv[i][m][t][1], P0[m]);
+                        P1[m] = dot2(b128_pair(hi, c43, 0), xv[i][m][t][2], t ? P1[m] : 0.f);
+                        P1[m] = dot2(b128_pair(hi, c43, 1), xv[i][m][t][3], P1[m]);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(dsc, P0[m] + P1[m], __builtin_fmaf(-c, xs[i][m], acc[m]));
             } else if constexpr (T == T_Q4_K) {
                 uint32_t sc, mn;
                 q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
@@ -321,7 +353,7 @@ static int resident_blocks(Kern kernel, size_t lds) {
 // meta 8). Returns the chunks the parts need, or -1.
 template <int T, int M>
 static int gv_parts(int64_t U, int* S, int* PU) {
-    const int64_t gran = (T == T_Q4_K || T == T_Q6_K) ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
+    const int64_t gran = kquant(T) ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
     for (int s = 1; s <= GV_WAVES; s *= 2) {
         const int64_t pu = ((U + s - 1) / s + gran - 1) / gran * gran;
         if (pu <= cap) {
@@ -385,6 +417,7 @@ int launch_gemv(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_gemv_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemv_t<T_Q4_K>(a, s);
+        case T_Q5_K: return launch_gemv_t<T_Q5_K>(a, s);
         case T_Q6_K: return launch_gemv_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemv_t<T_INT8>(a, s);
     }

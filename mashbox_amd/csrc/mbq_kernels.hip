@@ -2,7 +2,8 @@
 // mbq_gemv.hip; weight-stream GEMM: mbq_wsgemm.hip; LDS-tile MFMA GEMM: mbq_gemm.hip).
 //
 // Semantics follow reference src/mashbox/ops/__init__.py:594-632 (qmatmul: x @ W.T, float32 accumulation) with the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), and the int8 per-channel
+// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), and the
+// int8 per-channel
 // linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82. Plane layouts: mbq_layout.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,8 +18,8 @@ namespace mbq {
 
 
 // ------------------------------------------------------------------------------------------------------- dequant
-// One thread per 16-byte unit (Q4_K, Q6_K: 32 values; Q8_0: half a block, 16 values). Bit for bit the reference
-// dequantization: Q8_0 v = f32(q) * d, Q4_K v = (d*sc)*q - dmin*m and Q6_K v = (d*sc)*(q - 32), whose products are
+// One thread per 16-byte unit (K-quants: 32 values; Q8_0: half a block, 16 values). Bit for bit the reference
+// dequantization: Q8_0 v = f32(q) * d, Q4_K and Q5_K v = (d*sc)*q - dmin*m and Q6_K v = (d*sc)*(q - 32), whose products are
 // exact in float32 (Q6_K keeps the reference's order of the two products, which fixes the sign of a zero).
 template <int T>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base, int64_t stride,
@@ -57,6 +58,27 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
+    } else if constexpr (T == T_Q5_K) {
+        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
+        const uint32_t h = *reinterpret_cast<const uint32_t*>(base + hi_off + n * (K >> 3) + u * 4);
+        const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
+        uint32_t sc, mn;
+        q4k_scale_min(mt[1], mt[2], mt[3], (int)(u & 7), &sc, &mn);
+        const float dsc = f16f(mt[0]) * (float)sc;
+        const float dm = f16f(mt[0] >> 16) * (float)mn;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t lo, hi;
+            q5k_bytes(q[t], h, t, &lo, &hi);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = dsc * (float)((lo >> (8 * e)) & 0xFFu) - dm;
+                v[4 + e] = dsc * (float)((hi >> (8 * e)) & 0xFFu) - dm;
+            }
+            st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+            st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
+        }
     } else if constexpr (T == T_Q4_K) {
         const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
         const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
@@ -91,9 +113,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // ------------------------------------------------------------------------------------------------- raw dequant
 static int check_launch(const char* what);
 // The file's blocks (rows, row_bytes) -> float32 (rows, cols), without planes: reference src/mashbox/ops/reference.py
-// :398-409 (dequant) with :101-103 (Q8_0), :132-149 (Q4_K) and :164-173 (Q6_K), the rebuild of the exact path. One
-// thread per 32 values (a Q8_0 block, a Q4_K sub-block, two Q6_K sub-blocks); the blocks are 34 / 144 / 210 bytes
-// apart, so bytes are read one at a time.
+// :398-409 (dequant) with :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), the rebuild of the
+// exact path. One thread per 32 values (a Q8_0 block, a Q4_K / Q5_K sub-block, two Q6_K sub-blocks); the blocks are
+// 34 / 144 / 176 / 210 bytes apart, so bytes are read one at a time.
 template <int T>
 __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
                                                           float* __restrict__ w) {
@@ -106,6 +128,21 @@ __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restr
         const uint8_t* b = raw + (n * (K / 32) + u) * 34;
         const float d = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
         for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)b[2 + i] * d;
+    } else if constexpr (T == T_Q5_K) {
+        // value 32j + i of the super-block: nibble j % 2 of qs[32 (j / 2) + i] (qs at byte 48), bit j of qh[i] (byte 16)
+        const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 176;
+        const int j = (int)(u & 7);
+        const uint32_t s0 = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+        const uint32_t s1 = b[8] | (b[9] << 8) | (b[10] << 16) | ((uint32_t)b[11] << 24);
+        const uint32_t s2 = b[12] | (b[13] << 8) | (b[14] << 16) | ((uint32_t)b[15] << 24);
+        uint32_t sc, mn;
+        q4k_scale_min(s0, s1, s2, j, &sc, &mn);
+        const float dsc = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8)) * (float)sc;      // exact
+        const float dm = f16f((uint32_t)b[2] | ((uint32_t)b[3] << 8)) * (float)mn;       // exact
+        for (int i = 0; i < 32; ++i) {
+            const uint32_t q = ((b[48 + 32 * (j >> 1) + i] >> (4 * (j & 1))) & 15u) | (((b[16 + i] >> j) & 1u) << 4);
+            out[i] = dsc * (float)q - dm;
+        }
     } else if constexpr (T == T_Q6_K) {
         // value 32j + i of the super-block (j = 4g + r): nibble r / 2 of ql[64g + 32 (r % 2) + i], bits 2r, 2r + 1 of
         // qh[32g + i], sub-block scale sc[2j + i / 16]
@@ -138,6 +175,8 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
     const dim3 grid((unsigned)((units + 255) / 256));
     if (t == T_Q4_K)
         dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    else if (t == T_Q5_K)
+        dequant_raw_kernel<T_Q5_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
     else if (t == T_Q6_K)
         dequant_raw_kernel<T_Q6_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
     else
@@ -146,11 +185,11 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
 }
 
 // ------------------------------------------------------------------------------------------------ device repack
-// One thread per block: the file's bytes (unaligned, 34, 144 or 210 bytes apart) into the planes of mbq_layout.h.
+// One thread per block: the file's bytes (unaligned, 34, 144, 176 or 210 bytes apart) into the planes of mbq_layout.h.
 template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    const int bv = (T == T_Q8_0) ? 32 : 256, bb = (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : 210;
+    const int bv = (T == T_Q8_0) ? 32 : 256, bb = (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : (T == T_Q5_K) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (int64_t)N * nb) return;
@@ -162,6 +201,24 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         uint8_t* d = planes + sc_off + (n * nb + b) * 2;
         d[0] = src[0];
         d[1] = src[1];
+    } else if constexpr (T == T_Q5_K) {
+        uint8_t* meta = planes + sc_off + (n * nb + b) * 16;
+        for (int i = 0; i < 16; ++i) meta[i] = src[i];
+        uint32_t* qd = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 128);
+        uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + n * (K >> 3) + b * 32);
+        for (int j = 0; j < 8; ++j) {
+            uint32_t qw[4] = {0, 0, 0, 0}, hw = 0;
+            for (int i = 0; i < 32; ++i) {
+                const uint32_t lo = (src[48 + 32 * (j >> 1) + i] >> (4 * (j & 1))) & 15u;
+                const uint32_t hi = (src[16 + i] >> j) & 1u;
+                // slots of mbq_layout.h: low nibble dword i/8, byte i%4, bits 4 ((i/4)%2); high bit byte i%4,
+                // bit 2 (i/8) + (i/4)%2
+                qw[i >> 3] |= lo << (8 * (i & 3) + 4 * ((i >> 2) & 1));
+                hw |= hi << (8 * (i & 3) + 2 * (i >> 3) + ((i >> 2) & 1));
+            }
+            for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
+            hd[j] = hw;
+        }
     } else if constexpr (T == T_Q6_K) {
         uint8_t* sc = planes + sc_off + n * (K >> 4) + b * 16;
         for (int i = 0; i < 16; ++i) sc[i] = src[192 + i];
@@ -220,6 +277,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
     switch (t) {
         case T_Q8_0: return launch_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_t<T_Q4_K>(a, s);
+        case T_Q5_K: return launch_t<T_Q5_K>(a, s);
         case T_Q6_K: return launch_t<T_Q6_K>(a, s);
         case T_INT8: return launch_t<T_INT8>(a, s);
     }
@@ -234,6 +292,7 @@ int launch_dequant(int t, const Args& a, float* w, hipStream_t s) {
         kern<<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, (int)a.N, (int)a.K, w);
     };
     if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
+    else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
     return check_launch("dequant");
@@ -244,6 +303,7 @@ int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* plan
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
     if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
+    else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);
     return check_launch("repack");

@@ -11,6 +11,13 @@
 //                                  so ((dword >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair
 //                                  (128 + q[8t+2p], 128 + q[8t+2p+1]) in one AND-OR
 //     meta (N, K/256, 16 B)        the super-block's first 16 bytes as stored: d fp16, dmin fp16, 12 scale bytes
+//   Q5_K (ggml 13, 256 values / 176 B per super-block; reference src/mashbox/ops/reference.py:150-159)
+//     qs   (N, K/32, 16 B)         low 4 bits of the 5-bit quants q of 32 values, as the Q6_K low nibbles below
+//     qh   (N, K/32, 4 B)          their high bits; byte j, bit 2t + h = the high bit of q[8t+4h+j] (t = 0..3, h = 0, 1),
+//                                  so one rotate moves the high bits of four values to bit 4 of their bytes and one
+//                                  bit-field insert joins them to the low nibbles (q5k_bytes in mbq_device.h)
+//     meta (N, K/256, 16 B)        the super-block's first 16 bytes as stored: d fp16, dmin fp16, 12 scale bytes
+//   value = (d * sc) * q - dmin * m, one rounding (as Q4_K)
 //   Q6_K (ggml 14, 256 values / 210 B per super-block; reference src/mashbox/ops/reference.py:164-173)
 //     qs   (N, K/32, 16 B)         low 4 bits of the 6-bit quants q of 32 values; dword t, byte j: bits 0-3 = q[8t+j],
 //                                  bits 4-7 = q[8t+4+j] (values counted inside the unit of 32)
@@ -30,7 +37,10 @@
 
 namespace mbq {
 
-enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_INT8 = -8 };
+enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8 };
+
+// the K-quants: 256-value super-blocks, kernel units of 32 values (16 bytes of low nibbles)
+constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
@@ -40,8 +50,8 @@ struct Layout {
     int64_t qs_off, qs_bytes, hi_off, hi_bytes, sc_off, sc_bytes, d_off, d_bytes, total;
 };
 
-inline int block_values(int t) { return t == T_Q8_0 ? 32 : (t == T_Q4_K || t == T_Q6_K) ? 256 : 0; }
-inline int block_bytes(int t) { return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : 0; }
+inline int block_values(int t) { return t == T_Q8_0 ? 32 : kquant(t) ? 256 : 0; }
+inline int block_bytes(int t) { return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0; }
 
 inline Layout layout(int t, int64_t n, int64_t k) {
     Layout L{};
@@ -50,6 +60,10 @@ inline Layout layout(int t, int64_t n, int64_t k) {
         L.sc_bytes = n * (k / 32) * 2;
     } else if (t == T_Q4_K) {
         L.qs_bytes = n * (k / 2);
+        L.sc_bytes = n * (k / 256) * 16;
+    } else if (t == T_Q5_K) {
+        L.qs_bytes = n * (k / 2);
+        L.hi_bytes = n * (k / 8);
         L.sc_bytes = n * (k / 256) * 16;
     } else {  // T_Q6_K
         L.qs_bytes = n * (k / 2);
@@ -63,6 +77,14 @@ inline Layout layout(int t, int64_t n, int64_t k) {
     L.d_off = align256(L.sc_off + L.sc_bytes);
     L.total = align256(L.d_off + L.d_bytes);
     return L;
+}
+
+// Q5_K: where quant i (0..31) of a unit sits: low nibble as Q6_K's; high bit in qh byte i%4, bit 2 (i/8) + (i/4)%2
+inline void q5k_slot(int i, int* lo_byte, int* lo_bit, int* hi_byte, int* hi_bit) {
+    *lo_byte = 4 * (i >> 3) + (i & 3);
+    *lo_bit = 4 * ((i >> 2) & 1);
+    *hi_byte = i & 3;
+    *hi_bit = 2 * (i >> 3) + ((i >> 2) & 1);
 }
 
 // Q6_K: where quant i (0..31) of a unit sits: low nibble in qs dword i/8, byte i%4, bits 4 ((i/4)%2) ..; high bits in

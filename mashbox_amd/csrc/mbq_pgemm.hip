@@ -50,7 +50,7 @@ namespace mbq {
 constexpr int PG_THREADS = 256;    // 4 waves
 // x stages in LDS: 2 for Q4_K's 64 KiB stages of 256 rows x 128 values, else 4 (at most 128 KiB); Q6_K, with 4 weight
 // loads per row tile, always 2 (the loads in flight stay within the 63 that vmcnt counts)
-template <int T, int MT> constexpr int pg_stages() { return (T == T_Q6_K || (T == T_Q4_K && MT > 8)) ? 2 : 4; }
+template <int T, int MT> constexpr int pg_stages() { return (T == T_Q6_K || ((T == T_Q4_K || T == T_Q5_K) && MT > 8)) ? 2 : 4; }
 // weight iterations in flight per wave
 template <int T, int MT, int NT> constexpr int pg_wdepth() { return 4; }
 template <int T, int MT> constexpr size_t pg_lds_bytes() { return (size_t)pg_stages<T, MT>() * 16 * MT * ws_ki<T>() * 2; }
@@ -263,7 +263,7 @@ static int pg_launch(const Args& a, hipStream_t s) {
 
 template <int T, int MT, int NT>
 static int pg_launch_k(const Args& a, hipStream_t s) {
-    if constexpr (T == T_Q4_K || T == T_Q6_K) return pg_launch<T, MT, NT, true>(a, s);   // rows of whole 256-value blocks
+    if constexpr (kquant(T)) return pg_launch<T, MT, NT, true>(a, s);   // rows of whole 256-value blocks
     else return a.K % ws_ki<T>() == 0 ? pg_launch<T, MT, NT, true>(a, s) : pg_launch<T, MT, NT, false>(a, s);
 }
 
@@ -275,10 +275,10 @@ constexpr int PG_NSHAPES = (int)(sizeof PG_SHAPES / sizeof PG_SHAPES[0]);
 template <int T>
 static int pg_dispatch(const Args& a, int idx, hipStream_t s) {
     switch (idx) {
-        case 0: if constexpr (T != T_Q6_K) return pg_launch_k<T, 16, 4>(a, s); break;
+        case 0: if constexpr (T != T_Q5_K && T != T_Q6_K) return pg_launch_k<T, 16, 4>(a, s); break;
         case 1: return pg_launch_k<T, 16, 3>(a, s);
         case 2: return pg_launch_k<T, 16, 2>(a, s);
-        case 3: if constexpr (T != T_Q6_K) return pg_launch_k<T, 8, 5>(a, s); break;
+        case 3: if constexpr (T != T_Q5_K && T != T_Q6_K) return pg_launch_k<T, 8, 5>(a, s); break;
         case 4: return pg_launch_k<T, 8, 4>(a, s);
         case 5: return pg_launch_k<T, 8, 2>(a, s);
     }
@@ -307,12 +307,12 @@ static double pg_model(int64_t M, int64_t N, int64_t K, int cus, const PgShape& 
     return (double)rounds * sh.mt * sh.nt * (double)K / eff;
 }
 
-// Q6_K's weight buffers (4 loads per row tile) leave no registers for the 16 x 4 and 8 x 5 tiles
-static bool pg_type_has(int t, int i) { return t != T_Q6_K || (i != 0 && i != 3); }
+// the weight buffers of Q5_K and Q6_K (3 and 4 loads per row tile) leave no registers for the 16 x 4 and 8 x 5 tiles
+static bool pg_type_has(int t, int i) { return (t != T_Q5_K && t != T_Q6_K) || (i != 0 && i != 3); }
 
 static int pg_best(int t, int64_t M, int64_t N, int64_t K) {
     const int cus = pg_cus();
-    int best = t == T_Q6_K ? 1 : 0;
+    int best = (t == T_Q5_K || t == T_Q6_K) ? 1 : 0;
     double bt = 1e300;
     for (int i = 0; i < PG_NSHAPES; ++i) {
         if (16 * PG_SHAPES[i].mt > M || !pg_type_has(t, i)) continue;
@@ -347,6 +347,7 @@ int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s) {
         case T_INT8: return pg_dispatch<T_INT8>(a, idx, s);
         case T_Q8_0: return pg_dispatch<T_Q8_0>(a, idx, s);
         case T_Q4_K: return pg_dispatch<T_Q4_K>(a, idx, s);
+        case T_Q5_K: return pg_dispatch<T_Q5_K>(a, idx, s);
         case T_Q6_K: return pg_dispatch<T_Q6_K>(a, idx, s);
     }
     return set_error(MBQ_BAD_ARG, "weight-direct GEMM: no kernel for type %d", t);

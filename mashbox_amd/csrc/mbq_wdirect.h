@@ -8,9 +8,11 @@
 //          bfloat16, the value the LDS GEMM stores.
 //   Q4_K   one 16-byte unit = the 32 quants of sub-block k0/32 + g = 4 K steps; the B operand is (d sc) q - dmin m
 //          (exact in float32) rounded to nearest even bfloat16.
+//   Q5_K   the same 32 values: 16 bytes of low nibbles, the 4-byte high-bit word and the super-block's scales; the B
+//          operand is (d sc) q - dmin m (one rounding) rounded to nearest even bfloat16.
 //   Q6_K   the same 32 values: 16 bytes of low nibbles, 8 bytes of high bits, the two 16-value scales and the
 //          super-block scale; the B operand is (d sc) (q - 32) (exact in float32) rounded to nearest even bfloat16.
-// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :164-173 (Q6_K); plane layouts:
+// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K); plane layouts:
 // mbq_layout.h.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -21,8 +23,8 @@
 
 namespace mbq {
 
-template <int T> constexpr int ws_ki() { return (T == T_Q4_K || T == T_Q6_K) ? 128 : 64; }
-inline int ws_ki_of(int t) { return (t == T_Q4_K || t == T_Q6_K) ? 128 : 64; }
+template <int T> constexpr int ws_ki() { return kquant(T) ? 128 : 64; }
+inline int ws_ki_of(int t) { return kquant(t) ? 128 : 64; }
 
 // raw bytes of one iteration of one 16-row tile, as one lane holds them
 template <int T> struct WsRaw;
@@ -30,15 +32,17 @@ template <> struct WsRaw<T_INT8> { u32x4 q; };
 template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
 template <> struct WsRaw<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
-template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_K ? 4 : 2; }   // buffer loads per tile per iteration
+template <> struct WsRaw<T_Q5_K> { u32x4 q, meta; uint32_t h; };
+template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_K ? 4 : T == T_Q5_K ? 3 : 2; }   // buffer loads per tile per iteration
 
 // per-lane byte offsets of one weight row's planes (the iteration's part goes in the scalar offset)
 struct WsOff { uint32_t q, s, h, d; };
 template <int T>
 __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    WsOff o{row * (uint32_t)((T == T_Q4_K || T == T_Q6_K) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
+    WsOff o{row * (uint32_t)(kquant(T) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
     if constexpr (T == T_Q8_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
-    if constexpr (T == T_Q4_K) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 256) * 16u;
+    if constexpr (T == T_Q4_K || T == T_Q5_K) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 256) * 16u;
+    if constexpr (T == T_Q5_K) o.h = (uint32_t)hi_off + row * (uint32_t)(K / 8) + 4u * lg;
     if constexpr (T == T_Q6_K) {
         o.s = (uint32_t)sc_off + row * (uint32_t)(K / 16) + 2u * lg;
         o.h = (uint32_t)hi_off + row * (uint32_t)(K / 4) + 8u * lg;
@@ -51,12 +55,13 @@ __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_
 // gets scale 0 (the x it meets is zero, its quants may be any bytes)
 template <int T, bool KFULL>
 __device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, int kk, int K, int lg) {
-    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)((T == T_Q4_K || T == T_Q6_K) ? kk / 2 : kk), 2));
+    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)(kquant(T) ? kk / 2 : kk), 2));
     if constexpr (T == T_Q8_0) {
         w.d = bload2(wr, o.s, (uint32_t)(kk / 32) * 2u);
         if constexpr (!KFULL) w.d = (kk + 16 * lg < K) ? w.d : 0u;
     }
-    if constexpr (T == T_Q4_K) w.meta = bload16(wr, o.s, (uint32_t)(kk / 256) * 16u);
+    if constexpr (T == T_Q4_K || T == T_Q5_K) w.meta = bload16(wr, o.s, (uint32_t)(kk / 256) * 16u);
+    if constexpr (T == T_Q5_K) w.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, o.h, (uint32_t)(kk / 8), 2);
     if constexpr (T == T_Q6_K) {
         w.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, o.h, (uint32_t)(kk / 4), 2));
         w.s = bload2(wr, o.s, (uint32_t)(kk / 16));
@@ -65,7 +70,7 @@ __device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, 
 }
 
 // per-lane dequant constants of one tile's unit
-struct WsScale { float a, b, c, e; };   // Q8_0: d; Q4_K: d*sc, dmin*m, d*sc/16; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+struct WsScale { float a, b, c, e; };   // Q8_0: d; Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
 
 template <int T>
 __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
@@ -78,7 +83,7 @@ __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
         s.e = 32.f * s.c;
     } else if constexpr (T == T_Q8_0) {
         s.a = f16f(w.d);
-    } else if constexpr (T == T_Q4_K) {
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         uint32_t sc, mn;
         q4k_scale_min_sel(w.meta[1], w.meta[2], w.meta[3], q4k_sel(j), &sc, &mn);
         s.a = f16f(w.meta[0]) * (float)sc;          // exact
@@ -100,6 +105,13 @@ __device__ __forceinline__ uint32_t ws_bpair(const WsRaw<T>& w, const WsScale& s
         const int sh = (p & 1) * 16;
         const float ds = s < 2 ? sc.a : sc.c, m = s < 2 ? sc.b : sc.e;
         return pack_bf16(__builtin_fmaf((float)((v >> sh) & 0xFFu), ds, -m), __builtin_fmaf((float)((v >> (sh + 8)) & 0xFFu), ds, -m));
+    } else if constexpr (T == T_Q5_K) {
+        // values 8s .. 8s+3 (p = 0, 1) and 8s+4 .. 8s+7 (p = 2, 3) of the unit as bytes; (d sc) q - dmin m is one FMA
+        uint32_t lo, hi;
+        q5k_bytes(w.q[s], w.h, s, &lo, &hi);
+        const uint32_t v = p < 2 ? lo : hi;
+        const int sh = (p & 1) * 16;
+        return pack_bf16(__builtin_fmaf((float)((v >> sh) & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)((v >> (sh + 8)) & 0xFFu), sc.a, -sc.b));
     } else if constexpr (T == T_Q4_K) {
         // dword s of the unit: quant 8s+2p in bits 4p..4p+3, quant 8s+2p+1 in bits 16+4p.. (mbq_layout.h); the odd
         // nibble positions come out 16 times too large and take the scale d*sc/16

@@ -44,9 +44,9 @@ namespace mbq {
 constexpr int WS_THREADS = 256;    // 4 waves
 
 // iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_K, Q6_K) at 64 activation rows
-template <int T> constexpr int ws_depth() { return (T == T_Q4_K || T == T_Q6_K) ? 4 : 8; }
+template <int T> constexpr int ws_depth() { return kquant(T) ? 4 : 8; }
 // x rows staged: 16 MT, rounded so that every wave issues the same number of 1 KiB DMA instructions per stage
-template <int T, int MT> constexpr int ws_rows() { return (T == T_Q4_K || T == T_Q6_K) ? 16 * MT : (MT <= 2 ? 32 : 64); }
+template <int T, int MT> constexpr int ws_rows() { return kquant(T) ? 16 * MT : (MT <= 2 ? 32 : 64); }
 
 struct WsArgs {
     const uint8_t* base;        // planes of the weight (host layer applied)
@@ -284,7 +284,7 @@ static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStrea
 template <int T, int NT>
 static int ws_launch_m(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
     const bool kfull = a.K % ws_ki<T>() == 0;
-    if constexpr (T == T_Q4_K || T == T_Q6_K) {                       // rows of whole 256-value blocks
+    if constexpr (kquant(T)) {                       // rows of whole 256-value blocks
         switch ((a.M + 15) / 16) {
             case 1: return ws_launch<T, 1, NT, true>(a, S, kts, w, s);
             case 2: return ws_launch<T, 2, NT, true>(a, S, kts, w, s);
@@ -322,7 +322,7 @@ static size_t ws_partial_bytes(int64_t M, int nr) { return (size_t)((M + 15) / 1
 // the partial tiles within the workspace.
 static void ws_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int* nr, int* S) {
     const int64_t KT = (K + ws_ki_of(t) - 1) / ws_ki_of(t);
-    const int depth = (t == T_Q4_K || t == T_Q6_K) ? 4 : 8;
+    const int depth = kquant(t) ? 4 : 8;
     const int64_t tiles64 = (N + 63) / 64;
     if (tiles64 >= cus) {
         *nr = 128;
@@ -367,6 +367,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);
         case T_Q8_0: return nr == 64 ? ws_launch_m<T_Q8_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q8_0, 2>(a, S, (int)kts, w, s);
         case T_Q4_K: return nr == 64 ? ws_launch_m<T_Q4_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_K, 2>(a, S, (int)kts, w, s);
+        case T_Q5_K: return nr == 64 ? ws_launch_m<T_Q5_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q5_K, 2>(a, S, (int)kts, w, s);
         case T_Q6_K: return nr == 64 ? ws_launch_m<T_Q6_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q6_K, 2>(a, S, (int)kts, w, s);
     }
     return set_error(MBQ_BAD_ARG, "weight-stream GEMM: no kernel for type %d", t);

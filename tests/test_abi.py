@@ -40,23 +40,24 @@ def test_type_table_and_shapes():
     lib = L.lib()
     assert lib.mbq_version() >= 100
     assert lib.mbq_has_type(8) == 1 and lib.mbq_has_type(12) == 1 and lib.mbq_has_type(14) == 1
-    assert lib.mbq_has_type(13) == 0 and lib.mbq_has_type(2) == 0
+    assert lib.mbq_has_type(13) == 1 and lib.mbq_has_type(2) == 0 and lib.mbq_has_type(11) == 0
+    assert lib.mbq_row_bytes(13, 5120) == R.row_bytes(13, 5120) == 3520
     assert lib.mbq_row_bytes(14, 2560) == R.row_bytes(14, 2560) == 2100
     assert lib.mbq_row_bytes(8, 5120) == R.row_bytes(8, 5120) == 5440
     assert lib.mbq_row_bytes(12, 17408) == R.row_bytes(12, 17408) == 9792
     assert lib.mbq_row_bytes(12, 100) < 0
     assert KQ.kq_covers(8, (17408, 5120)) and KQ.kq_covers(12, (5120, 17408))
-    assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(13, (256, 256))
+    assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(11, (256, 256)) and KQ.kq_covers(13, (256, 256))
     assert KQ.kq_covers(14, (151936, 2560)) and not KQ.kq_covers(14, (8, 128))
     for t, (n, k) in [(8, (17408, 5120)), (12, (5120, 17408)), (12, (1, 256)), (8, (3, 32)), (14, (151936, 2560)),
-                      (14, (1, 256)), (14, (3, 512))]:
+                      (14, (1, 256)), (14, (3, 512)), (13, (1, 256)), (13, (17408, 5120))]:
         pb = KQ.plane_bytes(t, (n, k))
         file_bytes = n * R.row_bytes(t, k)
-        planes = 4 if t == 14 else 2                                  # each plane pads to 256 bytes
+        planes = {14: 4, 13: 3}.get(t, 2)                             # each plane pads to 256 bytes
         assert pb % 256 == 0 and file_bytes <= pb < file_bytes + 256 * planes
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_host_repack_is_lossless(t):
     rng = np.random.default_rng(40 + t)
     for n, kb in [(1, 1), (7, 3), (130, 2)]:
@@ -115,10 +116,33 @@ def test_q6_k_unit_layout_yields_quant_bytes():
             assert np.array_equal((hi >> np.uint32(8 * j)) & np.uint32(0xFF), q[:, :, 8 * t_ + 4 + j])
 
 
+def test_q5_k_unit_layout_yields_quant_bytes():
+    """a Q5_K unit: low nibbles as Q6_K's, and the high-bit word rotated right by 2t + 28 (2t + 29) so that bit 4 of
+    every byte is the high bit of value 8t + j (8t + 4 + j), as q5k_bytes does: checked on the host against the oracle's
+    dequant of blocks with d = 1, dmin = 0 and every scale 1 (its values are then q)"""
+    rng = np.random.default_rng(43)
+    raw = G.q5_k_raw(rng, 3, 512).reshape(6, 176)
+    raw[:, 0:4] = np.array([1.0, 0.0], np.float16).view(np.uint8)
+    raw[:, 4:16] = R.pack_scale_min_k4(np.ones((6, 8), np.uint8), np.zeros((6, 8), np.uint8))
+    raw = raw.reshape(3, 352)
+    q = R.dequant(raw, R.Q5_K, 512).astype(np.uint32).reshape(3, 16, 32)   # (row, unit, value)
+    p = KQ.repack_host(R.Q5_K, raw, (3, 512)).buf.numpy()
+    ql = p[:3 * 256].view(np.uint32).reshape(3, 16, 4)
+    qh = p[768:768 + 3 * 64].view(np.uint32).reshape(3, 16)
+    rot = lambda v, s: ((v >> np.uint32(s)) | (v << np.uint32(32 - s))) if s else v
+    m1, m0f = np.uint32(0x10101010), np.uint32(0x0F0F0F0F)
+    for t_ in range(4):
+        lo = (rot(qh, (2 * t_ + 28) % 32) & m1) | (ql[:, :, t_] & m0f)
+        hi = (rot(qh, (2 * t_ + 29) % 32) & m1) | ((ql[:, :, t_] >> np.uint32(4)) & m0f)
+        for j in range(4):
+            assert np.array_equal((lo >> np.uint32(8 * j)) & np.uint32(0xFF), q[:, :, 8 * t_ + j])
+            assert np.array_equal((hi >> np.uint32(8 * j)) & np.uint32(0xFF), q[:, :, 8 * t_ + 4 + j])
+
+
 def test_argument_errors_are_reported_without_a_launch():
     lib = L.lib()
     null = ctypes.c_void_p(0)
-    assert lib.mbq_matmul(13, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1
+    assert lib.mbq_matmul(11, null, 0, None, 1, null, 1, 8, 256, null, 0, null) == -1
     assert b"type" in lib.mbq_last_error()
     assert lib.mbq_matmul(12, null, 0, None, 1, null, 1, 8, 200, null, 0, null) == -1
     assert b"multiple" in lib.mbq_last_error()

@@ -22,11 +22,11 @@ from mashbox_amd import int8 as I8
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [R.Q8_0, R.Q4_K, R.Q6_K]
-NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q6_K: "Q6_K"}
-GEMM_TYPES = [R.Q8_0, R.Q4_K, R.Q6_K, "int8"]
-GEMM_IDS = ["Q8_0", "Q4_K", "Q6_K", "int8"]
-KQUANT = (R.Q4_K, R.Q6_K)                             # rows of whole 256-value super-blocks
+TYPES = [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K]
+NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
+GEMM_TYPES = [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K, "int8"]
+GEMM_IDS = ["Q8_0", "Q4_K", "Q5_K", "Q6_K", "int8"]
+KQUANT = (R.Q4_K, R.Q5_K, R.Q6_K)                     # rows of whole 256-value super-blocks
 
 
 def _bf16_tensor(bits: np.ndarray, dev) -> torch.Tensor:
@@ -288,7 +288,7 @@ def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cu
     included), split-K into 3 ranges against 1"""
     rng = np.random.default_rng([bm, bn, 0 if t == "int8" else t])
     m, n = bm + bm // 2 - 3, bn + 17
-    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, R.Q6_K: 256 * 3, "int8": 16 * 25}[t]
+    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, R.Q5_K: 256 * 3, R.Q6_K: 256 * 3, "int8": 16 * 25}[t]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
     xf = R.bf16_to_f32(xb).astype(np.float64)
@@ -338,10 +338,10 @@ def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
     a multiple of the kernel's iteration (64 values; 128 for Q4_K and Q6_K, whose K is always whole)"""
     if t in KQUANT and not kfull:
         pytest.skip("a K-quant K is a whole number of 256-value super-blocks")
-    if t == R.Q6_K and (mt, nt) in ((16, 4), (8, 5)):
-        pytest.skip("no Q6_K weight-direct kernel of this shape (test_weight_direct_q6_k_refuses_the_widest_shapes)")
+    if t in (R.Q5_K, R.Q6_K) and (mt, nt) in ((16, 4), (8, 5)):
+        pytest.skip("no Q5_K / Q6_K weight-direct kernel of this shape (test_weight_direct_refuses_the_widest_shapes)")
     bm, bn = 16 * mt, 64 * nt
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), R.Q6_K: (256 * 5, 256 * 5),
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), R.Q5_K: (256 * 5, 256 * 5), R.Q6_K: (256 * 5, 256 * 5),
          "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     for m, n in ((bm, bn + 17), (2 * bm + 37, 2 * bn + 17)):
         rng = np.random.default_rng([m, n, int(kfull), 0 if t == "int8" else t])
@@ -351,18 +351,19 @@ def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
         assert_product(run(), ref, f"{t} direct {bm}x{bn} m={m} n={n} k={k}")
 
 
-def test_weight_direct_q6_k_refuses_the_widest_shapes(forced_plan, cuda):
-    """the 16 x 4 and 8 x 5 row-tile shapes have no Q6_K kernel: a forced plan of them raises, launching nothing, and
-    the kernel's own shape choice avoids them"""
+@pytest.mark.parametrize("t", [R.Q5_K, R.Q6_K], ids=NAME.get)
+def test_weight_direct_refuses_the_widest_shapes(t, forced_plan, cuda):
+    """the 16 x 4 and 8 x 5 row-tile shapes have no Q5_K / Q6_K kernel: a forced plan of them raises, launching
+    nothing, and the kernel's own shape choice avoids them"""
     rng = np.random.default_rng(9)
     m, n, k = 256, 640, 512
-    run, ref = _direct_case(R.Q6_K, m, n, k, rng, cuda)
+    run, ref = _direct_case(t, m, n, k, rng, cuda)
     for bm, bn in ((256, 256), (128, 320)):
         forced_plan(LIB.KERNEL_DIRECT, bm, bn, 1)
         with pytest.raises(RuntimeError, match="no tile shape"):
             run()
     forced_plan(LIB.KERNEL_DIRECT, 0, 0, 0)
-    _, bm, bn, _ = LIB.gemm_plan(R.Q6_K, 4096, 8192, 4096)
+    _, bm, bn, _ = LIB.gemm_plan(t, 4096, 8192, 4096)
     assert (bm, bn) not in ((256, 256), (128, 320))
     assert_product(run(), ref)
 
@@ -396,7 +397,7 @@ def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
     whose K is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
     rng = np.random.default_rng([m, rows, int(kfull), 0 if t == "int8" else t])
     n = 3 * rows + 17
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), R.Q6_K: (256 * 5, 256 * 6),
+    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), R.Q5_K: (256 * 5, 256 * 6), R.Q6_K: (256 * 5, 256 * 6),
          "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
