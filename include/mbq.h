@@ -107,6 +107,14 @@ int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, f
 int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
                     void* y_dev, int out_dtype, void* stream);
 
+/* int8 embedding rows: y (T, D) = f32(q[r]) * s[r] per token, r = toks[t] (int32, device), plus N when negative and
+ * clamped to [0, N - 1] (jax.numpy indexing), then out_dtype (bfloat16 rounded to nearest even, or float32 for a pj
+ * hook). q_dev int8 (N, D) row-major, s_dev float32 (N,). Bit for bit the gather of embed(E, toks) for an int8 table
+ * E = {"q", "s"} (reference src/mashbox/models/qwen3_8_27b/model.py:132-139, whose int8_rows at :117-129 equals the
+ * plain gather q[toks]). */
+int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D, const int32_t* toks_dev, int64_t T,
+                   void* y_dev, int out_dtype, void* stream);
+
 /* Tuning and introspection (no counterpart in the reference, whose kernels are closed). For an activation batch of M
  * rows, mbq_gemm_plan reports how mbq_matmul / mbq_int8_linear would run a (N, K) weight of type t (MBQ_INT8 for the
  * int8 linear): the kernel (MBQ_KERNEL_*), *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses

@@ -28,6 +28,8 @@ _SIGS = {
     "mbq_dequant": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                _c.c_void_p, _c.c_void_p]),
     "mbq_dequant_raw": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
+    "mbq_int8_embed": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_void_p,
+                                  _c.c_int, _c.c_void_p]),
     "mbq_int8_linear": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                    _c.c_void_p, _c.c_int, _c.c_void_p]),
     "mbq_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64, _c.c_int64, _c.POINTER(_c.c_int),

@@ -383,6 +383,22 @@ int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_d
     return launch_matmul(T_INT8, a, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D, const int32_t* toks_dev, int64_t T,
+                   void* y_dev, int out_dtype, void* stream) {
+    if (int rc = check_out(out_dtype)) return rc;
+    if (N <= 0 || D <= 0 || T < 0 || N > INT32_MAX || D > INT32_MAX || T > 65535 * 64LL)
+        return set_error(MBQ_BAD_ARG, "embedding table (%lld, %lld), %lld tokens", (long long)N, (long long)D, (long long)T);
+    if (T == 0) return MBQ_OK;
+    if (!q_dev || !s_dev || !toks_dev || !y_dev) return set_error(MBQ_BAD_ARG, "q, s, toks or y is NULL");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    for (int64_t t0 = 0; t0 < T; t0 += 65535) {                     // grid.y holds at most 65535 tokens
+        const int64_t n = std::min<int64_t>(65535, T - t0);
+        void* y = reinterpret_cast<uint8_t*>(y_dev) + t0 * D * (out_dtype == MBQ_OUT_BF16 ? 2 : 4);
+        if (int rc = launch_int8_embed(q_dev, s_dev, N, D, toks_dev + t0, n, y, out_dtype == MBQ_OUT_BF16, st)) return rc;
+    }
+    return MBQ_OK;
+}
+
 int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits) {
     if (!kernel || !bm || !bn || !splits) return set_error(MBQ_BAD_ARG, "NULL output");
     if (t == T_INT8) {

@@ -261,6 +261,61 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     }
 }
 
+// ------------------------------------------------------------------------------------------ int8 embedding rows
+// y[t, :] = f32(q[r, :]) * s[r] (then rounded to bfloat16 when out_bf16), r = toks[t] (+ N when negative, clamped to
+// [0, N - 1]): reference src/mashbox/models/qwen3_8_27b/model.py:132-139 (embed, whose int8_rows at :117-129 equals the
+// plain gather bit for bit). HBM-bound: D bytes read and 2 D (4 D) written per token. VEC: D % 16 == 0, one thread per
+// 16 values (one 16-byte load, two or four 16-byte stores); else one thread per value.
+template <bool VEC>
+__global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ q, const float* __restrict__ s, int64_t N,
+                                                    int64_t D, const int32_t* __restrict__ toks, void* __restrict__ y,
+                                                    int out_bf16) {
+    const int64_t t = blockIdx.y;
+    int64_t r = toks[t];
+    r = r < 0 ? r + N : r;
+    r = r < 0 ? 0 : (r >= N ? N - 1 : r);
+    const float sc = s[r];
+    const int64_t per = VEC ? 16 : 1;
+    const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * per;
+    if (c >= D) return;
+    if constexpr (VEC) {
+        const u32x4 w = ld16(q + r * D + c);
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3))) * sc;
+        if (out_bf16) {
+            uint16_t* o = reinterpret_cast<uint16_t*>(y) + t * D + c;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                u32x4 p;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[e] = bf16_bits(v[8 * h + 2 * e]) | (bf16_bits(v[8 * h + 2 * e + 1]) << 16);
+                st16(o + 8 * h, p);
+            }
+        } else {
+            float* o = reinterpret_cast<float*>(y) + t * D + c;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                st16(o + 4 * h, u32x4{__float_as_uint(v[4 * h]), __float_as_uint(v[4 * h + 1]), __float_as_uint(v[4 * h + 2]),
+                                      __float_as_uint(v[4 * h + 3])});
+        }
+    } else {
+        store_y(y, t * D + c, (float)q[r * D + c] * sc, out_bf16);
+    }
+}
+
+int launch_int8_embed(const int8_t* q, const float* s, int64_t N, int64_t D, const int32_t* toks, int64_t T, void* y,
+                      int out_bf16, hipStream_t st) {
+    const bool vec = D % 16 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    const int64_t per = vec ? 16 : 1, threads = (D + per - 1) / per;
+    const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)T);
+    if (vec)
+        embed_kernel<true><<<grid, 256, 0, st>>>(q, s, N, D, toks, y, out_bf16);
+    else
+        embed_kernel<false><<<grid, 256, 0, st>>>(q, s, N, D, toks, y, out_bf16);
+    return check_launch("int8 embed");
+}
+
 // -------------------------------------------------------------------------------------------------- launchers
 static int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();

@@ -19,6 +19,8 @@ It restates, from scratch in NumPy, what the reference computes (reference = /ro
   exact-path product                src/mashbox/ops/__init__.py:574-576, 624-632 (_exact, qmatmul's Raw branch)
   int8 per-channel linear           src/mashbox/models/qwen3_8_27b/model.py:72-82 (linear)
   int8 per-row quantizer (fixture)  tests/cpu/qwen3_8_27b_checks.py:113-117 (int8_rows)
+  int8 embedding rows               src/mashbox/models/qwen3_8_27b/model.py:132-139 (embed; its int8_rows at :117-129
+                                    equals the plain gather q[toks])
 
 The reference's own arithmetic follows gguf-py 0.19.0 (gguf/quants.py), a third-party package absent here; its published
 algorithm is the one restated by the reference file above, and that is what this module follows.
@@ -42,6 +44,9 @@ How each function is pinned (tests/test_oracle.py):
                   loop (ggml-quants.c dequantize_row_q6_K, the algorithm gguf-py restates) on random blocks and on the
                   real llama-quantize blocks of the reference's fixture files; all-zero / all-0xFF blocks.
   qmatmul_exact   against a float64 product (reference bars: tests/contracts/test_ops.py:22-31), and chunked == whole.
+  int8_embed      against torch's own CPU float32 product and bfloat16 cast of the same gathered rows (an independent
+                  implementation of the two IEEE-754 roundings), and the index rule against jax.numpy's documented one
+                  (negative ids wrap once, the rest clamp) on every edge id.
   int8_linear     per element closed form: every bf16(x)*bf16(q) product is exact in float32; checked against a float64
                   product of the same values.
 """
@@ -240,3 +245,12 @@ def int8_rows(w: np.ndarray):
     am = np.abs(w32).max(-1)
     s = np.where(am > 0, am / np.float32(127.0), np.float32(1.0)).astype(np.float32)
     return np.clip(np.round(w32 / s[:, None]), -127, 127).astype(np.int8), s
+
+
+def int8_embed(q: np.ndarray, s: np.ndarray, toks) -> np.ndarray:
+    """rows of toks of the int8 table (q (N, D), s (N,)) as float32 f32(q) * s, before the rounding to bfloat16
+    (src/mashbox/models/qwen3_8_27b/model.py:132-139); ids index as jax.numpy: + N when negative, then clamped"""
+    n = q.shape[0]
+    t = np.asarray(toks, np.int64)
+    t = np.clip(np.where(t < 0, t + n, t), 0, n - 1)
+    return q[t].astype(np.float32) * np.asarray(s, np.float32)[t][..., None]
