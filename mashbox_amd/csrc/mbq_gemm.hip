@@ -730,6 +730,9 @@ static const Cand<T> CANDS[] = {cand<T, 256, 256, 1>(), cand<T, 256, 192, 1>(), 
                                 cand<T, 128, 64, 3>(),  cand<T, 64, 256, 3>(),  cand<T, 64, 192, 3>(),
                                 cand<T, 64, 128, 3>(),  cand<T, 64, 64, 3>()};
 
+// K-step time (us) of one block of each candidate when it runs alone on its CU (the order of CANDS)
+static constexpr double T1_US[] = {1.56, 1.20, 1.14, 1.10, 1.04, 0.83, 0.57, 0.84, 0.80, 0.58, 0.43};
+
 // Tile shape and K split for an (M, N, K) problem: the candidate with the least modelled time. A block's K step costs
 // about 0.1 us + 3.5e-5 us per output of its tile (fitted to MI355X timings of these kernels at 2048 and 64 activation
 // rows); blocks run in rounds over the CUs x the blocks of that shape a CU holds (LDS, registers). K is split only for
@@ -757,6 +760,27 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
         const int64_t rounds = (tiles * S + (int64_t)cus * occ - 1) / ((int64_t)cus * occ);
         const double t = (double)rounds * occ * (0.1 + 3.46e-5 * bm * bn) * kts;
         if (t < best_t) best_t = t, best = Plan{i, (int)S, (int)kts};
+    }
+    // A batch whose chosen tiles leave more than a fifth of the CUs idle (a small N, or M < 256): the model above, fitted
+    // to loaded CUs, misjudges it. Then every CU runs at most one block, and the tile with the least K-step time of a
+    // lone block (T1_US, measured on MI355X, Q4_K, one block per CU) times the steps wins among those whose tiles fit
+    // in one round: e.g. 2048 x 1024 x 5120 runs 128 x 64 tiles in 47 us instead of 64 x 192 in 66 us, 96 x 5120 x 17408
+    // 64 x 64 tiles in 112 us instead of 213 us; shapes whose tiles fill the CUs keep the model's choice.
+    static_assert(sizeof T1_US / sizeof T1_US[0] == sizeof CANDS<T> / sizeof CANDS<T>[0], "one lone-block time per candidate");
+    if (M > 64) {
+        const int bm = CANDS<T>[best.idx].bm, bn = CANDS<T>[best.idx].bn;
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * best.S;
+        if (tiles * 5 < (int64_t)cus * 4) {
+            double bt = 1e300;
+            for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i) {
+                const int cbm = CANDS<T>[i].bm, cbn = CANDS<T>[i].bn;
+                if (cbm > 64 && M <= cbm / 2) continue;
+                const int64_t ct = ((M + cbm - 1) / cbm) * ((N + cbn - 1) / cbn);
+                if (ct > cus) continue;
+                const double t = T1_US[i] * KT;
+                if (t < bt) bt = t, best = Plan{i, 1, (int)KT};
+            }
+        }
     }
     return best;
 }
