@@ -12,7 +12,10 @@
 // an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
 // block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
 // multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
-// the inner loop). The next item's loads (DEPTH - 1 items) are in flight while an item computes; every load is
+// the inner loop). Rows of few units (K = 2560: 80 units, a second chunk with 16 of 64 lanes busy) are packed R to an
+// item instead (S = 1, R in {2, 4}, R U a multiple of 64): R consecutive rows are one run of R U units in every plane,
+// lane l of chunk i takes unit f = 64 i + l of the run (row f / U, whose sums the lane adds to that row's), and the
+// x a lane multiplies is still the same for every item. The next item's loads (DEPTH - 1 items) are in flight while an item computes; every load is
 // unconditional (lanes past a part's end, chunks past it and items past a wave's last row read out of the buffer's
 // range: zero, and no memory traffic), so the compiler's vmcnt waits count exactly the next item's loads. An item's sums are reduced across the wave with DPP; with S > 1 the block
 // adds a row's parts through LDS at the end.
@@ -76,7 +79,7 @@ __device__ __forceinline__ void gv_i8x4(uint32_t w, uint32_t* lo, uint32_t* hi) 
     *hi = pack_bf16((float)(int8_t)((w >> 16) & 0xFFu), (float)(int8_t)(w >> 24));
 }
 
-template <int T, int M, int CH, int DEPTH = 2>
+template <int T, int M, int CH, int DEPTH = 2, int R = 1>
 __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     extern __shared__ float parts[];                                  // S > 1: (r1 - r0) x S x M
     constexpr int UW = gv_uw<T>(), TPU = gv_tpu<T>();
@@ -84,7 +87,9 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int N = g.N, K = g.K, S = g.S, PU = g.PU;
     const int P = gridDim.x;
-    const int r0 = (int)((int64_t)blockIdx.x * N / P), r1 = (int)((int64_t)(blockIdx.x + 1) * N / P);
+    // block b owns rows [r0, r1): N / P of them, whole groups of R rows (the last group may end past N)
+    const int G = (N + R - 1) / R;
+    const int r0 = R * (int)((int64_t)blockIdx.x * G / P), r1 = min(N, R * (int)((int64_t)(blockIdx.x + 1) * G / P));
     const int64_t lo = layer_offset(g.stride, g.layer_dev, g.nlayers);
     const bool ok = lo >= 0;
     const rsrc_t wr = make_rsrc(g.base + (ok ? lo : 0), (uint32_t)g.wbytes);
@@ -97,8 +102,8 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const int part = wave % S, rstep = GV_WAVES / S;
     const int u0 = part * PU, nu = max(0, min(PU, U - u0));
     const int lastc = max(0, (nu - 1) >> 6);                         // last chunk with a unit of the part
-    const int nrows = r1 - r0, first = wave / S;
-    const int nit = first < nrows ? (nrows - 1 - first) / rstep + 1 : 0;   // rows this wave takes
+    const int nrows = r1 - r0, first = wave / S, ngroups = (nrows + R - 1) / R;
+    const int nit = first < ngroups ? (ngroups - 1 - first) / rstep + 1 : 0;   // rows (groups of R rows) this wave takes
     const bool any = ok && nit > 0 && nu > 0;
 
     struct Raw { u32x4 q[CH]; u32x4 meta[CH]; uint32_t d[CH]; u32x2 h[CH]; uint32_t s[CH]; };
@@ -113,26 +118,30 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t vs = (uint32_t)lane * 2u, vs_last = lane_in ? vs : OOB_VOFF;          // Q6_K scale pairs
     const uint32_t vd6 = (uint32_t)(lane >> 3) * 2u, vd6_last = lane_in ? vd6 : OOB_VOFF;  // Q6_K super-block scales
     const uint32_t vh5 = (uint32_t)lane * 4u, vh5_last = lane_in ? vh5 : OOB_VOFF;        // Q5_K high bits
-    auto load = [&](Raw& R, int k) {                                  // the k-th row of the wave (clamped)
+    auto load = [&](Raw& W, int k) {                                  // the k-th item of the wave (clamped)
         const bool live = k < nit;                                    // wave-uniform
-        const int row = r0 + first + min(k, nit - 1) * rstep;
+        const int row = r0 + (first + min(k, nit - 1) * rstep) * R;   // the item's first row
+        const int nv = R > 1 ? min(R, r1 - row) * U : 0;              // R > 1: the item's units
         const uint32_t qs = (uint32_t)row * qstride + (uint32_t)u0 * 16u;
         const uint32_t ss = (uint32_t)g.sc_off + (uint32_t)row * sstride;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            const uint32_t c = (uint32_t)min(i, lastc);               // wave-uniform
-            auto off = [&](uint32_t full, uint32_t last) { return (!live || i > lastc) ? OOB_VOFF : (i < lastc ? full : last); };
-            R.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
-            if constexpr (T == T_Q8_0) R.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
-            if constexpr (T == T_Q4_K || T == T_Q5_K) R.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
+            const uint32_t c = (uint32_t)(R > 1 ? i : min(i, lastc));   // wave-uniform
+            auto off = [&](uint32_t full, uint32_t last) {
+                if constexpr (R > 1) return (!live || 64 * i + lane >= nv) ? OOB_VOFF : full;
+                else return (!live || i > lastc) ? OOB_VOFF : (i < lastc ? full : last);
+            };
+            W.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
+            if constexpr (T == T_Q8_0) W.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
+            if constexpr (T == T_Q4_K || T == T_Q5_K) W.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
             if constexpr (T == T_Q5_K)
-                R.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                W.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
                     wr, off(vh5, vh5_last), (uint32_t)g.hi_off + (uint32_t)row * (qstride >> 2) + (uint32_t)u0 * 4u + 256u * c, 2);
             if constexpr (T == T_Q6_K) {
-                R.h[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                W.h[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                     wr, off(vh, vh_last), (uint32_t)g.hi_off + (uint32_t)row * (qstride >> 1) + (uint32_t)u0 * 8u + 512u * c, 2));
-                R.s[i] = bload2(wr, off(vs, vs_last), ss + (uint32_t)u0 * 2u + 128u * c);
-                R.d[i] = bload2(wr, off(vd6, vd6_last), (uint32_t)g.d_off + (uint32_t)row * (uint32_t)(K >> 7) + ((uint32_t)u0 >> 2) + 16u * c);
+                W.s[i] = bload2(wr, off(vs, vs_last), ss + (uint32_t)u0 * 2u + 128u * c);
+                W.d[i] = bload2(wr, off(vd6, vd6_last), (uint32_t)g.d_off + (uint32_t)row * (uint32_t)(K >> 7) + ((uint32_t)u0 >> 2) + 16u * c);
             }
         }
     };
@@ -146,9 +155,11 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     // x of the lane's units (clamped to the row), per activation row, and for Q4_K the per-unit sums of x
     u32x4 xv[CH][M][TPU];
     float xs[CH][M], xs2[CH][M];                                      // Q6_K: sums of x over each half unit
+    int rsel[CH];                                                     // R > 1: the item row of the lane's unit
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-        const int u = min(u0 + lane + 64 * i, U - 1);
+        const int u = R > 1 ? (64 * i + lane) % U : min(u0 + lane + 64 * i, U - 1);
+        rsel[i] = (64 * i + lane) / U;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             float sum = 0.f, sum2 = 0.f;
@@ -171,18 +182,23 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t kmask = in_vgpr(0x000F000Fu), kmagic = in_vgpr(0x43004300u);
     const uint32_t c43 = in_vgpr(0x43434343u);
 
-    auto finish = [&](const Raw& R, int k) {
-        const int rl = first + k * rstep;
-        float acc[M];
+    auto finish = [&](const Raw& W, int k) {
+        const int rl = first + k * rstep;                             // R > 1: the item's group
+        const int nuk = R > 1 ? min(R, r1 - (r0 + rl * R)) * U : nu;  // units of the item
+        float acc[M], accr[R][M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] = 0.f;
+        for (int m = 0; m < M; ++m) {
+            acc[m] = 0.f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) accr[r][m] = 0.f;
+        }
         // chunk i; FULL: every lane holds a unit of the part (no zeroed scale)
         auto chunk = [&](auto FULL_, int i) {
             constexpr bool FULL = decltype(FULL_)::value;
-            const bool act = FULL || lane + 64 * i < nu;
+            const bool act = FULL || lane + 64 * i < nuk;
             if constexpr (T == T_Q6_K) {
-                const float d = f16f(R.d[i]);
-                float ds0 = d * (float)(int8_t)(R.s[i] & 0xFFu), ds1 = d * (float)(int8_t)((R.s[i] >> 8) & 0xFFu);   // exact
+                const float d = f16f(W.d[i]);
+                float ds0 = d * (float)(int8_t)(W.s[i] & 0xFFu), ds1 = d * (float)(int8_t)((W.s[i] >> 8) & 0xFFu);   // exact
                 if constexpr (!FULL) {
                     ds0 = act ? ds0 : 0.f;
                     ds1 = act ? ds1 : 0.f;
@@ -191,7 +207,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint32_t lo, hi;
-                    q6k_bytes(R.q[i][t], R.h[i][t >> 1], t, &lo, &hi);
+                    q6k_bytes(W.q[i][t], W.h[i][t >> 1], t, &lo, &hi);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         float& A = t < 2 ? A0[m] : A1[m];
@@ -209,9 +225,9 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                 }
             } else if constexpr (T == T_Q5_K) {
                 uint32_t sc, mn;
-                q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
-                float dsc = f16f(R.meta[i][0]) * (float)sc;             // exact
-                const float dm = f16f(R.meta[i][0] >> 16) * (float)mn;  // exact
+                q4k_scale_min_sel(W.meta[i][1], W.meta[i][2], W.meta[i][3], sel, &sc, &mn);
+                float dsc = f16f(W.meta[i][0]) * (float)sc;             // exact
+                const float dm = f16f(W.meta[i][0] >> 16) * (float)mn;  // exact
                 float c = 128.f * dsc + dm;
                 if constexpr (!FULL) {
                     dsc = act ? dsc : 0.f;
@@ -221,7 +237,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint32_t lo, hi;
-                    q5k_bytes(R.q[i][t], R.s[i], t, &lo, &hi);
+                    q5k_bytes(W.q[i][t], W.s[i], t, &lo, &hi);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         P0[m] = dot2(b128_pair(lo, c43, 0), xv[i][m][t][0], t ? P0[m] : 0.f);
@@ -234,9 +250,9 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                 for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(dsc, P0[m] + P1[m], __builtin_fmaf(-c, xs[i][m], acc[m]));
             } else if constexpr (T == T_Q4_K) {
                 uint32_t sc, mn;
-                q4k_scale_min_sel(R.meta[i][1], R.meta[i][2], R.meta[i][3], sel, &sc, &mn);
-                float dsc = f16f(R.meta[i][0]) * (float)sc;             // exact
-                const float dm = f16f(R.meta[i][0] >> 16) * (float)mn;  // exact
+                q4k_scale_min_sel(W.meta[i][1], W.meta[i][2], W.meta[i][3], sel, &sc, &mn);
+                float dsc = f16f(W.meta[i][0]) * (float)sc;             // exact
+                const float dm = f16f(W.meta[i][0] >> 16) * (float)mn;  // exact
                 float c = 128.f * dsc + dm;
                 if constexpr (!FULL) {
                     dsc = act ? dsc : 0.f;
@@ -247,7 +263,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                 for (int t = 0; t < 4; ++t)
 #pragma unroll
                     for (int pp = 0; pp < 4; ++pp) {
-                        const uint32_t pr = ((R.q[i][t] >> (4 * pp)) & kmask) | kmagic;
+                        const uint32_t pr = ((W.q[i][t] >> (4 * pp)) & kmask) | kmagic;
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
                             float& Pm = (pp & 1) ? P1[m] : P0[m];
@@ -258,13 +274,13 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                 for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(dsc, P0[m] + P1[m], __builtin_fmaf(-c, xs[i][m], acc[m]));
             } else {
                 float d = 1.f;
-                if constexpr (T == T_Q8_0) d = f16f(R.d[i]);
+                if constexpr (T == T_Q8_0) d = f16f(W.d[i]);
                 if constexpr (!FULL) d = act ? d : 0.f;
                 float P0[M], P1[M];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint32_t b0, b1;
-                    gv_i8x4(R.q[i][t], &b0, &b1);
+                    gv_i8x4(W.q[i][t], &b0, &b1);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         float& Pm = (t & 1) ? P1[m] : P0[m];
@@ -280,19 +296,38 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
         using Part = std::integral_constant<bool, false>;
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            if (64 * (i + 1) <= nu) chunk(Full{}, i);                  // wave-uniform
-            else if (64 * i < nu) chunk(Part{}, i);
-        }
+            if (64 * (i + 1) <= nuk) chunk(Full{}, i);                 // wave-uniform
+            else if (64 * i < nuk) chunk(Part{}, i);
+            if constexpr (R > 1) {                                    // the chunk's sums to the lanes' rows
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float v = wave_sum_dpp(acc[m]);
-            if (lane == 0) {
-                if (S == 1) {
-                    const int n = r0 + rl;
-                    const float sc = (T == T_INT8) ? g.srow[n] : 1.f;
-                    store_y(g.y, (int64_t)m * N + n, v * sc, g.out_bf16);
-                } else {
-                    parts[(rl * S + part) * M + m] = v;
+                for (int m = 0; m < M; ++m) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) accr[r][m] += rsel[i] == r ? acc[m] : 0.f;
+                    acc[m] = 0.f;
+                }
+            }
+        }
+        if constexpr (R > 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float v = wave_sum_dpp(accr[r][m]);
+                    const int n = r0 + rl * R + r;
+                    if (lane == 0 && n < r1) store_y(g.y, (int64_t)m * N + n, v * ((T == T_INT8) ? g.srow[n] : 1.f), g.out_bf16);
+                }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float v = wave_sum_dpp(acc[m]);
+                if (lane == 0) {
+                    if (S == 1) {
+                        const int n = r0 + rl;
+                        const float sc = (T == T_INT8) ? g.srow[n] : 1.f;
+                        store_y(g.y, (int64_t)m * N + n, v * sc, g.out_bf16);
+                    } else {
+                        parts[(rl * S + part) * M + m] = v;
+                    }
                 }
             }
         }
@@ -365,9 +400,9 @@ static int gv_parts(int64_t U, int* S, int* PU) {
     return -1;
 }
 
-template <int T, int M, int CH>
+template <int T, int M, int CH, int R = 1>
 static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
-    auto kern = gemv_kernel<T, M, CH>;
+    auto kern = gemv_kernel<T, M, CH, 2, R>;
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
     int P = resident_blocks(kern, 4096);
@@ -384,10 +419,26 @@ static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
     return 0;
 }
 
+// rows per item at one activation row: 4 when a row is 80 units (2560-value K-quant rows, 1280-value Q8_0 / int8 rows),
+// whose second chunk would have 16 of 64 lanes busy: 4 rows are 5 full chunks. Measured on MI355X (151936-row heads):
+// Q4_K 11 %, Q5_K 10 %, Q6_K 3 % faster; packing 2 rows of 96 or 160 units was slower (Q6_K K = 3072 by 8 %, Q8_0
+// K = 2560 by 3 %), so other rows keep one row per item.
+template <int T>
+static int gv_pack(int64_t U) {
+    return (U == 80 && 4 * U <= 64 * gv_chmax<T>(1)) ? 4 : 1;
+}
+
 template <int T, int M>
 static int launch_gemv_m(const Args& a, hipStream_t s) {
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "GEMV operands over 2 GiB");
+    if constexpr (M == 1) {
+        const int64_t U = a.K / gv_uw<T>();
+        const int r = gv_pack<T>(U);
+        if (r > 1) {
+            return launch_gemv_ch<T, 1, 5, 4>(a, 1, (int)(r * U), s);      // 4 rows of 80 units: 5 chunks
+        }
+    }
     int S = 1, PU = 0;
     const int ch = gv_parts<T, M>(a.K / gv_uw<T>(), &S, &PU);
     if (ch < 1) return set_error(MBQ_BAD_ARG, "GEMV K = %lld is too long for %d activation rows", (long long)a.K, M);

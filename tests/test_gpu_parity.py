@@ -220,6 +220,33 @@ def test_gemv_row_parts_past_the_row_end(t, m, cuda):
     assert_product(y, ref, f"{NAME[t]} m={m} k={k}")
 
 
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 130, 1027])
+def test_gemv_rows_of_80_units_packed_four_to_an_item(t, n, cuda):
+    """one activation row over rows of 80 units (2560 K-quant values, 1280 Q8_0 / int8 values): the GEMV packs 4 rows
+    into an item of 5 chunks; row counts that are not multiples of 4 leave a partial last group; a stack read at a
+    device layer (and one outside the stack: NaN) takes the same path"""
+    rng = np.random.default_rng([n, 80, 0 if t == "int8" else t])
+    k = 1280 if t in ("int8", R.Q8_0) else 2560
+    xb = G.acts(rng, 1, k)
+    x = _bf16_tensor(xb, cuda)
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    if t == "int8":
+        q, sc = G.int8_weights(rng, n, k)
+        y = _int8_f32(x, {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(sc).to(cuda)})
+        assert_product(y, (xf @ q.astype(np.float64).T) * sc, f"int8 n={n}")
+        return
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(2)])
+    planes = KQ.repack_host(t, st, (n, k)).to(cuda)
+    for layer in range(2):
+        ref = xf @ R.dequant(st[layer], t, k).astype(np.float64).T
+        assert_product(KQ.matmul(x, planes, layer=layer).cpu().numpy(), ref, f"{NAME[t]} n={n} layer {layer}")
+        dl = torch.tensor(layer, dtype=torch.int32, device=cuda)
+        assert_product(KQ.matmul(x, planes, layer=dl).cpu().numpy(), ref, f"{NAME[t]} n={n} device layer {layer}")
+    bad = KQ.matmul(x, planes, layer=torch.tensor(2, dtype=torch.int32, device=cuda)).cpu().numpy()
+    assert np.all(np.isnan(bad))
+
+
 def test_q6_k_output_head_full_size_sampled(cuda):
     """the reference's published Q6_K shape (an output head of 151936 x 2560, one activation row; reference
     CORE-CHANGES.md:73): repacked on the GPU from the file's blocks, run whole by the decode GEMV, and a seeded sample of
