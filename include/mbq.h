@@ -120,7 +120,8 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  * int8 linear): the kernel (MBQ_KERNEL_*), *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses
  * the per-device workspace below).
  *   MBQ_KERNEL_GEMV    M <= 4, bm = bn = splits = 0.
- *   MBQ_KERNEL_STREAM  weight-stream kernel, 5 <= M <= 64: bm = 16, bn = weight rows per block (64 or 128).
+ *   MBQ_KERNEL_STREAM  weight-stream kernel, 5 <= M <= 64: bm = 16, bn = weight rows per block (64 or 128); from
+ *                      17 rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
  *   MBQ_KERNEL_DIRECT  weight-direct kernel of large batches: 256x{256,192,128}, 128x{320,256,128}; splits = 1.
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges

@@ -838,7 +838,10 @@ static int choose(int t, const Args& a, Choice* c) {
         *c = Choice{K_TILES, g_force_bm.load(), g_force_bn.load(), std::max(1, g_force_s.load())};
         return 0;
     }
-    if (a.M <= WS_MAX_M) {
+    // 16 < M <= 64 over a weight whose 64-row tiles alone fill the CUs (the weight-stream kernel would run 128-row
+    // blocks): the LDS-tile kernel's 64 x 128 tiles are faster (MI355X, N = 17408, K = 5120, M = 64: int8 45 vs 52 us,
+    // Q8_0 59 vs 73, Q4_K 51 vs 57, Q6_K 54 vs 79; M = 16 keeps the weight stream, 41 vs 43 us int8)
+    if (a.M <= WS_MAX_M && !(a.M > 16 && (a.N + 63) / 64 >= cu_count())) {
         int nr = 0, S = 1;
         wsgemm_plan(t, a, &nr, &S);
         *c = Choice{K_STREAM, 16, nr, S};

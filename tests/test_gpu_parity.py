@@ -247,6 +247,22 @@ def test_gemv_rows_of_80_units_packed_four_to_an_item(t, n, cuda):
     assert np.all(np.isnan(bad))
 
 
+@pytest.mark.parametrize("t", GEMM_TYPES, ids=GEMM_IDS)
+@pytest.mark.parametrize("m", [16, 17, 64])
+def test_small_batches_over_tall_weights(t, m, cuda):
+    """17-64 activation rows over a weight of at least 64 rows per CU take the LDS-tile kernel's 64 x 128 tiles,
+    16 rows the weight stream; both give the exact product (a sample of 512 weight rows compared)"""
+    n = 64 * torch.cuda.get_device_properties(0).multi_processor_count + 37
+    k = 512 if t != "int8" else 272
+    tt = -8 if t == "int8" else t
+    kind, bm, bn, _ = LIB.gemm_plan(tt, m, n, k)
+    assert (kind, bm, bn) == ((LIB.KERNEL_STREAM, 16, 128) if m == 16 else (LIB.KERNEL_TILES, 64, 128))
+    rng = np.random.default_rng([m, n, 0 if t == "int8" else t])
+    run, ref = _direct_case(t, m, n, k, rng, cuda)
+    ns = np.sort(rng.choice(n, 512, replace=False))
+    assert_product(run()[:, ns], ref[:, ns], f"{t} m={m} n={n}")
+
+
 def test_q6_k_output_head_full_size_sampled(cuda):
     """the reference's published Q6_K shape (an output head of 151936 x 2560, one activation row; reference
     CORE-CHANGES.md:73): repacked on the GPU from the file's blocks, run whole by the decode GEMV, and a seeded sample of
