@@ -9,8 +9,9 @@
 //
 // Work split. A persistent grid; block b owns rows [b N / P, (b + 1) N / P). A row's U units (a unit: 16 bytes of quants
 // = 16 int8 values, or 32 K-quant values) are cut into S parts of PU units, at most 64 CH: one part of one row is
-// an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). S divides the
-// block's 8 waves, so wave w always takes part w % S (of rows w / S, w / S + 8 / S, ...): the x values its lanes
+// an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). Wave w always
+// takes part w % S (of rows j, j + n, j + 2 n, ... with j = w / S and n the number of waves of that part, 8 / S when S
+// divides 8): the x values its lanes
 // multiply are the same for every row and are held in registers for the whole kernel (read once from L2; no LDS in
 // the inner loop). Rows of few units (K = 2560: 80 units, a second chunk with 16 of 64 lanes busy) are packed R to an
 // item instead (S = 1, R in {2, 4}, R U a multiple of 64): R consecutive rows are one run of R U units in every plane,
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t sstride = (T == T_Q4_K || T == T_Q5_K) ? (uint32_t)(K >> 8) * 16u : (T == T_Q6_K) ? (uint32_t)(K >> 4) : (uint32_t)(K >> 5) * 2u;
 
     // this wave's part and its units
-    const int part = wave % S, rstep = GV_WAVES / S;
+    const int part = wave % S, rstep = (GV_WAVES - part + S - 1) / S;   // the waves that take this part
     const int u0 = part * PU, nu = max(0, min(PU, U - u0));
     const int lastc = max(0, (nu - 1) >> 6);                         // last chunk with a unit of the part
     const int nrows = r1 - r0, first = wave / S, ngroups = (nrows + R - 1) / R;
@@ -385,16 +386,26 @@ static int resident_blocks(Kern kernel, size_t lds) {
 
 // Parts per row: the fewest S in {1, 2, 4, 8} whose parts take at most GV_ITEM_CHUNKS chunks and fit the registers
 // (at M = 1: K <= 24576 int8 / Q8_0, 49152 Q4_K); PU rounded to the scale granularity (Q8_0 scales cover 2 units, Q4_K
-// meta 8). Returns the chunks the parts need, or -1.
+// meta 8). S = 3 instead when it raises the share of busy lanes by 20 points or more: its parts have 3, 3 and 2 waves,
+// so it wins only by filling chunks (MI355X, 5120 x 17408 Q4_K: 544 units as 3 parts of 3 chunks, 94 % busy, 13.6 us;
+// 4 parts, 71 % busy, 14.5 us; Q8_0 17408 x 5120 keeps S = 2: 17.3 us against 20.8 with S = 3). Returns the chunks
+// the parts need, or -1.
 template <int T, int M>
 static int gv_parts(int64_t U, int* S, int* PU) {
     const int64_t gran = kquant(T) ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
+    auto pu_of = [&](int s) { return ((U + s - 1) / s + gran - 1) / gran * gran; };
     for (int s = 1; s <= GV_WAVES; s *= 2) {
-        const int64_t pu = ((U + s - 1) / s + gran - 1) / gran * gran;
+        const int64_t pu = pu_of(s);
         if (pu <= cap) {
+            const int64_t ch = (pu + 63) / 64, pu3 = pu_of(3), ch3 = (pu3 + 63) / 64;
+            if (s > 3 && pu3 <= cap && 100 * U / (3 * 64 * ch3) >= 100 * U / (s * 64 * ch) + 20) {
+                *S = 3;
+                *PU = (int)pu3;
+                return (int)ch3;
+            }
             *S = s;
             *PU = (int)pu;
-            return (int)((pu + 63) / 64);
+            return (int)ch;
         }
     }
     return -1;

@@ -263,6 +263,21 @@ def test_small_batches_over_tall_weights(t, m, cuda):
     assert_product(run()[:, ns], ref[:, ns], f"{t} m={m} n={n}")
 
 
+@pytest.mark.parametrize("t", KQUANT, ids=NAME.get)
+@pytest.mark.parametrize("n", [1, 7, 300])
+def test_gemv_rows_in_three_parts(t, n, cuda):
+    """K = 17408 (544 units) at one activation row cuts a row into 3 parts of 184, 184 and 176 units, taken by 3, 3
+    and 2 of a block's 8 waves; the block adds the parts through LDS"""
+    rng = np.random.default_rng([t, n, 17408])
+    k = 17408
+    raw = G.RAW[t](rng, n, k)
+    xb = G.acts(rng, 1, k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    y = KQ.matmul(_bf16_tensor(xb, cuda), planes).cpu().numpy()
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    assert_product(y, ref, f"{NAME[t]} n={n}")
+
+
 def test_q6_k_output_head_full_size_sampled(cuda):
     """the reference's published Q6_K shape (an output head of 151936 x 2560, one activation row; reference
     CORE-CHANGES.md:73): repacked on the GPU from the file's blocks, run whole by the decode GEMV, and a seeded sample of
