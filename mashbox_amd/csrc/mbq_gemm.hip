@@ -204,8 +204,9 @@ struct GemmArgs {
 // Pipeline of depth P (1 or 3): x is DMA'd P steps ahead into P + 1 LDS stages, weight units are loaded into P + 1
 // register buffers P + 1 steps ahead, and the unit of step l + 1 is dequantized into one of 2 LDS weight stages during
 // step l. With split-K (S > 1) the blocks of one tile each run a contiguous range of K steps; each writes its float32
-// partial tile to the workspace, and the block that arrives last (an atomic counter per tile, reset by that block) adds
-// the S partials in split order, so the result does not depend on which block finishes last.
+// partial tile to the workspace with device-coherent stores, and the block that arrives last (an atomic counter per
+// tile, reset by that block) adds the S partials in split order with device-coherent loads, so the result does not
+// depend on which block finishes last.
 template <int T, int BM, int BN, int P, bool KFULL>
 __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kernel(const GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint16_t gemm_lds[];   // [A stage 0 .. P][B stage 0][B stage 1]
@@ -353,33 +354,39 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 
     // epilogue: lane holds column n = lane & 15 and rows 4 * (lane >> 4) + r of each 16 x 16 tile
     if (g.S > 1) {
-        // this split's partial tile, in the lanes' own layout
-        f32x4_t* slot = reinterpret_cast<f32x4_t*>(g.ws) + (int64_t)(tile * g.S + kz) * (BM * BN / 4);
+        // this split's partial tile, in the lanes' own layout, stored and read with sc1 (device-coherent) buffer
+        // accesses: written through the XCD's L2, so the block that arrives last reads every split's partial without an
+        // L2-wide fence (__threadfence writes back and invalidates the whole L2 on gfx950)
+        const rsrc_t pr = make_rsrc(g.ws, (uint32_t)WS_BYTES);
+        constexpr uint32_t E = (uint32_t)BM * BN * 4u;                  // bytes of one partial tile
+        const uint32_t lofs = (uint32_t)((wave * TI * TJ) * 64 + lane) * 16u;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) slot[((wave * TI + i) * TJ + j) * 64 + lane] = acc[i][j];
-        __threadfence();
+            for (int j = 0; j < TJ; ++j)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr, lofs + (uint32_t)((i * TJ + j) * 64) * 16u,
+                                                       (uint32_t)(tile * g.S + kz) * E, 16);
+        wait_vm<0>();                                                 // the partial is in device-coherent memory
         __syncthreads();
         int* flag = reinterpret_cast<int*>(gemm_lds);
         if (tid == 0) {
-            const int old = atomicAdd(g.cnt + tile, 1);
+            const int old = __hip_atomic_fetch_add(g.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *flag = old == g.S - 1;
-            if (old == g.S - 1) g.cnt[tile] = 0;         // every split has arrived: ready for the next launch
+            if (old == g.S - 1) __hip_atomic_store(g.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next launch
         }
         __syncthreads();
         if (!*flag) return;
-        __threadfence();
-        const f32x4_t* first = reinterpret_cast<const f32x4_t*>(g.ws) + (int64_t)tile * g.S * (BM * BN / 4);
+        const uint32_t first = (uint32_t)(tile * g.S) * E;
+        for (int z = 0; z < g.S; ++z) {                               // split order: the same sum whoever is last
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const int e = ((wave * TI + i) * TJ + j) * 64 + lane;
-                f32x4_t v = first[e];
-                for (int z = 1; z < g.S; ++z) v += first[(int64_t)z * (BM * BN / 4) + e];
-                acc[i][j] = v;
-            }
+                for (int j = 0; j < TJ; ++j) {
+                    const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                          pr, lofs + (uint32_t)((i * TJ + j) * 64) * 16u, first + (uint32_t)z * E, 16));
+                    acc[i][j] = z == 0 ? v : acc[i][j] + v;
+                }
+        }
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -779,6 +786,25 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
                 if (ct > cus) continue;
                 const double t = T1_US[i] * KT;
                 if (t < bt) bt = t, best = Plan{i, 1, (int)KT};
+            }
+        }
+    }
+    // Small tiles (at most 8192 outputs) that leave CUs idle split K until about two blocks run per CU, at most 4
+    // ranges of at least 4 steps (MI355X, Q4_K: 96 x 5120 x 17408 64 x 64 tiles 107 -> 64 us with 3 ranges; 512 x 1024
+    // x 5120 33 -> 20 us with 4; 64 x 17408 x 5120 64 x 128 tiles 51 -> 38 us with 3; 2048 x 1024 x 5120 128 x 64 tiles
+    // -6 % with 2). Larger tiles keep one range: their partial tiles cost more than the split saves (64 x 192 and
+    // 128 x 192 tiles 15-20 % slower with 2 ranges).
+    {
+        const int bm = CANDS<T>[best.idx].bm, bn = CANDS<T>[best.idx].bn;
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        if (bm * bn <= 8192 && tiles <= cus && tiles <= WS_TILES) {
+            int64_t S = std::min<int64_t>({4, 2 * (int64_t)cus / tiles, KT / 4});
+            S = std::min<int64_t>(S, (int64_t)(WS_BYTES / ((size_t)tiles * bm * bn * 4)));
+            if (S >= 2) {
+                const int64_t kts = (KT + S - 1) / S;
+                best = Plan{best.idx, (int)((KT + kts - 1) / kts), (int)kts};
+            } else {
+                best = Plan{best.idx, 1, (int)KT};
             }
         }
     }
