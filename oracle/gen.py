@@ -33,6 +33,15 @@ def q8_0_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
     return np.concatenate([d, q], axis=-1).reshape(n, nb * 34)
 
 
+def q4_0_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
+    """(n, row_bytes) uint8 Q4_0 blocks: d fp16 ~ U(lo, hi); 4-bit quants uniform in [0, 15], two per byte (value i in
+    the low nibble of byte i, value 16 + i in its high nibble; src/mashbox/ops/reference.py:66-70)"""
+    nb = k // 32
+    d = rng.uniform(lo, hi, (n, nb)).astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    q = rng.integers(0, 16, (n, nb, 2, 16), dtype=np.uint8)
+    return np.concatenate([d, q[:, :, 0] | (q[:, :, 1] << 4)], axis=-1).reshape(n, nb * 18)
+
+
 def q4_k_raw(rng, n: int, k: int, lo=1e-3, hi=1e-2) -> np.ndarray:
     """(n, row_bytes) uint8 Q4_K super-blocks: d, dmin fp16 ~ U(lo, hi); 8 six-bit scales and mins uniform in
     [0, 63]; 4-bit quants uniform in [0, 15] (packed two per byte as the Q4_K layout holds them)"""
@@ -83,7 +92,7 @@ def int8_weights(rng, n: int, k: int, lo=1e-3, hi=1e-2):
     return q, s
 
 
-RAW = {R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw, R.Q5_K: q5_k_raw, R.Q6_K: q6_k_raw}
+RAW = {R.Q4_0: q4_0_raw, R.Q8_0: q8_0_raw, R.Q4_K: q4_k_raw, R.Q5_K: q5_k_raw, R.Q6_K: q6_k_raw}
 
 
 def config(idx: int, seed: int = 0, scale: float = 1.0):

@@ -9,6 +9,7 @@ It restates, from scratch in NumPy, what the reference computes (reference = /ro
   ggml type table, row bytes        src/mashbox/ops/reference.py:22-29, 390-395
   little-endian fp16 -> f32         src/mashbox/ops/reference.py:37-51   (_u16le, _f16)
   nibble split                      src/mashbox/ops/reference.py:58-60   (_nib)
+  Q4_0 block                        src/mashbox/ops/reference.py:66-70   (_q4_0)
   Q8_0 block                        src/mashbox/ops/reference.py:101-103 (_q8_0)
   6-bit scale/min unpack            src/mashbox/ops/reference.py:132-139 (_scale_min_k4)
   Q4_K super-block                  src/mashbox/ops/reference.py:142-149 (_q4_k)
@@ -28,6 +29,9 @@ algorithm is the one restated by the reference file above, and that is what this
 How each function is pinned (tests/test_oracle.py):
   f16_to_f32      every one of the 65,536 fp16 bit patterns against an independent decoder built from the IEEE-754
                   binary16 definition (sign, exponent, fraction; subnormals; inf; NaN).
+  dequant Q4_0    closed form: v = d * (q - 8) is exact in float32 (at most 11 + 4 significant bits), checked against
+                  `fractions` on every code at several d; the nibble order against a per-index restatement of llama.cpp's
+                  scalar loop (dequantize_row_q4_0) on random blocks; all-zero / all-0xFF blocks, zero signs included.
   dequant Q8_0    closed form: v = q * d is exact in float32 for every finite fp16 d and int8 q (<= 19 significant bits),
                   checked against Python `fractions` arithmetic on a brute-force grid; all-zero / all-0xFF blocks.
   dequant Q4_K    closed form: v = RN_f32(d*sc*q - dmin*m) with a single rounding, checked against exact `fractions`
@@ -55,9 +59,10 @@ from __future__ import annotations
 import numpy as np
 
 # ggml type id -> (name, values per block, bytes per block) for the types on this path
-# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these four)
-TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+# (src/mashbox/ops/reference.py:22-29 lists every ggml type; the kernel path covers these five, the types the
+# reference's own kernel package gives planes: src/mashbox/ops/bundle.py:39)
+TYPES = {2: ("Q4_0", 32, 18), 8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
 QK_K = 256
 EXACT_CHUNK = 1 << 24          # src/mashbox/ops/__init__.py:555
 
@@ -100,6 +105,16 @@ def as_bf16(x: np.ndarray) -> np.ndarray:
 def nib(qs: np.ndarray) -> np.ndarray:
     """(..., n) bytes -> (..., 2, n): low nibbles, then high nibbles (src/mashbox/ops/reference.py:58-60)"""
     return np.stack([qs & np.uint8(0x0F), qs >> np.uint8(4)], axis=-2)
+
+
+def q4_0_blocks(b: np.ndarray) -> np.ndarray:
+    """(N, 18) blocks -> (N, 32) float32: d * f32(q - 8), q = low nibbles of bytes 2-17 (values 0-15) then their high
+    nibbles (values 16-31) (src/mashbox/ops/reference.py:66-70)"""
+    n = b.shape[0]
+    d = f16_to_f32(b[:, :2])                                  # (N, 1)
+    q = nib(b[:, 2:]).reshape(n, 32).astype(np.int8) - np.int8(8)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return d * q.astype(np.float32)
 
 
 def q8_0_blocks(b: np.ndarray) -> np.ndarray:
@@ -175,7 +190,7 @@ def q6_k_blocks(b: np.ndarray) -> np.ndarray:
         return (ds * q).reshape(n, QK_K)
 
 
-BLOCKS = {Q8_0: q8_0_blocks, Q4_K: q4_k_blocks, Q5_K: q5_k_blocks, Q6_K: q6_k_blocks}
+BLOCKS = {Q4_0: q4_0_blocks, Q8_0: q8_0_blocks, Q4_K: q4_k_blocks, Q5_K: q5_k_blocks, Q6_K: q6_k_blocks}
 
 
 def dequant(raw: np.ndarray, t: int, cols: int) -> np.ndarray:

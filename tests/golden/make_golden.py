@@ -35,8 +35,8 @@ KQUANT = [("qwen3-kquant", ["blk.0.attn_k.weight", "blk.0.ffn_gate.weight", "blk
 
 
 def main(ref_root):
-    names = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
-    for t in (R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K):
+    names = {R.Q4_0: "Q4_0", R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
+    for t in (R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K):
         for kb in (1, 2, 16):
             rng = np.random.default_rng(7000 + 10 * t + kb)
             cols = R.TYPES[t][1] * kb

@@ -9,6 +9,8 @@ Each check compares the oracle with something independent of its own formula, ch
     ggml-quants.c (get_scale_min_k4, dequantize_row_q4_K; the published algorithm gguf-py 0.19.0 restates in vector
     form and reference src/mashbox/ops/reference.py:132-149 follows) on random bytes (a nibble order, a sub-block
     grouping or a scale/min swap fails);
+  - Q4_0: the scalar loop of llama.cpp's dequantize_row_q4_0 per index and the exact closed form over every code (a
+    nibble-half swap or a dropped -8 fails), edge blocks;
   - Q5_K: the scalar loop of llama.cpp's dequantize_row_q5_K per index, in exact rationals rounded once (a high bit
     taken from the wrong qh bit or nibble half fails), random and edge blocks, real llama-quantize Q5_K blocks;
   - Q6_K: the scalar loop of llama.cpp's dequantize_row_q6_K per index, in exact rationals rounded once (a swapped
@@ -207,6 +209,46 @@ def test_q4_k_edge_blocks():
     assert np.array_equal(v[2], want.astype(np.float32))
 
 
+# ------------------------------------------------------------------------------------------------------------- Q4_0
+def ggml_q4_0_row(block: bytes):
+    """llama.cpp dequantize_row_q4_0 for one block (fp16 d, qs[16]), per index; an exact zero takes the sign float32
+    x0 * d gives it"""
+    d = f16_from_definition(block[0] | block[1] << 8)
+    y = [None] * 32
+    for j in range(16):
+        x0, x1 = (block[2 + j] & 0x0F) - 8, (block[2 + j] >> 4) - 8
+        for idx, xv in ((j, x0), (j + 16, x1)):
+            with np.errstate(all="ignore"):
+                zero = np.float32(xv) * np.float32(d)
+            y[idx] = f32_round(Fraction(d) * xv, zero)
+    return np.array(y, np.float32)
+
+
+def test_q4_0_matches_the_scalar_loop_on_random_blocks():
+    rng = np.random.default_rng(16)
+    raw = rng.integers(0, 256, (40, 18), dtype=np.uint8)
+    d = rng.choice(np.array([2.0 ** -24, 3e-5, 1e-3, 0.5, 7.0, 65504.0, -2.5, 0.0, -0.0], np.float16), 40)
+    raw[:, 0:2] = d.view(np.uint8).reshape(40, 2)
+    got = R.dequant(raw, R.Q4_0, 32)
+    for i in range(raw.shape[0]):
+        assert diff_bits(got[i], ggml_q4_0_row(bytes(raw[i]))) == 0, i
+
+
+def test_q4_0_closed_form_and_edge_blocks():
+    for dv in (np.float16(65504.0), np.float16(-1.0009765625), np.float16(2.0 ** -24), np.float16(-0.0999)):
+        raw = np.zeros((16, 18), np.uint8)
+        raw[:, 0:2] = np.array([dv], np.float16).view(np.uint8)
+        raw[:, 2:] = (np.arange(16, dtype=np.uint8) * 17)[:, None]        # code c in both nibbles of every byte
+        v = R.dequant(raw, R.Q4_0, 32)
+        for c in range(16):
+            assert np.all(v[c] == np.float32(Fraction(float(dv)) * (c - 8)))
+        assert np.all(np.signbit(v[8]) == np.signbit(np.float32(dv)))    # d * (+0) keeps the sign of d
+    raw = np.zeros((2, 18), np.uint8)
+    raw[1] = 0xFF
+    v = R.dequant(raw, R.Q4_0, 32)
+    assert np.all(v[0] == 0) and np.all(np.isnan(v[1]))
+
+
 # ------------------------------------------------------------------------------------------------------------- Q5_K
 def ggml_q5_k_row(block: bytes):
     """llama.cpp dequantize_row_q5_K for one super-block (d, dmin, scales[12], qh[32], qs[128]), per index, in exact
@@ -366,7 +408,7 @@ def test_exact_chunk_rows_is_the_largest_fitting_divisor():
         assert R.exact_chunk_rows(r, c) == want
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_exact_product_meets_the_float32_bars(t):
     """reference tests/contracts/test_ops.py:19-35: NMSE <= 1e-8 and |y - ref| <= gamma_K (|x| @ |W|.T)"""
     rng = np.random.default_rng(20 + t)
