@@ -30,6 +30,7 @@ extern "C" {
 
 /* ggml type ids on this path (reference src/mashbox/ops/reference.py:22-29); MBQ_INT8 is not a ggml type: it names the
  * int8 per-output-channel weights of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 */
+#define MBQ_Q4_0 2
 #define MBQ_Q8_0 8
 #define MBQ_Q4_K 12
 #define MBQ_Q5_K 13
@@ -50,7 +51,8 @@ int mbq_version(void);
 /* Message of the calling thread's last failure ("" if none). The pointer stays valid until the thread's next call. */
 const char* mbq_last_error(void);
 
-/* 1 if type t is a ggml type with kernel planes here (Q8_0, Q4_K, Q5_K, Q6_K), else 0.
+/* 1 if type t is a ggml type with kernel planes here (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K: the types of reference
+ * src/mashbox/ops/bundle.py:39), else 0.
  * Replaces the membership test `t in mod.TYPES` (reference src/mashbox/ops/__init__.py:21,303). */
 int mbq_has_type(int t);
 

@@ -8,7 +8,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("MBQ_LIB", os.path.join(HERE, "libmbq.so"))
 
-Q8_0, Q4_K, Q5_K, Q6_K, INT8 = 8, 12, 13, 14, -8
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, INT8 = 2, 8, 12, 13, 14, -8
 OUT_F32, OUT_BF16 = 0, 1
 
 # every symbol include/mbq.h declares, with its ctypes signature

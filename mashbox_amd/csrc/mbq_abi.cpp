@@ -27,13 +27,13 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
-static bool is_type(int t) { return t == T_Q8_0 || kquant(t); }
+static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_0 || kquant(t); }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // shape rules shared by every entry point of a ggml type
 static int check_shape(int t, int64_t rows, int64_t cols) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14)", t);
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14)", t);
     if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
     if (cols % block_values(t))
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
@@ -130,6 +130,23 @@ static void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                 memcpy(d + b * 2, row + b * bb, 2);
                 memcpy(q + b * 32, row + b * bb + 2, 32);
             }
+        } else if (t == T_Q4_0) {
+            // reference src/mashbox/ops/reference.py:66-70: value i (i < 16) is the low nibble of qs[i], value 16 + i
+            // its high nibble (qs at byte 2)
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(d + b * 2, src, 2);
+                uint32_t unit[4] = {0, 0, 0, 0};
+                for (int i = 0; i < 32; ++i) {
+                    const uint32_t v = (src[2 + (i & 15)] >> (4 * (i >> 4))) & 15u;
+                    int dw, bit;
+                    q4k_slot(i, &dw, &bit);
+                    unit[dw] |= v << bit;
+                }
+                memcpy(q + b * 16, unit, 16);  // little-endian host, as the GPU
+            }
         } else {
             uint8_t* q = planes + L.qs_off + n * (K / 2);
             uint8_t* meta = planes + L.sc_off + n * nb * 16;
@@ -206,6 +223,21 @@ static void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
             for (int64_t b = 0; b < nb; ++b) {
                 memcpy(row + b * bb, d + b * 2, 2);
                 memcpy(row + b * bb + 2, q + b * 32, 32);
+            }
+        } else if (t == T_Q4_0) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, d + b * 2, 2);
+                memset(dst + 2, 0, 16);
+                uint32_t unit[4];
+                memcpy(unit, q + b * 16, 16);
+                for (int i = 0; i < 32; ++i) {
+                    int dw, bit;
+                    q4k_slot(i, &dw, &bit);
+                    dst[2 + (i & 15)] |= (uint8_t)(((unit[dw] >> bit) & 15u) << (4 * (i >> 4)));
+                }
             }
         } else {
             const uint8_t* q = planes + L.qs_off + n * (K / 2);

@@ -1,8 +1,8 @@
 // gfx950 MFMA GEMM of the quantized linear for the prefill / batched-decode regime (many activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K),
-// :150-159 (Q5_K) and :164-173 (Q6_K),
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0),
+// :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K),
 // and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // Block tile BM x 256 (activation rows x weight rows), K step 64, 512 threads = 8 waves in a 2 x 4 grid; each wave owns a
@@ -10,15 +10,17 @@
 // Per K step every thread
 //   - copies ACH 16-byte chunks of the x tile (bfloat16) into LDS,
 //   - dequantizes one 32-value weight unit into LDS as bfloat16 (Q4_K: a sub-block, 16 bytes of nibbles + the
-//     super-block's scales; Q6_K: 16 bytes of low nibbles, 8 of high bits, 2 sub-block scales and the super-block
-//     scale; Q8_0 / int8: 32 bytes of quants); each value is the float32 dequantization (d*sc)*q - dmin*m,
-//     (d*sc)*(q - 32) resp. q*d rounded to nearest even (int8 values are exact),
+//     super-block's scales; Q4_0: a block, 16 bytes of nibbles and its scale; Q6_K: 16 bytes of low nibbles, 8 of high
+//     bits, 2 sub-block scales and the super-block scale; Q8_0 / int8: 32 bytes of quants); each value is the float32
+//     dequantization (d*sc)*q - dmin*m, d*(q - 8), (d*sc)*(q - 32) resp. q*d rounded to nearest even (int8 values are
+//     exact),
 //   - runs 2 K-substeps of MFMAs on the tiles of the step before, from the other LDS stage.
 // Pipeline: the raw bytes of step k+2 are loaded into registers at the top of step k, the raw bytes of step k+1 (loaded
 // one step earlier) are dequantized into LDS stage (k+1)&1 in slices placed between the MFMAs of step k, so global
 // latency hides behind a whole step and the VALU dequant behind the matrix work; one barrier per step. The main loop is
 // branch free: loads past the last row or step are clamped to valid addresses (they only feed outputs that are never
-// stored, or an LDS stage nobody reads); only a K that is not a multiple of 64 (Q8_0, int8) zeroes the x chunks past K.
+// stored, or an LDS stage nobody reads); only a K that is not a multiple of 64 (Q4_0, Q8_0, int8) zeroes the x chunks
+// past K.
 // LDS rows are 64 bfloat16 (8 chunks of 16 bytes) with chunk c stored at c ^ (row & 7), so the 16-byte MFMA operand
 // reads of 8 consecutive rows hit distinct banks. Tiles are mapped to blocks XCD by XCD (blocks are dealt to the 8 XCDs
 // round robin), so the blocks that share an x row-panel run on one XCD at once and share its L2.
@@ -49,6 +51,7 @@ __device__ __forceinline__ void dma16(rsrc_t r, uint16_t* lds_wave, uint32_t vof
 // the raw bytes of one weight unit (32 values of one row), as loaded from the planes
 template <int T> struct BUnit;
 template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
+template <> struct BUnit<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
@@ -66,11 +69,12 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     else if constexpr (T == T_Q5_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
+    else if constexpr (T == T_Q4_0) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
     else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
 }
 
-// loads unit u of the K step at k0; with KFULL false, a Q8_0 unit past K gets scale 0 (its quants may be any bytes;
-// the x they meet is zero)
+// loads unit u of the K step at k0; with KFULL false, a Q4_0 / Q8_0 unit past K gets scale 0 (its quants may be any
+// bytes; the x they meet is zero)
 template <int T, bool KFULL>
 __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int K, int k0, int u) {
     if constexpr (T == T_Q6_K) {
@@ -82,6 +86,10 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
         if constexpr (T == T_Q5_K) b.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, o.h, (uint32_t)k0 >> 3, 0);
+    } else if constexpr (T == T_Q4_0) {
+        b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
+        b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
+        if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
     } else {
         b.q0 = bload16(r, o.q, (uint32_t)k0);
         b.q1 = bload16(r, o.q + 16, (uint32_t)k0);
@@ -108,7 +116,8 @@ __device__ __forceinline__ void i8x4(uint32_t w, float d, float d128, uint32_t* 
 }
 
 // per-unit dequant constants
-struct BScale { float a, b, c, e; };   // Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q8_0: d, 128 d; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+// Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q4_0: d, 8 d, d/16; Q8_0: d, 128 d; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+struct BScale { float a, b, c, e; };
 
 template <int T>
 __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
@@ -125,6 +134,10 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
         s.b = f16f(b.meta[0] >> 16) * (float)mn;             // exact
         s.c = s.a * 0.0625f;                                 // exact: a power-of-two scale
+    } else if constexpr (T == T_Q4_0) {
+        s.a = f16f(b.d);
+        s.b = 8.f * s.a;                                     // q d - 8 d = (q - 8) d, exact in float32
+        s.c = s.a * 0.0625f;
     } else if constexpr (T == T_Q8_0) {
         s.a = f16f(b.d);
         s.b = 128.f * s.a;
@@ -159,7 +172,7 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         o[1] = pack_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(lo >> 24), s.a, -s.b));
         o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((hi >> 8) & 0xFFu), s.a, -s.b));
         o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(hi >> 24), s.a, -s.b));
-    } else if constexpr (T == T_Q4_K) {
+    } else if constexpr (nib4(T)) {
         // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h)
         const uint32_t w = sel4(b.q, t);
         const uint32_t m0 = opaque(w & 0x000F000Fu), m1 = opaque(w & 0x00F000F0u);
@@ -916,6 +929,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
     Plan p;
     int rc;
     switch (t) {
+        case T_Q4_0: rc = pick<T_Q4_0>(a, &p); if (!rc) *bm = CANDS<T_Q4_0>[p.idx].bm, *bn = CANDS<T_Q4_0>[p.idx].bn; break;
         case T_Q8_0: rc = pick<T_Q8_0>(a, &p); if (!rc) *bm = CANDS<T_Q8_0>[p.idx].bm, *bn = CANDS<T_Q8_0>[p.idx].bn; break;
         case T_Q4_K: rc = pick<T_Q4_K>(a, &p); if (!rc) *bm = CANDS<T_Q4_K>[p.idx].bm, *bn = CANDS<T_Q4_K>[p.idx].bn; break;
         case T_Q5_K: rc = pick<T_Q5_K>(a, &p); if (!rc) *bm = CANDS<T_Q5_K>[p.idx].bm, *bn = CANDS<T_Q5_K>[p.idx].bn; break;
@@ -953,6 +967,7 @@ int force_gemm_plan(int kernel, int bm, int bn, int splits) {
 
 int launch_gemm(int t, const Args& a, hipStream_t s) {
     switch (t) {
+        case T_Q4_0: return launch_gemm_t<T_Q4_0>(a, s);
         case T_Q8_0: return launch_gemm_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemm_t<T_Q4_K>(a, s);
         case T_Q5_K: return launch_gemm_t<T_Q5_K>(a, s);

@@ -1,14 +1,14 @@
 // gfx950 decode GEMV of the quantized linear (M <= GEMV_MAX_M activation rows).
 //
 // y (M, N) = x (M, K) @ W.T with float32 accumulation: reference src/mashbox/ops/__init__.py:594-632 (qmatmul) on the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), and
-// the int8 per-channel
+// weights of reference src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and
+// :164-173 (Q6_K), and the int8 per-channel
 // linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (dot, then * s). Plane layouts: mbq_layout.h.
 //
 // HBM-bound: every weight byte is read once, 16 bytes per lane, each wave-wide load 1 KiB of one row (non-temporal).
 //
 // Work split. A persistent grid; block b owns rows [b N / P, (b + 1) N / P). A row's U units (a unit: 16 bytes of quants
-// = 16 int8 values, or 32 K-quant values) are cut into S parts of PU units, at most 64 CH: one part of one row is
+// = 16 int8 values, or 32 Q4_0 / K-quant values) are cut into S parts of PU units, at most 64 CH: one part of one row is
 // an item of CH chunks, one chunk = one 16-byte load per lane (lane l takes unit 64 i + l of the part). Wave w always
 // takes part w % S (of rows j, j + n, j + 2 n, ... with j = w / S and n the number of waves of that part, 8 / S when S
 // divides 8): the x values its lanes
@@ -27,6 +27,7 @@
 //   Q4_K          ((w >> 4p) & 0x000F000F) | 0x43004300 is the bfloat16 pair (128 + q, 128 + q'); per unit
 //                 y += (d sc) * sum(x (128 + q)) - (128 d sc + dmin m) * sum(x); the per-unit sums of x are computed
 //                 once per wave from its x registers.
+//   Q4_0          the Q4_K pairs; per unit (one block) y += d * sum(x (128 + q)) - 136 d * sum(x).
 //   Q5_K          q5k_bytes (a rotate and a bit-field insert per four values) then one byte permute per pair make
 //                 (128 + q, 128 + q'); per unit the Q4_K sum.
 //   Q6_K          an AND, an AND-OR and at most one shift per four values leave the 6-bit quants as bytes
@@ -52,11 +53,11 @@ constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_ROWS_2BPC = 16;
 constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
 
-template <int T> constexpr int gv_uw() { return kquant(T) ? 32 : 16; }   // values per 16-byte unit
+template <int T> constexpr int gv_uw() { return unit32(T) ? 32 : 16; }   // values per 16-byte unit
 template <int T> constexpr int gv_tpu() { return gv_uw<T>() / 8; }            // 16-byte x chunks per unit
 // chunks per item that the registers hold (x of M rows for CH chunks, and two items' loads in flight)
 template <int T> constexpr int gv_chmax(int M) {
-    return kquant(T) ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
+    return unit32(T) ? (M == 1 ? 5 : M == 2 ? 2 : 1) : T == T_Q8_0 ? (M == 1 ? 5 : M == 2 ? 3 : 2) : (M == 1 ? 6 : M == 2 ? 4 : M == 3 ? 3 : 2);
 }
 
 struct GvArgs {
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
     const uint32_t vd = (uint32_t)(lane >> 1) * 2u, vd_last = lane_in ? vd : OOB_VOFF;
     const uint32_t vm = (uint32_t)(lane >> 3) * 16u, vm_last = lane_in ? vm : OOB_VOFF;
     const uint32_t vh = (uint32_t)lane * 8u, vh_last = lane_in ? vh : OOB_VOFF;          // Q6_K high bits
-    const uint32_t vs = (uint32_t)lane * 2u, vs_last = lane_in ? vs : OOB_VOFF;          // Q6_K scale pairs
+    const uint32_t vs = (uint32_t)lane * 2u, vs_last = lane_in ? vs : OOB_VOFF;          // Q6_K scale pairs, Q4_0 scales
     const uint32_t vd6 = (uint32_t)(lane >> 3) * 2u, vd6_last = lane_in ? vd6 : OOB_VOFF;  // Q6_K super-block scales
     const uint32_t vh5 = (uint32_t)lane * 4u, vh5_last = lane_in ? vh5 : OOB_VOFF;        // Q5_K high bits
     auto load = [&](Raw& W, int k) {                                  // the k-th item of the wave (clamped)
@@ -134,6 +135,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
             };
             W.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off(vq, vq_last), qs + 1024u * c, 2));
             if constexpr (T == T_Q8_0) W.d[i] = bload2(wr, off(vd, vd_last), ss + (uint32_t)u0 + 64u * c);
+            if constexpr (T == T_Q4_0) W.d[i] = bload2(wr, off(vs, vs_last), ss + (uint32_t)u0 * 2u + 128u * c);
             if constexpr (T == T_Q4_K || T == T_Q5_K) W.meta[i] = bload16(wr, off(vm, vm_last), ss + (uint32_t)u0 * 2u + 128u * c);
             if constexpr (T == T_Q5_K)
                 W.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 #pragma unroll
             for (int t = 0; t < TPU; ++t) {
                 xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
-                if constexpr (kquant(T)) {
+                if constexpr (unit32(T)) {
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         if (T == T_Q6_K && t >= 2) sum2 = dot2(xv[i][m][t][p], BF16_ONES, sum2);
@@ -249,12 +251,18 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
                 }
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(dsc, P0[m] + P1[m], __builtin_fmaf(-c, xs[i][m], acc[m]));
-            } else if constexpr (T == T_Q4_K) {
-                uint32_t sc, mn;
-                q4k_scale_min_sel(W.meta[i][1], W.meta[i][2], W.meta[i][3], sel, &sc, &mn);
-                float dsc = f16f(W.meta[i][0]) * (float)sc;             // exact
-                const float dm = f16f(W.meta[i][0] >> 16) * (float)mn;  // exact
-                float c = 128.f * dsc + dm;
+            } else if constexpr (nib4(T)) {
+                float dsc, c;
+                if constexpr (T == T_Q4_0) {
+                    dsc = f16f(W.d[i]);
+                    c = 136.f * dsc;                                    // (128 + q) d - 136 d = (q - 8) d
+                } else {
+                    uint32_t sc, mn;
+                    q4k_scale_min_sel(W.meta[i][1], W.meta[i][2], W.meta[i][3], sel, &sc, &mn);
+                    dsc = f16f(W.meta[i][0]) * (float)sc;               // exact
+                    const float dm = f16f(W.meta[i][0] >> 16) * (float)mn;  // exact
+                    c = 128.f * dsc + dm;
+                }
                 if constexpr (!FULL) {
                     dsc = act ? dsc : 0.f;
                     c = act ? c : 0.f;
@@ -385,14 +393,14 @@ static int resident_blocks(Kern kernel, size_t lds) {
 }
 
 // Parts per row: the fewest S in {1, 2, 4, 8} whose parts take at most GV_ITEM_CHUNKS chunks and fit the registers
-// (at M = 1: K <= 24576 int8 / Q8_0, 49152 Q4_K); PU rounded to the scale granularity (Q8_0 scales cover 2 units, Q4_K
-// meta 8). S = 3 instead when it raises the share of busy lanes by 20 points or more: its parts have 3, 3 and 2 waves,
+// (at M = 1: K <= 24576 int8 / Q8_0, 49152 Q4_0 / K-quants); PU rounded to the scale granularity (Q8_0 scales cover
+// 2 units, Q4_K meta 8, Q4_0 scales 1). S = 3 instead when it raises the share of busy lanes by 20 points or more: its parts have 3, 3 and 2 waves,
 // so it wins only by filling chunks (MI355X, 5120 x 17408 Q4_K: 544 units as 3 parts of 3 chunks, 94 % busy, 13.6 us;
 // 4 parts, 71 % busy, 14.5 us; Q8_0 17408 x 5120 keeps S = 2: 17.3 us against 20.8 with S = 3). Returns the chunks
 // the parts need, or -1.
 template <int T, int M>
 static int gv_parts(int64_t U, int* S, int* PU) {
-    const int64_t gran = kquant(T) ? 8 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
+    const int64_t gran = kquant(T) ? 8 : T == T_Q4_0 ? 1 : 2, cap = 64 * std::min(GV_ITEM_CHUNKS, gv_chmax<T>(M));
     auto pu_of = [&](int s) { return ((U + s - 1) / s + gran - 1) / gran * gran; };
     for (int s = 1; s <= GV_WAVES; s *= 2) {
         const int64_t pu = pu_of(s);
@@ -477,6 +485,7 @@ static int launch_gemv_t(const Args& a, hipStream_t s) {
 
 int launch_gemv(int t, const Args& a, hipStream_t s) {
     switch (t) {
+        case T_Q4_0: return launch_gemv_t<T_Q4_0>(a, s);
         case T_Q8_0: return launch_gemv_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_gemv_t<T_Q4_K>(a, s);
         case T_Q5_K: return launch_gemv_t<T_Q5_K>(a, s);

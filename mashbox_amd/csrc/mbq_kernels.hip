@@ -2,9 +2,8 @@
 // mbq_gemv.hip; weight-stream GEMM: mbq_wsgemm.hip; LDS-tile MFMA GEMM: mbq_gemm.hip).
 //
 // Semantics follow reference src/mashbox/ops/__init__.py:594-632 (qmatmul: x @ W.T, float32 accumulation) with the
-// weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), and the
-// int8 per-channel
-// linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82. Plane layouts: mbq_layout.h.
+// weights of reference src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and
+// :164-173 (Q6_K), and the int8 per-channel linear of reference src/mashbox/models/qwen3_8_27b/model.py:72-82. Plane layouts: mbq_layout.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -18,14 +17,15 @@ namespace mbq {
 
 
 // ------------------------------------------------------------------------------------------------------- dequant
-// One thread per 16-byte unit (K-quants: 32 values; Q8_0: half a block, 16 values). Bit for bit the reference
-// dequantization: Q8_0 v = f32(q) * d, Q4_K and Q5_K v = (d*sc)*q - dmin*m and Q6_K v = (d*sc)*(q - 32), whose products are
-// exact in float32 (Q6_K keeps the reference's order of the two products, which fixes the sign of a zero).
+// One thread per 16-byte unit (K-quants and Q4_0: 32 values; Q8_0: half a block, 16 values). Bit for bit the reference
+// dequantization: Q8_0 v = f32(q) * d, Q4_0 v = d * f32(q - 8), Q4_K and Q5_K v = (d*sc)*q - dmin*m and
+// Q6_K v = (d*sc)*(q - 32), whose products are exact in float32 (Q4_0 and Q6_K keep the reference's order of the
+// operands, which fixes the sign of a zero).
 template <int T>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base, int64_t stride,
                                                       const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
                                                       int64_t hi_off, int64_t d_off, int N, int K, float* __restrict__ w) {
-    const int64_t uw = (T == T_Q8_0) ? 16 : 32;
+    const int64_t uw = unit32(T) ? 32 : 16;
     const int64_t units = (int64_t)N * (K / uw);
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= units) return;
@@ -79,6 +79,20 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
+    } else if constexpr (T == T_Q4_0) {
+        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
+        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + (n * (K >> 5) + u) * 2));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int bit = 16 * (e & 1) + 4 * (e >> 1);
+                v[e] = d * (float)((int)((q[t] >> bit) & 15u) - 8);
+            }
+            st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
+            st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
+        }
     } else if constexpr (T == T_Q4_K) {
         const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
         const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
@@ -113,9 +127,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 // ------------------------------------------------------------------------------------------------- raw dequant
 static int check_launch(const char* what);
 // The file's blocks (rows, row_bytes) -> float32 (rows, cols), without planes: reference src/mashbox/ops/reference.py
-// :398-409 (dequant) with :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), the rebuild of the
-// exact path. One thread per 32 values (a Q8_0 block, a Q4_K / Q5_K sub-block, two Q6_K sub-blocks); the blocks are
-// 34 / 144 / 176 / 210 bytes apart, so bytes are read one at a time.
+// :398-409 (dequant) with :66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), the
+// rebuild of the exact path. One thread per 32 values (a Q4_0 / Q8_0 block, a Q4_K / Q5_K sub-block, two Q6_K
+// sub-blocks); the blocks are 18 / 34 / 144 / 176 / 210 bytes apart, so bytes are read one at a time.
 template <int T>
 __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
                                                           float* __restrict__ w) {
@@ -128,6 +142,11 @@ __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restr
         const uint8_t* b = raw + (n * (K / 32) + u) * 34;
         const float d = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
         for (int i = 0; i < 32; ++i) out[i] = (float)(int8_t)b[2 + i] * d;
+    } else if constexpr (T == T_Q4_0) {
+        // value i < 16: low nibble of qs[i]; value 16 + i: its high nibble (qs at byte 2)
+        const uint8_t* b = raw + (n * (K / 32) + u) * 18;
+        const float d = f16f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+        for (int i = 0; i < 32; ++i) out[i] = d * (float)((int)((b[2 + (i & 15)] >> (4 * (i >> 4))) & 15u) - 8);
     } else if constexpr (T == T_Q5_K) {
         // value 32j + i of the super-block: nibble j % 2 of qs[32 (j / 2) + i] (qs at byte 48), bit j of qh[i] (byte 16)
         const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 176;
@@ -173,7 +192,9 @@ __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restr
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s) {
     const int64_t units = rows * (K / 32);
     const dim3 grid((unsigned)((units + 255) / 256));
-    if (t == T_Q4_K)
+    if (t == T_Q4_0)
+        dequant_raw_kernel<T_Q4_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    else if (t == T_Q4_K)
         dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
     else if (t == T_Q5_K)
         dequant_raw_kernel<T_Q5_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
@@ -185,11 +206,13 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
 }
 
 // ------------------------------------------------------------------------------------------------ device repack
-// One thread per block: the file's bytes (unaligned, 34, 144, 176 or 210 bytes apart) into the planes of mbq_layout.h.
+// One thread per block: the file's bytes (unaligned, 18, 34, 144, 176 or 210 bytes apart) into the planes of
+// mbq_layout.h.
 template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    const int bv = (T == T_Q8_0) ? 32 : 256, bb = (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : (T == T_Q5_K) ? 176 : 210;
+    const int bv = (T == T_Q8_0 || T == T_Q4_0) ? 32 : 256;
+    const int bb = (T == T_Q4_0) ? 18 : (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : (T == T_Q5_K) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (int64_t)N * nb) return;
@@ -201,6 +224,19 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         uint8_t* d = planes + sc_off + (n * nb + b) * 2;
         d[0] = src[0];
         d[1] = src[1];
+    } else if constexpr (T == T_Q4_0) {
+        uint8_t* d = planes + sc_off + (n * nb + b) * 2;
+        d[0] = src[0];
+        d[1] = src[1];
+        uint32_t* dst = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 16);
+        for (int t = 0; t < 4; ++t) {
+            uint32_t v = 0;
+            for (int e = 0; e < 8; ++e) {
+                const int i = t * 8 + e;                               // slot of mbq_layout.h: dword i/8, bits 16 (e&1) + 4 (e/2)
+                v |= ((uint32_t)(src[2 + (i & 15)] >> (4 * (i >> 4))) & 15u) << (16 * (e & 1) + 4 * (e >> 1));
+            }
+            dst[t] = v;
+        }
     } else if constexpr (T == T_Q5_K) {
         uint8_t* meta = planes + sc_off + (n * nb + b) * 16;
         for (int i = 0; i < 16; ++i) meta[i] = src[i];
@@ -330,6 +366,7 @@ static int launch_t(const Args& a, hipStream_t s) {
 
 int launch_matmul(int t, const Args& a, hipStream_t s) {
     switch (t) {
+        case T_Q4_0: return launch_t<T_Q4_0>(a, s);
         case T_Q8_0: return launch_t<T_Q8_0>(a, s);
         case T_Q4_K: return launch_t<T_Q4_K>(a, s);
         case T_Q5_K: return launch_t<T_Q5_K>(a, s);
@@ -340,13 +377,14 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
 }
 
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s) {
-    const int64_t uw = (t == T_Q8_0) ? 16 : 32;
+    const int64_t uw = unit32(t) ? 32 : 16;
     const int64_t units = a.N * (a.K / uw);
     const dim3 grid((unsigned)((units + 255) / 256));
     auto run = [&](auto kern) {
         kern<<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, (int)a.N, (int)a.K, w);
     };
-    if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
+    if (t == T_Q4_0) run(dequant_kernel<T_Q4_0>);
+    else if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -357,7 +395,8 @@ int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* plan
     const int64_t blocks = N * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
-    if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
+    if (t == T_Q4_0) run(repack_kernel<T_Q4_0>);
+    else if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

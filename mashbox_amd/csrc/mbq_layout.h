@@ -2,6 +2,10 @@
 //
 // The GGUF blocks of a row are split into two planes so that every lane of a wave reads whole 16-byte vectors:
 //
+//   Q4_0 (ggml 2, 32 values / 18 B per block; reference src/mashbox/ops/reference.py:66-70)
+//     qs   (N, K/32, 16 B)         one 16-byte unit per block, its 32 quants in the Q4_K unit order below
+//     d    fp16  (N, K/32)         the blocks' scales (in the sc plane, as Q8_0's)
+//   value = d * (q - 8), exact in float32
 //   Q8_0 (ggml 8, 32 values / 34 B per block; reference src/mashbox/ops/reference.py:101-103)
 //     qs   int8  (N, K)            the blocks' 32 quants, in file order
 //     d    fp16  (N, K/32)         the blocks' scales
@@ -37,10 +41,15 @@
 
 namespace mbq {
 
-enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8 };
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8 };
 
 // the K-quants: 256-value super-blocks, kernel units of 32 values (16 bytes of low nibbles)
 constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+// types whose kernel unit is 16 bytes of nibbles for 32 values (the K-quants and Q4_0); Q8_0 and int8 units are 16
+// bytes for 16 values
+constexpr bool unit32(int t) { return kquant(t) || t == T_Q4_0; }
+// Q4_0 and Q4_K: a unit's 16 bytes are the whole 4-bit quants, in the Q4_K order
+constexpr bool nib4(int t) { return t == T_Q4_K || t == T_Q4_0; }
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
@@ -50,13 +59,18 @@ struct Layout {
     int64_t qs_off, qs_bytes, hi_off, hi_bytes, sc_off, sc_bytes, d_off, d_bytes, total;
 };
 
-inline int block_values(int t) { return t == T_Q8_0 ? 32 : kquant(t) ? 256 : 0; }
-inline int block_bytes(int t) { return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0; }
+inline int block_values(int t) { return (t == T_Q8_0 || t == T_Q4_0) ? 32 : kquant(t) ? 256 : 0; }
+inline int block_bytes(int t) {
+    return t == T_Q4_0 ? 18 : t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
+}
 
 inline Layout layout(int t, int64_t n, int64_t k) {
     Layout L{};
     if (t == T_Q8_0) {
         L.qs_bytes = n * k;
+        L.sc_bytes = n * (k / 32) * 2;
+    } else if (t == T_Q4_0) {
+        L.qs_bytes = n * (k / 2);
         L.sc_bytes = n * (k / 32) * 2;
     } else if (t == T_Q4_K) {
         L.qs_bytes = n * (k / 2);
@@ -96,7 +110,7 @@ inline void q6k_slot(int i, int* lo_byte, int* lo_bit, int* hi_byte, int* hi_bit
     *hi_bit = 2 * ((i >> 2) & 3);
 }
 
-// Q4_K: position of quant i (0..31) of a sub-block inside its 16-byte unit: (dword index, bit offset)
+// Q4_K, Q4_0: position of quant i (0..31) of a sub-block (block) inside its 16-byte unit: (dword index, bit offset)
 inline void q4k_slot(int i, int* dword, int* bit) {
     const int e = i & 7;
     *dword = i >> 3;

@@ -2,9 +2,8 @@
 // weights from HBM straight into MFMA operands, activations shared through LDS.
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
-// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
-// :164-173 (Q6_K),
-// and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
+// float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0),
+// :132-149 (Q4_K), :150-159 (Q5_K) and :164-173 (Q6_K), and reference src/mashbox/models/qwen3_8_27b/model.py:72-82 (int8 per output channel: dot, then * s).
 //
 // Block = 4 waves, one per SIMD (one block per CU: the float32 accumulators of a 16 MT x 16 NT wave tile live in the
 // accumulation registers). The block's tile is 16 MT activation rows x 64 NT weight rows; wave w owns weight rows
@@ -16,8 +15,8 @@
 // So per MFMA a wave spends about 26 / MT VALU instructions on dequantization and 1 KiB / NT of LDS reads: with
 // MT = 16 and NT >= 3 neither the VALU nor the LDS keeps up with less than the matrix cores.
 //
-// Pipeline: a ring of D LDS stages of x (D - 1 iterations in flight; D = 2 for Q4_K's 64 KiB stages of 256 rows, else
-// 4) and a ring of DW = 4 register buffers of weights (DW iterations in flight). Step l:
+// Pipeline: a ring of D LDS stages of x (D - 1 iterations in flight; D = 2 for the 64 KiB stages of 256 rows of Q4_0 and the
+// K-quants, else 4) and a ring of DW = 4 register buffers of weights (DW iterations in flight). Step l:
 // wait for x stage l % D (an exact vmcnt: the loads issued after its DMA), one barrier (the stage has landed for every
 // wave; stage (l - 1) % D is no longer read), DMA x of iteration l + D - 1 into stage (l - 1) % D, dequantize and
 // multiply, then load the weights of iteration l + DW into the buffer just used. The weights of iteration l were loaded
@@ -48,9 +47,9 @@
 namespace mbq {
 
 constexpr int PG_THREADS = 256;    // 4 waves
-// x stages in LDS: 2 for Q4_K's 64 KiB stages of 256 rows x 128 values, else 4 (at most 128 KiB); Q6_K, with 4 weight
+// x stages in LDS: 2 for the 64 KiB stages of 256 rows x 128 values (Q4_0, K-quants), else 4 (at most 128 KiB); Q6_K, with 4 weight
 // loads per row tile, always 2 (the loads in flight stay within the 63 that vmcnt counts)
-template <int T, int MT> constexpr int pg_stages() { return (T == T_Q6_K || ((T == T_Q4_K || T == T_Q5_K) && MT > 8)) ? 2 : 4; }
+template <int T, int MT> constexpr int pg_stages() { return (T == T_Q6_K || (unit32(T) && MT > 8)) ? 2 : 4; }
 // weight iterations in flight per wave
 template <int T, int MT, int NT> constexpr int pg_wdepth() { return 4; }
 template <int T, int MT> constexpr size_t pg_lds_bytes() { return (size_t)pg_stages<T, MT>() * 16 * MT * ws_ki<T>() * 2; }
@@ -345,6 +344,7 @@ int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s) {
     if (a.M < 16 * mt) return set_error(MBQ_BAD_ARG, "weight-direct GEMM: %lld activation rows, fewer than a tile's %d", (long long)a.M, 16 * mt);
     switch (t) {
         case T_INT8: return pg_dispatch<T_INT8>(a, idx, s);
+        case T_Q4_0: return pg_dispatch<T_Q4_0>(a, idx, s);
         case T_Q8_0: return pg_dispatch<T_Q8_0>(a, idx, s);
         case T_Q4_K: return pg_dispatch<T_Q4_K>(a, idx, s);
         case T_Q5_K: return pg_dispatch<T_Q5_K>(a, idx, s);

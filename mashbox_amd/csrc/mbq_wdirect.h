@@ -1,5 +1,6 @@
 // Weight-direct MFMA operands, shared by the GEMMs that take their weights from HBM straight into registers
-// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_K and Q6_K), 64
+// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_0 and the
+// K-quants), 64
 // contiguous bytes of each row of the quant plane. Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
 // (g = l >> 4, the lane group). The MFMA sums over K, so any K order works when x follows it: in K step s of an
 // iteration, lane group g holds the 8 values K = k0 + g KI/4 + 8 s + e (e = 0..7) for both operands.
@@ -8,11 +9,13 @@
 //          bfloat16, the value the LDS GEMM stores.
 //   Q4_K   one 16-byte unit = the 32 quants of sub-block k0/32 + g = 4 K steps; the B operand is (d sc) q - dmin m
 //          (exact in float32) rounded to nearest even bfloat16.
+//   Q4_0   one 16-byte unit = the 32 quants of block k0/32 + g (the Q4_K order); the B operand is d (q - 8) (exact in
+//          float32) rounded to nearest even bfloat16.
 //   Q5_K   the same 32 values: 16 bytes of low nibbles, the 4-byte high-bit word and the super-block's scales; the B
 //          operand is (d sc) q - dmin m (one rounding) rounded to nearest even bfloat16.
 //   Q6_K   the same 32 values: 16 bytes of low nibbles, 8 bytes of high bits, the two 16-value scales and the
 //          super-block scale; the B operand is (d sc) (q - 32) (exact in float32) rounded to nearest even bfloat16.
-// Weights: reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K); plane layouts:
+// Weights: reference src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K); plane layouts:
 // mbq_layout.h.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -23,14 +26,15 @@
 
 namespace mbq {
 
-template <int T> constexpr int ws_ki() { return kquant(T) ? 128 : 64; }
-inline int ws_ki_of(int t) { return kquant(t) ? 128 : 64; }
+template <int T> constexpr int ws_ki() { return unit32(T) ? 128 : 64; }
+inline int ws_ki_of(int t) { return unit32(t) ? 128 : 64; }
 
 // raw bytes of one iteration of one 16-row tile, as one lane holds them
 template <int T> struct WsRaw;
 template <> struct WsRaw<T_INT8> { u32x4 q; };
 template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
+template <> struct WsRaw<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct WsRaw<T_Q5_K> { u32x4 q, meta; uint32_t h; };
 template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_K ? 4 : T == T_Q5_K ? 3 : 2; }   // buffer loads per tile per iteration
@@ -39,8 +43,9 @@ template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_
 struct WsOff { uint32_t q, s, h, d; };
 template <int T>
 __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    WsOff o{row * (uint32_t)(kquant(T) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
+    WsOff o{row * (uint32_t)(unit32(T) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
     if constexpr (T == T_Q8_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
+    if constexpr (T == T_Q4_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * lg;
     if constexpr (T == T_Q4_K || T == T_Q5_K) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 256) * 16u;
     if constexpr (T == T_Q5_K) o.h = (uint32_t)hi_off + row * (uint32_t)(K / 8) + 4u * lg;
     if constexpr (T == T_Q6_K) {
@@ -51,14 +56,18 @@ __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_
     return o;
 }
 
-// the lane's bytes of the iteration at K offset kk (non-temporal quant loads); with KFULL false a Q8_0 block past K
-// gets scale 0 (the x it meets is zero, its quants may be any bytes)
+// the lane's bytes of the iteration at K offset kk (non-temporal quant loads); with KFULL false a Q4_0 / Q8_0 block
+// past K gets scale 0 (the x it meets is zero, its quants may be any bytes)
 template <int T, bool KFULL>
 __device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, int kk, int K, int lg) {
-    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)(kquant(T) ? kk / 2 : kk), 2));
+    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)(unit32(T) ? kk / 2 : kk), 2));
     if constexpr (T == T_Q8_0) {
         w.d = bload2(wr, o.s, (uint32_t)(kk / 32) * 2u);
         if constexpr (!KFULL) w.d = (kk + 16 * lg < K) ? w.d : 0u;
+    }
+    if constexpr (T == T_Q4_0) {
+        w.d = bload2(wr, o.s, (uint32_t)(kk / 32) * 2u);
+        if constexpr (!KFULL) w.d = (kk + 32 * lg < K) ? w.d : 0u;
     }
     if constexpr (T == T_Q4_K || T == T_Q5_K) w.meta = bload16(wr, o.s, (uint32_t)(kk / 256) * 16u);
     if constexpr (T == T_Q5_K) w.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, o.h, (uint32_t)(kk / 8), 2);
@@ -70,7 +79,8 @@ __device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, 
 }
 
 // per-lane dequant constants of one tile's unit
-struct WsScale { float a, b, c, e; };   // Q8_0: d; Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+// Q8_0: d; Q4_K, Q5_K: d*sc, dmin*m, d*sc/16; Q4_0: d, 8 d, d/16; Q6_K: d*sc0, 32 d*sc0, d*sc1, 32 d*sc1
+struct WsScale { float a, b, c, e; };
 
 template <int T>
 __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
@@ -83,6 +93,10 @@ __device__ __forceinline__ WsScale ws_scale(const WsRaw<T>& w, int j) {
         s.e = 32.f * s.c;
     } else if constexpr (T == T_Q8_0) {
         s.a = f16f(w.d);
+    } else if constexpr (T == T_Q4_0) {
+        s.a = f16f(w.d);
+        s.b = 8.f * s.a;                            // q d - 8 d = (q - 8) d, exact in float32
+        s.c = s.a * 0.0625f;
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         uint32_t sc, mn;
         q4k_scale_min_sel(w.meta[1], w.meta[2], w.meta[3], q4k_sel(j), &sc, &mn);
@@ -112,7 +126,7 @@ __device__ __forceinline__ uint32_t ws_bpair(const WsRaw<T>& w, const WsScale& s
         const uint32_t v = p < 2 ? lo : hi;
         const int sh = (p & 1) * 16;
         return pack_bf16(__builtin_fmaf((float)((v >> sh) & 0xFFu), sc.a, -sc.b), __builtin_fmaf((float)((v >> (sh + 8)) & 0xFFu), sc.a, -sc.b));
-    } else if constexpr (T == T_Q4_K) {
+    } else if constexpr (nib4(T)) {
         // dword s of the unit: quant 8s+2p in bits 4p..4p+3, quant 8s+2p+1 in bits 16+4p.. (mbq_layout.h); the odd
         // nibble positions come out 16 times too large and take the scale d*sc/16
         const uint32_t v = w.q[s];

@@ -43,10 +43,10 @@ namespace mbq {
 
 constexpr int WS_THREADS = 256;    // 4 waves
 
-// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_K, Q6_K) at 64 activation rows
-template <int T> constexpr int ws_depth() { return kquant(T) ? 4 : 8; }
+// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_0, K-quants) at 64 activation rows
+template <int T> constexpr int ws_depth() { return unit32(T) ? 4 : 8; }
 // x rows staged: 16 MT, rounded so that every wave issues the same number of 1 KiB DMA instructions per stage
-template <int T, int MT> constexpr int ws_rows() { return kquant(T) ? 16 * MT : (MT <= 2 ? 32 : 64); }
+template <int T, int MT> constexpr int ws_rows() { return unit32(T) ? 16 * MT : (MT <= 2 ? 32 : 64); }
 
 struct WsArgs {
     const uint8_t* base;        // planes of the weight (host layer applied)
@@ -322,7 +322,7 @@ static size_t ws_partial_bytes(int64_t M, int nr) { return (size_t)((M + 15) / 1
 // 16), at most 8 ranges of at least D iterations, the partial tiles within the workspace.
 static void ws_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int* nr, int* S) {
     const int64_t KT = (K + ws_ki_of(t) - 1) / ws_ki_of(t);
-    const int depth = kquant(t) ? 4 : 8;
+    const int depth = unit32(t) ? 4 : 8;
     const int64_t tiles64 = (N + 63) / 64;
     if (tiles64 >= cus) {
         *nr = 128;
@@ -365,6 +365,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
     }
     switch (t) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);
+        case T_Q4_0: return nr == 64 ? ws_launch_m<T_Q4_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_0, 2>(a, S, (int)kts, w, s);
         case T_Q8_0: return nr == 64 ? ws_launch_m<T_Q8_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q8_0, 2>(a, S, (int)kts, w, s);
         case T_Q4_K: return nr == 64 ? ws_launch_m<T_Q4_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_K, 2>(a, S, (int)kts, w, s);
         case T_Q5_K: return nr == 64 ? ws_launch_m<T_Q5_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q5_K, 2>(a, S, (int)kts, w, s);

@@ -3,7 +3,8 @@
 mashbox's ops boundary imports a kernel package by module name (reference src/mashbox/ops/__init__.py:273-311,
 env MASHBOX_GGUF_KERNELS) and uses this surface (reference src/mashbox/ops/__init__.py:11-34):
 
-    TYPES                                    ggml type ids with kernel planes: Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14)
+    TYPES                                    ggml type ids with kernel planes: Q4_0 (2), Q8_0 (8), Q4_K (12), Q5_K (13),
+                                             Q6_K (14)
     repack_host(t, raw, shape) -> planes     host NumPy blocks (..., rows, row_bytes) -> planes (host, then .to(dev))
     repack(t, raw, shape, stacked=False)     device blocks (torch uint8 on the GPU) -> planes on the GPU
     matmul(x, planes, layer=None) -> y       x (..., cols) @ W.T as float32 (..., rows); layer= reads one weight of a
@@ -25,11 +26,13 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import INT8, OUT_BF16, OUT_F32, Q4_K, Q5_K, Q6_K, Q8_0, check, lib
+from ._lib import INT8, OUT_BF16, OUT_F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, check, lib
 
-TYPES = frozenset({Q8_0, Q4_K, Q5_K, Q6_K})
-NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}   # values and bytes per block (reference ops/reference.py:22-29)
+# the types the reference's kernel package gives planes (reference src/mashbox/ops/bundle.py:39)
+TYPES = frozenset({Q4_0, Q8_0, Q4_K, Q5_K, Q6_K})
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+# values and bytes per block (reference ops/reference.py:22-29)
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 picks_layer = True
 version = "0.1.0"
 

@@ -45,7 +45,7 @@ PREFLIGHT_DTYPE = torch.bfloat16      # the preflight's input dtype: the forward
 FORCE = ("kernels-package", "quant-kernel")
 
 # ggml type id -> (name, values per block, bytes per block) of the types this path reads (reference ops/reference.py:22-29)
-TYPES = {8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
+TYPES = {2: ("Q4_0", 32, 18), 8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
 
 _KERNELS = {"module": None, "types": frozenset(), "name": None, "error": None}
 _KQ_RAN: dict = {}       # (type, shape) -> True when the kq preflight ran, else why it failed

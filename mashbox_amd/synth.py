@@ -5,8 +5,8 @@ quants uniform in [-127, 127], Q4_K six-bit scales and mins uniform in [0, 63] p
 them (reference src/mashbox/ops/reference.py:132-139), four-bit quants uniform in [0, 15], int8 per-row scales
 ~ U(1e-3, 1e-2), activations ~ N(0, 1) rounded to bfloat16; Q6_K (the reference's Q6_K output-head shape, not a
 BASELINE config): d ~ U(1e-3, 1e-2) / 64, int8 sub-block scales uniform in [-127, 127], six-bit quants uniform in
-[0, 63]. The bytes are the file's block layout (Q8_0 34 B per 32 values, Q4_K 144 B and Q6_K 210 B per 256), ready
-for repack.
+[0, 63]; Q4_0: d ~ U(1e-3, 1e-2), four-bit quants uniform in [0, 15]. The bytes are the file's block layout (Q4_0
+18 B and Q8_0 34 B per 32 values, Q4_K 144 B and Q6_K 210 B per 256), ready for repack.
 """
 from __future__ import annotations
 
@@ -36,6 +36,17 @@ def q8_0_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> 
     d = _uniform_f16_bytes(g, (n, nb, 1), lo, hi, device)                       # (n, nb, 2)
     q = torch.randint(-127, 128, (n, nb, 32), generator=g, device=device, dtype=torch.int8).view(torch.uint8)
     return torch.cat([d, q], dim=-1).reshape(n, nb * 34)
+
+
+def q4_0_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:
+    """(n, k/32*18) uint8 Q4_0 blocks: d, then value i in the low nibble of byte i, value 16 + i in its high nibble
+    (reference src/mashbox/ops/reference.py:66-70)"""
+    g = _gen(seed, device)
+    nb = k // 32
+    d = _uniform_f16_bytes(g, (n, nb, 1), lo, hi, device)
+    q = torch.randint(0, 16, (n, nb, 2, 16), generator=g, device=device, dtype=torch.int32)
+    qs = (q[:, :, 0] | (q[:, :, 1] << 4)).to(torch.uint8)
+    return torch.cat([d, qs], dim=-1).reshape(n, nb * 18)
 
 
 def q4_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:

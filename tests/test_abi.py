@@ -40,7 +40,9 @@ def test_type_table_and_shapes():
     lib = L.lib()
     assert lib.mbq_version() >= 100
     assert lib.mbq_has_type(8) == 1 and lib.mbq_has_type(12) == 1 and lib.mbq_has_type(14) == 1
-    assert lib.mbq_has_type(13) == 1 and lib.mbq_has_type(2) == 0 and lib.mbq_has_type(11) == 0
+    assert lib.mbq_has_type(13) == 1 and lib.mbq_has_type(2) == 1 and lib.mbq_has_type(11) == 0
+    assert lib.mbq_has_type(3) == 0 and lib.mbq_has_type(6) == 0
+    assert lib.mbq_row_bytes(2, 4096) == R.row_bytes(2, 4096) == 2304
     assert lib.mbq_row_bytes(13, 5120) == R.row_bytes(13, 5120) == 3520
     assert lib.mbq_row_bytes(14, 2560) == R.row_bytes(14, 2560) == 2100
     assert lib.mbq_row_bytes(8, 5120) == R.row_bytes(8, 5120) == 5440
@@ -49,15 +51,17 @@ def test_type_table_and_shapes():
     assert KQ.kq_covers(8, (17408, 5120)) and KQ.kq_covers(12, (5120, 17408))
     assert not KQ.kq_covers(12, (5, 100)) and not KQ.kq_covers(11, (256, 256)) and KQ.kq_covers(13, (256, 256))
     assert KQ.kq_covers(14, (151936, 2560)) and not KQ.kq_covers(14, (8, 128))
+    assert KQ.kq_covers(2, (5, 96)) and not KQ.kq_covers(2, (5, 100))
     for t, (n, k) in [(8, (17408, 5120)), (12, (5120, 17408)), (12, (1, 256)), (8, (3, 32)), (14, (151936, 2560)),
-                      (14, (1, 256)), (14, (3, 512)), (13, (1, 256)), (13, (17408, 5120))]:
+                      (14, (1, 256)), (14, (3, 512)), (13, (1, 256)), (13, (17408, 5120)), (2, (1, 32)),
+                      (2, (4096, 4096)), (2, (7, 96))]:
         pb = KQ.plane_bytes(t, (n, k))
         file_bytes = n * R.row_bytes(t, k)
         planes = {14: 4, 13: 3}.get(t, 2)                             # each plane pads to 256 bytes
         assert pb % 256 == 0 and file_bytes <= pb < file_bytes + 256 * planes
 
 
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_host_repack_is_lossless(t):
     rng = np.random.default_rng(40 + t)
     for n, kb in [(1, 1), (7, 3), (130, 2)]:
@@ -86,6 +90,31 @@ def test_q4_k_unit_layout_yields_bf16_pairs():
         for t_ in range(4):
             assert np.array_equal(lo[:, :, t_], q[:, :, 8 * t_ + 2 * p_])
             assert np.array_equal(hi[:, :, t_], q[:, :, 8 * t_ + 2 * p_ + 1])
+
+
+def test_q4_0_unit_layout_yields_bf16_pairs():
+    """a Q4_0 unit holds its block's 32 quants in the Q4_K order, so the Q4_K pair rule gives (128 + q, 128 + q') of
+    values 8t + 2p, 8t + 2p + 1; and the d plane holds the blocks' scales in file order: checked on the host against the
+    oracle's dequant of blocks with d = 1 (its values are then q - 8)"""
+    rng = np.random.default_rng(44)
+    raw = G.q4_0_raw(rng, 3, 160).reshape(15, 18)
+    d = raw[:, 0:2].copy()
+    raw[:, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    raw = raw.reshape(3, 90)
+    q = (R.dequant(raw, R.Q4_0, 160) + 8).astype(np.int64).reshape(3, 5, 32)   # (row, unit, value)
+    p = KQ.repack_host(R.Q4_0, raw, (3, 160)).buf.numpy()
+    units = p[:3 * 80].view(np.uint32).reshape(3, 5, 4)
+    for p_ in range(4):
+        pair = ((units >> np.uint32(4 * p_)) & np.uint32(0x000F000F)) | np.uint32(0x43004300)
+        lo = R.bf16_to_f32((pair & 0xFFFF).astype(np.uint16)) - 128
+        hi = R.bf16_to_f32((pair >> 16).astype(np.uint16)) - 128
+        for t_ in range(4):
+            assert np.array_equal(lo[:, :, t_], q[:, :, 8 * t_ + 2 * p_])
+            assert np.array_equal(hi[:, :, t_], q[:, :, 8 * t_ + 2 * p_ + 1])
+    raw = raw.reshape(15, 18)
+    raw[:, 0:2] = d
+    p = KQ.repack_host(R.Q4_0, raw.reshape(3, 90), (3, 160)).buf.numpy()
+    assert np.array_equal(p[256:256 + 30], d.reshape(-1))           # the d plane starts at the next 256-byte boundary
 
 
 def test_q6_k_unit_layout_yields_quant_bytes():

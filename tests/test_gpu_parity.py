@@ -22,11 +22,12 @@ from mashbox_amd import int8 as I8
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K]
-NAME = {R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
-GEMM_TYPES = [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K, "int8"]
-GEMM_IDS = ["Q8_0", "Q4_K", "Q5_K", "Q6_K", "int8"]
+TYPES = [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K]
+NAME = {R.Q4_0: "Q4_0", R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K"}
+GEMM_TYPES = [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K, "int8"]
+GEMM_IDS = ["Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "int8"]
 KQUANT = (R.Q4_K, R.Q5_K, R.Q6_K)                     # rows of whole 256-value super-blocks
+UNIT32 = (R.Q4_0,) + KQUANT                           # GEMV units of 32 values
 
 
 def _bf16_tensor(bits: np.ndarray, dev) -> torch.Tensor:
@@ -205,11 +206,12 @@ def test_batched_gemm_full_config_sampled(idx, cuda):
         assert_product(got, ref, f"config {idx} {name}")
 
 
-@pytest.mark.parametrize("t", KQUANT, ids=NAME.get)
+@pytest.mark.parametrize("t", UNIT32, ids=NAME.get)
 @pytest.mark.parametrize("m", [3, 4])
 def test_gemv_row_parts_past_the_row_end(t, m, cuda):
-    """K = 8448 (264 units of 32 values) at 3-4 activation rows: the GEMV cuts a row into 8 parts of 40 units, so the
-    last part starts past the row's end and holds nothing; the block's sum over the parts must leave it out"""
+    """K = 8448 (264 units of 32 values) at 3-4 activation rows: the GEMV cuts a K-quant row into 8 parts of 40 units
+    (Q4_0: 33), so the last part starts past the row's end and holds nothing; the block's sum over the parts must leave
+    it out"""
     rng = np.random.default_rng([t, m, 8448])
     n, k = 70, 8448
     raw = G.RAW[t](rng, n, k)
@@ -263,7 +265,7 @@ def test_small_batches_over_tall_weights(t, m, cuda):
     assert_product(run()[:, ns], ref[:, ns], f"{t} m={m} n={n}")
 
 
-@pytest.mark.parametrize("t", KQUANT, ids=NAME.get)
+@pytest.mark.parametrize("t", UNIT32, ids=NAME.get)
 @pytest.mark.parametrize("n", [1, 7, 300])
 def test_gemv_rows_in_three_parts(t, n, cuda):
     """K = 17408 (544 units) at one activation row cuts a row into 3 parts of 184, 184 and 176 units, taken by 3, 3
@@ -343,10 +345,10 @@ def forced_plan():
 @pytest.mark.parametrize("bm,bn", GEMM_TILES)
 def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cuda):
     """partial tiles on both edges, K over several steps (a Q8_0 / int8 K that is not a multiple of the 64-value step
-    included), split-K into 3 ranges against 1"""
+    included, Q4_0 the same), split-K into 3 ranges against 1"""
     rng = np.random.default_rng([bm, bn, 0 if t == "int8" else t])
     m, n = bm + bm // 2 - 3, bn + 17
-    k = {R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, R.Q5_K: 256 * 3, R.Q6_K: 256 * 3, "int8": 16 * 25}[t]
+    k = {R.Q4_0: 32 * 13, R.Q8_0: 32 * 13, R.Q4_K: 256 * 3, R.Q5_K: 256 * 3, R.Q6_K: 256 * 3, "int8": 16 * 25}[t]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
     xf = R.bf16_to_f32(xb).astype(np.float64)
@@ -393,13 +395,13 @@ DIRECT_SHAPES = [(16, 4), (16, 3), (16, 2), (8, 5), (8, 4), (8, 2)]
 def test_weight_direct_gemm_every_shape(t, mt, nt, kfull, forced_plan, cuda):
     """the weight-direct kernel of large batches: every tile shape, a batch of exactly one activation tile and one of
     2 tiles + a ragged rest (the last tile shifted back over the one before), ragged weight rows, a K that is or is not
-    a multiple of the kernel's iteration (64 values; 128 for Q4_K and Q6_K, whose K is always whole)"""
+    a multiple of the kernel's iteration (64 values; 128 for Q4_0 and the K-quants, whose K is always whole)"""
     if t in KQUANT and not kfull:
         pytest.skip("a K-quant K is a whole number of 256-value super-blocks")
     if t in (R.Q5_K, R.Q6_K) and (mt, nt) in ((16, 4), (8, 5)):
         pytest.skip("no Q5_K / Q6_K weight-direct kernel of this shape (test_weight_direct_refuses_the_widest_shapes)")
     bm, bn = 16 * mt, 64 * nt
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), R.Q5_K: (256 * 5, 256 * 5), R.Q6_K: (256 * 5, 256 * 5),
+    k = {R.Q4_0: (32 * 27, 128 * 7), R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 5), R.Q5_K: (256 * 5, 256 * 5), R.Q6_K: (256 * 5, 256 * 5),
          "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     for m, n in ((bm, bn + 17), (2 * bm + 37, 2 * bn + 17)):
         rng = np.random.default_rng([m, n, int(kfull), 0 if t == "int8" else t])
@@ -451,11 +453,11 @@ def test_kernel_choice_by_batch_and_forced_auto_shapes(t, forced_plan, cuda):
 @pytest.mark.parametrize("kfull", [False, True], ids=["k_ragged", "k_full"])
 def test_weight_stream_gemm_every_shape(t, m, rows, kfull, forced_plan, cuda):
     """the weight-stream kernel (4 < M <= 64): 1-4 tiles of 16 activation rows, 64 and 128 weight rows per block,
-    ragged weight rows, a K that is or is not a multiple of the kernel's iteration (64 values; 128 for Q4_K and Q6_K,
-    whose K is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
+    ragged weight rows, a K that is or is not a multiple of the kernel's iteration (64 values; 128 for Q4_0 and the
+    K-quants, whose K is always whole), K split into 3 ranges (a split with fewer iterations than waves included) against 1"""
     rng = np.random.default_rng([m, rows, int(kfull), 0 if t == "int8" else t])
     n = 3 * rows + 17
-    k = {R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), R.Q5_K: (256 * 5, 256 * 6), R.Q6_K: (256 * 5, 256 * 6),
+    k = {R.Q4_0: (32 * 27, 128 * 7), R.Q8_0: (32 * 27, 64 * 13), R.Q4_K: (256 * 5, 256 * 6), R.Q5_K: (256 * 5, 256 * 6), R.Q6_K: (256 * 5, 256 * 6),
          "int8": (16 * 57, 64 * 15)}[t][int(kfull)]
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)

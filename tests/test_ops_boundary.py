@@ -25,7 +25,7 @@ def _reset():
 
 # ------------------------------------------------------------------------------------------------ CPU: routing
 def test_weight_path_and_device_bytes():
-    assert ops.load_kernels() == frozenset({8, 12, 13, 14})
+    assert ops.load_kernels() == frozenset({2, 8, 12, 13, 14})
     assert ops.weight_path(12, (5120, 17408)) == "kq" and ops.weight_path(8, (17408, 5120)) == "kq"
     assert ops.weight_path(14, (256, 256)) == "kq"
     assert ops.weight_path(14, (256, 256), kernel_types=frozenset({8, 12})) == "exact"   # Q6_K left to the exact path
@@ -64,7 +64,7 @@ def _x(rng, m, k, cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_kernel_and_exact_paths_match_the_oracle(t, cuda):
     import torch
     ops.load_kernels()
@@ -153,7 +153,7 @@ def test_kq_failure_falls_back_to_the_exact_path(fail, cuda, monkeypatch, capsys
     monkeypatch.setitem(sys.modules, name, _stub(name, fail, calls))
     if fail.startswith("force:"):
         monkeypatch.setenv("MASHBOX_FAULT", fail)
-    assert ops.load_kernels(module=name) == frozenset({8, 12, 13, 14})
+    assert ops.load_kernels(module=name) == frozenset({2, 8, 12, 13, 14})
     rng = np.random.default_rng(31)
     shapes = [(8, (40, 256)), (8, (40, 256)), (12, (24, 512)), (12, (24, 512)), (8, (16, 64))]
     raws = [G.RAW[t](rng, *s) for t, s in shapes]
@@ -176,7 +176,7 @@ def test_kq_failure_falls_back_to_the_exact_path(fail, cuda, monkeypatch, capsys
 def test_kq_preflight_runs_once_per_type_and_shape(cuda, monkeypatch):
     calls = {"repack": 0, "matmul": 0}
     monkeypatch.setitem(sys.modules, "_stub_mbq_ok", _stub("_stub_mbq_ok", None, calls))
-    assert ops.load_kernels(module="_stub_mbq_ok") == frozenset({8, 12, 13, 14})
+    assert ops.load_kernels(module="_stub_mbq_ok") == frozenset({2, 8, 12, 13, 14})
     rng = np.random.default_rng(32)
     shapes = [(8, (40, 256))] * 3 + [(12, (24, 512))] * 2
     hs = [ops.prepare(G.RAW[t](rng, *s), t, s) for t, s in shapes]
@@ -188,7 +188,7 @@ def test_kq_preflight_runs_once_per_type_and_shape(cuda, monkeypatch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_layer_stack_is_read_in_place(t, cuda):
     """a stack of layers loads as one Packed handle; scan_split holds it whole and scan_join hands the loop body
     At(stack, layer); the product equals the sliced layer's and the exact path's"""
@@ -213,7 +213,7 @@ def test_layer_stack_is_read_in_place(t, cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
 def test_contract_check_and_take_rows(t, cuda):
     ops.load_kernels()
     rng = np.random.default_rng(50 + t)
