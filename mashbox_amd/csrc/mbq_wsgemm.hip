@@ -43,8 +43,10 @@ namespace mbq {
 
 constexpr int WS_THREADS = 256;    // 4 waves
 
-// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_0, K-quants) at 64 activation rows
-template <int T> constexpr int ws_depth() { return unit32(T) ? 4 : 8; }
+// iterations in flight (= LDS stages of x): x stages of 8 KB (int8, Q8_0) or 16 KB (Q4_0, K-quants) at 64 activation
+// rows. 4 for every type: int8 and Q8_0 ran 1-8 % faster with 4 than with 8 on MI355X at 8-64 rows over 1024-17408-row
+// weights (twice the blocks fit a CU's LDS), except 5120 x 17408 int8 at 8 rows (+4 %)
+template <int T> constexpr int ws_depth() { return 4; }
 // x rows staged: 16 MT, rounded so that every wave issues the same number of 1 KiB DMA instructions per stage
 template <int T, int MT> constexpr int ws_rows() { return unit32(T) ? 16 * MT : (MT <= 2 ? 32 : 64); }
 
@@ -319,10 +321,11 @@ static size_t ws_partial_bytes(int64_t M, int nr) { return (size_t)((M + 15) / 1
 // Rows per block (64 or 128) and K splits, from timings on MI355X at 64 activation rows: when the 64-row tiles alone
 // fill the CUs, 128-row blocks (each x stage feeds twice the weights) and no split; else 64-row blocks and as many K
 // splits as fit the CUs in one round (3 for 80 tiles: 5120 x 17408 in 38 us instead of 50 with 2; 2 for 96, 8 for
-// 16), at most 8 ranges of at least D iterations, the partial tiles within the workspace.
+// 16), at most 8 ranges of at least 512 K values (4 iterations of 128, 8 of 64), the partial tiles within the
+// workspace.
 static void ws_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int* nr, int* S) {
     const int64_t KT = (K + ws_ki_of(t) - 1) / ws_ki_of(t);
-    const int depth = unit32(t) ? 4 : 8;
+    const int depth = unit32(t) ? 4 : 8;                          // iterations of 512 K values
     const int64_t tiles64 = (N + 63) / 64;
     if (tiles64 >= cus) {
         *nr = 128;
