@@ -1,4 +1,4 @@
-"""mashbox_amd — MI355X-native quantized linear for mashbox (GGUF Q8_0 / Q4_K / Q5_K / Q6_K and int8 per-channel weights).
+"""mashbox_amd — MI355X-native quantized linear for mashbox (GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K and int8 per-channel weights).
 
     mashbox_amd.kernels   mashbox's kernel-package surface (TYPES, repack_host, repack, matmul, dequant, plane_bytes,
                           kq_covers, picks_layer) on the hand-written gfx950 kernels of libmbq.so

@@ -657,12 +657,9 @@ template <int T, int BM, int BN, int P, bool KFULL>
 static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
     auto kern = gemm_kernel<T, BM, BN, P, KFULL>;
     const size_t lds = lds_bytes<T, BM, BN, P>();
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
     GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
                (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt};
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
@@ -675,12 +672,9 @@ static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStr
 template <int T, bool KFULL>
 static int launch_sg(const Args& a, hipStream_t s) {
     auto kern = sgemm_kernel<T, KFULL>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)SG_LDS) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", SG_LDS);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (set_lds_limit((const void*)kern, SG_LDS, lds_set) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", SG_LDS);
     GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
                (int)a.N, (int)a.K, a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr};
     const int64_t tiles = ((a.M + SG_BM - 1) / SG_BM) * ((a.N + SG_BN - 1) / SG_BN);

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace mbq {
 
 enum : int { MBQ_BAD_ARG = -1, MBQ_LAUNCH_FAIL = -2, MBQ_SMALL_CAP = -3 };
@@ -41,6 +43,19 @@ constexpr int64_t BUF_MAX_BYTES = 0x7FFFFF00;
 
 // records the calling thread's error message; returns code
 int set_error(int code, const char* fmt, ...);
+
+// Raises a kernel's dynamic-LDS limit to `lds` bytes on the current device, once per kernel (one `done` flag word per
+// kernel) and device: the attribute belongs to the kernel on a device, so a process that launches on several GPUs sets
+// it on each. Thread-safe; returns the HIP error of the first failing call.
+inline hipError_t set_lds_limit(const void* kernel, size_t lds, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const uint64_t bit = (dev >= 0 && dev < 64) ? (uint64_t{1} << dev) : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
 
 int launch_matmul(int t, const Args& a, hipStream_t s);
 int launch_gemv(int t, const Args& a, hipStream_t s);   // M <= GEMV_MAX_M (mbq_gemv.hip)

@@ -245,12 +245,9 @@ template <int T, int MT, int NT, bool KFULL>
 static int pg_launch(const Args& a, hipStream_t s) {
     auto kern = pgemm_kernel<T, MT, NT, KFULL>;
     const size_t lds = pg_lds_bytes<T, MT>();
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "weight-direct GEMM: %zu bytes of LDS refused", lds);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "weight-direct GEMM: %zu bytes of LDS refused", lds);
     const int64_t mtiles = (a.M + 16 * MT - 1) / (16 * MT), ntiles = (a.N + 64 * NT - 1) / (64 * NT);
     PgArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
              a.y, a.out_bf16, (int)mtiles, (int)(mtiles * ntiles)};

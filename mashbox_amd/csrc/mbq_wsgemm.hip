@@ -268,12 +268,9 @@ template <int T, int MT, int NT, bool KFULL>
 static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStream_t s) {
     auto kern = wsgemm_kernel<T, MT, NT, KFULL>;
     const size_t lds = ws_lds_bytes<T, MT>();
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "weight-stream GEMM: %zu bytes of LDS refused", lds);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "weight-stream GEMM: %zu bytes of LDS refused", lds);
     WsArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
              a.y, a.out_bf16, S, kts, w.ws, w.cnt};
     const int64_t tiles = (a.N + 64 * NT - 1) / (64 * NT);
