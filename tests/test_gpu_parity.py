@@ -298,6 +298,25 @@ def test_q6_k_output_head_full_size_sampled(cuda):
         assert_product(y[:, ns], R.bf16_to_f32(xb).astype(np.float64) @ w.T, f"Q6_K head m={m}")
 
 
+def test_q4_0_config_2_shape_full_size_sampled(cuda):
+    """Q4_0 at config 2's weight shape (17408 x 5120), repacked on the GPU from the file's blocks; dequant of a seeded
+    sample of 1024 rows bit for bit, and the decode GEMV (1 row), the weight stream (16 rows) and the LDS tiles (64
+    rows over a weight this tall, and 300 rows) on the same sample within the product bars"""
+    n, k = 17408, 5120
+    rng = np.random.default_rng(2)
+    raw = G.q4_0_raw(rng, n, k)
+    planes = KQ.repack(R.Q4_0, torch.from_numpy(raw).to(cuda), (n, k))
+    ns = np.sort(rng.choice(n, 1024, replace=False))
+    w = R.dequant(raw[ns], R.Q4_0, k)
+    assert diff_bits(KQ.dequant(planes).cpu().numpy()[ns], w) == 0
+    for m, kind in ((1, LIB.KERNEL_GEMV), (16, LIB.KERNEL_STREAM), (64, LIB.KERNEL_TILES), (300, LIB.KERNEL_TILES)):
+        assert LIB.gemm_plan(R.Q4_0, m, n, k)[0] == kind
+        xb = G.acts(rng, m, k)
+        y = KQ.matmul(_bf16_tensor(xb, cuda), planes).cpu().numpy()
+        assert np.all(np.isfinite(y))
+        assert_product(y[:, ns], R.bf16_to_f32(xb).astype(np.float64) @ w.astype(np.float64).T, f"Q4_0 m={m}")
+
+
 # ------------------------------------------------------------------------------------------------ golden fixtures
 import os  # noqa: E402
 
