@@ -638,8 +638,12 @@ int workspace(Workspace* out) {
     if (!w.ws) {
         void *p = nullptr, *c = nullptr;
         if (hipMalloc(&p, WS_BYTES) != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
-        if (hipMalloc(&c, WS_TILES * sizeof(int)) != hipSuccess || hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess) {
+        // the counters are zeroed on the null stream and waited for here, once: the first kernel that uses them may run
+        // on a non-blocking stream, which does not wait for the null stream
+        if (hipMalloc(&c, WS_TILES * sizeof(int)) != hipSuccess || hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess ||
+            hipStreamSynchronize(nullptr) != hipSuccess) {
             (void)hipFree(p);
+            if (c) (void)hipFree(c);
             return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K counter allocation failed");
         }
         w.ws = static_cast<float*>(p);
