@@ -354,8 +354,8 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
     const Layout L = layout(t, rows, cols);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     // zero the alignment padding, then write every plane byte
-    if (!for_each_gap(L, [&](int64_t off, int64_t n) { return hipMemsetAsync(planes_dev + off, 0, (size_t)n, s) == hipSuccess; }))
-        return set_error(MBQ_E_HIP, "hipMemsetAsync failed");
+    int rc = 0;
+    if (!for_each_gap(L, [&](int64_t off, int64_t n) { return (rc = launch_zero(planes_dev + off, n, s)) == 0; })) return rc;
     return launch_repack(t, raw_dev, rows, cols, planes_dev, L, s);
 }
 

@@ -205,6 +205,20 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
     return check_launch("dequant_raw");
 }
 
+// -------------------------------------------------------------------------------------------------- zero fill
+// n bytes at p set to zero, one byte per thread (the planes' alignment padding: under 256 bytes a run). A kernel, not
+// hipMemsetAsync, so that a repack recorded into a HIP graph replays correctly.
+__global__ __launch_bounds__(256) void zero_kernel(uint8_t* __restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+int launch_zero(uint8_t* p, int64_t n, hipStream_t s) {
+    if (n <= 0) return 0;
+    zero_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, s>>>(p, n);
+    return check_launch("zero fill");
+}
+
 // ------------------------------------------------------------------------------------------------ device repack
 // One thread per block: the file's bytes (unaligned, 18, 34, 144, 176 or 210 bytes apart) into the planes of
 // mbq_layout.h.

@@ -78,6 +78,7 @@ int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
 int launch_int8_embed(const int8_t* q, const float* s, int64_t N, int64_t D, const int32_t* toks, int64_t T, void* y,
                       int out_bf16, hipStream_t st);
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s);
+int launch_zero(uint8_t* p, int64_t n, hipStream_t s);   // n bytes at device address p set to zero
 struct Layout;
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s);
 

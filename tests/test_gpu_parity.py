@@ -75,6 +75,23 @@ def test_device_repack_equals_host_repack(t, cuda):
     assert torch.equal(host.buf, dev.buf.cpu())
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_device_repack_zeroes_the_padding_of_a_dirty_buffer(t, cuda):
+    """mbq_repack_dev into a buffer full of 0xAB: the planes and their alignment padding equal the host repack's bytes
+    (the padding is cleared by a fill kernel, so a captured repack replays the same)"""
+    import ctypes
+    from mashbox_amd import _lib as L
+    rng = np.random.default_rng(3100 + t)
+    raw, cols = _random_blocks(t, 13, 3, rng)
+    host = KQ.repack_host(t, raw, (13, cols)).buf
+    planes = torch.full((host.numel(),), 0xAB, dtype=torch.uint8, device=cuda)
+    raw_d = torch.from_numpy(raw).to(cuda)
+    rc = L.lib().mbq_repack_dev(t, ctypes.c_void_p(raw_d.data_ptr()), 13, cols, ctypes.c_void_p(planes.data_ptr()),
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    assert torch.equal(planes.cpu(), host)
+
+
 MM_SHAPES = [(1, 1), (9, 2), (37, 3), (130, 4)]        # (weight rows N, K in blocks)
 MM_ROWS = [1, 2, 3, 4, 5, 16, 64, 130]
 
