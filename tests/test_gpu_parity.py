@@ -545,3 +545,52 @@ def test_split_k_repeats_bit_for_bit(t, m, plan, forced_plan, cuda):
     assert_product(first, ref)
     for _ in range(4):
         assert np.array_equal(run().view(np.uint32), first.view(np.uint32))
+
+
+# ----------------------------------------------------------------------------------------------- HIP graph replays
+GRAPH_CASES = [  # (type, activation rows, weight rows, K, forced plan or None, stack of layers read at a device index)
+    (R.Q4_K, 1, 700, 2048, None, False),                       # decode GEMV
+    (R.Q8_0, 3, 700, 1024, None, True),                         # GEMV, device layer of a stack
+    ("int8", 64, 1024, 5120, (1, 16, 64, 4), False),           # weight stream, 4 K ranges (arrival counters)
+    (R.Q4_0, 130, 640, 2048, (2, 64, 128, 3), False),           # LDS tiles, 3 K ranges
+    (R.Q6_K, 300, 512, 1024, None, True),                       # LDS tiles, device layer
+]
+
+
+@pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: f"{c[0] if c[0] == 'int8' else NAME[c[0]]}-m{c[1]}")
+def test_graph_replays_match_the_eager_result(case, forced_plan, cuda):
+    """calls recorded into a HIP graph (torch.cuda.graph) replay bit for bit equal to the eager call, on every replay,
+    with eager calls of the same kernels between the replays (the K-split counters reset themselves, and the library
+    records no memset node)"""
+    t, m, n, k, plan, stacked = case
+    rng = np.random.default_rng([m, n, k])
+    xb = G.acts(rng, m, k)
+    x = _bf16_tensor(xb, cuda)
+    x_other = _bf16_tensor(G.acts(rng, m, k), cuda)
+    if plan is not None:
+        forced_plan(*plan)
+    if t == "int8":
+        q, s = G.int8_weights(rng, n, k)
+        w = {"q": torch.from_numpy(q).to(cuda), "s": torch.from_numpy(s).to(cuda)}
+        run = lambda xx: I8.linear(xx, w, pj=lambda v: v)
+        ref = (R.bf16_to_f32(xb).astype(np.float64) @ q.astype(np.float64).T) * s
+    else:
+        layers = 3 if stacked else 1
+        st = np.stack([G.RAW[t](rng, n, k) for _ in range(layers)])
+        planes = KQ.repack_host(t, st if stacked else st[0], (n, k)).to(cuda)
+        li = torch.tensor(layers - 1, dtype=torch.int32, device=cuda)
+        run = (lambda xx: KQ.matmul(xx, planes, layer=li)) if stacked else (lambda xx: KQ.matmul(xx, planes))
+        ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(st[-1], t, k).astype(np.float64).T
+    eager = run(x).float().cpu().numpy()
+    assert_product(eager, ref)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = run(x)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.float().cpu().numpy().view(np.uint32), eager.view(np.uint32))
+        run(x_other)                                              # eager work between the replays
+        torch.cuda.synchronize()
+    del g
