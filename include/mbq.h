@@ -60,8 +60,10 @@ int mbq_has_type(int t);
  * multiple of the type's block. Restates reference src/mashbox/ops/reference.py:390-395. */
 int64_t mbq_row_bytes(int t, int64_t cols);
 
-/* 1 if the kernels run a (rows, cols) weight of type t, else 0 (cols must be a whole number of blocks).
- * Replaces the optional kq_covers(t, (rows, cols)) (reference src/mashbox/ops/__init__.py:359-363). */
+/* 1 if the kernels run a (rows, cols) weight of type t at every batch size, else 0: cols must be a whole number of
+ * blocks, and the weight's planes must fit one buffer range (at most 0x7FFFFF00 bytes; mbq_matmul cuts activations
+ * into row chunks within that range itself). Replaces the optional kq_covers(t, (rows, cols)) (reference
+ * src/mashbox/ops/__init__.py:359-363), whose contract is that a covered shape runs. */
 int mbq_covers(int t, int64_t rows, int64_t cols);
 
 /* Device bytes of one (rows, cols) weight's kernel planes, 256-byte aligned, so that a stack of L weights is
@@ -86,7 +88,7 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
  * planes_dev: a stack of weights laid out as mbq_plane_bytes apart; `layer` picks one of them (0 for a lone weight),
  * read in place. layer_dev, when not NULL, is a device int32 holding the layer index instead (read by the kernel, so a
  * captured graph or a device-side layer loop never syncs with the host); nlayers bounds it (an index outside
- * [0, nlayers) yields zeros... never an out-of-range read).
+ * [0, nlayers) makes every output NaN and is never read out of range).
  * M = 0 launches nothing. Replaces matmul(x, planes[, layer=]) (reference src/mashbox/ops/__init__.py:17-19,613-616;
  * call contract src/mashbox/ops/bundle.py:559-598: x as bf16, f32 result). */
 int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
@@ -121,9 +123,10 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  * rows, mbq_gemm_plan reports how mbq_matmul / mbq_int8_linear would run a (N, K) weight of type t (MBQ_INT8 for the
  * int8 linear): the kernel (MBQ_KERNEL_*), *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses
  * the per-device workspace below).
- *   MBQ_KERNEL_GEMV    M <= 4, bm = bn = splits = 0.
- *   MBQ_KERNEL_STREAM  weight-stream kernel, 5 <= M <= 64: bm = 16, bn = weight rows per block (64 or 128); from
- *                      17 rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
+ *   MBQ_KERNEL_GEMV    M <= 4 on rows the GEMV's registers hold, bm = bn = splits = 0.
+ *   MBQ_KERNEL_STREAM  weight-stream kernel, M <= 64 (M <= 4 when the GEMV has no plan: e.g. K = 17408 at 3-4 rows,
+ *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
+ *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
  *   MBQ_KERNEL_DIRECT  weight-direct kernel of large batches: 256x{256,192,128}, 128x{320,256,128}; splits = 1.
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
@@ -131,7 +134,8 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  * its own tile choice).
  * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
  * counters), allocated by the first such call on a device and kept until the process ends; GEMM calls on one device
- * that overlap in time must not both split K. */
+ * that overlap in time must not both split K. That first call cannot run on a stream that is capturing a HIP graph: it
+ * returns MBQ_E_ARG and launches nothing (make one eager call on the device before capturing). */
 #define MBQ_KERNEL_AUTO 0
 #define MBQ_KERNEL_GEMV 0
 #define MBQ_KERNEL_STREAM 1

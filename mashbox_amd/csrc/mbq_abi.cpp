@@ -301,6 +301,24 @@ static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t
     return 0;
 }
 
+// launch_matmul over row chunks of x whose bytes stay within one buffer resource's range (a chunk of rows is an
+// independent product; every row is computed exactly as in one launch)
+static int launch_rows(int t, Args a, hipStream_t s) {
+    const int64_t rows = std::max<int64_t>(1, BUF_MAX_BYTES / (a.K * 2));
+    if (a.M <= rows) return launch_matmul(t, a, s);
+    const int64_t M = a.M;
+    const uint16_t* x = a.x;
+    uint8_t* y = static_cast<uint8_t*>(a.y);
+    const int64_t ybytes = a.out_bf16 ? 2 : 4;
+    for (int64_t m0 = 0; m0 < M; m0 += rows) {
+        a.M = std::min(rows, M - m0);
+        a.x = x + m0 * a.K;
+        a.y = y + m0 * a.N * ybytes;
+        if (int rc = launch_matmul(t, a, s)) return rc;
+    }
+    return 0;
+}
+
 }  // namespace mbq
 
 using namespace mbq;
@@ -321,7 +339,13 @@ int64_t mbq_row_bytes(int t, int64_t cols) {
     return cols / block_values(t) * block_bytes(t);
 }
 
-int mbq_covers(int t, int64_t rows, int64_t cols) { return check_shape(t, rows, cols) == 0 ? 1 : 0; }
+// Every kernel addresses one weight's planes through a buffer resource (32-bit offsets): weights whose planes exceed
+// BUF_MAX_BYTES are refused at every batch size, so they are not covered. Activations are cut into row chunks within
+// that range by mbq_matmul, so every batch size of a covered weight runs.
+int mbq_covers(int t, int64_t rows, int64_t cols) {
+    if (check_shape(t, rows, cols) != 0) return 0;
+    return layout(t, rows, cols).total <= BUF_MAX_BYTES ? 1 : 0;
+}
 
 int64_t mbq_plane_bytes(int t, int64_t rows, int64_t cols) {
     if (int rc = check_shape(t, rows, cols)) return rc;
@@ -372,7 +396,7 @@ int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* l
     a.M = M;
     a.y = y_dev;
     a.out_bf16 = out_dtype == MBQ_OUT_BF16;
-    return launch_matmul(t, a, reinterpret_cast<hipStream_t>(stream));
+    return launch_rows(t, a, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
@@ -412,7 +436,7 @@ int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_d
     a.K = K;
     a.y = y_dev;
     a.out_bf16 = out_dtype == MBQ_OUT_BF16;
-    return launch_matmul(T_INT8, a, reinterpret_cast<hipStream_t>(stream));
+    return launch_rows(T_INT8, a, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D, const int32_t* toks_dev, int64_t T,
@@ -439,14 +463,19 @@ int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, 
         return rc;
     }
     if (M < 0 || M > INT32_MAX) return set_error(MBQ_BAD_ARG, "M = %lld", (long long)M);
-    if (M <= GEMV_MAX_M) {
-        *kernel = *bm = *bn = *splits = 0;
+    if (M == 0) {
+        *kernel = *bm = *bn = *splits = 0;                                   // nothing is launched
         return MBQ_OK;
     }
     Args a{};
-    a.M = M;
+    a.M = std::min<int64_t>(M, std::max<int64_t>(1, BUF_MAX_BYTES / (K * 2)));   // the row chunk mbq_matmul launches
     a.N = N;
     a.K = K;
+    a.wbytes = t == T_INT8 ? N * K : layout(t, N, K).total;
+    if (a.M <= GEMV_MAX_M && gemv_runs(t, a)) {
+        *kernel = *bm = *bn = *splits = 0;
+        return MBQ_OK;
+    }
     return gemm_plan(t, a, kernel, bm, bn, splits);
 }
 

@@ -627,8 +627,10 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
 // ------------------------------------------------------------------------------------------------- workspace
 // Split-K partials and arrival counters, one set per device, allocated (and the counters cleared) by the first GEMM
 // call that splits K on that device and kept until the process ends. GEMM calls on one device that overlap in time
-// (two streams) must not both split K; the dispatcher sizes splits to fit the fixed size.
-int workspace(Workspace* out) {
+// (two streams) must not both split K; the dispatcher sizes splits to fit the fixed size. The allocation cannot be
+// recorded into a HIP graph: a first split-K call on a stream that is capturing is refused with an error (nothing is
+// launched), so that a caller makes one eager call before capturing.
+int workspace(Workspace* out, hipStream_t s) {
     static Workspace per_dev[64];
     static std::mutex mu;
     int dev = 0;
@@ -636,6 +638,10 @@ int workspace(Workspace* out) {
     std::lock_guard<std::mutex> lk(mu);
     Workspace& w = per_dev[dev];
     if (!w.ws) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return set_error(MBQ_BAD_ARG, "GEMM: the first split-K call on device %d allocates its workspace, which a "
+                                          "stream being captured into a graph cannot do: make one eager call first", dev);
         void *p = nullptr, *c = nullptr;
         if (hipMalloc(&p, WS_BYTES) != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
         // the counters are zeroed on the null stream and waited for here, once: the first kernel that uses them may run
@@ -699,19 +705,6 @@ static int launch_k(const Args& a, int S, int kts, const Workspace& w, hipStream
         if (BM == SG_BM && BN == SG_BN && S == 1) return (a.K % GK == 0) ? launch_sg<T, true>(a, s) : launch_sg<T, false>(a, s);
         return (a.K % GK == 0) ? launch_tile<T, BM, BN, P, true>(a, S, kts, w, s) : launch_tile<T, BM, BN, P, false>(a, S, kts, w, s);
     }
-}
-
-// compute units of the current device (cached per device)
-static int cu_count() {
-    static int cache[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cache[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cache[dev] = n;
-    }
-    return cache[dev];
 }
 
 struct Plan { int idx, S, kts; };
@@ -834,7 +827,7 @@ static int find_cand(int bm, int bn) {
 
 template <int T>
 static int pick(const Args& a, Plan* p) {
-    *p = plan_gemm<T>(a.M, a.N, a.K, cu_count());
+    *p = plan_gemm<T>(a.M, a.N, a.K, cus_of_device());
     if (g_force_kind.load() == K_TILES && g_force_bm.load() > 0) {
         const int fbm = g_force_bm.load(), fbn = g_force_bn.load(), fs = g_force_s.load();
         const int i = find_cand<T>(fbm, fbn);
@@ -849,15 +842,15 @@ static int pick(const Args& a, Plan* p) {
     return 0;
 }
 
-// The kernel of a batch of M > GEMV_MAX_M rows: the weight-stream kernel (mbq_wsgemm.hip) up to WS_MAX_M rows, else the
+// The kernel of a batch the GEMV does not run: the weight-stream kernel (mbq_wsgemm.hip) up to WS_MAX_M rows, else the
 // LDS-tile kernel; a forced plan overrides it (and is the only way to the weight-direct kernel, mbq_pgemm.hip).
 struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block; K_DIRECT: bm = 16 mt, bn = 64 nt
 
 static int choose(int t, const Args& a, Choice* c) {
     const int fk = g_force_kind.load();
     if (fk == K_STREAM) {
-        if (a.M <= GEMV_MAX_M || a.M > WS_MAX_M)
-            return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs %lld < M <= %lld", (long long)GEMV_MAX_M, (long long)WS_MAX_M);
+        if (a.M > WS_MAX_M)
+            return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
         return 0;
     }
@@ -878,7 +871,8 @@ static int choose(int t, const Args& a, Choice* c) {
     // 16 < M <= 64 over a weight whose 64-row tiles alone fill the CUs (the weight-stream kernel would run 128-row
     // blocks): the LDS-tile kernel's 64 x 128 tiles are faster (MI355X, N = 17408, K = 5120, M = 64: int8 45 vs 52 us,
     // Q8_0 59 vs 73, Q4_K 51 vs 57, Q6_K 54 vs 79; M = 16 keeps the weight stream, 41 vs 43 us int8)
-    if (a.M <= WS_MAX_M && !(a.M > 16 && (a.N + 63) / 64 >= cu_count())) {
+    // M <= GEMV_MAX_M arrives here only when the GEMV has no plan for the shape (launch_t): the weight stream takes it
+    if (a.M <= WS_MAX_M && !(a.M > 16 && (a.N + 63) / 64 >= cus_of_device())) {
         int nr = 0, S = 1;
         wsgemm_plan(t, a, &nr, &S);
         *c = Choice{K_STREAM, 16, nr, S};
@@ -902,7 +896,7 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
     if (p.S > 1)
-        if (int rc = workspace(&w)) return rc;
+        if (int rc = workspace(&w, s)) return rc;
     return CANDS<T>[p.idx].launch(a, p.S, p.kts, w, s);
 }
 

@@ -447,30 +447,47 @@ static int gv_pack(int64_t U) {
     return (U == 80 && 4 * U <= 64 * gv_chmax<T>(1)) ? 4 : 1;
 }
 
+// The GEMV's plan for a call: rows per item R (4 for 80-unit rows at one activation row, else 1), parts S, units per
+// part PU and chunks per item CH; false when the GEMV does not run the shape (operands over the buffer range, a row
+// too long for the activation rows' registers, or the parts' sums over the LDS of one block). mbq_matmul then runs the
+// weight-stream kernel, which takes any K.
+struct GvPlan { int R, S, PU, CH; };
 template <int T, int M>
-static int launch_gemv_m(const Args& a, hipStream_t s) {
-    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
-        return set_error(MBQ_BAD_ARG, "GEMV operands over 2 GiB");
-    if constexpr (M == 1) {
-        const int64_t U = a.K / gv_uw<T>();
-        const int r = gv_pack<T>(U);
-        if (r > 1) {
-            return launch_gemv_ch<T, 1, 5, 4>(a, 1, (int)(r * U), s);      // 4 rows of 80 units: 5 chunks
-        }
+static bool gv_plan(const Args& a, GvPlan* p) {
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES) return false;
+    const int64_t U = a.K / gv_uw<T>();
+    if (M == 1 && gv_pack<T>(U) > 1) {
+        *p = GvPlan{gv_pack<T>(U), 1, (int)(gv_pack<T>(U) * U), 5};         // 4 rows of 80 units: 5 chunks
+        return true;
     }
     int S = 1, PU = 0;
-    const int ch = gv_parts<T, M>(a.K / gv_uw<T>(), &S, &PU);
-    if (ch < 1) return set_error(MBQ_BAD_ARG, "GEMV K = %lld is too long for %d activation rows", (long long)a.K, M);
-    constexpr int C = gv_chmax<T>(M);
-    switch (ch) {
-        case 1: return launch_gemv_ch<T, M, 1>(a, S, PU, s);
-        case 2: if constexpr (C >= 2) return launch_gemv_ch<T, M, 2>(a, S, PU, s); break;
-        case 3: if constexpr (C >= 3) return launch_gemv_ch<T, M, 3>(a, S, PU, s); break;
-        case 4: if constexpr (C >= 4) return launch_gemv_ch<T, M, 4>(a, S, PU, s); break;
-        case 5: if constexpr (C >= 5) return launch_gemv_ch<T, M, 5>(a, S, PU, s); break;
-        case 6: if constexpr (C >= 6) return launch_gemv_ch<T, M, 6>(a, S, PU, s); break;
+    const int ch = gv_parts<T, M>(U, &S, &PU);
+    if (ch < 1) return false;
+    // the parts' sums of a block's rows in LDS: at most ceil(N / min(CUs, N)) rows per block
+    const int64_t blocks = std::min<int64_t>(cus_of_device(), a.N), rows_max = (a.N + blocks - 1) / blocks;
+    if (S > 1 && rows_max * S * M * 4 > 64 * 1024) return false;
+    *p = GvPlan{1, S, PU, ch};
+    return true;
+}
+
+template <int T, int M>
+static int launch_gemv_m(const Args& a, hipStream_t s) {
+    GvPlan p;
+    if (!gv_plan<T, M>(a, &p)) return set_error(MBQ_BAD_ARG, "GEMV has no plan for K = %lld at %d activation rows", (long long)a.K, M);
+    if (p.R > 1) {
+        if constexpr (M == 1) return launch_gemv_ch<T, 1, 5, 4>(a, 1, p.PU, s);
+        return set_error(MBQ_BAD_ARG, "GEMV: packed rows at %d activation rows", M);
     }
-    return set_error(MBQ_BAD_ARG, "GEMV: no kernel for %d chunks", ch);
+    constexpr int C = gv_chmax<T>(M);
+    switch (p.CH) {
+        case 1: return launch_gemv_ch<T, M, 1>(a, p.S, p.PU, s);
+        case 2: if constexpr (C >= 2) return launch_gemv_ch<T, M, 2>(a, p.S, p.PU, s); break;
+        case 3: if constexpr (C >= 3) return launch_gemv_ch<T, M, 3>(a, p.S, p.PU, s); break;
+        case 4: if constexpr (C >= 4) return launch_gemv_ch<T, M, 4>(a, p.S, p.PU, s); break;
+        case 5: if constexpr (C >= 5) return launch_gemv_ch<T, M, 5>(a, p.S, p.PU, s); break;
+        case 6: if constexpr (C >= 6) return launch_gemv_ch<T, M, 6>(a, p.S, p.PU, s); break;
+    }
+    return set_error(MBQ_BAD_ARG, "GEMV: no kernel for %d chunks", p.CH);
 }
 
 template <int T>
@@ -479,8 +496,9 @@ static int launch_gemv_t(const Args& a, hipStream_t s) {
         case 1: return launch_gemv_m<T, 1>(a, s);
         case 2: return launch_gemv_m<T, 2>(a, s);
         case 3: return launch_gemv_m<T, 3>(a, s);
-        default: return launch_gemv_m<T, 4>(a, s);
+        case 4: return launch_gemv_m<T, 4>(a, s);
     }
+    return set_error(MBQ_BAD_ARG, "GEMV: M = %lld", (long long)a.M);
 }
 
 int launch_gemv(int t, const Args& a, hipStream_t s) {
@@ -493,6 +511,30 @@ int launch_gemv(int t, const Args& a, hipStream_t s) {
         case T_INT8: return launch_gemv_t<T_INT8>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMV for type %d", t);
+}
+
+template <int T>
+static bool gemv_runs_t(const Args& a) {
+    GvPlan p;
+    switch (a.M) {
+        case 1: return gv_plan<T, 1>(a, &p);
+        case 2: return gv_plan<T, 2>(a, &p);
+        case 3: return gv_plan<T, 3>(a, &p);
+        case 4: return gv_plan<T, 4>(a, &p);
+    }
+    return false;
+}
+
+bool gemv_runs(int t, const Args& a) {
+    switch (t) {
+        case T_Q4_0: return gemv_runs_t<T_Q4_0>(a);
+        case T_Q8_0: return gemv_runs_t<T_Q8_0>(a);
+        case T_Q4_K: return gemv_runs_t<T_Q4_K>(a);
+        case T_Q5_K: return gemv_runs_t<T_Q5_K>(a);
+        case T_Q6_K: return gemv_runs_t<T_Q6_K>(a);
+        case T_INT8: return gemv_runs_t<T_INT8>(a);
+    }
+    return false;
 }
 
 }  // namespace mbq

@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "mbq_device.h"
 #include "mbq_launch.h"
@@ -373,9 +374,24 @@ static int check_launch(const char* what) {
     return 0;
 }
 
+// Decode batches (M <= GEMV_MAX_M) run the GEMV when it has a plan for the shape; a row too long for the activation
+// rows' registers (e.g. K = 17408 at 3-4 rows, or a Q8_0 / int8 K over 24576) runs the weight-stream kernel instead,
+// which takes any K (launch_gemm routes M <= GEMV_MAX_M there).
 template <int T>
 static int launch_t(const Args& a, hipStream_t s) {
-    return a.M <= GEMV_MAX_M ? launch_gemv(T, a, s) : launch_gemm(T, a, s);
+    return a.M <= GEMV_MAX_M && gemv_runs(T, a) ? launch_gemv(T, a, s) : launch_gemm(T, a, s);
+}
+
+int cus_of_device() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 int launch_matmul(int t, const Args& a, hipStream_t s) {

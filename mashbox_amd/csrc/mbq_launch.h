@@ -11,8 +11,6 @@ enum : int { MBQ_BAD_ARG = -1, MBQ_LAUNCH_FAIL = -2, MBQ_SMALL_CAP = -3 };
 
 // activation rows up to which the GEMV runs; more rows take the MFMA GEMM
 constexpr int64_t GEMV_MAX_M = 4;
-// activations (M x K bfloat16) up to this many bytes are staged in LDS by the GEMV; larger ones are read from the caches
-constexpr int64_t GEMV_MAX_LDS = 64 * 1024;
 
 struct Args {
     const uint8_t* base;       // planes of the weight (layer already applied when the layer is a host value)
@@ -35,7 +33,7 @@ struct Args {
 constexpr size_t WS_BYTES = (size_t)64 << 20;
 constexpr int WS_TILES = 1 << 16;
 struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
-int workspace(Workspace* out);
+int workspace(Workspace* out, hipStream_t s);   // refused while s is capturing and nothing is allocated yet
 
 // largest weight plane or activation range a kernel addresses through a buffer resource (32-bit offsets; below the
 // out-of-range offset OOB_VOFF of mbq_device.h)
@@ -57,8 +55,12 @@ inline hipError_t set_lds_limit(const void* kernel, size_t lds, std::atomic<uint
     return e;
 }
 
+// compute units of the current device (cached per device; 256 if the query fails)
+int cus_of_device();
+
 int launch_matmul(int t, const Args& a, hipStream_t s);
 int launch_gemv(int t, const Args& a, hipStream_t s);   // M <= GEMV_MAX_M (mbq_gemv.hip)
+bool gemv_runs(int t, const Args& a);                   // the GEMV has a plan for this call (else the weight stream runs it)
 int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
 // weight-stream GEMM (mbq_wsgemm.hip) for GEMV_MAX_M < M <= WS_MAX_M: rows_per_block 32 or 64, splits >= 1
 constexpr int64_t WS_MAX_M = 64;

@@ -1,5 +1,5 @@
-// gfx950 weight-stream GEMM of the quantized linear for small activation batches (GEMV_MAX_M < M <= WS_MAX_M): the
-// batched-decode regime.
+// gfx950 weight-stream GEMM of the quantized linear for small activation batches (M <= WS_MAX_M): the batched-decode
+// regime, and decode batches whose rows are too long for the GEMV's registers.
 //
 // y (M, N) = x (M, K) @ W.T with W dequantized on the fly: reference src/mashbox/ops/__init__.py:594-632 (qmatmul,
 // float32 accumulation) on the weights of reference src/mashbox/ops/reference.py:101-103 (Q8_0), :132-149 (Q4_K) and
@@ -300,17 +300,6 @@ static int ws_launch_m(const Args& a, int S, int kts, const Workspace& w, hipStr
     }
 }
 
-static int cus_now() {
-    static int cache[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cache[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cache[dev] = n;
-    }
-    return cache[dev];
-}
 
 // float32 bytes of one block's partial tile
 static size_t ws_partial_bytes(int64_t M, int nr) { return (size_t)((M + 15) / 16) * (nr / 64) * 1024 * 4; }
@@ -337,7 +326,7 @@ static void ws_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int* nr, 
 }
 
 int wsgemm_plan(int t, const Args& a, int* rows_per_block, int* splits) {
-    ws_choose(t, a.M, a.N, a.K, cus_now(), rows_per_block, splits);
+    ws_choose(t, a.M, a.N, a.K, cus_of_device(), rows_per_block, splits);
     return 0;
 }
 
@@ -349,7 +338,7 @@ void wsgemm_effective(int t, const Args& a, int* nr, int* S) {
 }
 
 int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
-    if (a.M <= GEMV_MAX_M || a.M > WS_MAX_M) return set_error(MBQ_BAD_ARG, "weight-stream GEMM: M = %lld", (long long)a.M);
+    if (a.M < 1 || a.M > WS_MAX_M) return set_error(MBQ_BAD_ARG, "weight-stream GEMM: M = %lld", (long long)a.M);
     if (nr != 64 && nr != 128) return set_error(MBQ_BAD_ARG, "weight-stream GEMM: %d rows per block (64 or 128)", nr);
     wsgemm_effective(t, a, &nr, &S);
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES)
@@ -361,7 +350,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
     if (S > 1) {
         if (tiles > WS_TILES || (size_t)tiles * S * ws_partial_bytes(a.M, nr) > WS_BYTES)
             return set_error(MBQ_BAD_ARG, "weight-stream GEMM: %lld tiles x %d splits do not fit the workspace", (long long)tiles, S);
-        if (int rc = workspace(&w)) return rc;
+        if (int rc = workspace(&w, s)) return rc;
     }
     switch (t) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);

@@ -40,3 +40,21 @@ def assert_product(y, ref, what=""):
     nmse, mr = product_errors(y, ref)
     assert nmse <= NMSE_BF16 and mr <= MAX_REL, f"{what}: NMSE {nmse:.3e} (bar {NMSE_BF16}), max rel {mr:.3e} (bar {MAX_REL})"
     return nmse, mr
+
+
+def assert_product_dev(y, ref, what=""):
+    """assert_product on GPU tensors (torch, any float dtype; ref float64): every output finite, NMSE and max-rel
+    computed in float64 on the device, so full-size outputs are compared whole without a host copy"""
+    import torch
+    y = y.to(torch.float64)
+    ref = ref.to(torch.float64)
+    assert tuple(y.shape) == tuple(ref.shape), (tuple(y.shape), tuple(ref.shape))
+    assert bool(torch.isfinite(y).all()), f"{what}: non-finite output"
+    den = float((ref * ref).sum())
+    if den == 0.0:
+        assert bool((y == 0).all()), f"{what}: reference is exactly zero, output is not"
+        return 0.0, 0.0
+    nmse = float(((y - ref) ** 2).sum()) / den
+    mr = float((y - ref).abs().max() / ref.abs().max())
+    assert nmse <= NMSE_BF16 and mr <= MAX_REL, f"{what}: NMSE {nmse:.3e} (bar {NMSE_BF16}), max rel {mr:.3e} (bar {MAX_REL})"
+    return nmse, mr
