@@ -8,8 +8,9 @@
  * Conventions
  *   - Plain pointers and sizes only. "dev" pointers are device (HBM) addresses owned by the caller; "host" pointers are
  *     host memory. Every device entry point is stream-ordered on `stream` (a hipStream_t; NULL = the default stream)
- *     and returns before the work finishes; none allocates, except the GEMM's one-time split-K workspace (see
- *     mbq_gemm_plan), and none holds a host lock.
+ *     and returns before the work finishes; none allocates, except the GEMM's one-time split-K workspace of
+ *     mbq_matmul and mbq_int8_linear (see mbq_gemm_plan; mbq_matmul_noalloc never allocates), and none holds a host
+ *     lock.
  *   - Matrices are row-major. Activations x are bfloat16 bits (uint16) of shape (M, K); results y are (M, N) as
  *     float32 (out_dtype MBQ_OUT_F32) or bfloat16 bits rounded to nearest even (MBQ_OUT_BF16).
  *   - Weights have N rows (outputs) and K columns (inputs), as the GGUF reader orders them (reference
@@ -93,6 +94,17 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
  * call contract src/mashbox/ops/bundle.py:559-598: x as bf16, f32 result). */
 int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
                const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream);
+
+/* mbq_matmul for callers that cannot allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. No counterpart in the reference. It runs the same plans and kernels as mbq_matmul, with identical results,
+ * and calls no hipMalloc, hipFree or allocating library routine: a batch that splits K keeps its float32 partial tiles
+ * and arrival counters in the library's static scratch array (16 MiB of partials and 4096 counters; every GPU the
+ * library runs on holds its own copy until the process ends), instead of mbq_matmul's allocated workspace. A plan whose
+ * partials exceed the scratch (none of the automatic plans on up to 256 CUs; a forced plan can) returns MBQ_E_ARG and
+ * launches nothing. Every call on one GPU shares that GPU's scratch: calls that overlap in time on one GPU (two streams)
+ * race, and must not both split K. */
+int mbq_matmul_noalloc(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                       const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream);
 
 /* W (N, K) float32 from the planes of one weight (layer / layer_dev as in mbq_matmul). Bit for bit the reference
  * dequantization (NaN where it has NaN). Replaces dequant(planes) (reference src/mashbox/ops/__init__.py:20,691-705). */

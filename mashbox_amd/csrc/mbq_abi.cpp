@@ -323,6 +323,10 @@ static int launch_rows(int t, Args a, hipStream_t s) {
 
 using namespace mbq;
 
+static int matmul_call(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                       const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream,
+                       bool noalloc);
+
 extern "C" {
 
 int mbq_version(void) { return 100; }
@@ -385,7 +389,23 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
 
 int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
                const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream) {
+    return matmul_call(t, planes_dev, layer, layer_dev, nlayers, x_dev, M, N, K, y_dev, out_dtype, stream, false);
+}
+
+// mbq_matmul with every split-K partial in the library's static scratch array instead of the allocated workspace: the
+// same plans, kernels and results, and no allocation on any call
+int mbq_matmul_noalloc(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                       const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream) {
+    return matmul_call(t, planes_dev, layer, layer_dev, nlayers, x_dev, M, N, K, y_dev, out_dtype, stream, true);
+}
+
+}  // extern "C"
+
+static int matmul_call(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                       const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev, int out_dtype, void* stream,
+                       bool noalloc) {
     Args a{};
+    a.noalloc = noalloc;
     if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
     if (int rc = check_out(out_dtype)) return rc;
     if (M < 0 || M > INT32_MAX) return set_error(MBQ_BAD_ARG, "M = %lld", (long long)M);
@@ -398,6 +418,8 @@ int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* l
     a.out_bf16 = out_dtype == MBQ_OUT_BF16;
     return launch_rows(t, a, reinterpret_cast<hipStream_t>(stream));
 }
+
+extern "C" {
 
 int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
                 int64_t K, float* w_dev, void* stream) {

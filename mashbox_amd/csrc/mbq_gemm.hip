@@ -212,6 +212,7 @@ struct GemmArgs {
     int S, kts;                 // K splits and K steps per split
     float* ws;                  // S > 1: partial tiles, BM x BN floats per (tile, split)
     int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
+    uint32_t ws_bytes;          // S > 1: bytes of ws
 };
 
 // Pipeline of depth P (1 or 3): x is DMA'd P steps ahead into P + 1 LDS stages, weight units are loaded into P + 1
@@ -370,7 +371,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
         // this split's partial tile, in the lanes' own layout, stored and read with sc1 (device-coherent) buffer
         // accesses: written through the XCD's L2, so the block that arrives last reads every split's partial without an
         // L2-wide fence (__threadfence writes back and invalidates the whole L2 on gfx950)
-        const rsrc_t pr = make_rsrc(g.ws, (uint32_t)WS_BYTES);
+        const rsrc_t pr = make_rsrc(g.ws, g.ws_bytes);
         constexpr uint32_t E = (uint32_t)BM * BN * 4u;                  // bytes of one partial tile
         const uint32_t lofs = (uint32_t)((wave * TI * TJ) * 64 + lane) * 16u;
 #pragma unroll
@@ -654,9 +655,56 @@ int workspace(Workspace* out, hipStream_t s) {
         }
         w.ws = static_cast<float*>(p);
         w.cnt = static_cast<int*>(c);
+        w.bytes = WS_BYTES;
+        w.tiles = WS_TILES;
     }
     *out = w;
     return 0;
+}
+
+// --------------------------------------------------------------------------------------------------- scratch
+// The split-K partials and arrival counters of mbq_matmul_noalloc, for callers that cannot allocate (code under HIP
+// graph capture, serving loops, harnesses that forbid hipMalloc): one static device array, which every GPU the library
+// runs on holds at its own address until the process ends. Its SCRATCH_BYTES of partial tiles cover every automatic
+// split plan on up to 256 CUs: the weight stream splits only while its tiles x splits fit the CUs (at most 256 blocks
+// of 16 KiB at 64 activation rows), the LDS tiles while tiles x splits stay within two blocks per CU (at most 512
+// partial tiles of 64 x 128 floats, 32 KiB each); a plan that needs more is refused. In host code the name `scratch`
+// is not a device address: the address is taken once per device with hipGetSymbolAddress and used from then on.
+constexpr size_t SCRATCH_BYTES = (size_t)16 << 20;
+constexpr int SCRATCH_TILES = 4096;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES + SCRATCH_TILES * sizeof(int)];
+
+// the scratch's device address on the current device, set up once per device: the address from hipGetSymbolAddress
+// (the current device's copy of the array), and the arrival counters cleared by a fill kernel on the caller's stream
+// (they must start at zero; each split-K launch leaves the counters it used at zero)
+static int scratch_workspace(hipStream_t s, Workspace* out) {
+    static void* addr[64] = {};
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MBQ_LAUNCH_FAIL, "GEMM: no device");
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return set_error(MBQ_LAUNCH_FAIL, "GEMM: the scratch array's address on device %d: %s", dev, hipGetErrorString(e));
+        if (int rc = launch_zero(static_cast<uint8_t*>(p) + SCRATCH_BYTES, (int64_t)SCRATCH_TILES * sizeof(int), s)) return rc;
+        addr[dev] = p;
+    }
+    out->ws = static_cast<float*>(addr[dev]);
+    out->cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(addr[dev]) + SCRATCH_BYTES);
+    out->bytes = SCRATCH_BYTES;
+    out->tiles = SCRATCH_TILES;
+    return 0;
+}
+
+int split_workspace(const Args& a, int64_t tiles, size_t bytes, hipStream_t s, Workspace* out) {
+    const size_t cap = a.noalloc ? SCRATCH_BYTES : WS_BYTES;
+    const int ntiles = a.noalloc ? SCRATCH_TILES : WS_TILES;
+    if (tiles > ntiles || bytes > cap)                                // checked before any set-up: nothing launches
+        return set_error(MBQ_BAD_ARG, "GEMM: a split-K plan of %lld tiles and %zu partial bytes exceeds the %s (%d tiles, %zu bytes)",
+                         (long long)tiles, bytes, a.noalloc ? "scratch of mbq_matmul_noalloc" : "workspace", ntiles, cap);
+    return a.noalloc ? scratch_workspace(s, out) : workspace(out, s);
 }
 
 // ------------------------------------------------------------------------------------------------- launchers
@@ -671,7 +719,7 @@ static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStr
     if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
         return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
     GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
-               (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt};
+               (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes};
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     kern<<<dim3((unsigned)(tiles * S)), GT, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -686,7 +734,7 @@ static int launch_sg(const Args& a, hipStream_t s) {
     if (set_lds_limit((const void*)kern, SG_LDS, lds_set) != hipSuccess)
         return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", SG_LDS);
     GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
-               (int)a.N, (int)a.K, a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr};
+               (int)a.N, (int)a.K, a.y, a.out_bf16, 1, (int)((a.K + GK - 1) / GK), nullptr, nullptr, 0u};
     const int64_t tiles = ((a.M + SG_BM - 1) / SG_BM) * ((a.N + SG_BN - 1) / SG_BN);
     kern<<<dim3((unsigned)tiles), GT, SG_LDS, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -895,8 +943,10 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
-    if (p.S > 1)
-        if (int rc = workspace(&w, s)) return rc;
+    if (p.S > 1) {
+        const int64_t tiles = ((a.M + CANDS<T>[p.idx].bm - 1) / CANDS<T>[p.idx].bm) * ((a.N + CANDS<T>[p.idx].bn - 1) / CANDS<T>[p.idx].bn);
+        if (int rc = split_workspace(a, tiles, (size_t)tiles * p.S * CANDS<T>[p.idx].bm * CANDS<T>[p.idx].bn * 4, s, &w)) return rc;
+    }
     return CANDS<T>[p.idx].launch(a, p.S, p.kts, w, s);
 }
 

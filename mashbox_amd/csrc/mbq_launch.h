@@ -25,6 +25,7 @@ struct Args {
     int64_t M, N, K;
     void* y;
     int out_bf16;
+    bool noalloc = false;      // mbq_matmul_noalloc: split-K partials in the static scratch array, never allocated
 };
 
 // Split-K partials and arrival counters of the GEMM kernels, one set per device (mbq_gemm.hip): WS_BYTES of float32
@@ -32,8 +33,12 @@ struct Args {
 // and kept until the process ends. Every kernel that uses them leaves the counters it touched at zero.
 constexpr size_t WS_BYTES = (size_t)64 << 20;
 constexpr int WS_TILES = 1 << 16;
-struct Workspace { float* ws = nullptr; int* cnt = nullptr; };
+struct Workspace { float* ws = nullptr; int* cnt = nullptr; size_t bytes = 0; int tiles = 0; };
 int workspace(Workspace* out, hipStream_t s);   // refused while s is capturing and nothing is allocated yet
+// The workspace of a split-K launch whose partial tiles take `bytes` over `tiles` arrival counters: the static scratch
+// array when a.noalloc (mbq_matmul_noalloc; never allocated), else the allocated per-device workspace. An error, with
+// nothing launched, when the plan does not fit it.
+int split_workspace(const Args& a, int64_t tiles, size_t bytes, hipStream_t s, Workspace* out);
 
 // largest weight plane or activation range a kernel addresses through a buffer resource (32-bit offsets; below the
 // out-of-range offset OOB_VOFF of mbq_device.h)

@@ -65,6 +65,7 @@ struct WsArgs {
     int S, kts;                 // K splits and iterations per split
     float* ws;                  // S > 1: partial tiles, one block's outputs per (tile, split)
     int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
+    uint32_t ws_bytes;          // S > 1: bytes of ws
 };
 
 template <int T, int MT, int NT, bool KFULL>
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
     if (g.S > 1) {
         // 16-byte element ((w MT + i) NT + j) 64 + lane of the block's partial tile, in the lanes' own layout, stored and
         // read with sc1 (device-coherent) buffer accesses, which the compiler batches
-        const rsrc_t pr = make_rsrc(g.ws, (uint32_t)WS_BYTES);
+        const rsrc_t pr = make_rsrc(g.ws, g.ws_bytes);
         const uint32_t mine = (uint32_t)((tile * g.S + kz) * E) * 4u, part = (uint32_t)E * 4u;
         const uint32_t lofs = (uint32_t)((wave * MT * NT) * 64 + lane) * 16u;
 #pragma unroll
@@ -272,7 +273,7 @@ static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStrea
     if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
         return set_error(MBQ_LAUNCH_FAIL, "weight-stream GEMM: %zu bytes of LDS refused", lds);
     WsArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
-             a.y, a.out_bf16, S, kts, w.ws, w.cnt};
+             a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes};
     const int64_t tiles = (a.N + 64 * NT - 1) / (64 * NT);
     kern<<<dim3((unsigned)(tiles * S)), WS_THREADS, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
@@ -347,11 +348,8 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
     const int64_t kts = (KT + S - 1) / S;
     const int64_t tiles = (a.N + nr - 1) / nr;
     Workspace w;
-    if (S > 1) {
-        if (tiles > WS_TILES || (size_t)tiles * S * ws_partial_bytes(a.M, nr) > WS_BYTES)
-            return set_error(MBQ_BAD_ARG, "weight-stream GEMM: %lld tiles x %d splits do not fit the workspace", (long long)tiles, S);
-        if (int rc = workspace(&w, s)) return rc;
-    }
+    if (S > 1)
+        if (int rc = split_workspace(a, tiles, (size_t)tiles * S * ws_partial_bytes(a.M, nr), s, &w)) return rc;
     switch (t) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);
         case T_Q4_0: return nr == 64 ? ws_launch_m<T_Q4_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_0, 2>(a, S, (int)kts, w, s);

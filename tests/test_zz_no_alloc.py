@@ -1,0 +1,85 @@
+"""mbq_matmul_noalloc, through the C ABI: the entry point that allocates nothing (its split-K partials live in the
+library's static scratch array) equals mbq_matmul bit for bit on the same inputs, and both meet the product bars against
+the oracle's exact weights. Two calls in a row, the second with a smaller input, each splitting K (LDS tiles, then the
+weight stream); a decode call that needs no scratch; and a forced plan whose partials exceed the scratch, which the
+entry point refuses with an error while mbq_matmul (whose workspace is larger) runs it.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gen as G
+from oracle import ref as R
+from tests._check import assert_product_dev
+
+from mashbox_amd import _lib as LIB
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # (type, activation rows, weight rows, K): the second smaller than the first
+    (R.Q8_0, 64, 17408, 5120),      # LDS tiles 64 x 128, K in 3 ranges: 13.4 MB of partials
+    (R.Q4_K, 16, 1024, 5120),       # weight stream, K in 8 ranges
+    (R.Q5_K, 4, 5120, 17408),       # decode rows too long for the GEMV: weight stream, K in 3 ranges
+    (R.Q6_K, 1, 2048, 2560),        # decode GEMV: no scratch
+]
+
+
+def _call(fn, t, planes, x, m, n, k, y):
+    return fn(t, ctypes.c_void_p(planes.data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()), m, n, k,
+              ctypes.c_void_p(y.data_ptr()), LIB.OUT_F32, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def _case(t, m, n, k, seed, dev):
+    rng = np.random.default_rng(seed)
+    raw = G.RAW[t](rng, n, k)
+    pb = LIB.check(LIB.lib().mbq_plane_bytes(t, n, k), "plane_bytes")
+    host = torch.empty(pb, dtype=torch.uint8)
+    LIB.check(LIB.lib().mbq_repack_host(t, raw.ctypes.data_as(ctypes.c_void_p), n, k, ctypes.c_void_p(host.data_ptr()),
+                                        pb, 0), "repack_host")
+    xb = G.acts(rng, m, k)
+    x = torch.from_numpy(xb.astype(np.int16)).view(torch.bfloat16).to(dev)
+    w64 = torch.from_numpy(R.dequant(raw, t, k)).to(dev).to(torch.float64)
+    return host.to(dev), x, x.to(torch.float64) @ w64.T
+
+
+def test_noalloc_equals_matmul_on_consecutive_calls():
+    dev = torch.device("cuda", 0)
+    L = LIB.lib()
+    for i, (t, m, n, k) in enumerate(CASES):
+        print(f"case {i}: type {t} {m}x{n}x{k} plan {LIB.plan_str(t, m, n, k)}", flush=True)
+        if i < 3:
+            assert LIB.gemm_plan(t, m, n, k)[3] > 1, "the case must split K"
+        planes, x, ref = _case(t, m, n, k, 100 + i, dev)
+        y_ref = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        LIB.check(_call(L.mbq_matmul, t, planes, x, m, n, k, y_ref), "mbq_matmul")
+        LIB.check(_call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y), "mbq_matmul_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), f"case {i}: noalloc differs from mbq_matmul"
+        assert_product_dev(y, ref, f"case {i}")
+        # the same call again: the scratch keeps the last call's contents, and the arrival counters are back at zero
+        y.fill_(float("nan"))
+        LIB.check(_call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y), "mbq_matmul_noalloc again")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), f"case {i}: a repeated call differs"
+
+
+def test_noalloc_refuses_a_plan_beyond_its_scratch():
+    dev = torch.device("cuda", 0)
+    L = LIB.lib()
+    t, m, n, k = R.Q8_0, 64, 17408, 1024
+    planes, x, ref = _case(t, m, n, k, 7, dev)
+    LIB.force_gemm_plan(LIB.KERNEL_TILES, 64, 64, 4)        # 272 tiles x 4 ranges x 16 KiB = 17.8 MB of partials
+    try:
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        rc = _call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y)
+        assert rc == -1 and b"scratch" in L.mbq_last_error()
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(y).all()), "a refused call must launch nothing"
+        LIB.check(_call(L.mbq_matmul, t, planes, x, m, n, k, y), "mbq_matmul")
+        torch.cuda.synchronize()
+        assert_product_dev(y, ref, "forced 64x64/4")
+    finally:
+        LIB.force_gemm_plan()
