@@ -64,7 +64,24 @@ def run_config(idx, steps, warmup, rotate_bytes):
         seed = (1000 * idx if isinstance(idx, int) else 9000) + pi
         x = synth.acts(M, K, seed=seed, device=dev)
         y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        if t == "int8":
+        if t == "int8" and M > 4:
+            # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes)
+            q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
+            pb = check(L.mbq_plane_bytes(LIB.I8T, N, K), "int8 plane_bytes")
+            planes = torch.empty(pb, dtype=torch.uint8, device=dev)
+            check(L.mbq_int8_repack_dev(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(s.data_ptr()), N, K,
+                                        ctypes.c_void_p(planes.data_ptr()),
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "int8 repack")
+            del q, s
+            wbytes = pb
+            copies = max(1, math.ceil(rotate_bytes / wbytes))
+            bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
+
+            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K):
+                return L.mbq_matmul(LIB.I8T, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1,
+                                    ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        elif t == "int8":
             q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
             wbytes = N * K + 4 * N
             copies = max(1, math.ceil(rotate_bytes / wbytes))
@@ -118,7 +135,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
         out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
                                     "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
                                     "rotation_MB": round(copies * wbytes / 1e6, 1),
-                                    "plan": LIB.plan_str(-8 if t == "int8" else t, M, N, K)}
+                                    "plan": LIB.plan_str((LIB.I8T if M > 4 else LIB.INT8) if t == "int8" else t, M, N, K)}
         total_us += us
         total_bytes += ab
         total_flops += fl

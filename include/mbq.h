@@ -37,6 +37,9 @@ extern "C" {
 #define MBQ_Q5_K 13
 #define MBQ_Q6_K 14
 #define MBQ_INT8 (-8)
+/* int8 per-output-channel weights repacked once at load into 16-row tiles (mbq_int8_repack_host / _dev): the planes
+ * mbq_matmul, mbq_matmul_noalloc, mbq_plane_bytes, mbq_covers and mbq_gemm_plan take with this type id */
+#define MBQ_I8T (-9)
 
 #define MBQ_OUT_F32 0
 #define MBQ_OUT_BF16 1
@@ -123,6 +126,19 @@ int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, f
 int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,
                     void* y_dev, int out_dtype, void* stream);
 
+/* Load-time repack of int8 per-output-channel weights (the (rows, cols) int8 quants q, row-major, and the (rows,)
+ * float32 scales s of reference src/mashbox/models/qwen3_8_27b/weights.py:55-74) into planes of type MBQ_I8T: 16-row
+ * tiles whose 16 rows x 64 bytes are one contiguous KiB (the MFMA operand tile the kernels load), then the scales;
+ * cols a multiple of 16, padding zero; mbq_plane_bytes(MBQ_I8T, rows, cols) bytes. mbq_matmul(MBQ_I8T, planes, ...)
+ * then returns (x @ bf16(q).T accumulated in float32) * s, as mbq_int8_linear does on the unpacked weights.
+ * The host form uses up to `threads` host threads (0 = all cores); the device form runs from q and s in HBM
+ * (16-byte aligned q). mbq_int8_unpack_host inverts the host form (q and s back, to prove it lossless). */
+int mbq_int8_repack_host(const int8_t* q, const float* s, int64_t rows, int64_t cols, uint8_t* planes_host, size_t cap,
+                         int threads);
+int mbq_int8_repack_dev(const int8_t* q_dev, const float* s_dev, int64_t rows, int64_t cols, uint8_t* planes_dev,
+                        void* stream);
+int mbq_int8_unpack_host(const uint8_t* planes_host, int64_t rows, int64_t cols, int8_t* q, float* s);
+
 /* int8 embedding rows: y (T, D) = f32(q[r]) * s[r] per token, r = toks[t] (int32, device), plus N when negative and
  * clamped to [0, N - 1] (jax.numpy indexing), then out_dtype (bfloat16 rounded to nearest even, or float32 for a pj
  * hook). q_dev int8 (N, D) row-major, s_dev float32 (N,). Bit for bit the gather of embed(E, toks) for an int8 table
@@ -140,10 +156,8 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
- *   MBQ_KERNEL_DIRECT  weight-direct kernel of large batches: 256x{256,192,128}, 128x{320,256,128}; splits = 1.
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
- * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES or MBQ_KERNEL_DIRECT: that kernel with
- * its own tile choice).
+ * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice).
  * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
  * counters), allocated by the first such call on a device and kept until the process ends; GEMM calls on one device
  * that overlap in time must not both split K. That first call cannot run on a stream that is capturing a HIP graph: it
@@ -152,7 +166,6 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
 #define MBQ_KERNEL_GEMV 0
 #define MBQ_KERNEL_STREAM 1
 #define MBQ_KERNEL_TILES 2
-#define MBQ_KERNEL_DIRECT 3
 int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits);
 int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits);
 

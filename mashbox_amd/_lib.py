@@ -8,7 +8,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("MBQ_LIB", os.path.join(HERE, "libmbq.so"))
 
-Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, INT8 = 2, 8, 12, 13, 14, -8
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, INT8, I8T = 2, 8, 12, 13, 14, -8, -9
 OUT_F32, OUT_BF16 = 0, 1
 
 # every symbol include/mbq.h declares, with its ctypes signature
@@ -32,6 +32,10 @@ _SIGS = {
     "mbq_dequant_raw": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
     "mbq_int8_embed": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_void_p,
                                   _c.c_int, _c.c_void_p]),
+    "mbq_int8_repack_host": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_size_t,
+                                        _c.c_int]),
+    "mbq_int8_repack_dev": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
+    "mbq_int8_unpack_host": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
     "mbq_int8_linear": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                    _c.c_void_p, _c.c_int, _c.c_void_p]),
     "mbq_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64, _c.c_int64, _c.POINTER(_c.c_int),
@@ -42,8 +46,8 @@ _SIGS = {
 
 # GEMM kernels of gemm_plan / force_gemm_plan (MBQ_KERNEL_* of include/mbq.h)
 KERNEL_AUTO = KERNEL_GEMV = 0
-KERNEL_STREAM, KERNEL_TILES, KERNEL_DIRECT = 1, 2, 3
-KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_STREAM: "stream", KERNEL_TILES: "tiles", KERNEL_DIRECT: "direct"}
+KERNEL_STREAM, KERNEL_TILES = 1, 2
+KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_STREAM: "stream", KERNEL_TILES: "tiles"}
 
 
 def gemm_plan(t: int, m: int, n: int, k: int):
@@ -61,7 +65,7 @@ def force_gemm_plan(kernel: int = KERNEL_AUTO, bm: int = 0, bn: int = 0, splits:
 
 
 def plan_str(t: int, m: int, n: int, k: int) -> str:
-    """the plan as text, e.g. 'direct 256x192/1'"""
+    """the plan as text, e.g. 'tiles 256x192/1'"""
     kn, bm, bn, sp = gemm_plan(t, m, n, k)
     return "gemv" if kn == KERNEL_GEMV else f"{KERNEL_NAMES[kn]} {bm}x{bn}/{sp}"
 

@@ -42,6 +42,16 @@ static int check_shape(int t, int64_t rows, int64_t cols) {
     return 0;
 }
 
+// shape rules of an entry point that takes kernel planes: a ggml type's, or the tiled int8 planes' (T_I8T: any rows, a
+// row of whole 16-value units)
+static int check_planes_shape(int t, int64_t rows, int64_t cols) {
+    if (t != T_I8T) return check_shape(t, rows, cols);
+    if (rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX)
+        return set_error(MBQ_BAD_ARG, "int8 shape (%lld, %lld)", (long long)rows, (long long)cols);
+    if (cols % 16) return set_error(MBQ_BAD_ARG, "int8 K = %lld must be a multiple of 16", (long long)cols);
+    return 0;
+}
+
 // run f(row_begin, row_end) over [0, rows) on up to `threads` host threads
 template <class F>
 static void parallel_rows(int64_t rows, int threads, F f) {
@@ -281,7 +291,7 @@ static int check_out(int out_dtype) {
 // resolves the planes of one weight of a stack: host layer -> base pointer; device layer -> kernel argument
 static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
                       int64_t K, Args* a) {
-    if (int rc = check_shape(t, N, K)) return rc;
+    if (int rc = check_planes_shape(t, N, K)) return rc;
     if (!planes || !aligned16(planes)) return set_error(MBQ_BAD_ARG, "planes pointer is NULL or not 16-byte aligned");
     if (nlayers < 1 || nlayers > INT32_MAX) return set_error(MBQ_BAD_ARG, "nlayers %lld must be >= 1", (long long)nlayers);
     if (layer_dev == nullptr && (layer < 0 || layer >= nlayers))
@@ -299,6 +309,41 @@ static int plane_args(int t, const uint8_t* planes, int64_t layer, const int32_t
     a->N = N;
     a->K = K;
     return 0;
+}
+
+// tiled int8 planes (mbq_layout.h): 16-row tiles [t0, t1) from the row-major (N, K) quants and (N,) scales; padding
+// rows and columns zero
+static void i8t_pack_tiles(const int8_t* q, const float* s, int64_t N, int64_t K, uint8_t* planes, const Layout& L,
+                           int64_t t0, int64_t t1) {
+    const int64_t kc_n = (K + 63) / 64;
+    for (int64_t rt = t0; rt < t1; ++rt) {
+        for (int64_t kc = 0; kc < kc_n; ++kc) {
+            uint8_t* blk = planes + L.qs_off + (rt * kc_n + kc) * 1024;
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = rt * 16 + r, c0 = kc * 64, n = row < N ? std::min<int64_t>(64, K - c0) : 0;
+                if (n > 0) memcpy(blk + r * 64, q + row * K + c0, (size_t)n);
+                if (n < 64) memset(blk + r * 64 + std::max<int64_t>(n, 0), 0, (size_t)(64 - std::max<int64_t>(n, 0)));
+            }
+        }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = rt * 16 + r;
+            const float v = row < N ? s[row] : 0.f;
+            memcpy(planes + L.sc_off + row * 4, &v, 4);
+        }
+    }
+}
+
+static void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t* q, float* s, const Layout& L,
+                             int64_t t0, int64_t t1) {
+    const int64_t kc_n = (K + 63) / 64;
+    for (int64_t rt = t0; rt < t1; ++rt)
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = rt * 16 + r;
+            if (row >= N) continue;
+            for (int64_t kc = 0; kc < kc_n; ++kc)
+                memcpy(q + row * K + kc * 64, planes + L.qs_off + (rt * kc_n + kc) * 1024 + r * 64, (size_t)std::min<int64_t>(64, K - kc * 64));
+            memcpy(s + row, planes + L.sc_off + row * 4, 4);
+        }
 }
 
 // launch_matmul over row chunks of x whose bytes stay within one buffer resource's range (a chunk of rows is an
@@ -347,12 +392,12 @@ int64_t mbq_row_bytes(int t, int64_t cols) {
 // BUF_MAX_BYTES are refused at every batch size, so they are not covered. Activations are cut into row chunks within
 // that range by mbq_matmul, so every batch size of a covered weight runs.
 int mbq_covers(int t, int64_t rows, int64_t cols) {
-    if (check_shape(t, rows, cols) != 0) return 0;
+    if (check_planes_shape(t, rows, cols) != 0) return 0;
     return layout(t, rows, cols).total <= BUF_MAX_BYTES ? 1 : 0;
 }
 
 int64_t mbq_plane_bytes(int t, int64_t rows, int64_t cols) {
-    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (int rc = check_planes_shape(t, rows, cols)) return rc;
     return layout(t, rows, cols).total;
 }
 
@@ -385,6 +430,36 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
     int rc = 0;
     if (!for_each_gap(L, [&](int64_t off, int64_t n) { return (rc = launch_zero(planes_dev + off, n, s)) == 0; })) return rc;
     return launch_repack(t, raw_dev, rows, cols, planes_dev, L, s);
+}
+
+int mbq_int8_repack_host(const int8_t* q, const float* s, int64_t rows, int64_t cols, uint8_t* planes_host, size_t cap,
+                         int threads) {
+    if (int rc = check_planes_shape(T_I8T, rows, cols)) return rc;
+    if (!q || !s || !planes_host) return set_error(MBQ_BAD_ARG, "NULL buffer");
+    const Layout L = layout(T_I8T, rows, cols);
+    if (cap < (size_t)L.total) return set_error(MBQ_E_CAP, "planes buffer of %zu bytes < %lld", cap, (long long)L.total);
+    for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes_host + off, 0, (size_t)n); return true; });
+    parallel_rows((rows + 15) / 16, threads, [&](int64_t a, int64_t b) { i8t_pack_tiles(q, s, rows, cols, planes_host, L, a, b); });
+    return MBQ_OK;
+}
+
+int mbq_int8_unpack_host(const uint8_t* planes_host, int64_t rows, int64_t cols, int8_t* q, float* s) {
+    if (int rc = check_planes_shape(T_I8T, rows, cols)) return rc;
+    if (!q || !s || !planes_host) return set_error(MBQ_BAD_ARG, "NULL buffer");
+    const Layout L = layout(T_I8T, rows, cols);
+    parallel_rows((rows + 15) / 16, 0, [&](int64_t a, int64_t b) { i8t_unpack_tiles(planes_host, rows, cols, q, s, L, a, b); });
+    return MBQ_OK;
+}
+
+int mbq_int8_repack_dev(const int8_t* q_dev, const float* s_dev, int64_t rows, int64_t cols, uint8_t* planes_dev, void* stream) {
+    if (int rc = check_planes_shape(T_I8T, rows, cols)) return rc;
+    if (!q_dev || !s_dev || !planes_dev || !aligned16(q_dev) || !aligned16(planes_dev))
+        return set_error(MBQ_BAD_ARG, "q, s or planes is NULL, or q / planes not 16-byte aligned");
+    const Layout L = layout(T_I8T, rows, cols);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int rc = 0;
+    if (!for_each_gap(L, [&](int64_t off, int64_t n) { return (rc = launch_zero(planes_dev + off, n, st)) == 0; })) return rc;
+    return launch_i8t_repack(q_dev, s_dev, rows, cols, planes_dev, L, st);
 }
 
 int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
@@ -423,6 +498,7 @@ extern "C" {
 
 int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
                 int64_t K, float* w_dev, void* stream) {
+    if (t == T_I8T) return set_error(MBQ_BAD_ARG, "int8 planes have no dequant: their values are the int8 quants, scaled per row after the dot");
     Args a{};
     if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
     if (!w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "w is NULL or not 16-byte aligned");
@@ -481,7 +557,7 @@ int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, 
     if (!kernel || !bm || !bn || !splits) return set_error(MBQ_BAD_ARG, "NULL output");
     if (t == T_INT8) {
         if (N <= 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX || K % 16) return set_error(MBQ_BAD_ARG, "int8 shape (%lld, %lld)", (long long)N, (long long)K);
-    } else if (int rc = check_shape(t, N, K)) {
+    } else if (int rc = check_planes_shape(t, N, K)) {
         return rc;
     }
     if (M < 0 || M > INT32_MAX) return set_error(MBQ_BAD_ARG, "M = %lld", (long long)M);

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mbq_layout.h"
+
 namespace mbq {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -123,6 +125,15 @@ __device__ __forceinline__ int64_t layer_offset(int64_t stride, const int32_t* l
     const int l = *layer_dev;
     if (l < 0 || l >= nlayers) return -1;
     return (int64_t)l * stride;
+}
+
+// the factor a kernel applies to output row n's float32 sum: the int8 per-row scale (T_INT8: the caller's scale array;
+// T_I8T: the planes' scale plane of the weight read, base + lo its first byte), else 1
+template <int T>
+__device__ __forceinline__ float row_scale(const float* srow, const uint8_t* wbase, int64_t sc_off, int n) {
+    if constexpr (T == T_INT8) return srow[n];
+    else if constexpr (T == T_I8T) return reinterpret_cast<const float*>(wbase + sc_off)[n];
+    else return 1.f;
 }
 
 __device__ __forceinline__ void store_y(void* y, int64_t i, float v, int out_bf16) {

@@ -54,6 +54,7 @@ template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
+template <> struct BUnit<T_I8T> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct BUnit<T_Q5_K> { u32x4 q, meta; uint32_t h; };
 template <int T> constexpr int b_loads() { return T == T_Q6_K ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
@@ -70,6 +71,7 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
     else if constexpr (T == T_Q4_0) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
+    else if constexpr (T == T_I8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 32 * u), 0, 0, 0};   // 16-row tiles
     else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
 }
 
@@ -91,8 +93,9 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
         if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
     } else {
-        b.q0 = bload16(r, o.q, (uint32_t)k0);
-        b.q1 = bload16(r, o.q + 16, (uint32_t)k0);
+        const uint32_t qk = T == T_I8T ? (uint32_t)k0 * 16u : (uint32_t)k0;     // T_I8T: a KiB per 64 values
+        b.q0 = bload16(r, o.q, qk);
+        b.q1 = bload16(r, o.q + 16, qk);
         if constexpr (T == T_Q8_0) {
             b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
             if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
     for (int j = 0; j < TJ; ++j) {
         const int nn = n0 + wn * (BN / 4) + j * 16 + (lane & 15);
         if (nn >= N) continue;
-        const float s = (T == T_INT8) ? g.srow[nn] : 1.f;
+        const float s = row_scale<T>(g.srow, base, g.sc_off, nn);
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         for (int j = 0; j < 3; ++j) {
             const int nn = n0 + br + 32 * j;
             if (nn >= N) continue;
-            const float sc = (T == T_INT8) ? g.srow[nn] : 1.f;
+            const float sc = row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -891,8 +894,8 @@ static int pick(const Args& a, Plan* p) {
 }
 
 // The kernel of a batch the GEMV does not run: the weight-stream kernel (mbq_wsgemm.hip) up to WS_MAX_M rows, else the
-// LDS-tile kernel; a forced plan overrides it (and is the only way to the weight-direct kernel, mbq_pgemm.hip).
-struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block; K_DIRECT: bm = 16 mt, bn = 64 nt
+// LDS-tile kernel; a forced plan overrides it.
+struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block
 
 static int choose(int t, const Args& a, Choice* c) {
     const int fk = g_force_kind.load();
@@ -900,16 +903,6 @@ static int choose(int t, const Args& a, Choice* c) {
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
-        return 0;
-    }
-    if (fk == K_DIRECT) {
-        int bm = g_force_bm.load(), bn = g_force_bn.load();
-        if (bm == 0) {                                       // the kernel's own tile choice
-            int mt = 0, nt = 0;
-            pgemm_shape(t, a.M, a.N, a.K, &mt, &nt);
-            bm = 16 * mt, bn = 64 * nt;
-        }
-        *c = Choice{K_DIRECT, bm, bn, 1};
         return 0;
     }
     if (fk == K_TILES) {
@@ -939,7 +932,6 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     Choice c;
     if (int rc = choose(T, a, &c)) return rc;
     if (c.kind == K_STREAM) return launch_wsgemm(T, a, c.bn, c.S, s);
-    if (c.kind == K_DIRECT) return launch_pgemm(T, a, c.bm / 16, c.bn / 64, s);
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
@@ -962,12 +954,6 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         *splits = S;
         return 0;
     }
-    if (c.kind == K_DIRECT) {
-        *bm = c.bm;
-        *bn = c.bn;
-        *splits = 1;
-        return 0;
-    }
     Plan p;
     int rc;
     switch (t) {
@@ -977,6 +963,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_Q5_K: rc = pick<T_Q5_K>(a, &p); if (!rc) *bm = CANDS<T_Q5_K>[p.idx].bm, *bn = CANDS<T_Q5_K>[p.idx].bn; break;
         case T_Q6_K: rc = pick<T_Q6_K>(a, &p); if (!rc) *bm = CANDS<T_Q6_K>[p.idx].bm, *bn = CANDS<T_Q6_K>[p.idx].bn; break;
         case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
+        case T_I8T: rc = pick<T_I8T>(a, &p); if (!rc) *bm = CANDS<T_I8T>[p.idx].bm, *bn = CANDS<T_I8T>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -993,10 +980,6 @@ int force_gemm_plan(int kernel, int bm, int bn, int splits) {
             break;
         case K_TILES:
             if ((bm || bn) && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no LDS GEMM tile %d x %d", bm, bn);
-            break;
-        case K_DIRECT:
-            if ((bm || bn) && (bm % 16 || bn % 64 || splits > 1 || !pgemm_shape_known(bm / 16, bn / 64)))
-                return set_error(MBQ_BAD_ARG, "no weight-direct GEMM tile %d x %d (splits %d)", bm, bn, splits);
             break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM kernel %d", kernel);
     }
@@ -1015,6 +998,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_Q5_K: return launch_gemm_t<T_Q5_K>(a, s);
         case T_Q6_K: return launch_gemm_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemm_t<T_INT8>(a, s);
+        case T_I8T: return launch_gemm_t<T_I8T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

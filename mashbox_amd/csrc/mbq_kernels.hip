@@ -312,6 +312,32 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     }
 }
 
+// ------------------------------------------------------------------------------------------- tiled int8 repack
+// One thread per 16 bytes of the quant plane (mbq_layout.h, T_I8T): thread g fills bytes 16 (g % 4) .. of row g / 4 % 16
+// of block g / 64, from the row-major quants, or zero past N or K; the first NP threads also write the scale plane.
+// HBM-bound, load-time only.
+__global__ __launch_bounds__(256) void i8t_repack_kernel(const int8_t* __restrict__ q, const float* __restrict__ sc, int64_t N,
+                                                         int64_t K, uint8_t* __restrict__ planes, int64_t sc_off, int64_t chunks,
+                                                         int64_t np) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t kc_n = (K + 63) / 64;
+    if (g < chunks) {
+        const int64_t blk = g >> 6, c = g & 63, r = c >> 2, part = c & 3;
+        const int64_t row = (blk / kc_n) * 16 + r, col = (blk % kc_n) * 64 + 16 * part;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row < N && col < K) v = ld16(q + row * K + col);           // K % 16 == 0: whole 16-byte pieces
+        st16(planes + blk * 1024 + r * 64 + 16 * part, v);
+    }
+    if (g < np) reinterpret_cast<float*>(planes + sc_off)[g] = g < N ? sc[g] : 0.f;
+}
+
+int launch_i8t_repack(const int8_t* q, const float* sc, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
+    const int64_t chunks = L.qs_bytes / 16, np = (N + 15) / 16 * 16;
+    const int64_t threads = std::max(chunks, np);
+    i8t_repack_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, s>>>(q, sc, N, K, planes, L.sc_off, chunks, np);
+    return check_launch("int8 repack");
+}
+
 // ------------------------------------------------------------------------------------------ int8 embedding rows
 // y[t, :] = f32(q[r, :]) * s[r] (then rounded to bfloat16 when out_bf16), r = toks[t] (+ N when negative, clamped to
 // [0, N - 1]): reference src/mashbox/models/qwen3_8_27b/model.py:132-139 (embed, whose int8_rows at :117-129 equals the
@@ -402,6 +428,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_Q5_K: return launch_t<T_Q5_K>(a, s);
         case T_Q6_K: return launch_t<T_Q6_K>(a, s);
         case T_INT8: return launch_t<T_INT8>(a, s);
+        case T_I8T: return launch_t<T_I8T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }

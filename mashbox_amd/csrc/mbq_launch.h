@@ -72,13 +72,8 @@ constexpr int64_t WS_MAX_M = 64;
 int launch_wsgemm(int t, const Args& a, int rows_per_block, int splits, hipStream_t s);
 int wsgemm_plan(int t, const Args& a, int* rows_per_block, int* splits);
 void wsgemm_effective(int t, const Args& a, int* rows_per_block, int* splits);   // what a launch with these runs
-// weight-direct GEMM (mbq_pgemm.hip) of large batches, run by a forced plan (the LDS-tile kernel is faster on MI355X at
-// every batch measured, 256..2048 rows): tiles of 16 mt activation rows x 64 nt weight rows
-int launch_pgemm(int t, const Args& a, int mt, int nt, hipStream_t s);
-int pgemm_shape(int t, int64_t M, int64_t N, int64_t K, int* mt, int* nt);
-bool pgemm_shape_known(int mt, int nt);
 // GEMM kernels (the values of MBQ_KERNEL_* in mbq.h)
-enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2, K_DIRECT = 3 };
+enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2 };
 int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits);
 int force_gemm_plan(int kernel, int bm, int bn, int splits);
 int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
@@ -88,5 +83,7 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
 int launch_zero(uint8_t* p, int64_t n, hipStream_t s);   // n bytes at device address p set to zero
 struct Layout;
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s);
+// tiled int8 planes from the (N, K) int8 quants and (N,) float32 scales (padding rows and columns written as zero)
+int launch_i8t_repack(const int8_t* q, const float* sc, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s);
 
 }  // namespace mbq

@@ -33,6 +33,14 @@
 //     d    (N, K/256)  fp16        the super-block scales
 //   value = (d * sc) * (q - 32), exact in float32
 //
+//   int8 per output channel (MBQ_INT8 planes, repacked once at load from the (N, K) int8 quants and (N,) float32
+//   scales of reference src/mashbox/models/qwen3_8_27b/model.py:72-82; internal type T_I8T)
+//     qs   (NP / 16, KP / 64) blocks of 1 KiB (NP = N rounded up to 16, KP = K rounded up to 64): block (rt, kc) holds
+//                                  rows 16 rt .. 16 rt + 15, 64 bytes each (values 64 kc .. 64 kc + 63), so the 16
+//                                  rows x 64 bytes a wave loads as one MFMA B tile are one contiguous KiB
+//     s    f32 (NP)                the per-row scales
+//   padding rows and columns are zero (scale 0)
+//
 // Every plane starts 256-byte aligned and the whole is rounded up to 256 bytes, so a stack of weights is a plain array
 // of these records (mbq_plane_bytes apart). The byte count is the file's plus at most 256 bytes of zero padding per
 // plane.
@@ -41,7 +49,15 @@
 
 namespace mbq {
 
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8 };
+// T_INT8: the caller's row-major int8 weights (mbq_int8_linear); T_I8T: int8 weights repacked into 16-row tiles
+// (mbq_matmul with MBQ_INT8 planes)
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9 };
+// int8 types: 16-byte units of 16 values, a per-row float32 scale applied to the sum
+constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
+// T_I8T: bytes between consecutive 16-row tiles of the quant plane, and the byte offset of (row, K offset k0) (k0 a
+// multiple of 64)
+constexpr int64_t i8t_tile_bytes(int64_t k) { return (k + 63) / 64 * 1024; }
+constexpr int64_t i8t_off(int64_t row, int64_t k, int64_t k0) { return (row >> 4) * i8t_tile_bytes(k) + (k0 >> 6) * 1024 + (row & 15) * 64; }
 
 // the K-quants: 256-value super-blocks, kernel units of 32 values (16 bytes of low nibbles)
 constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
@@ -79,6 +95,10 @@ inline Layout layout(int t, int64_t n, int64_t k) {
         L.qs_bytes = n * (k / 2);
         L.hi_bytes = n * (k / 8);
         L.sc_bytes = n * (k / 256) * 16;
+    } else if (t == T_I8T) {
+        const int64_t np = (n + 15) / 16 * 16;
+        L.qs_bytes = np * ((k + 63) / 64 * 64);
+        L.sc_bytes = np * 4;
     } else {  // T_Q6_K
         L.qs_bytes = n * (k / 2);
         L.hi_bytes = n * (k / 4);

@@ -1,7 +1,7 @@
 // Weight-direct MFMA operands, shared by the GEMMs that take their weights from HBM straight into registers
-// (mbq_wsgemm.hip, mbq_pgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_0 and the
-// K-quants), 64
-// contiguous bytes of each row of the quant plane. Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
+// (mbq_wsgemm.hip): one iteration = KI values of K (64 for int8 and Q8_0, 128 for Q4_0 and the
+// K-quants), 64 contiguous bytes of each row of the quant plane (tiled int8 planes: the 16 rows' 64 bytes are one
+// contiguous KiB). Lane l holds 16 bytes of row (l & 15) of a 16-row tile at byte 16 g
 // (g = l >> 4, the lane group). The MFMA sums over K, so any K order works when x follows it: in K step s of an
 // iteration, lane group g holds the 8 values K = k0 + g KI/4 + 8 s + e (e = 0..7) for both operands.
 //   int8   16 quants = 2 K steps; bf16(q) is exact; the per-row scale multiplies the float32 sum in the epilogue.
@@ -32,18 +32,20 @@ inline int ws_ki_of(int t) { return unit32(t) ? 128 : 64; }
 // raw bytes of one iteration of one 16-row tile, as one lane holds them
 template <int T> struct WsRaw;
 template <> struct WsRaw<T_INT8> { u32x4 q; };
+template <> struct WsRaw<T_I8T> { u32x4 q; };
 template <> struct WsRaw<T_Q8_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q4_K> { u32x4 q, meta; };
 template <> struct WsRaw<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct WsRaw<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct WsRaw<T_Q5_K> { u32x4 q, meta; uint32_t h; };
-template <int T> constexpr int ws_wloads() { return T == T_INT8 ? 1 : T == T_Q6_K ? 4 : T == T_Q5_K ? 3 : 2; }   // buffer loads per tile per iteration
+template <int T> constexpr int ws_wloads() { return int8_type(T) ? 1 : T == T_Q6_K ? 4 : T == T_Q5_K ? 3 : 2; }   // buffer loads per tile per iteration
 
 // per-lane byte offsets of one weight row's planes (the iteration's part goes in the scalar offset)
 struct WsOff { uint32_t q, s, h, d; };
 template <int T>
 __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_off, int64_t hi_off, int64_t d_off) {
     WsOff o{row * (uint32_t)(unit32(T) ? K / 2 : K) + 16u * lg, 0u, 0u, 0u};
+    if constexpr (T == T_I8T) o.q = (uint32_t)i8t_off(row, K, 0) + 16u * lg;          // one contiguous KiB per tile
     if constexpr (T == T_Q8_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * (lg >> 1);
     if constexpr (T == T_Q4_0) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 32) * 2u + 2u * lg;
     if constexpr (T == T_Q4_K || T == T_Q5_K) o.s = (uint32_t)sc_off + row * (uint32_t)(K / 256) * 16u;
@@ -60,7 +62,8 @@ __device__ __forceinline__ WsOff ws_off(uint32_t row, int K, int lg, int64_t sc_
 // past K gets scale 0 (the x it meets is zero, its quants may be any bytes)
 template <int T, bool KFULL>
 __device__ __forceinline__ void ws_load(WsRaw<T>& w, rsrc_t wr, const WsOff& o, int kk, int K, int lg) {
-    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, (uint32_t)(unit32(T) ? kk / 2 : kk), 2));
+    const uint32_t qk = T == T_I8T ? (uint32_t)kk * 16u : (uint32_t)(unit32(T) ? kk / 2 : kk);   // T_I8T: KiB per 64 values
+    w.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.q, qk, 2));
     if constexpr (T == T_Q8_0) {
         w.d = bload2(wr, o.s, (uint32_t)(kk / 32) * 2u);
         if constexpr (!KFULL) w.d = (kk + 16 * lg < K) ? w.d : 0u;

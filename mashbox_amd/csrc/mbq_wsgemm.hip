@@ -250,7 +250,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
     for (int j = 0; j < NT; ++j) {
         const int nn = n0 + 16 * j + r16;
         if (nn >= N) continue;
-        const float s = (T == T_INT8) ? g.srow[nn] : 1.f;
+        const float s = row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -352,6 +352,7 @@ int launch_wsgemm(int t, const Args& a, int nr, int S, hipStream_t s) {
         if (int rc = split_workspace(a, tiles, (size_t)tiles * S * ws_partial_bytes(a.M, nr), s, &w)) return rc;
     switch (t) {
         case T_INT8: return nr == 64 ? ws_launch_m<T_INT8, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_INT8, 2>(a, S, (int)kts, w, s);
+        case T_I8T: return nr == 64 ? ws_launch_m<T_I8T, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_I8T, 2>(a, S, (int)kts, w, s);
         case T_Q4_0: return nr == 64 ? ws_launch_m<T_Q4_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_0, 2>(a, S, (int)kts, w, s);
         case T_Q8_0: return nr == 64 ? ws_launch_m<T_Q8_0, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q8_0, 2>(a, S, (int)kts, w, s);
         case T_Q4_K: return nr == 64 ? ws_launch_m<T_Q4_K, 1>(a, S, (int)kts, w, s) : ws_launch_m<T_Q4_K, 2>(a, S, (int)kts, w, s);

@@ -186,3 +186,30 @@ def test_argument_errors_are_reported_without_a_launch():
                                small.ctypes.data_as(ctypes.c_void_p), small.size, 1) == -3
     with pytest.raises(L.MbqError):
         L.check(-1, "x")
+
+
+@pytest.mark.parametrize("n,k", [(1, 16), (17, 48), (33, 1040), (130, 4096)])
+def test_int8_tiled_repack_is_lossless(n, k):
+    """the load-time int8 repack (16-row tiles of 16 rows x 64 bytes, then the scales) inverts exactly; its padding
+    rows and columns are zero; plane bytes = 16-row-rounded rows x 64-rounded K + the scale plane, each 256-aligned"""
+    from mashbox_amd import int8 as I8
+    rng = np.random.default_rng([n, k])
+    q, s = G.int8_weights(rng, n, k)
+    p = I8.repack_host(q, s, threads=3)
+    np16, kp = (n + 15) // 16 * 16, (k + 63) // 64 * 64
+    a256 = lambda v: (v + 255) // 256 * 256
+    assert p.stride == a256(a256(np16 * kp) + np16 * 4)
+    buf = p.buf.numpy()
+    q2, s2 = np.zeros_like(q), np.zeros_like(s)
+    assert L.lib().mbq_int8_unpack_host(buf.ctypes.data_as(ctypes.c_void_p), n, k, q2.ctypes.data_as(ctypes.c_void_p),
+                                        s2.ctypes.data_as(ctypes.c_void_p)) == 0
+    assert np.array_equal(q2, q) and np.array_equal(s2.view(np.uint32), s.view(np.uint32))
+    # tile (rt, kc) row r holds q[16 rt + r, 64 kc : 64 kc + 64], zero past n or k
+    tiles = buf[:np16 * kp].reshape(np16 // 16, kp // 64, 16, 64).view(np.int8)
+    full = np.zeros((np16, kp), np.int8)
+    full[:n, :k] = q
+    assert np.array_equal(tiles.transpose(0, 2, 1, 3).reshape(np16, kp), full)
+    sc = buf[a256(np16 * kp):a256(np16 * kp) + np16 * 4].view(np.float32)
+    assert np.array_equal(sc[:n].view(np.uint32), s.view(np.uint32)) and not sc[n:].any()
+    assert L.lib().mbq_covers(L.I8T, n, k) == 1 and L.lib().mbq_covers(L.I8T, n, k + 8) == 0
+    assert L.lib().mbq_dequant(L.I8T, None, 0, None, 1, n, k, None, None) < 0
