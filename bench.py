@@ -82,6 +82,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
                                     ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16,
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         elif t == "int8":
+            # decode int8: the reference's row-major weights, run by the decode GEMV
             q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
             wbytes = N * K + 4 * N
             copies = max(1, math.ceil(rotate_bytes / wbytes))

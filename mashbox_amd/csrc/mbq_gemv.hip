@@ -149,13 +149,9 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
         }
     };
 
-    Raw A, B, C;
-    if (any) {
-        load(A, 0);
-        if constexpr (DEPTH == 3) load(B, 1);
-    }
-
-    // x of the lane's units (clamped to the row), per activation row, and for Q4_K the per-unit sums of x
+    // x of the lane's units (clamped to the row), per activation row, and for Q4_K the per-unit sums of x. The x loads
+    // are issued before the first item's weights: loads complete in order, so the sums of x then wait for x only, with
+    // the weights still in flight.
     u32x4 xv[CH][M][TPU];
     float xs[CH][M], xs2[CH][M];                                      // Q6_K: sums of x over each half unit
     int rsel[CH];                                                     // R > 1: the item row of the lane's unit
@@ -164,18 +160,28 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
         const int u = R > 1 ? (64 * i + lane) % U : min(u0 + lane + 64 * i, U - 1);
         rsel[i] = (64 * i + lane) / U;
 #pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int t = 0; t < TPU; ++t) xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
+    }
+    Raw A, B, C;
+    if (any) {
+        load(A, 0);
+        if constexpr (DEPTH == 3) load(B, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+#pragma unroll
         for (int m = 0; m < M; ++m) {
             float sum = 0.f, sum2 = 0.f;
+            if constexpr (unit32(T)) {
 #pragma unroll
-            for (int t = 0; t < TPU; ++t) {
-                xv[i][m][t] = bload16(xr, (uint32_t)(((int64_t)m * K + (int64_t)u * UW + t * 8) * 2), 0);
-                if constexpr (unit32(T)) {
+                for (int t = 0; t < TPU; ++t)
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         if (T == T_Q6_K && t >= 2) sum2 = dot2(xv[i][m][t][p], BF16_ONES, sum2);
                         else sum = dot2(xv[i][m][t][p], BF16_ONES, sum);
                     }
-                }
             }
             xs[i][m] = sum;
             xs2[i][m] = sum2;
