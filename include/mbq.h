@@ -114,6 +114,13 @@ int mbq_matmul_noalloc(int t, const uint8_t* planes_dev, int64_t layer, const in
 int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers, int64_t N,
                 int64_t K, float* w_dev, void* stream);
 
+/* Rows of W as float32: w (count, K) row r = dequantized weight row rows_dev[r] (device int32 ids; an id below zero
+ * counts from the end, and ids are then clamped to [0, N - 1], as jax.numpy indexes), bit for bit the rows of
+ * mbq_dequant, reading only those rows. Replaces take_rows(h, ids) on kernel planes (reference
+ * src/mashbox/ops/__init__.py:527-548: the embedding lookup of a quantized table). */
+int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                     int64_t N, int64_t K, const int32_t* rows_dev, int64_t count, float* w_dev, void* stream);
+
 /* W (rows, cols) float32 straight from the file's blocks raw_dev (rows, row_bytes) in HBM, no planes: the exact path's
  * rebuild, bit for bit the reference dequantization (NaN where it has NaN). Replaces dequant(raw, t, cols) of
  * reference src/mashbox/ops/reference.py:398-409 as the exact path calls it (src/mashbox/ops/__init__.py:574-576). */

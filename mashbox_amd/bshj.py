@@ -1,6 +1,6 @@
 """Reader of .bshj weight files and the int8 per-row linears they hold.
 
-The container (reference src/mashbox/bshj.py:1-16, the format of the reference's TPU weight files), little endian:
+The container is the reference's TPU weight format (reference src/mashbox/bshj.py:1-16), little endian:
 
     0   4    magic b"BSHJ"             28  4   flags (bit 0: tensors packed back to back in header order)
     4   2+2  major (1), minor (<= 1)   32  8   data_len
@@ -8,21 +8,26 @@ The container (reference src/mashbox/bshj.py:1-16, the format of the reference's
     16  8    data_offset (% align = 0) 48  16  reserved, zero
     24  4    align (>= 4096)           64  ..  JSON {"tensors": {name: {dtype, shape, offset, nbytes, layout}}, ...}
 
-Tensors start at data_offset + offset. A tensor is a zero-copy NumPy view of the memory-mapped file; bfloat16 tensors
-are viewed as their uint16 bits (`torch_tensor` gives torch.bfloat16). The checks on open follow reference
-src/mashbox/bshj.py:33-53: a bad magic, major, newer minor, nonzero reserved bytes, a misaligned or overlapping data
-section, or a tensor record whose bytes disagree with its shape or run past the data raise ValueError.
+Tensors start at data_offset + offset. The file is parsed once into a `Header` and one `Record` per tensor, and every
+problem found is reported together in one ValueError: a wrong magic or major version, a newer minor version, reserved
+bytes that are not zero, a data section that is misaligned, overlaps the JSON header or runs past the end of the file,
+and tensor records with an unknown dtype, a byte count that disagrees with their shape, a misaligned offset or bytes
+past the data section (the checks of reference src/mashbox/bshj.py:33-53). A tensor is a zero-copy NumPy view of the
+memory-mapped file; bfloat16 tensors are viewed as their uint16 bits (`torch_tensor` gives torch.bfloat16).
 
 int8 per-row linears (reference src/mashbox/models/qwen3_8_27b/weights.py:31-118): `<name>.weight` int8 (out, in) plus
 `<name>.weight_scale` float32 (out,), weight = q * s per output row. `int8_weight` moves one to the GPU as the
-{"q", "s"} form mashbox_amd.int8.linear / embed take; `int8_stack` fills one (L, out, in) + (L, out) buffer pair in
-place, layer by layer, for the layer loop (weight l is {"q": q[l], "s": s[l]}).
+{"q", "s"} form mashbox_amd.int8.linear / embed take, or repacks it at load into the tiled planes the batched kernels
+stream (packed=True); `int8_stack` fills one (L, out, in) + (L, out) buffer pair in place, layer by layer, for the
+layer loop (weight l is {"q": q[l], "s": s[l]}).
 """
 from __future__ import annotations
 
 import json
 import mmap
+import os
 import struct
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -33,79 +38,136 @@ DTYPES = {"bf16": np.dtype("<u2"), "f16": np.dtype("<f2"), "f32": np.dtype("<f4"
           "i32": np.dtype("<i4"), "u32": np.dtype("<u4"), "i64": np.dtype("<i8"), "u64": np.dtype("<u8")}
 
 
+@dataclass(frozen=True)
+class Header:
+    """the fixed 64 bytes of a .bshj file"""
+    magic: bytes
+    major: int
+    minor: int
+    json_len: int
+    data_offset: int
+    align: int
+    flags: int
+    data_len: int
+    header_hash: int
+    reserved: bytes
+
+    @classmethod
+    def parse(cls, raw: bytes) -> "Header":
+        return cls(*FIXED.unpack(raw))
+
+    def problems(self, file_len: int) -> list:
+        if self.magic != b"BSHJ" or self.major != 1:
+            return [f"magic {self.magic!r} version {self.major}.{self.minor} is not BSHJ 1.x"]
+        out = []
+        if self.minor > MAX_MINOR:
+            out.append(f"version 1.{self.minor} is newer than this reader (1.{MAX_MINOR})")
+        if any(self.reserved):
+            out.append("reserved header bytes are not zero")
+        if self.align == 0 or self.data_offset % self.align:
+            out.append(f"data offset {self.data_offset} is not a multiple of the alignment {self.align}")
+        if self.data_offset < FIXED.size + self.json_len:
+            out.append(f"data offset {self.data_offset} overlaps the {self.json_len}-byte JSON header")
+        if self.data_offset + self.data_len > file_len:
+            out.append(f"data section [{self.data_offset}, {self.data_offset + self.data_len}) runs past the "
+                       f"{file_len}-byte file")
+        return out
+
+
+@dataclass(frozen=True)
+class Record:
+    """one tensor of the JSON header; offset is relative to the data section"""
+    name: str
+    dtype: str
+    shape: tuple
+    offset: int
+    nbytes: int
+
+    @property
+    def np_dtype(self) -> np.dtype:
+        return DTYPES[self.dtype]
+
+    def problem(self, align: int, data_len: int):
+        if self.dtype not in DTYPES:
+            return f"tensor {self.name}: unknown dtype {self.dtype!r}"
+        want = int(np.prod(self.shape, dtype=np.int64)) * self.np_dtype.itemsize
+        if self.nbytes != want:
+            return f"tensor {self.name}: {self.nbytes} bytes for shape {list(self.shape)} of {self.dtype} ({want})"
+        if self.offset % align:
+            return f"tensor {self.name}: offset {self.offset} is not a multiple of the alignment {align}"
+        if self.offset + self.nbytes > data_len:
+            return f"tensor {self.name}: bytes [{self.offset}, {self.offset + self.nbytes}) run past the data section"
+        return None
+
+
 class File:
-    """an open .bshj file: header(), meta(), tensors (name -> record), array(name), torch_tensor(name, device)"""
+    """an open .bshj file: meta(), tensors (name -> JSON record), records (name -> Record), array(name),
+    torch_tensor(name, device), advise(name); a context manager"""
 
     def __init__(self, path: str):
         self.path = path
-        self._f = open(path, "rb")
+        self._fd = os.open(path, os.O_RDONLY)
+        self._mm = None
         try:
-            self._mm = mmap.mmap(self._f.fileno(), 0, access=mmap.ACCESS_READ)
-        except ValueError as e:                                       # an empty file cannot be mapped
-            self._f.close()
-            raise ValueError(f"{path}: not a BSHJ 1.x file ({e})") from None
-        try:
-            self._open()
+            size = os.fstat(self._fd).st_size
+            if size < FIXED.size:
+                raise ValueError(f"{path}: {size} bytes, shorter than the {FIXED.size}-byte BSHJ header")
+            self._mm = mmap.mmap(self._fd, 0, access=mmap.ACCESS_READ)
+            self.fixed = Header.parse(self._mm[:FIXED.size])
+            bad = self.fixed.problems(size)
+            if not bad:
+                text = bytes(self._mm[FIXED.size:FIXED.size + self.fixed.json_len]).decode("utf-8")
+                self.header = json.loads(text)
+                self.tensors = self.header["tensors"]
+                self.records = {n: Record(n, t["dtype"], tuple(t["shape"]), int(t["offset"]), int(t["nbytes"]))
+                                for n, t in self.tensors.items()}
+                bad = [p for r in self.records.values() if (p := r.problem(self.fixed.align, self.fixed.data_len))]
+            if bad:
+                raise ValueError(f"{path}: not a readable BSHJ file: " + "; ".join(bad))
         except Exception:
             self.close()
             raise
-
-    def _open(self):
-        path, mm = self.path, self._mm
-        if len(mm) < FIXED.size:
-            raise ValueError(f"{path}: not a BSHJ 1.x file (shorter than its fixed header)")
-        magic, major, minor, jl, off, align, _flags, data_len, _hash, reserved = FIXED.unpack(mm[:FIXED.size])
-        if magic != b"BSHJ" or major != 1:
-            raise ValueError(f"{path}: not a BSHJ 1.x file")
-        if minor > MAX_MINOR:
-            raise ValueError(f"{path}: BSHJ 1.{minor} is newer than this reader (1.{MAX_MINOR})")
-        if any(reserved) or align == 0 or off % align or off < FIXED.size + jl or off + data_len > len(mm):
-            raise ValueError(f"{path}: bad container header")
-        self.data_offset, self.align, self.data_len = off, align, data_len
-        self.header = json.loads(bytes(mm[FIXED.size:FIXED.size + jl]).rstrip(b" \t\n\r").decode("utf-8"))
-        self.tensors = self.header["tensors"]
-        for name, t in self.tensors.items():
-            dt = DTYPES.get(t["dtype"])
-            if dt is None:
-                raise ValueError(f"{path}: tensor {name} has unknown dtype {t['dtype']!r}")
-            n = int(np.prod(t["shape"], dtype=np.int64)) * dt.itemsize
-            if t["nbytes"] != n or t["offset"] % align or t["offset"] + n > data_len:
-                raise ValueError(f"{path}: bad tensor record {name}")
+        self.data_offset, self.align, self.data_len = self.fixed.data_offset, self.fixed.align, self.fixed.data_len
 
     def meta(self) -> dict:
-        return {k: v for k, v in self.header.items() if k != "tensors"}
+        """the JSON header without its tensor table"""
+        out = dict(self.header)
+        out.pop("tensors", None)
+        return out
 
     def array(self, name: str) -> np.ndarray:
         """zero-copy view of a tensor (bfloat16 as uint16 bits)"""
-        t = self.tensors[name]
-        dt = DTYPES[t["dtype"]]
-        return np.frombuffer(self._mm, dtype=dt, count=t["nbytes"] // dt.itemsize,
-                             offset=self.data_offset + t["offset"]).reshape(t["shape"])
+        r = self.records[name]
+        start = self.data_offset + r.offset
+        return np.frombuffer(self._mm, dtype=r.np_dtype, count=r.nbytes // r.np_dtype.itemsize, offset=start).reshape(r.shape)
 
     def torch_tensor(self, name: str, device=None):
         """a tensor copied into a torch tensor (bfloat16 as torch.bfloat16), on `device` if given"""
         import torch
-        a = self.array(name)
-        x = torch.from_numpy(np.array(a))                            # own the bytes: the map may close
-        if self.tensors[name]["dtype"] == "bf16":
+        x = torch.from_numpy(self.array(name).copy())                 # owns its bytes: the map may close
+        if self.records[name].dtype == "bf16":
             x = x.view(torch.int16).view(torch.bfloat16)
         return x if device is None else x.to(device)
 
     def advise(self, name: str) -> None:
-        """tell the OS a tensor is about to be read (read-ahead on a cold page cache)"""
-        t = self.tensors[name]
-        start = (self.data_offset + t["offset"]) & ~(mmap.PAGESIZE - 1)
-        try:
-            self._mm.madvise(mmap.MADV_WILLNEED, start, self.data_offset + t["offset"] + t["nbytes"] - start)
-        except (AttributeError, OSError, ValueError):
-            pass
+        """ask the kernel to read a tensor's bytes ahead (a cold page cache); a hint only, never an error"""
+        r = self.records[name]
+        if hasattr(os, "posix_fadvise"):
+            try:
+                os.posix_fadvise(self._fd, self.data_offset + r.offset, r.nbytes, os.POSIX_FADV_WILLNEED)
+            except OSError:
+                pass
 
     def close(self) -> None:
-        try:
-            self._mm.close()
-        except BufferError:                                           # a caller still holds a view
-            pass
-        self._f.close()
+        if self._mm is not None:
+            try:
+                self._mm.close()
+            except BufferError:                                       # a view of a tensor is still alive: the map
+                pass                                                  # stays until it goes
+            self._mm = None
+        if self._fd is not None:
+            os.close(self._fd)
+            self._fd = None
 
     def __enter__(self):
         return self
@@ -124,21 +186,24 @@ def quantised(f: File, name: str) -> bool:
     return name + ".weight_scale" in f.tensors
 
 
-def _check_int8(f: File, name: str):
-    q, s = f.tensors.get(name), f.tensors.get(name + "_scale")
-    if q is None or s is None or q["dtype"] != "i8" or s["dtype"] != "f32" or len(q["shape"]) != 2 \
-            or list(s["shape"]) != [q["shape"][0]]:
+def _int8_shape(f: File, name: str) -> tuple:
+    q, s = f.records.get(name), f.records.get(name + "_scale")
+    if q is None or s is None or q.dtype != "i8" or s.dtype != "f32" or len(q.shape) != 2 or s.shape != q.shape[:1]:
         raise ValueError(f"{f.path}: {name} is not an int8 (out, in) weight with a float32 (out,) scale")
-    return tuple(q["shape"])
+    return q.shape
 
 
-def int8_weight(f: File, name: str, device="cuda") -> dict:
-    """`<name>` (ending in ".weight") -> {"q": int8 (out, in), "s": float32 (out,)} on the device"""
+def int8_weight(f: File, name: str, device="cuda", packed: bool = False):
+    """`<name>` (ending in ".weight") -> {"q": int8 (out, in), "s": float32 (out,)} on the device, or with packed=True
+    its load-time repack into tiled planes (mashbox_amd.int8.Int8Planes)"""
     import torch
-    _check_int8(f, name)
+    _int8_shape(f, name)
     f.advise(name)
-    q = torch.from_numpy(np.array(f.array(name))).to(device)
-    s = torch.from_numpy(np.array(f.array(name + "_scale"))).to(device)
+    q = torch.from_numpy(f.array(name).copy()).to(device)
+    s = torch.from_numpy(f.array(name + "_scale").copy()).to(device)
+    if packed:
+        from . import int8
+        return int8.repack(q, s)
     return {"q": q, "s": s}
 
 
@@ -147,7 +212,7 @@ def int8_stack(f: File, names, device="cuda") -> dict:
     allocated once on the device and filled in place layer by layer"""
     import torch
     names = list(names)
-    shapes = {_check_int8(f, n) for n in names}
+    shapes = {_int8_shape(f, n) for n in names}
     if len(shapes) != 1:
         raise ValueError(f"{f.path}: a stack needs one shape, got {sorted(shapes)}")
     (out, inp), = shapes
@@ -155,9 +220,9 @@ def int8_stack(f: File, names, device="cuda") -> dict:
     s = torch.empty((len(names), out), dtype=torch.float32, device=device)
     for i, n in enumerate(names):
         f.advise(n)
-        q[i].copy_(torch.from_numpy(np.array(f.array(n))))
-        s[i].copy_(torch.from_numpy(np.array(f.array(n + "_scale"))))
+        q[i].copy_(torch.from_numpy(f.array(n).copy()))
+        s[i].copy_(torch.from_numpy(f.array(n + "_scale").copy()))
     return {"q": q, "s": s}
 
 
-__all__ = ["File", "FIXED", "DTYPES", "prefix", "quantised", "int8_weight", "int8_stack"]
+__all__ = ["File", "Header", "Record", "FIXED", "DTYPES", "prefix", "quantised", "int8_weight", "int8_stack"]

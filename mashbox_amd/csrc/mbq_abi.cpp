@@ -502,7 +502,18 @@ int mbq_dequant(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* 
     Args a{};
     if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
     if (!w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "w is NULL or not 16-byte aligned");
-    return launch_dequant(t, a, w_dev, reinterpret_cast<hipStream_t>(stream));
+    return launch_dequant(t, a, w_dev, nullptr, 0, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* layer_dev, int64_t nlayers,
+                     int64_t N, int64_t K, const int32_t* rows_dev, int64_t count, float* w_dev, void* stream) {
+    if (t == T_I8T) return set_error(MBQ_BAD_ARG, "int8 planes have no dequant: their values are the int8 quants, scaled per row after the dot");
+    Args a{};
+    if (int rc = plane_args(t, planes_dev, layer, layer_dev, nlayers, N, K, &a)) return rc;
+    if (count < 0 || count > INT32_MAX) return set_error(MBQ_BAD_ARG, "%lld rows", (long long)count);
+    if (count == 0) return MBQ_OK;
+    if (!rows_dev || !w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "rows or w is NULL, or w not 16-byte aligned");
+    return launch_dequant(t, a, w_dev, rows_dev, count, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream) {

@@ -22,19 +22,28 @@ namespace mbq {
 // dequantization: Q8_0 v = f32(q) * d, Q4_0 v = d * f32(q - 8), Q4_K and Q5_K v = (d*sc)*q - dmin*m and
 // Q6_K v = (d*sc)*(q - 32), whose products are exact in float32 (Q4_0 and Q6_K keep the reference's order of the
 // operands, which fixes the sign of a zero).
+// With `rows` (out_rows device row ids) it writes row r of w from weight row rows[r] (plus N when negative, clamped to
+// [0, N - 1], as jax.numpy indexes): the rows of a lookup, without the rest of the weight.
 template <int T>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ base, int64_t stride,
                                                       const int32_t* __restrict__ layer_dev, int nlayers, int64_t sc_off,
-                                                      int64_t hi_off, int64_t d_off, int N, int K, float* __restrict__ w) {
+                                                      int64_t hi_off, int64_t d_off, int N, int K, float* __restrict__ w,
+                                                      const int32_t* __restrict__ rows, int64_t out_rows) {
     const int64_t uw = unit32(T) ? 32 : 16;
-    const int64_t units = (int64_t)N * (K / uw);
+    const int64_t units = out_rows * (K / uw);
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= units) return;
     const int64_t lo = layer_offset(stride, layer_dev, nlayers);
     const bool ok = lo >= 0;
     base += ok ? lo : 0;
-    const int64_t n = g / (K / uw), u = g % (K / uw);
-    float* out = w + n * K + u * uw;
+    const int64_t o = g / (K / uw), u = g % (K / uw);
+    int64_t n = o;
+    if (rows != nullptr) {
+        n = rows[o];
+        n = n < 0 ? n + N : n;
+        n = n < 0 ? 0 : (n >= N ? N - 1 : n);
+    }
+    float* out = w + o * K + u * uw;
     if (!ok) {
         for (int i = 0; i < uw; ++i) out[i] = __builtin_nanf("");
         return;
@@ -433,12 +442,14 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
 
-int launch_dequant(int t, const Args& a, float* w, hipStream_t s) {
+int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t out_rows, hipStream_t s) {
     const int64_t uw = unit32(t) ? 32 : 16;
-    const int64_t units = a.N * (a.K / uw);
+    const int64_t units = (rows ? out_rows : a.N) * (a.K / uw);
+    if (units == 0) return 0;
     const dim3 grid((unsigned)((units + 255) / 256));
     auto run = [&](auto kern) {
-        kern<<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, (int)a.N, (int)a.K, w);
+        kern<<<grid, 256, 0, s>>>(a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.hi_off, a.d_off, (int)a.N, (int)a.K, w,
+                                  rows, rows ? out_rows : a.N);
     };
     if (t == T_Q4_0) run(dequant_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);

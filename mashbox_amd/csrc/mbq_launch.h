@@ -76,7 +76,7 @@ void wsgemm_effective(int t, const Args& a, int* rows_per_block, int* splits);  
 enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2 };
 int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits);
 int force_gemm_plan(int kernel, int bm, int bn, int splits);
-int launch_dequant(int t, const Args& a, float* w, hipStream_t s);
+int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t out_rows, hipStream_t s);   // rows: a row gather, or nullptr
 int launch_int8_embed(const int8_t* q, const float* s, int64_t N, int64_t D, const int32_t* toks, int64_t T, void* y,
                       int out_bf16, hipStream_t st);
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s);

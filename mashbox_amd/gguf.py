@@ -9,11 +9,16 @@ ready for mashbox_amd.kernels.repack_host / repack. Mirrors the reference's read
     metadata: (string key, u32 value type, value) ...        strings are u64 length + UTF-8 bytes
     tensor infos: (string name, u32 n_dims, u64 dims[n_dims] innermost first, u32 ggml type, u64 offset) ...
     tensor data: from the first multiple of general.alignment (default 32) after the directory; offsets are relative
+
+A model split into shards (`<name>-00001-of-0000N.gguf`, reference src/mashbox/gguf/reader.py:14,49-65) is read as one:
+opening any shard opens all N, their tensors together and each metadata key from the first shard that holds it; a
+missing shard is an error naming it.
 """
 from __future__ import annotations
 
 import mmap
 import os
+import re
 import struct
 
 import numpy as np
@@ -100,14 +105,51 @@ class _Cursor:
         raise GGUFError(f"unknown GGUF metadata value type {vt}")
 
 
+SPLIT = re.compile(r"-(\d{5})-of-(\d{5})\.gguf$")
+
+
+def shard_paths(path: str) -> list:
+    """every shard of the model `path` belongs to (itself when it is not a split file); GGUFError when one is missing"""
+    m = SPLIT.search(path)
+    if not m:
+        return [path]
+    count = int(m.group(2))
+    paths = [f"{path[:m.start()]}-{i:05d}-of-{count:05d}.gguf" for i in range(1, count + 1)]
+    missing = [os.path.basename(p) for p in paths if not os.path.exists(p)]
+    if missing:
+        raise GGUFError(f"{os.path.basename(path)} is shard {int(m.group(1))} of {count}; missing: {', '.join(missing)}")
+    return paths
+
+
 class File:
-    """One GGUF file: .meta (key -> value), .tensors (name -> Tensor over the mmap; bytes are never copied)"""
+    """A GGUF model, one file or all the shards of a split one: .meta (key -> value), .tensors (name -> Tensor over the
+    mmaps; bytes are never copied), .paths, .size"""
 
     def __init__(self, path: str):
         self.path = path
+        self.paths = shard_paths(path)
+        self._maps = []
+        self.meta, self.tensors = {}, {}
+        try:
+            for p in self.paths:
+                meta, tensors = self._read(p)
+                for k, v in meta.items():
+                    self.meta.setdefault(k, v)
+                dup = set(tensors) & set(self.tensors)
+                if dup:
+                    raise GGUFError(f"{os.path.basename(p)}: tensor {sorted(dup)[0]} is also in an earlier shard")
+                self.tensors.update(tensors)
+        except Exception:
+            self.close()
+            raise
+        self.size = sum(os.path.getsize(p) for p in self.paths)
+
+    def _read(self, path: str):
+        """one file -> (metadata, tensors)"""
         with open(path, "rb") as f:
-            self._mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
-        buf = memoryview(self._mm)
+            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+        self._maps.append(mm)
+        buf = memoryview(mm)
         c = _Cursor(buf)
         if len(buf) < 24 or bytes(buf[:4]) != MAGIC:
             raise GGUFError(f"{os.path.basename(path)} is not a GGUF file (magic {bytes(buf[:4])!r})")
@@ -117,10 +159,10 @@ class File:
             raise GGUFError(f"{os.path.basename(path)}: GGUF version {self.version} (big-endian or unknown); "
                             "only little-endian v2/v3 files are read")
         nt, nkv = c.take("<Q"), c.take("<Q")
-        self.meta = {}
+        meta = {}
         for _ in range(nkv):
             k = c.string()
-            self.meta[k] = c.value(c.take("<I"))
+            meta[k] = c.value(c.take("<I"))
         infos = []
         for _ in range(nt):
             name = c.string()
@@ -128,10 +170,10 @@ class File:
             dims = [c.take("<Q") for _ in range(nd)]
             t, off = c.take("<I"), c.take("<Q")
             infos.append((name, dims, t, off))
-        align = int(self.meta.get("general.alignment", 32))
+        align = int(meta.get("general.alignment", 32))
         start = (c.pos + align - 1) // align * align
-        data = np.frombuffer(self._mm, dtype=np.uint8)
-        self.tensors = {}
+        data = np.frombuffer(mm, dtype=np.uint8)
+        tensors = {}
         for name, dims, t, off in infos:
             if t not in GGML_TYPES:
                 raise GGUFError(f"{name}: unknown ggml type {t}")
@@ -143,18 +185,37 @@ class File:
             a = start + off
             if a + n > data.size:
                 raise GGUFError(f"{name}: tensor bytes run past the end of the file")
-            self.tensors[name] = Tensor(name, t, shape, data[a:a + n])
+            tensors[name] = Tensor(name, t, shape, data[a:a + n])
+        return meta, tensors
+
+    def get(self, key: str, default=None):
+        return self.meta.get(key, default)
+
+    def keys(self) -> list:
+        return list(self.meta)
 
     @property
     def arch(self):
         return self.meta.get("general.architecture")
 
+    def census(self):
+        """-> ({type name: {"type", "tensors", "bytes"}} largest first, total tensor bytes)"""
+        out, total = {}, 0
+        for t in self.tensors.values():
+            e = out.setdefault(t.type_name, {"type": t.type, "tensors": 0, "bytes": 0})
+            e["tensors"] += 1
+            e["bytes"] += t.nbytes
+            total += t.nbytes
+        return dict(sorted(out.items(), key=lambda kv: -kv[1]["bytes"])), total
+
     def close(self):
         self.tensors = {}
-        try:
-            self._mm.close()
-        except BufferError:
-            pass            # a caller still holds a view; the map closes with the last one
+        for mm in self._maps:
+            try:
+                mm.close()
+            except BufferError:
+                pass        # a caller still holds a view; the map closes with the last one
+        self._maps = []
 
     def __enter__(self):
         return self

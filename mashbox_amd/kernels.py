@@ -209,5 +209,21 @@ def dequant(p: Planes, layer=None) -> torch.Tensor:
     return w.reshape(p.lead + (p.N, p.K))
 
 
-__all__ = ["TYPES", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers", "picks_layer",
+def take_rows(p: Planes, ids, layer=None) -> torch.Tensor:
+    """rows `ids` (any int shape; below zero counts from the end, then clamped, as jax.numpy indexes) of the weight as
+    float32 (*ids.shape, cols), dequantizing only those rows: bit for bit dequant(p)[ids]"""
+    if not p.buf.is_cuda:
+        raise ValueError(f"{p} is on the host: move the planes to the GPU (planes.to('cuda'))")
+    ids = torch.as_tensor(ids, device=p.buf.device)
+    idx = ids.reshape(-1).to(torch.int32).contiguous()
+    if layer is None and p.lead:
+        raise ValueError(f"{p}: a stack needs layer= (or index it first)")
+    q, lh, ld, nl = (p, 0, None, 1) if layer is None else _layer_args(p, layer)
+    w = torch.empty((idx.numel(), p.K), dtype=torch.float32, device=p.buf.device)
+    check(lib().mbq_dequant_rows(p.t, _ptr(q.buf), lh, None if ld is None else _ptr(ld), nl, p.N, p.K, _ptr(idx),
+                                 idx.numel(), _ptr(w), _stream()), f"take_rows {p}")
+    return w.reshape(tuple(ids.shape) + (p.K,))
+
+
+__all__ = ["TYPES", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers", "picks_layer",
            "row_bytes", "INT8"]

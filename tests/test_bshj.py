@@ -2,7 +2,8 @@
 int8 embedding rows. CPU only.
 
 Mirrors the reference's loader checks: tensors read back bit for bit (bf16, f32, int8), a bad magic / major / newer
-minor / nonzero reserved bytes / misaligned data / a record whose bytes disagree with its shape raise ValueError
+minor / nonzero reserved bytes / misaligned data / a record whose bytes disagree with its shape raise one ValueError
+naming each problem
 (reference src/mashbox/bshj.py:33-53); the int8 per-row weights are found by their `_scale` companion and the layer
 prefix by its first name (reference src/mashbox/models/qwen3_8_27b/weights.py:27-28, 49-50)."""
 import json
@@ -56,8 +57,8 @@ def _raw_file(tmp_path, **kw):
     return p
 
 
-@pytest.mark.parametrize("kw,msg", [(dict(magic=b"GGUF"), "not a BSHJ"), (dict(major=2), "not a BSHJ"),
-                                    (dict(minor=2), "newer"), (dict(reserved=b"\x01" + bytes(15)), "bad container")])
+@pytest.mark.parametrize("kw,msg", [(dict(magic=b"GGUF"), "is not BSHJ 1.x"), (dict(major=2), "is not BSHJ 1.x"),
+                                    (dict(minor=2), "newer"), (dict(reserved=b"\x01" + bytes(15)), "reserved")])
 def test_rejects_bad_fixed_headers(tmp_path, kw, msg):
     with pytest.raises(ValueError, match=msg):
         bshj.File(_raw_file(tmp_path, **kw))
@@ -70,13 +71,13 @@ def test_rejects_bad_layouts_and_records(tmp_path):
     bad = bytearray(b)
     bad[16:24] = struct.pack("<Q", struct.unpack("<Q", b[16:24])[0] + 8)
     open(p, "wb").write(bad)
-    with pytest.raises(ValueError, match="bad container"):
+    with pytest.raises(ValueError, match="not a multiple of the alignment"):
         bshj.File(p)
     # data running past the end of the file
     bad = bytearray(b)
     bad[32:40] = struct.pack("<Q", 1 << 40)
     open(p, "wb").write(bad)
-    with pytest.raises(ValueError, match="bad container"):
+    with pytest.raises(ValueError, match="runs past"):
         bshj.File(p)
     # a record whose nbytes disagrees with its shape
     jl = struct.unpack("<Q", b[8:16])[0]
@@ -86,10 +87,10 @@ def test_rejects_bad_layouts_and_records(tmp_path):
     bad = bytearray(b)
     bad[64:64 + jl] = raw + b" " * (jl - len(raw))
     open(p, "wb").write(bad)
-    with pytest.raises(ValueError, match="bad tensor record a"):
+    with pytest.raises(ValueError, match="tensor a: 9 bytes"):
         bshj.File(p)
     open(p, "wb").close()
-    with pytest.raises(ValueError, match="not a BSHJ"):
+    with pytest.raises(ValueError, match="shorter than"):
         bshj.File(p)
 
 

@@ -162,7 +162,7 @@ def test_kq_failure_falls_back_to_the_exact_path(fail, cuda, monkeypatch, capsys
     err = capsys.readouterr().err
     assert all(isinstance(h, ops.Raw) for h in hs), hs
     assert err.count("kq planes for") == 3, err                          # one per (type, shape)
-    assert all(v is not True for v in ops._KQ_RAN.values()) and len(ops._KQ_RAN) == 3
+    assert all(v is not True for v in ops._KERNELS.preflight.values()) and len(ops._KERNELS.preflight) == 3
     want = "forced" if fail.startswith("force:") else "forced failure"
     assert want in err and "exact path" in err, err
     ops.load_kernels(module="off")
@@ -182,9 +182,9 @@ def test_kq_preflight_runs_once_per_type_and_shape(cuda, monkeypatch):
     hs = [ops.prepare(G.RAW[t](rng, *s), t, s) for t, s in shapes]
     assert all(isinstance(h, ops.Packed) for h in hs)
     assert calls["matmul"] == 2 and calls["repack"] == 5, calls
-    assert all(v is True for v in ops._KQ_RAN.values()) and len(ops._KQ_RAN) == 2
+    assert all(v is True for v in ops._KERNELS.preflight.values()) and len(ops._KERNELS.preflight) == 2
     ops.load_kernels(module="_stub_mbq_ok")
-    assert ops._KQ_RAN == {}, "load_kernels starts the preflight over"
+    assert ops._KERNELS.preflight == {}, "load_kernels starts the preflight over"
 
 
 @pytest.mark.gpu
@@ -198,7 +198,7 @@ def test_layer_stack_is_read_in_place(t, cuda):
     L, n, k = 3, 40, R.TYPES[t][1] * 2
     st = np.stack([G.RAW[t](rng, n, k) for _ in range(L)])
     h = ops.prepare(st, t, (n, k))
-    assert isinstance(h, ops.Packed) and ops._KQ_LAYER.get((t, (n, k))) is True
+    assert isinstance(h, ops.Packed) and ops._KERNELS.layer_preflight.get((t, (n, k))) is True
     held, xs = ops.scan_split({"mlp": {"wg": h, "bias": "b"}})
     assert held["mlp"]["wg"] is h and xs["mlp"]["wg"] is None and xs["mlp"]["bias"] == "b"
     xb, x = _x(rng, 4, k, cuda)
@@ -226,3 +226,92 @@ def test_contract_check_and_take_rows(t, cuda):
     for h in (ops.prepare(raw, t, (9, k)), ops.prepare(raw, t, (9, k), use_kernel=False)):
         got = ops.take_rows(h, [3, 0, -1, 1]).cpu().numpy()
         assert diff_bits(got, w[[3, 0, -1, 1]]) == 0
+
+
+# ------------------------------------------------------------------------------------------- mixed block types
+def _mixed_case(rng, types, n, k):
+    return [(G.RAW[t](rng, n, k), t) for t in types]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("index", ["host", "device"])
+def test_mixed_role_picks_each_layer(index, cuda):
+    """one role whose block types differ by layer (a Q4_K_M file keeps some layers' ffn_down in Q6_K): stack_mixed
+    holds one stack per type with which / sub; scan_split keeps it whole and scan_join hands the loop body a Pick; the
+    Pick's product, dequant and rows equal the layer's own handle bit for bit and the oracle (reference
+    src/mashbox/ops/__init__.py:216-270,515,606; gguf/archs/dense.py:206-218)"""
+    import torch
+    ops.load_kernels()
+    rng = np.random.default_rng(60)
+    types = [R.Q4_K, R.Q6_K, R.Q4_K, R.Q6_K, R.Q4_K]
+    n, k = 48, 512
+    layers = _mixed_case(rng, types, n, k)
+    h = ops.stack_mixed(layers, (n, k))
+    assert isinstance(h, ops.Mixed) and h.types == (R.Q4_K, R.Q6_K) and len(h.stacks) == 2
+    assert all(isinstance(s, ops.Packed) for s in h.stacks)
+    assert h.which.tolist() == [0, 1, 0, 1, 0] and h.sub.tolist() == [0, 0, 1, 1, 2]
+    held, xs = ops.scan_split({"mlp": {"wd": h, "norm": "n"}})
+    assert held["mlp"]["wd"] is h and xs["mlp"]["norm"] == "n"
+    xb, x = _x(rng, 3, k, cuda)
+    for layer, (raw, t) in enumerate(layers):
+        li = torch.tensor(layer, dtype=torch.int32, device=cuda) if index == "device" else layer
+        w = ops.scan_join(held, xs, li)["mlp"]["wd"]
+        assert isinstance(w, ops.Pick)
+        one = ops.prepare(raw, t, (n, k))
+        got = ops.qmatmul(x, w)
+        assert np.array_equal(got.view(torch.int16).cpu().numpy(), ops.qmatmul(x, one).view(torch.int16).cpu().numpy())
+        wf = R.dequant(raw, t, k)
+        assert_product(got.float().cpu().numpy(), R.bf16_to_f32(xb).astype(np.float64) @ wf.astype(np.float64).T)
+        assert diff_bits(ops.dequant(w).cpu().numpy(), wf) == 0
+        assert diff_bits(ops.take_rows(w, [5, -1, 0]).cpu().numpy(), wf[[5, -1, 0]]) == 0
+        assert diff_bits(ops.dequant(ops.slice_layer(h, layer)).cpu().numpy(), wf) == 0
+
+
+@pytest.mark.gpu
+def test_mixed_role_with_an_exact_path_stack(cuda):
+    """a Mixed whose Q6_K stack runs on the exact path (kernel types without Q6_K): the Pick reads its index on the host
+    and each layer equals its own exact or kernel handle"""
+    import torch
+    ops.load_kernels()
+    rng = np.random.default_rng(61)
+    types = [R.Q8_0, R.Q6_K, R.Q8_0]
+    n, k = 40, 256
+    layers = _mixed_case(rng, types, n, k)
+    saved = ops._KERNELS.types
+    ops._KERNELS.types = frozenset({R.Q8_0})
+    try:
+        h = ops.stack_mixed(layers, (n, k))
+    finally:
+        ops._KERNELS.types = saved
+    assert isinstance(h.stacks[0], ops.Packed) and isinstance(h.stacks[1], ops.Raw)
+    held, xs = ops.scan_split([h])
+    xb, x = _x(rng, 2, k, cuda)
+    for layer, (raw, t) in enumerate(layers):
+        w = ops.scan_join(held, xs, torch.tensor(layer, dtype=torch.int32, device=cuda))[0]
+        wf = R.dequant(raw, t, k)
+        assert_product(ops.qmatmul(x, w).float().cpu().numpy(), R.bf16_to_f32(xb).astype(np.float64) @ wf.astype(np.float64).T)
+        assert diff_bits(ops.dequant(w).cpu().numpy(), wf) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+def test_take_rows_reads_only_the_rows_asked(t, cuda):
+    """kernel planes: take_rows dequantizes the asked rows only (mbq_dequant_rows), bit for bit dequant(h)[ids], ids of
+    any shape, negative ids from the end and past-the-end ids clamped as jax.numpy indexes; a stack's layer too"""
+    import torch
+    ops.load_kernels()
+    rng = np.random.default_rng(70 + t)
+    n, k = 300, R.TYPES[t][1] * 3
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(2)])
+    planes = KQ.repack_host(t, st, (n, k)).to(cuda)
+    ids = np.array([[0, 7, n - 1], [-1, -n, 150]])
+    for layer in range(2):
+        w = R.dequant(st[layer], t, k)
+        got = KQ.take_rows(planes, torch.from_numpy(ids).to(cuda), layer=layer).cpu().numpy()
+        assert got.shape == (2, 3, k) and diff_bits(got, w[ids]) == 0
+        dl = torch.tensor(layer, dtype=torch.int32, device=cuda)
+        assert diff_bits(KQ.take_rows(planes, torch.from_numpy(ids).to(cuda), layer=dl).cpu().numpy(), w[ids]) == 0
+    one = planes[1]
+    clamp = KQ.take_rows(one, torch.tensor([n + 5, -n - 3], device=cuda)).cpu().numpy()
+    w = R.dequant(st[1], t, k)
+    assert diff_bits(clamp, w[[n - 1, 0]]) == 0
