@@ -1,0 +1,306 @@
+// Host repack of one weight into kernel planes, and its inverse (no HIP: also built alone, under the host
+// sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
+// src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
+// int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
+#pragma once
+#include <stdint.h>
+
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "mbq_layout.h"
+
+namespace mbq {
+
+// run f(row_begin, row_end) over [0, rows) on up to `threads` host threads
+template <class F>
+inline void parallel_rows(int64_t rows, int threads, F f) {
+    int hw = (int)std::thread::hardware_concurrency();
+    if (threads <= 0) threads = hw > 0 ? hw : 1;
+    threads = (int)std::min<int64_t>(threads, std::max<int64_t>(1, rows / 64));
+    if (threads <= 1) {
+        f(0, rows);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const int64_t step = (rows + threads - 1) / threads;
+    for (int i = 0; i < threads; ++i) {
+        const int64_t a = i * step, b = std::min(rows, a + step);
+        if (a >= b) break;
+        pool.emplace_back(f, a, b);
+    }
+    for (auto& th : pool) th.join();
+}
+
+// Q6_K: the 6-bit quant i (0..31) of unit j (0..7) of a super-block, from the file's ql / qh bytes
+// (reference src/mashbox/ops/reference.py:164-173: value 128g + 32r + i takes nibble r / 2 of ql[64g + 32 (r % 2) + i]
+// and bits 2r, 2r + 1 of qh[32g + i])
+inline uint32_t q6k_file_quant(const uint8_t* blk, int j, int i) {
+    const int g = j >> 2, r = j & 3;
+    const uint32_t lo = (blk[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15u;
+    const uint32_t hi = (blk[128 + 32 * g + i] >> (2 * r)) & 3u;
+    return lo | (hi << 4);
+}
+
+inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
+    const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
+    for (int64_t n = r0; n < r1; ++n) {
+        const uint8_t* row = raw + n * rb;
+        if (t == T_Q5_K) {
+            // reference src/mashbox/ops/reference.py:150-159: value 32j + i takes nibble j % 2 of qs[32 (j / 2) + i]
+            // (qs at byte 48) and bit j of qh[i] (qh at byte 16)
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* h = planes + L.hi_off + n * (K / 8);
+            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(meta + b * 16, src, 16);
+                for (int j = 0; j < 8; ++j) {
+                    uint8_t* qu = q + b * 128 + j * 16;
+                    uint8_t* hu = h + b * 32 + j * 4;
+                    memset(qu, 0, 16);
+                    memset(hu, 0, 4);
+                    for (int i = 0; i < 32; ++i) {
+                        const uint32_t lo = (src[48 + 32 * (j >> 1) + i] >> (4 * (j & 1))) & 15u;
+                        const uint32_t hi = (src[16 + i] >> j) & 1u;
+                        int lb, lbit, hb, hbit;
+                        q5k_slot(i, &lb, &lbit, &hb, &hbit);
+                        qu[lb] |= (uint8_t)(lo << lbit);
+                        hu[hb] |= (uint8_t)(hi << hbit);
+                    }
+                }
+            }
+        } else if (t == T_Q6_K) {
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* h = planes + L.hi_off + n * (K / 4);
+            uint8_t* sc = planes + L.sc_off + n * (K / 16);
+            uint8_t* d = planes + L.d_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(sc + b * 16, src + 192, 16);
+                memcpy(d + b * 2, src + 208, 2);
+                for (int j = 0; j < 8; ++j) {
+                    uint8_t* qu = q + b * 128 + j * 16;
+                    uint8_t* hu = h + b * 64 + j * 8;
+                    memset(qu, 0, 16);
+                    memset(hu, 0, 8);
+                    for (int i = 0; i < 32; ++i) {
+                        const uint32_t v = q6k_file_quant(src, j, i);
+                        int lb, lbit, hb, hbit;
+                        q6k_slot(i, &lb, &lbit, &hb, &hbit);
+                        qu[lb] |= (uint8_t)((v & 15u) << lbit);
+                        hu[hb] |= (uint8_t)((v >> 4) << hbit);
+                    }
+                }
+            }
+        } else if (t == T_Q8_0) {
+            uint8_t* q = planes + L.qs_off + n * K;
+            uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                memcpy(d + b * 2, row + b * bb, 2);
+                memcpy(q + b * 32, row + b * bb + 2, 32);
+            }
+        } else if (t == T_Q4_0) {
+            // reference src/mashbox/ops/reference.py:66-70: value i (i < 16) is the low nibble of qs[i], value 16 + i
+            // its high nibble (qs at byte 2)
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(d + b * 2, src, 2);
+                uint32_t unit[4] = {0, 0, 0, 0};
+                for (int i = 0; i < 32; ++i) {
+                    const uint32_t v = (src[2 + (i & 15)] >> (4 * (i >> 4))) & 15u;
+                    int dw, bit;
+                    q4k_slot(i, &dw, &bit);
+                    unit[dw] |= v << bit;
+                }
+                memcpy(q + b * 16, unit, 16);  // little-endian host, as the GPU
+            }
+        } else {
+            uint8_t* q = planes + L.qs_off + n * (K / 2);
+            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint8_t* src = row + b * bb;
+                memcpy(meta + b * 16, src, 16);
+                const uint8_t* qs = src + 16;
+                for (int j = 0; j < 8; ++j) {
+                    uint32_t unit[4] = {0, 0, 0, 0};
+                    for (int i = 0; i < 32; ++i) {
+                        const uint8_t byte = qs[32 * (j >> 1) + i];
+                        const uint32_t v = (j & 1) ? (byte >> 4) : (byte & 15u);
+                        int dw, bit;
+                        q4k_slot(i, &dw, &bit);
+                        unit[dw] |= v << bit;
+                    }
+                    memcpy(q + b * 128 + j * 16, unit, 16);  // little-endian host, as the GPU
+                }
+            }
+        }
+    }
+}
+
+inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, const Layout& L, int64_t r0, int64_t r1) {
+    const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
+    for (int64_t n = r0; n < r1; ++n) {
+        uint8_t* row = raw + n * rb;
+        if (t == T_Q5_K) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* h = planes + L.hi_off + n * (K / 8);
+            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, meta + b * 16, 16);
+                memset(dst + 16, 0, 160);
+                for (int j = 0; j < 8; ++j) {
+                    const uint8_t* qu = q + b * 128 + j * 16;
+                    const uint8_t* hu = h + b * 32 + j * 4;
+                    for (int i = 0; i < 32; ++i) {
+                        int lb, lbit, hb, hbit;
+                        q5k_slot(i, &lb, &lbit, &hb, &hbit);
+                        const uint8_t lo = (qu[lb] >> lbit) & 15u, hi = (hu[hb] >> hbit) & 1u;
+                        dst[48 + 32 * (j >> 1) + i] |= (uint8_t)(lo << (4 * (j & 1)));
+                        dst[16 + i] |= (uint8_t)(hi << j);
+                    }
+                }
+            }
+        } else if (t == T_Q6_K) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* h = planes + L.hi_off + n * (K / 4);
+            const uint8_t* sc = planes + L.sc_off + n * (K / 16);
+            const uint8_t* d = planes + L.d_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memset(dst, 0, 192);
+                memcpy(dst + 192, sc + b * 16, 16);
+                memcpy(dst + 208, d + b * 2, 2);
+                for (int j = 0; j < 8; ++j) {
+                    const uint8_t* qu = q + b * 128 + j * 16;
+                    const uint8_t* hu = h + b * 64 + j * 8;
+                    const int g = j >> 2, r = j & 3;
+                    for (int i = 0; i < 32; ++i) {
+                        int lb, lbit, hb, hbit;
+                        q6k_slot(i, &lb, &lbit, &hb, &hbit);
+                        const uint8_t lo = (qu[lb] >> lbit) & 15u, hi = (hu[hb] >> hbit) & 3u;
+                        dst[64 * g + 32 * (r & 1) + i] |= (uint8_t)(lo << (4 * (r >> 1)));
+                        dst[128 + 32 * g + i] |= (uint8_t)(hi << (2 * r));
+                    }
+                }
+            }
+        } else if (t == T_Q8_0) {
+            const uint8_t* q = planes + L.qs_off + n * K;
+            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                memcpy(row + b * bb, d + b * 2, 2);
+                memcpy(row + b * bb + 2, q + b * 32, 32);
+            }
+        } else if (t == T_Q4_0) {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, d + b * 2, 2);
+                memset(dst + 2, 0, 16);
+                uint32_t unit[4];
+                memcpy(unit, q + b * 16, 16);
+                for (int i = 0; i < 32; ++i) {
+                    int dw, bit;
+                    q4k_slot(i, &dw, &bit);
+                    dst[2 + (i & 15)] |= (uint8_t)(((unit[dw] >> bit) & 15u) << (4 * (i >> 4)));
+                }
+            }
+        } else {
+            const uint8_t* q = planes + L.qs_off + n * (K / 2);
+            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            for (int64_t b = 0; b < nb; ++b) {
+                uint8_t* dst = row + b * bb;
+                memcpy(dst, meta + b * 16, 16);
+                uint8_t* qs = dst + 16;
+                memset(qs, 0, 128);
+                for (int j = 0; j < 8; ++j) {
+                    uint32_t unit[4];
+                    memcpy(unit, q + b * 128 + j * 16, 16);
+                    for (int i = 0; i < 32; ++i) {
+                        int dw, bit;
+                        q4k_slot(i, &dw, &bit);
+                        const uint8_t v = (unit[dw] >> bit) & 15u;
+                        qs[32 * (j >> 1) + i] |= (j & 1) ? (uint8_t)(v << 4) : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// calls f(offset, bytes) on every run of alignment padding between and after the planes; false if f fails
+template <class F>
+inline bool for_each_gap(const Layout& L, F f) {
+    const int64_t ends[4][2] = {{L.qs_off + L.qs_bytes, L.hi_off}, {L.hi_off + L.hi_bytes, L.sc_off},
+                                {L.sc_off + L.sc_bytes, L.d_off}, {L.d_off + L.d_bytes, L.total}};
+    for (const auto& e : ends)
+        if (e[1] > e[0] && !f(e[0], e[1] - e[0])) return false;
+    return true;
+}
+
+// tiled int8 planes (mbq_layout.h): 16-row tiles [t0, t1) from the row-major (N, K) quants and (N,) scales; padding
+// rows and columns zero
+inline void i8t_pack_tiles(const int8_t* q, const float* s, int64_t N, int64_t K, uint8_t* planes, const Layout& L,
+                           int64_t t0, int64_t t1) {
+    const int64_t kc_n = (K + 63) / 64;
+    for (int64_t rt = t0; rt < t1; ++rt) {
+        for (int64_t kc = 0; kc < kc_n; ++kc) {
+            uint8_t* blk = planes + L.qs_off + (rt * kc_n + kc) * 1024;
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = rt * 16 + r, c0 = kc * 64, n = row < N ? std::min<int64_t>(64, K - c0) : 0;
+                if (n > 0) memcpy(blk + r * 64, q + row * K + c0, (size_t)n);
+                if (n < 64) memset(blk + r * 64 + std::max<int64_t>(n, 0), 0, (size_t)(64 - std::max<int64_t>(n, 0)));
+            }
+        }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = rt * 16 + r;
+            const float v = row < N ? s[row] : 0.f;
+            memcpy(planes + L.sc_off + row * 4, &v, 4);
+        }
+    }
+}
+
+inline void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t* q, float* s, const Layout& L,
+                             int64_t t0, int64_t t1) {
+    const int64_t kc_n = (K + 63) / 64;
+    for (int64_t rt = t0; rt < t1; ++rt)
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = rt * 16 + r;
+            if (row >= N) continue;
+            for (int64_t kc = 0; kc < kc_n; ++kc)
+                memcpy(q + row * K + kc * 64, planes + L.qs_off + (rt * kc_n + kc) * 1024 + r * 64, (size_t)std::min<int64_t>(64, K - kc * 64));
+            memcpy(s + row, planes + L.sc_off + row * 4, 4);
+        }
+}
+
+// whole weights: the padding zeroed, then the rows (16-row tiles for int8) on up to `threads` host threads (0: every
+// hardware thread). The caller checks the shape and the buffer sizes.
+inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
+    const Layout L = layout(t, rows, cols);
+    for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
+    parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
+}
+
+inline void unpack_host(int t, const uint8_t* planes, int64_t rows, int64_t cols, uint8_t* raw, int threads) {
+    const Layout L = layout(t, rows, cols);
+    parallel_rows(rows, threads, [&](int64_t a, int64_t b) { unpack_rows(t, planes, cols, raw, L, a, b); });
+}
+
+inline void i8t_repack_host(const int8_t* q, const float* s, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
+    const Layout L = layout(T_I8T, rows, cols);
+    for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
+    parallel_rows((rows + 15) / 16, threads, [&](int64_t a, int64_t b) { i8t_pack_tiles(q, s, rows, cols, planes, L, a, b); });
+}
+
+inline void i8t_unpack_host(const uint8_t* planes, int64_t rows, int64_t cols, int8_t* q, float* s, int threads) {
+    const Layout L = layout(T_I8T, rows, cols);
+    parallel_rows((rows + 15) / 16, threads, [&](int64_t a, int64_t b) { i8t_unpack_tiles(planes, rows, cols, q, s, L, a, b); });
+}
+
+}  // namespace mbq

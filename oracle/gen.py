@@ -1,8 +1,9 @@
 """Seeded synthetic inputs for the five BASELINE configs. TEST INFRASTRUCTURE (see oracle/ref.py header).
 
 Draws use numpy.random.default_rng(seed) in the order the config text lists them; fp16 and bf16 values are made by
-round-to-nearest-even casts. The bench and the parity tests use these same generators, so a parity test at a reduced
-size and the bench at full size see inputs from one definition.
+round-to-nearest-even casts. The parity tests use these generators (seed 0 for the full-size config tests). The bench
+does not import the oracle: its inputs come from mashbox_amd/synth.py, torch's RNG on the GPU with the same value
+ranges and block layouts, so its timings are of the same kind of data but not of these exact draws.
 
 Block generators follow the value ranges of BASELINE.json's configs; the Q8_0 one has the same form as the reference's
 own generator tests/cpu/test_moe_bundle_dense.py:81-87 (fp16 d uniform, int8 q uniform in [-127, 127]).

@@ -1,6 +1,6 @@
 """The kernels that issue v_mfma through inline asm (mfma_acc / mfma32_acc in mbq_device.h: mbq_gemm.hip's specialized
-kernel, mbq_pgemm.hip) pin their accumulators the compiler cannot see as MFMA results, so the compiler inserts no wait
-states after them. This test compiles both sources to gfx950 assembly (hipcc, no GPU) and checks that within 20 wait
+kernel) pin their accumulators the compiler cannot see as MFMA results, so the compiler inserts no wait
+states after them. This test compiles the sources to gfx950 assembly (hipcc, no GPU) and checks that within 20 wait
 states after every MFMA (one per instruction, N + 1 per s_nop N) no non-MFMA instruction reads or writes its
 destination registers: the copies the compiler may place at loop edges must come after the kernels' mfma_drain."""
 import os
