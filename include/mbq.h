@@ -173,6 +173,7 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
 #define MBQ_KERNEL_GEMV 0
 #define MBQ_KERNEL_STREAM 1
 #define MBQ_KERNEL_TILES 2
+#define MBQ_KERNEL_KGROUP 3
 int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits);
 int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits);
 

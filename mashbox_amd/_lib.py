@@ -48,8 +48,8 @@ _SIGS = {
 
 # GEMM kernels of gemm_plan / force_gemm_plan (MBQ_KERNEL_* of include/mbq.h)
 KERNEL_AUTO = KERNEL_GEMV = 0
-KERNEL_STREAM, KERNEL_TILES = 1, 2
-KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_STREAM: "stream", KERNEL_TILES: "tiles"}
+KERNEL_STREAM, KERNEL_TILES, KERNEL_KGROUP = 1, 2, 3
+KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_STREAM: "stream", KERNEL_TILES: "tiles", KERNEL_KGROUP: "kgroup"}
 
 
 def gemm_plan(t: int, m: int, n: int, k: int):

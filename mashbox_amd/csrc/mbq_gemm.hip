@@ -405,11 +405,19 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
                 }
         }
     }
+    // every scale is loaded before the first store: a scale load between stores would make each store wait for the ones
+    // before it (vmcnt counts stores)
+    float sc[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int nn = n0 + wn * (BN / 4) + j * 16 + (lane & 15);
+        sc[j] = nn < N ? row_scale<T>(g.srow, base, g.sc_off, nn) : 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int nn = n0 + wn * (BN / 4) + j * 16 + (lane & 15);
         if (nn >= N) continue;
-        const float s = row_scale<T>(g.srow, base, g.sc_off, nn);
+        const float s = sc[j];
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -502,11 +510,17 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
             mfma_drain();
         }
         // lane holds weight row n0 + 96 cn + 32 j + (lane & 31) and activation rows m0 + 128 cm + 32 i + 8 e + 4 (lane >> 5) + r
+        float scs[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int nn = n0 + br + 32 * j;
+            scs[j] = nn < N ? row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn) : 0.f;
+        }
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int nn = n0 + br + 32 * j;
             if (nn >= N) continue;
-            const float sc = row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn);
+            const float sc = scs[j];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -895,10 +909,19 @@ static int pick(const Args& a, Plan* p) {
 
 // The kernel of a batch the GEMV does not run: the weight-stream kernel (mbq_wsgemm.hip) up to WS_MAX_M rows, else the
 // LDS-tile kernel; a forced plan overrides it.
-struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block
+struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block; K_KGROUP: bn rows per block
 
 static int choose(int t, const Args& a, Choice* c) {
     const int fk = g_force_kind.load();
+    // tiled int8 planes up to 64 rows: the K-group kernel (mbq_kgemm.hip), unless another kernel is forced
+    if (t == T_I8T && a.M <= WS_MAX_M && (fk == K_AUTO || fk == K_KGROUP)) {
+        int R = 0, S = 0;
+        if (int rc = kgemm_plan(a, fk == K_KGROUP ? g_force_s.load() : 0, &R, &S)) return rc;
+        *c = Choice{K_KGROUP, 16, R, S};
+        return 0;
+    }
+    if (fk == K_KGROUP && a.M <= WS_MAX_M)
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled int8 planes (MBQ_I8T) only");
     if (fk == K_STREAM) {
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
@@ -932,6 +955,7 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     Choice c;
     if (int rc = choose(T, a, &c)) return rc;
     if (c.kind == K_STREAM) return launch_wsgemm(T, a, c.bn, c.S, s);
+    if (c.kind == K_KGROUP) return launch_kgemm(a, c.S, s);
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
@@ -946,6 +970,12 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
     Choice c;
     if (int rc = choose(t, a, &c)) return rc;
     *kernel = c.kind;
+    if (c.kind == K_KGROUP) {
+        *bm = 16;
+        *bn = c.bn;
+        *splits = c.S;
+        return 0;
+    }
     if (c.kind == K_STREAM) {
         int nr = c.bn, S = c.S;
         wsgemm_effective(t, a, &nr, &S);
@@ -980,6 +1010,9 @@ int force_gemm_plan(int kernel, int bm, int bn, int splits) {
             break;
         case K_TILES:
             if ((bm || bn) && find_cand<T_Q4_K>(bm, bn) < 0) return set_error(MBQ_BAD_ARG, "no LDS GEMM tile %d x %d", bm, bn);
+            break;
+        case K_KGROUP:
+            if (bm || bn) return set_error(MBQ_BAD_ARG, "the K-group kernel chooses its own rows per block (bm = bn = 0)");
             break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM kernel %d", kernel);
     }

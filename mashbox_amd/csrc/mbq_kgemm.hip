@@ -1,0 +1,434 @@
+// gfx950 K-group GEMM of the int8 per-channel linear on tiled planes (T_I8T) for decode batches of 5..64 activation
+// rows: y (M, N) = (x (M, K) @ bf16(q).T, float32 accumulation) * s, reference
+// src/mashbox/models/qwen3_8_27b/model.py:72-82, with the weights repacked once at load into 16-row tiles
+// (mbq_layout.h) from reference src/mashbox/models/qwen3_8_27b/weights.py:55-74.
+//
+// What bounds this regime on MI355X is the vector-memory throughput of a CU, not the MFMAs: a CU streams its share of
+// the weights from HBM (about 25 GB/s at the chip's ~6.5 TB/s) and must also bring in the x its weights meet, 128
+// bytes per K value at 64 rows, from L2. A CU moves about 50 GB/s with 4 waves and 70 GB/s with 8 (b128 loads,
+// measured), so the x bytes per weight byte are what the design minimises:
+//   * one block of 8 waves per CU: RG row groups x KG K groups (RG KG = 8). The waves of a K group walk the chunks
+//     (64 K values) c = kg, kg + KG, ... of the block's K range; x of a chunk is copied once into that K group's LDS
+//     ring by DMA (contiguous 8-row x 128-byte loads) and read by its RG waves as MFMA A operands, so every x byte
+//     enters the CU once per block;
+//   * a block owns any row range [r0, r1) of the weight, not a multiple of 16: N is cut into as many equal ranges as
+//     fill the CUs (17408 rows = 256 ranges of 68), and a wave loads only its rows of the 16-row tiles it touches
+//     (the rest of a tile reads zero through the buffer range check: no traffic); the MFMAs of those rows are wasted;
+//   * K splits S (blocks per row range) cut the x bytes per block by S at the cost of float32 partials: each split
+//     stores its partial tile with device-coherent (sc1) stores, and the split that arrives last (an atomic counter
+//     per range, which it resets) adds the S partials in split order, so the sum does not depend on arrival order.
+// Weights go from HBM (non-temporal loads) straight into B-operand registers, D chunks in flight per wave. After the
+// K loop the K groups of a row group add their accumulators through LDS in a fixed tree order.
+//
+// Lane layout (the weight-stream kernel's, mbq_wdirect.h): in K step s (32 values) of a chunk, lane l holds K values
+// 16 (l >> 4) + 8 s + e (e = 0..7) of x row 16 i + (l & 15) and of weight row (l & 15) of a tile; the MFMA sums over
+// K, so this K order is as good as any. x stage layout: 16 MT rows of 128 bytes, the 16-byte piece p of row r at slot
+// p ^ (r & 7); the DMA applies the swizzle through each lane's source address.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+#include <utility>
+
+#include "mbq_device.h"
+#include "mbq_launch.h"
+#include "mbq_layout.h"
+#include "mbq_wdirect.h"
+
+namespace mbq {
+
+constexpr int KGM_THREADS = 512;   // 8 waves: 2 per SIMD
+
+struct KgmArgs {
+    const uint8_t* base;           // planes (host layer applied)
+    int64_t stride;                // bytes between stacked weights (layer_dev)
+    const int32_t* layer_dev;
+    int nlayers;
+    int64_t sc_off, wbytes;
+    const uint16_t* x;
+    int M, N, K;
+    void* y;
+    int out_bf16;
+    int R;                         // rows per block
+    int S, kcs;                    // K splits per row range and chunks per split
+    float* ws;                     // S > 1: partial tiles, (range, split) -> E floats
+    int* cnt;                      // S > 1: arrival counter per row range (zero between launches)
+    uint32_t ws_bytes;
+};
+
+// K groups and LDS stages per K group
+template <int RG> constexpr int kgm_kg() { return 8 / RG; }
+template <int RG> constexpr int kgm_depth() { return RG == 1 ? 2 : 3; }
+// dynamic LDS: the x rings, or the K-group reduction's buffer if larger
+template <int MT, int RG, int NTW>
+constexpr size_t kgm_lds() {
+    const size_t ring = (size_t)kgm_kg<RG>() * kgm_depth<RG>() * 16 * MT * 128;
+    const size_t red = (size_t)RG * (kgm_kg<RG>() / 2) * MT * NTW * 1024;
+    return ring > red ? ring : red;
+}
+// floats of one block's partial tile: RG row groups x MT x NTW 16x16 tiles
+template <int MT, int RG, int NTW> constexpr int kgm_elems() { return RG * MT * NTW * 256; }
+
+// f(integral_constant<int, P>) for each P of the sequence, in order
+template <class F, int... P>
+__device__ __forceinline__ void kgm_each(F&& f, std::integer_sequence<int, P...>) {
+    (f(std::integral_constant<int, P>{}), ...);
+}
+
+template <int MT, int RG, int NTW, bool KFULL>
+__global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
+    __shared__ int kgm_last;
+    constexpr int KG = kgm_kg<RG>(), D = kgm_depth<RG>();
+    constexpr int STAGE = 16 * MT * 128;                 // bytes of one x stage (16 MT rows x 64 values)
+    constexpr int NX = 2 * MT / RG;                      // x DMA instructions per wave per chunk (1 KiB each)
+    static_assert(NX * RG == 2 * MT, "the RG waves of a K group issue whole DMA instructions");
+    constexpr int VMT = (D - 1) * NTW + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
+    static_assert(VMT < 64, "vmcnt range");
+    const int M = g.M, N = g.N, K = g.K;
+    const int lane = threadIdx.x & 63, lg = lane >> 4, r16 = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kg = wave % KG, q = wave / KG;             // K group, row group
+    const int rr = blockIdx.x / g.S, z = blockIdx.x - rr * g.S;
+
+    // rows of this wave's row group: [rq0, rq1); its tiles start at tile rq0 / 16
+    const int r0 = rr * g.R, r1 = min(N, r0 + g.R);
+    const int RQ = (g.R + RG - 1) / RG;
+    const int rq0 = min(r1, r0 + q * RQ), rq1 = min(r1, rq0 + RQ);
+    const int t0 = rq0 >> 4;
+
+    const int64_t lo = layer_offset(g.stride, g.layer_dev, g.nlayers);
+    const bool ok = lo >= 0;
+    const uint8_t* wb = g.base + (ok ? lo : 0);
+    const rsrc_t wr = make_rsrc(wb, (uint32_t)g.wbytes);
+    const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
+
+    // chunks of this split: [c0, c1); K group kg takes c0 + kg + KG l for l < its count; every group walks `steps`
+    // steps (the block's barrier keeps them together), a step past its count loads zero through the range check
+    const int KC = (K + 63) / 64;
+    const int c0 = z * g.kcs, c1 = min(KC, c0 + g.kcs);
+    const int nch = ok ? max(0, c1 - c0) : 0;
+    const int steps = (nch + KG - 1) / KG;
+    const int mine = (nch - kg + KG - 1) / KG;           // chunks of this K group
+
+    // weight offsets: tile t0 + j, row r16, the lane group's 16 bytes; rows outside [rq0, rq1) read zero
+    uint32_t wo[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+        const int row = 16 * (t0 + j) + r16;
+        wo[j] = (row >= rq0 && row < rq1) ? (uint32_t)i8t_off(row, K, 0) + 16u * (uint32_t)lg : OOB_VOFF;
+    }
+    // x DMA: instruction i of this wave fills rows 8 (q + RG i) .. + 7 of the stage; lane l writes slot l % 8 of row
+    // l / 8, which holds piece (l % 8) ^ (row & 7); rows past M read zero
+    uint32_t xvo[NX];
+    int xk[NX];
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int r = 8 * (q + RG * i) + (lane >> 3), p = (lane & 7) ^ (r & 7);
+        xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + 8 * p) * 2) : OOB_VOFF;
+        xk[i] = 8 * p;
+    }
+    uint8_t* ring = kgm_lds_buf + (size_t)kg * D * STAGE;
+    auto chunk_of = [&](int l) __attribute__((always_inline)) { return c0 + kg + KG * l; };            // valid while l < mine
+    auto dma_x = [&](int st, int l) __attribute__((always_inline)) {
+        const int c = chunk_of(l);
+        const bool live = l < mine;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            uint32_t v = live ? xvo[i] : OOB_VOFF;
+            if constexpr (!KFULL) v = (64 * c + xk[i] < K) ? v : OOB_VOFF;
+            ws_dma16(xr, reinterpret_cast<uint16_t*>(ring + st * STAGE + 8 * (q + RG * i) * 128), v,
+                     live ? (uint32_t)c * 128u : 0u);
+        }
+    };
+    auto load_w = [&](u32x4* W, int l) __attribute__((always_inline)) {
+        const int c = chunk_of(l);
+        const bool live = l < mine;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+            W[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? wo[j] : OOB_VOFF,
+                                                                                  live ? (uint32_t)c * 1024u : 0u, 2));
+    };
+    // A operand: x row 16 i + (lane & 15), piece 2 (lane >> 4) + s of stage st
+    auto a_op = [&](int st, int i, int s) __attribute__((always_inline)) {
+        const int r = 16 * i + r16, p = (2 * lg + s) ^ (r & 7);
+        return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * 128 + (p << 4));
+    };
+
+    f32x4_t acc[MT][NTW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4 W[D][NTW];
+
+    // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
+    // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
+    auto step = [&](auto U_, int l) __attribute__((always_inline)) {
+        constexpr int U = decltype(U_)::value;                            // l % D
+        wait_vm<VMT>();
+        barrier_nofence();                                                // stage U landed for every wave; stage
+        __builtin_amdgcn_sched_barrier(0);                                // (l - 1) % D is no longer read
+        dma_x((U + D - 1) % D, l + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            bf16x8_t A[MT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) A[i] = a_op(U, i, s);
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
+                const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
+                const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
+#pragma unroll
+                for (int i = 0; i < MT; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(W[U], l + D);
+    };
+
+    if (steps > 0) {                                                      // block-uniform
+#pragma unroll
+        for (int p = 0; p < D; ++p) {
+            if (p < D - 1) dma_x(p, p);
+            load_w(W[p], p);
+        }
+        int l = 0;
+        for (; l + D <= steps; l += D)
+            kgm_each([&](auto P) __attribute__((always_inline)) { step(P, l + decltype(P)::value); }, std::make_integer_sequence<int, D>{});
+        kgm_each([&](auto P) __attribute__((always_inline)) {
+            if (l + decltype(P)::value < steps) step(P, l + decltype(P)::value);
+        }, std::make_integer_sequence<int, D - 1>{});
+        wait_vm<0>();                                                     // no DMA may land after the rings are reused
+    }
+    __syncthreads();
+
+    // K groups of a row group: kg in [h, 2h) hands its accumulators to kg - h through LDS, h = KG/2 .. 1
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(kgm_lds_buf);
+#pragma unroll
+    for (int h = KG / 2; h >= 1; h /= 2) {
+        if (kg >= h && kg < 2 * h) {
+            f32x4_t* dst = red + ((size_t)(q * (KG / 2) + (kg - h)) * MT * NTW) * 64;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) dst[(i * NTW + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (kg < h) {
+            const f32x4_t* src = red + ((size_t)(q * (KG / 2) + kg) * MT * NTW) * 64;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) acc[i][j] += src[(i * NTW + j) * 64 + lane];
+        }
+        __syncthreads();
+    }
+
+    // the K group 0 wave of each row group holds the block's sums of its rows
+    constexpr int E = kgm_elems<MT, RG, NTW>();
+    if (g.S > 1) {
+        const rsrc_t pr = make_rsrc(g.ws, g.ws_bytes);
+        const uint32_t lofs = (uint32_t)(q * MT * NTW * 64 + lane) * 16u;
+        if (kg == 0) {
+            const uint32_t own = (uint32_t)(blockIdx.x * E) * 4u;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NTW; ++j)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr,
+                                                           lofs + (uint32_t)((i * NTW + j) * 64) * 16u, own, 16);
+            wait_vm<0>();                                                 // the partial is in device-coherent memory
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int old = __hip_atomic_fetch_add(g.cnt + rr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            kgm_last = old == g.S - 1;
+            if (old == g.S - 1) __hip_atomic_store(g.cnt + rr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!kgm_last) return;
+        if (kg == 0) {
+            const uint32_t first = (uint32_t)(rr * g.S * E) * 4u;
+            for (int zz = 0; zz < g.S; ++zz) {                            // split order, whoever arrived last
+                f32x4_t v[MT][NTW];
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < NTW; ++j)
+                        v[i][j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                      pr, lofs + (uint32_t)((i * NTW + j) * 64) * 16u, first + (uint32_t)(zz * E) * 4u, 16));
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < NTW; ++j) acc[i][j] = zz == 0 ? v[i][j] : acc[i][j] + v[i][j];
+            }
+        }
+    }
+    if (kg != 0) return;
+    // every scale first (one wait), then the stores back to back: a store past M or outside [rq0, rq1) gets an offset
+    // out of y's range (no write), so the loop has no branches and no wait between stores
+    float sc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+        const int n = 16 * (t0 + j) + r16;
+        sc[j] = (ok && n >= rq0 && n < rq1) ? row_scale<T_I8T>(nullptr, wb, g.sc_off, n) : __builtin_nanf("");
+    }
+    const uint32_t esz = g.out_bf16 ? 2u : 4u;
+    const rsrc_t yr = make_rsrc(g.y, (uint32_t)M * (uint32_t)N * esz);
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+        const int n = 16 * (t0 + j) + r16;
+        const bool col = n >= rq0 && n < rq1;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * i + 4 * lg + r;
+                const uint32_t off = (col && m < M) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : OOB_VOFF;
+                const float v = acc[i][j][r] * sc[j];
+                if (g.out_bf16)
+                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)pack_bf16(v, 0.f), yr, off, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, off, 0, 0);
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------ planner
+// A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
+struct KgmPlan { int S, R, RG, NTW; };
+constexpr int KGM_MAX_NTW = 6;
+
+// the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
+static int kgm_ntw(int64_t N, int64_t R, int RG) {
+    const int64_t ranges = (N + R - 1) / R, RQ = (R + RG - 1) / RG;
+    int64_t most = 0;
+    for (int64_t rr = 0; rr < ranges; ++rr) {
+        const int64_t r0 = rr * R, r1 = std::min(N, r0 + R);
+        for (int q = 0; q < RG; ++q) {
+            const int64_t a = std::min(r1, r0 + q * RQ), b = std::min(r1, a + RQ);
+            if (b > a) most = std::max(most, (b - 1) / 16 - a / 16 + 1);
+        }
+    }
+    return (int)most;
+}
+
+// The plan of least estimated cost per block, in bytes a CU moves (its weights, the x of its K range, and for S > 1
+// its partial tile written plus, for the last arriver, S partials read) plus the MFMA rows spent on rows outside the
+// block's range and the K groups left idle in a block's last step; the weights reflect MI355X timings of the 7
+// projections of a 27B-class layer at 64 rows against forced split counts, over S in {1, 2, 3, 4, 6, 8} (only `force_s` when
+// it is set) and RG in {1, 2}, with rows per block chosen so that the ranges fill the CUs once.
+static KgmPlan kgm_choose(int64_t M, int64_t N, int64_t K, int cus, int force_s) {
+    const int64_t KC = (K + 63) / 64;
+    const int MT = (int)((M + 15) / 16);
+    KgmPlan best{0, 0, 0, 0};
+    double best_cost = 0;
+    for (int S : {1, 2, 3, 4, 6, 8}) {
+        if (force_s > 0) S = force_s;
+        if (KC >= S) {
+            const int64_t ranges = std::max<int64_t>(1, cus / S);
+            const int64_t R = (N + ranges - 1) / ranges;
+            for (int RG : {1, 2}) {
+                const int KG = 8 / RG;
+                const int ntw = kgm_ntw(N, R, RG);
+                if (ntw > KGM_MAX_NTW) continue;
+                const int64_t kcs = (KC + S - 1) / S;
+                const double w = (double)R * kcs * 64;                          // weight bytes
+                const double x = 0.5 * 16 * MT * 128 * kcs;                     // x bytes (L2 hits: half weight)
+                // partial tile written, and S read by the last arriver at the end of its work (twice the weight)
+                const double part = S > 1 ? (double)RG * MT * ntw * 1024 * (1 + 2 * S) : 0.0;
+                const double waste = 0.5 * (double)std::max<int64_t>(0, RG * ntw * 16 - R) * kcs * 64;
+                const double idle = (double)((kcs + KG - 1) / KG * KG - kcs) / (double)kcs;
+                const double cost = (w + x + part + waste) * (1.0 + idle);
+                if (best.S == 0 || cost < best_cost) {
+                    best = KgmPlan{S, (int)R, RG, ntw};
+                    best_cost = cost;
+                }
+            }
+        }
+        if (force_s > 0) break;
+    }
+    return best;
+}
+
+// ------------------------------------------------------------------------------------------------------ launchers
+template <int MT, int RG, int NTW, bool KFULL>
+static int kgm_launch(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
+    auto kern = kgemm_kernel<MT, RG, NTW, KFULL>;
+    const size_t lds = kgm_lds<MT, RG, NTW>();
+    static std::atomic<uint64_t> lds_set{0};
+    if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM: %zu bytes of LDS refused", lds);
+    const int64_t KC = (a.K + 63) / 64;
+    const int kcs = (int)((KC + p.S - 1) / p.S);
+    KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
+              a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes};
+    const int64_t ranges = (a.N + p.R - 1) / p.R;
+    kern<<<dim3((unsigned)(ranges * p.S)), KGM_THREADS, lds, s>>>(g);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
+template <int MT, int RG, bool KFULL>
+static int kgm_launch_ntw(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
+    switch (p.NTW) {
+        case 1: return kgm_launch<MT, RG, 1, KFULL>(a, p, w, s);
+        case 2: return kgm_launch<MT, RG, 2, KFULL>(a, p, w, s);
+        case 3: return kgm_launch<MT, RG, 3, KFULL>(a, p, w, s);
+        case 4: return kgm_launch<MT, RG, 4, KFULL>(a, p, w, s);
+        case 5: return kgm_launch<MT, RG, 5, KFULL>(a, p, w, s);
+        case 6: return kgm_launch<MT, RG, 6, KFULL>(a, p, w, s);
+    }
+    return set_error(MBQ_BAD_ARG, "K-group GEMM: %d tiles per wave", p.NTW);
+}
+
+template <int MT, bool KFULL>
+static int kgm_launch_rg(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
+    if (p.RG == 1) return kgm_launch_ntw<MT, 1, KFULL>(a, p, w, s);
+    return kgm_launch_ntw<MT, 2, KFULL>(a, p, w, s);
+}
+
+// bytes of the partial tiles of a plan
+static size_t kgm_ws_bytes(int64_t M, int64_t N, const KgmPlan& p) {
+    const int MT = (int)((M + 15) / 16);
+    const int64_t ranges = (N + p.R - 1) / p.R;
+    return (size_t)ranges * p.S * p.RG * MT * p.NTW * 256 * 4;
+}
+
+int kgemm_plan(const Args& a, int force_s, int* rows_per_block, int* splits) {
+    const KgmPlan p = kgm_choose(a.M, a.N, a.K, cus_of_device(), force_s);
+    if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
+                                   (long long)a.N, (long long)a.K, force_s);
+    *rows_per_block = p.R;
+    *splits = p.S;
+    return 0;
+}
+
+int launch_kgemm(const Args& a, int force_s, hipStream_t s) {
+    if (a.M < 1 || a.M > 64) return set_error(MBQ_BAD_ARG, "K-group GEMM: M = %lld", (long long)a.M);
+    if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES || a.M * a.N * 4 > BUF_MAX_BYTES)
+        return set_error(MBQ_BAD_ARG, "K-group GEMM operands over 2 GiB");
+    const KgmPlan p = kgm_choose(a.M, a.N, a.K, cus_of_device(), force_s);
+    if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
+                                   (long long)a.N, (long long)a.K, force_s);
+    Workspace w;
+    if (p.S > 1) {
+        const int64_t ranges = (a.N + p.R - 1) / p.R;
+        if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.M, a.N, p), s, &w)) return rc;
+    }
+    const bool kfull = a.K % 64 == 0;
+    switch ((a.M + 15) / 16) {
+        case 1: return kfull ? kgm_launch_rg<1, true>(a, p, w, s) : kgm_launch_rg<1, false>(a, p, w, s);
+        case 2: return kfull ? kgm_launch_rg<2, true>(a, p, w, s) : kgm_launch_rg<2, false>(a, p, w, s);
+        case 3: return kfull ? kgm_launch_rg<3, true>(a, p, w, s) : kgm_launch_rg<3, false>(a, p, w, s);
+        default: return kfull ? kgm_launch_rg<4, true>(a, p, w, s) : kgm_launch_rg<4, false>(a, p, w, s);
+    }
+}
+
+}  // namespace mbq

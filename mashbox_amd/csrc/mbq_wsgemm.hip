@@ -246,11 +246,19 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
                 for (int j = 0; j < NT; ++j) acc[i][j] = z == 0 ? v[i][j] : acc[i][j] + v[i][j];
         }
     }
+    // every scale is loaded before the first store: a scale load between stores would make each store wait for the ones
+    // before it (vmcnt counts stores)
+    float sc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int nn = n0 + 16 * j + r16;
+        sc[j] = nn < N ? row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn) : 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const int nn = n0 + 16 * j + r16;
         if (nn >= N) continue;
-        const float s = row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn);
+        const float s = sc[j];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll

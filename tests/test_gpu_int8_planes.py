@@ -3,7 +3,8 @@ MBQ_I8T planes), against the reference's int8 linear (reference src/mashbox/mode
 (x @ bf16(q).T, float32 accumulation) * s.
 
 Oracle: the float64 product of the exact int8 weights and scales from the oracle's seeded generator (tests/_check.py
-bars). Batches past the decode GEMV run the same plans as the unpacked linear, so there the two are equal bit for bit.
+bars). Batches of 5-64 rows run the K-group kernel (mbq_kgemm.hip), which only the tiled planes have; batches past 64
+rows run the same LDS-tile plans as the unpacked linear, so there the two are equal bit for bit.
 """
 import numpy as np
 import pytest
@@ -62,9 +63,11 @@ def test_planes_linear_matches_reference(n, k, m, cuda):
     yb = I8.linear(x, p)
     assert yb.dtype == torch.bfloat16
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y))
-    if m > 4:                                                  # the same plan as the unpacked weights: same bits
+    if m > 64:                                                 # the same plan as the unpacked weights: same bits
         assert LIB.plan_str(LIB.I8T, m, n, k) == LIB.plan_str(LIB.INT8, m, n, k)
         assert np.array_equal(y.view(np.uint32), _f32(x, w).cpu().numpy().view(np.uint32))
+    elif m > 4:
+        assert LIB.gemm_plan(LIB.I8T, m, n, k)[0] == LIB.KERNEL_KGROUP
 
 
 @pytest.mark.parametrize("m", [1, 4, 64, 300])
@@ -148,6 +151,64 @@ def test_graph_replays_on_planes(forced_plan, cuda):
     _, x2 = _x(rng, m, k, cuda)
     p = I8.repack(torch.from_numpy(q).to(cuda), torch.from_numpy(s).to(cuda))
     forced_plan(LIB.KERNEL_STREAM, 16, 64, 4)
+    eager = _f32(x, p).cpu().numpy()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = _f32(x, p)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), eager.view(np.uint32))
+        _f32(x2, p)
+        torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------------------------- K-group kernel
+@pytest.mark.parametrize("m", [5, 16, 17, 33, 64])
+@pytest.mark.parametrize("n,k", [(1000, 16 * 57), (4500, 64 * 40), (70, 64 * 3), (7, 16)])
+def test_kgroup_every_split_count(m, n, k, forced_plan, cuda):
+    """the K-group kernel at every split count the planner can take (each split count fixes rows per block, row groups
+    and tiles per wave), on ragged row counts (blocks whose row ranges start and end inside 16-row tiles) and ragged K
+    (a last chunk partly past K), against the float64 product"""
+    rng = np.random.default_rng([m, n, k, 5])
+    q, s = G.int8_weights(rng, n, k)
+    xb, x = _x(rng, m, k, cuda)
+    ref = (R.bf16_to_f32(xb).astype(np.float64) @ q.astype(np.float64).T) * s
+    p = I8.repack(torch.from_numpy(q).to(cuda), torch.from_numpy(s).to(cuda))
+    kc = (k + 63) // 64
+    for splits in (0, 1, 2, 3, 4, 6, 8):
+        if splits > kc:
+            continue
+        forced_plan(LIB.KERNEL_KGROUP, 0, 0, splits)
+        plan = LIB.gemm_plan(LIB.I8T, m, n, k)
+        assert plan[0] == LIB.KERNEL_KGROUP and (splits == 0 or plan[3] == splits), plan
+        print(f"kgroup m={m} n={n} k={k} plan {plan}", flush=True)
+        y = _f32(x, p).cpu().numpy()
+        assert_product(y, ref, f"kgroup m={m} n={n} k={k} plan {plan}")
+        # a split K repeats bit for bit (partials added in split order, whichever block arrives last)
+        assert np.array_equal(_f32(x, p).cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+
+def test_kgroup_plans_of_config_4():
+    """the automatic plans of config 4's projections at 64 rows: the K-group kernel, with the split counts that measured
+    fastest on MI355X (q, o, gate, up: 1-2; k, v, down: 4)"""
+    for name, (n, k) in G.LAYER_27B.items():
+        kern, _, rows, splits = LIB.gemm_plan(LIB.I8T, 64, n, k)
+        assert kern == LIB.KERNEL_KGROUP, name
+        assert splits in ((4,) if name in ("k", "v", "down") else (1, 2)), (name, rows, splits)
+
+
+def test_kgroup_graph_replays(forced_plan, cuda):
+    """a split-K K-group call recorded into a HIP graph replays bit for bit equal to the eager call, with eager calls of
+    the same kernel in between"""
+    rng = np.random.default_rng(78)
+    m, n, k = 64, 1024, 5120
+    q, s = G.int8_weights(rng, n, k)
+    xb, x = _x(rng, m, k, cuda)
+    _, x2 = _x(rng, m, k, cuda)
+    p = I8.repack(torch.from_numpy(q).to(cuda), torch.from_numpy(s).to(cuda))
+    forced_plan(LIB.KERNEL_KGROUP, 0, 0, 4)
     eager = _f32(x, p).cpu().numpy()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()

@@ -83,3 +83,31 @@ def test_noalloc_refuses_a_plan_beyond_its_scratch():
         assert_product_dev(y, ref, "forced 64x64/4")
     finally:
         LIB.force_gemm_plan()
+
+
+def test_noalloc_int8_planes_split_k():
+    """tiled int8 planes at decode batches run the K-group kernel; with K splits its partials sit in the scratch too:
+    two calls in a row (the second smaller), bit for bit equal to mbq_matmul and within the product bars"""
+    dev = torch.device("cuda", 0)
+    L = LIB.lib()
+    for i, (m, n, k) in enumerate([(64, 5120, 17408), (40, 1024, 5120)]):
+        plan = LIB.gemm_plan(LIB.I8T, m, n, k)
+        print(f"int8 planes case {i}: {m}x{n}x{k} plan {plan}", flush=True)
+        assert plan[0] == LIB.KERNEL_KGROUP and plan[3] > 1, "the case must split K"
+        rng = np.random.default_rng(300 + i)
+        q, s = G.int8_weights(rng, n, k)
+        pb = LIB.check(L.mbq_plane_bytes(LIB.I8T, n, k), "plane_bytes")
+        host = torch.empty(pb, dtype=torch.uint8)
+        LIB.check(L.mbq_int8_repack_host(q.ctypes.data_as(ctypes.c_void_p), s.ctypes.data_as(ctypes.c_void_p), n, k,
+                                         ctypes.c_void_p(host.data_ptr()), pb, 0), "int8 repack_host")
+        planes = host.to(dev)
+        xb = G.acts(rng, m, k)
+        x = torch.from_numpy(xb.astype(np.int16)).view(torch.bfloat16).to(dev)
+        ref = (x.to(torch.float64) @ torch.from_numpy(q).to(dev).to(torch.float64).T) * torch.from_numpy(s).to(dev).to(torch.float64)
+        y_ref = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        LIB.check(_call(L.mbq_matmul, LIB.I8T, planes, x, m, n, k, y_ref), "mbq_matmul")
+        LIB.check(_call(L.mbq_matmul_noalloc, LIB.I8T, planes, x, m, n, k, y), "mbq_matmul_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), f"int8 case {i}: noalloc differs"
+        assert_product_dev(y, ref, f"int8 planes case {i}")
