@@ -238,6 +238,15 @@ __device__ __forceinline__ void mfma_drain() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Split-K partial exchange between the blocks of a tile, by the MI355X memory model at agent scope. The blocks that
+// store a partial release it before their arrival atomic: buffer_wbl2 sc1 writes the XCD's L2 dirty lines back, and
+// the s_waitcnt vmcnt(0) that follows waits for it and for the stores. The last block acquires before it reads the
+// partials: buffer_inv sc1 drops its XCD's L2 lines, which another XCD may have written since. Device-coherent (sc1)
+// stores and loads alone do not order this: a partial can still be dirty in the writer's L2 when the last block reads
+// it from memory (seen on MI355X as stale 64-byte sectors of a partial).
+__device__ __forceinline__ void split_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void split_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
 // v as a register value the compiler cannot look through (so byte extracts stay register ops on it), without the
 // ordering constraints of a volatile asm
 __device__ __forceinline__ uint32_t hide(uint32_t v) {

@@ -216,14 +216,16 @@ struct GemmArgs {
     float* ws;                  // S > 1: partial tiles, BM x BN floats per (tile, split)
     int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
     uint32_t ws_bytes;          // S > 1: bytes of ws
+    int fenced;                 // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
 // Pipeline of depth P (1 or 3): x is DMA'd P steps ahead into P + 1 LDS stages, weight units are loaded into P + 1
 // register buffers P + 1 steps ahead, and the unit of step l + 1 is dequantized into one of 2 LDS weight stages during
 // step l. With split-K (S > 1) the blocks of one tile each run a contiguous range of K steps; each writes its float32
-// partial tile to the workspace with device-coherent stores, and the block that arrives last (an atomic counter per
-// tile, reset by that block) adds the S partials in split order with device-coherent loads, so the result does not
-// depend on which block finishes last.
+// partial tile to the workspace, and the block that arrives last (an atomic counter per tile, reset by that block)
+// adds the S partials in split order, so the result does not depend on which block finishes last. The workspace is
+// uncached device memory (no fence needed), or the static scratch of mbq_matmul_noalloc, where the exchange releases
+// and acquires at agent scope.
 template <int T, int BM, int BN, int P, bool KFULL>
 __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kernel(const GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint16_t gemm_lds[];   // [A stage 0 .. P][B stage 0][B stage 1]
@@ -383,7 +385,8 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
             for (int j = 0; j < TJ; ++j)
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr, lofs + (uint32_t)((i * TJ + j) * 64) * 16u,
                                                        (uint32_t)(tile * g.S + kz) * E, 16);
-        wait_vm<0>();                                                 // the partial is in device-coherent memory
+        if (g.fenced) split_release();                                // the partial is visible at agent scope
+        else wait_vm<0>();
         __syncthreads();
         int* flag = reinterpret_cast<int*>(gemm_lds);
         if (tid == 0) {
@@ -393,6 +396,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
         }
         __syncthreads();
         if (!*flag) return;
+        if (g.fenced) split_acquire();                                // the other blocks' partials, not stale lines
         const uint32_t first = (uint32_t)(tile * g.S) * E;
         for (int z = 0; z < g.S; ++z) {                               // split order: the same sum whoever is last
 #pragma unroll
@@ -660,16 +664,17 @@ int workspace(Workspace* out, hipStream_t s) {
         if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return set_error(MBQ_BAD_ARG, "GEMM: the first split-K call on device %d allocates its workspace, which a "
                                           "stream being captured into a graph cannot do: make one eager call first", dev);
+        // Uncached device memory: no L2 holds its lines, so a partial one XCD stores is what another XCD loads after the
+        // arrival count, with no cache write-back or invalidation between (the exchange of every split-K kernel). It is
+        // kept until the process ends (never freed, also on a failed set-up).
         void *p = nullptr, *c = nullptr;
-        if (hipMalloc(&p, WS_BYTES) != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
+        if (hipExtMallocWithFlags(&p, WS_BYTES, hipDeviceMallocUncached) != hipSuccess)
+            return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
         // the counters are zeroed on the null stream and waited for here, once: the first kernel that uses them may run
         // on a non-blocking stream, which does not wait for the null stream
-        if (hipMalloc(&c, WS_TILES * sizeof(int)) != hipSuccess || hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess ||
-            hipStreamSynchronize(nullptr) != hipSuccess) {
-            (void)hipFree(p);
-            if (c) (void)hipFree(c);
+        if (hipExtMallocWithFlags(&c, WS_TILES * sizeof(int), hipDeviceMallocUncached) != hipSuccess ||
+            hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess)
             return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K counter allocation failed");
-        }
         w.ws = static_cast<float*>(p);
         w.cnt = static_cast<int*>(c);
         w.bytes = WS_BYTES;
@@ -712,6 +717,7 @@ static int scratch_workspace(hipStream_t s, Workspace* out) {
     out->cnt = reinterpret_cast<int*>(static_cast<uint8_t*>(addr[dev]) + SCRATCH_BYTES);
     out->bytes = SCRATCH_BYTES;
     out->tiles = SCRATCH_TILES;
+    out->fenced = 1;
     return 0;
 }
 
@@ -736,7 +742,7 @@ static int launch_tile(const Args& a, int S, int kts, const Workspace& w, hipStr
     if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
         return set_error(MBQ_LAUNCH_FAIL, "GEMM: %zu bytes of LDS refused", lds);
     GemmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M,
-               (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes};
+               (int)a.N, (int)a.K, a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     kern<<<dim3((unsigned)(tiles * S)), GT, lds, s>>>(g);
     const hipError_t e = hipGetLastError();

@@ -15,8 +15,9 @@
 //     fill the CUs (17408 rows = 256 ranges of 68), and a wave loads only its rows of the 16-row tiles it touches
 //     (the rest of a tile reads zero through the buffer range check: no traffic); the MFMAs of those rows are wasted;
 //   * K splits S (blocks per row range) cut the x bytes per block by S at the cost of float32 partials: each split
-//     stores its partial tile with device-coherent (sc1) stores, and the split that arrives last (an atomic counter
-//     per range, which it resets) adds the S partials in split order, so the sum does not depend on arrival order.
+//     stores its partial tile, and the split that arrives last (an atomic counter per range, which it resets) adds the
+//     S partials in split order, so the sum does not depend on arrival order. The partials sit in uncached device
+//     memory, or (mbq_matmul_noalloc) in the static scratch with an agent-scope release / acquire around the exchange.
 // Weights go from HBM (non-temporal loads) straight into B-operand registers, D chunks in flight per wave. After the
 // K loop the K groups of a row group add their accumulators through LDS in a fixed tree order.
 //
@@ -56,6 +57,7 @@ struct KgmArgs {
     float* ws;                     // S > 1: partial tiles, (range, split) -> E floats
     int* cnt;                      // S > 1: arrival counter per row range (zero between launches)
     uint32_t ws_bytes;
+    int fenced;                    // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
 // K groups and LDS stages per K group
@@ -169,8 +171,10 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     auto step = [&](auto U_, int l) __attribute__((always_inline)) {
         constexpr int U = decltype(U_)::value;                            // l % D
         wait_vm<VMT>();
-        barrier_nofence();                                                // stage U landed for every wave; stage
-        __builtin_amdgcn_sched_barrier(0);                                // (l - 1) % D is no longer read
+        // stage U landed for every wave; stage (l - 1) % D is no longer read. With one row group a wave reads only the
+        // stages it fills, but the block-wide barrier still measured faster (it keeps the waves' x reads together)
+        barrier_nofence();
+        __builtin_amdgcn_sched_barrier(0);
         dma_x((U + D - 1) % D, l + D - 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -242,7 +246,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                 for (int j = 0; j < NTW; ++j)
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr,
                                                            lofs + (uint32_t)((i * NTW + j) * 64) * 16u, own, 16);
-            wait_vm<0>();                                                 // the partial is in device-coherent memory
+            if (g.fenced) split_release();                                // the partial is visible at agent scope
+            else wait_vm<0>();
         }
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -252,6 +257,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         }
         __syncthreads();
         if (!kgm_last) return;
+        if (g.fenced) split_acquire();                                              // the other blocks' partials, not stale lines
         if (kg == 0) {
             const uint32_t first = (uint32_t)(rr * g.S * E) * 4u;
             for (int zz = 0; zz < g.S; ++zz) {                            // split order, whoever arrived last
@@ -367,7 +373,7 @@ static int kgm_launch(const Args& a, const KgmPlan& p, const Workspace& w, hipSt
     const int64_t KC = (a.K + 63) / 64;
     const int kcs = (int)((KC + p.S - 1) / p.S);
     KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
-              a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes};
+              a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
     const int64_t ranges = (a.N + p.R - 1) / p.R;
     kern<<<dim3((unsigned)(ranges * p.S)), KGM_THREADS, lds, s>>>(g);
     const hipError_t e = hipGetLastError();

@@ -33,7 +33,10 @@ struct Args {
 // and kept until the process ends. Every kernel that uses them leaves the counters it touched at zero.
 constexpr size_t WS_BYTES = (size_t)64 << 20;
 constexpr int WS_TILES = 1 << 16;
-struct Workspace { float* ws = nullptr; int* cnt = nullptr; size_t bytes = 0; int tiles = 0; };
+// fenced: the memory is ordinary cached memory (the static scratch of mbq_matmul_noalloc), so the blocks that exchange
+// partials through it release and acquire at agent scope (split_release / split_acquire); the allocated workspace is
+// uncached device memory, which no L2 holds, so its device-coherent stores and loads need no fence
+struct Workspace { float* ws = nullptr; int* cnt = nullptr; size_t bytes = 0; int tiles = 0; int fenced = 0; };
 int workspace(Workspace* out, hipStream_t s);   // refused while s is capturing and nothing is allocated yet
 // The workspace of a split-K launch whose partial tiles take `bytes` over `tiles` arrival counters: the static scratch
 // array when a.noalloc (mbq_matmul_noalloc; never allocated), else the allocated per-device workspace. An error, with

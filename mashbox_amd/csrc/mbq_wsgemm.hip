@@ -25,9 +25,10 @@
 // to it (they fill buffers nobody reads).
 //
 // K split (S > 1): the blocks of a tile each run a contiguous range of iterations and store their float32 partial
-// tile with device-coherent stores (sc1: written through the XCD's L2); the block that arrives last, by an atomic
-// counter per tile that it resets, reads the S partials with device-coherent loads and adds them in split order, so the
-// result does not depend on which block finishes last. No L2-wide fence is needed.
+// tile; the block that arrives last, by an atomic counter per tile that it resets, reads the S partials and adds them
+// in split order, so the result does not depend on which block finishes last. The partials live in uncached device
+// memory (no XCD's L2 holds them, so no cache write-back or invalidation is needed), or, for mbq_matmul_noalloc, in
+// the static scratch array, where the exchange releases and acquires at agent scope (split_release / split_acquire).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -66,6 +67,7 @@ struct WsArgs {
     float* ws;                  // S > 1: partial tiles, one block's outputs per (tile, split)
     int* cnt;                   // S > 1: per-tile arrival counters (zero between launches)
     uint32_t ws_bytes;          // S > 1: bytes of ws
+    int fenced;                 // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
 template <int T, int MT, int NT, bool KFULL>
@@ -222,7 +224,8 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
 #pragma unroll
             for (int j = 0; j < NT; ++j)
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr, lofs + (uint32_t)((i * NT + j) * 64) * 16u, mine, 16);
-        wait_vm<0>();                                                 // the partial is in device-coherent memory
+        if (g.fenced) split_release();                                // the partial is visible at agent scope
+        else wait_vm<0>();
         __syncthreads();
         if (threadIdx.x == 0) {
             const int old = __hip_atomic_fetch_add(g.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -231,6 +234,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
         }
         __syncthreads();
         if (!ws_flag) return;
+        if (g.fenced) split_acquire();                                              // the other blocks' partials, not stale lines
         const uint32_t first = (uint32_t)(tile * g.S * E) * 4u;
         for (int z = 0; z < g.S; ++z) {                               // split order: the same sum whoever is last
             f32x4_t v[MT][NT];
@@ -281,7 +285,7 @@ static int ws_launch(const Args& a, int S, int kts, const Workspace& w, hipStrea
     if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
         return set_error(MBQ_LAUNCH_FAIL, "weight-stream GEMM: %zu bytes of LDS refused", lds);
     WsArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.srow, a.x, (int)a.M, (int)a.N, (int)a.K,
-             a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes};
+             a.y, a.out_bf16, S, kts, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
     const int64_t tiles = (a.N + 64 * NT - 1) / (64 * NT);
     kern<<<dim3((unsigned)(tiles * S)), WS_THREADS, lds, s>>>(g);
     const hipError_t e = hipGetLastError();
