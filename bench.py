@@ -14,7 +14,13 @@ Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAG
 distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
 for K timed launches bracketed by torch.cuda.synchronize() and HIP events on the stream the kernels run on. The kernel's
 average launch duration is the event time / K. The CPU baseline is the oracle's restatement of mashbox's exact path
-(rebuild float32 weights per call, float32 dot) on the host's cores, on a bounded sample of config 2.
+(rebuild float32 weights per call, float32 dot; int8: float32 dot then the scales) on the host's cores, every config at
+full size (a few seconds each); `cpu_baseline` is config 2's.
+
+Profiling modes (rocprofv3 runs of committed files; summaries in profiles/): --pmc-probe [CONFIGS] launches each
+config's projections a few times plus a calibration copy; --summarize-pmc turns a FETCH_SIZE and a WRITE_SIZE run of
+it into profiles/traffic.json; --summarize-counters prints a counter run's means per kernel; --summarize-stats prints a
+--kernel-trace --stats CSV.
 """
 import argparse
 import ctypes
@@ -47,7 +53,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def run_config(idx, steps, warmup, rotate_bytes):
+def setup_projection(idx, pi, rotate_bytes):
+    """one projection of a config, ready to launch: seeded synthetic weights in HBM (repacked as a load would), cycled
+    over >= rotate_bytes of distinct copies -> (launch(copy) -> rc, copies, weight bytes, plan text, (t, M, N, K))"""
     import torch
     from mashbox_amd import synth
     from mashbox_amd import _lib as LIB
@@ -56,61 +64,71 @@ def run_config(idx, steps, warmup, rotate_bytes):
     L = lib()
     dev = torch.device("cuda", 0)
     t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
+    name, N, K = projs[pi]
+    seed = (1000 * idx if isinstance(idx, int) else 9000) + pi
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    x = synth.acts(M, K, seed=seed, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if t == "int8" and M > 4:
+        # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes)
+        q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
+        pb = check(L.mbq_plane_bytes(LIB.I8T, N, K), "int8 plane_bytes")
+        planes = torch.empty(pb, dtype=torch.uint8, device=dev)
+        check(L.mbq_int8_repack_dev(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(s.data_ptr()), N, K,
+                                    ctypes.c_void_p(planes.data_ptr()), st()), "int8 repack")
+        del q, s
+        wbytes = pb
+        copies = max(1, math.ceil(rotate_bytes / wbytes))
+        bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
+
+        def launch(c):
+            return L.mbq_matmul(LIB.I8T, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
+                                M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
+        plan = LIB.plan_str(LIB.I8T, M, N, K)
+    elif t == "int8":
+        # decode int8: the reference's row-major weights, run by the decode GEMV
+        q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
+        wbytes = N * K + 4 * N
+        copies = max(1, math.ceil(rotate_bytes / wbytes))
+        bufs = [(q, s)] + [(q.clone(), s.clone()) for _ in range(copies - 1)]
+
+        def launch(c):
+            qq, ss = bufs[c]
+            return L.mbq_int8_linear(ctypes.c_void_p(qq.data_ptr()), ctypes.c_void_p(ss.data_ptr()),
+                                     ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
+        plan = LIB.plan_str(LIB.INT8, M, N, K)
+    else:
+        raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
+        pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
+        planes = torch.empty(pb, dtype=torch.uint8, device=dev)
+        check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st()), "repack")
+        del raw
+        wbytes = pb
+        copies = max(1, math.ceil(rotate_bytes / wbytes))
+        bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
+
+        def launch(c):
+            return L.mbq_matmul(t, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
+                                M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
+        plan = LIB.plan_str(t, M, N, K)
+    torch.cuda.synchronize()
+    check(launch(0), f"config {idx} {name}")          # eager call: argument errors surface here, not in a capture
+    torch.cuda.synchronize()
+    return launch, copies, wbytes, plan, (t, M, N, K)
+
+
+def run_config(idx, steps, warmup, rotate_bytes):
+    import torch
+    from mashbox_amd import synth
+    from mashbox_amd._lib import check
+
+    t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
     out = {"projections": {}}
     total_us = 0.0
     total_bytes = 0
     total_flops = 0
     for pi, (name, N, K) in enumerate(projs):
-        seed = (1000 * idx if isinstance(idx, int) else 9000) + pi
-        x = synth.acts(M, K, seed=seed, device=dev)
-        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        if t == "int8" and M > 4:
-            # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes)
-            q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
-            pb = check(L.mbq_plane_bytes(LIB.I8T, N, K), "int8 plane_bytes")
-            planes = torch.empty(pb, dtype=torch.uint8, device=dev)
-            check(L.mbq_int8_repack_dev(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(s.data_ptr()), N, K,
-                                        ctypes.c_void_p(planes.data_ptr()),
-                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "int8 repack")
-            del q, s
-            wbytes = pb
-            copies = max(1, math.ceil(rotate_bytes / wbytes))
-            bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
-
-            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K):
-                return L.mbq_matmul(LIB.I8T, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1,
-                                    ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16,
-                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        elif t == "int8":
-            # decode int8: the reference's row-major weights, run by the decode GEMV
-            q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
-            wbytes = N * K + 4 * N
-            copies = max(1, math.ceil(rotate_bytes / wbytes))
-            bufs = [(q, s)] + [(q.clone(), s.clone()) for _ in range(copies - 1)]
-
-            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K):
-                qq, ss = bufs[c]
-                return L.mbq_int8_linear(ctypes.c_void_p(qq.data_ptr()), ctypes.c_void_p(ss.data_ptr()),
-                                         ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()),
-                                         OUT_BF16, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        else:
-            raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
-            pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
-            planes = torch.empty(pb, dtype=torch.uint8, device=dev)
-            check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()),
-                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "repack")
-            del raw
-            wbytes = pb
-            copies = max(1, math.ceil(rotate_bytes / wbytes))
-            bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
-
-            def launch(c, bufs=bufs, x=x, y=y, M=M, N=N, K=K, t=t):
-                return L.mbq_matmul(t, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
-                                    M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16,
-                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        torch.cuda.synchronize()
-        check(launch(0), f"config {idx} {name}")          # eager call: argument errors surface here, not in capture
-        torch.cuda.synchronize()
+        launch, copies, wbytes, plan, _ = setup_projection(idx, pi, rotate_bytes)
 
         def capture(n):
             g = torch.cuda.CUDAGraph()
@@ -135,12 +153,11 @@ def run_config(idx, steps, warmup, rotate_bytes):
         fl = 2 * M * N * K
         out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
                                     "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
-                                    "rotation_MB": round(copies * wbytes / 1e6, 1),
-                                    "plan": LIB.plan_str((LIB.I8T if M > 4 else LIB.INT8) if t == "int8" else t, M, N, K)}
+                                    "rotation_MB": round(copies * wbytes / 1e6, 1), "plan": plan}
         total_us += us
         total_bytes += ab
         total_flops += fl
-        del bufs, g
+        del launch, g
         torch.cuda.empty_cache()
     gbs = total_bytes / total_us / 1e3
     tfl = total_flops / total_us / 1e6
@@ -156,14 +173,24 @@ def run_config(idx, steps, warmup, rotate_bytes):
 
 
 def measured_peaks():
-    """the box's achievable HBM rates with plain torch kernels on 2 GiB: read (a float32 sum) and copy (read + write)"""
+    """the box's achievable rates, measured by libmbq's probes (mbq_probe.hip) and torch: HBM read (every KiB of 2 GiB
+    read once by a streaming kernel), device copy (torch, read + write) and bf16 MFMA (back-to-back MFMAs on every SIMD)"""
     import torch
+    from mashbox_amd._lib import check, lib
+
+    L = lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     n = (2 << 30) // 4
     a = torch.ones(n, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
+    sink = torch.zeros(16, dtype=torch.float32, device="cuda")
+    flops = ctypes.c_int64(0)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = {}
-    for name, fn, nbytes in (("read_GBps", lambda: a.sum(), 4 * n), ("copy_GBps", lambda: b.copy_(a), 8 * n)):
+    for name, fn, nbytes in (
+            ("read_GBps", lambda: check(L.mbq_probe_read(ctypes.c_void_p(a.data_ptr()), 4 * n,
+                                                         ctypes.c_void_p(sink.data_ptr()), st), "read probe"), 4 * n),
+            ("copy_GBps", lambda: b.copy_(a), 8 * n)):
         fn()
         torch.cuda.synchronize()
         e0.record()
@@ -172,69 +199,114 @@ def measured_peaks():
         e1.record()
         torch.cuda.synchronize()
         out[name] = round(nbytes * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    check(L.mbq_probe_mfma(20000, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flops), st), "MFMA probe")
+    torch.cuda.synchronize()
+    e0.record()
+    check(L.mbq_probe_mfma(20000, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flops), st), "MFMA probe")
+    e1.record()
+    torch.cuda.synchronize()
+    out["mfma_bf16_TFLOPs"] = round(flops.value / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1)
+    out["how"] = ("read: mbq_probe_read over 2 GiB (4 waves per CU, 16 KiB in flight each); copy: torch copy of 2 GiB "
+                  "(bytes read + written); MFMA: mbq_probe_mfma, v_mfma_f32_16x16x32_bf16 x 8 independent "
+                  "accumulators, 8 waves per CU")
     del a, b
     torch.cuda.empty_cache()
     return out
 
 
-def cpu_baseline(seconds):
-    """oracle restatement of mashbox's exact path on config 2 (Q8_0 17408 x 5120, M = 1), host cores"""
+def _cpu_threads():
+    """host threads for the CPU baselines: torch's intra-op count, which follows OMP_NUM_THREADS (the GPU box allots 16
+    host cores to a one-GPU job and sets OMP_NUM_THREADS=16; the container's own count otherwise)"""
+    import torch
+    return max(1, torch.get_num_threads())
+
+
+def _cpu_model():
+    try:
+        return next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
+    except OSError:
+        return "?"
+
+
+def cpu_baselines(seconds_per_config, configs=(1, 2, 3, 4, 5), min_calls=5):
+    """the oracle's restatement of mashbox's exact path (oracle/ref.py) on the host cores, per config, seed-0 inputs of
+    oracle/gen.py at full size: GGUF configs rebuild float32 weights from the blocks per call (row chunks of
+    exact_chunk_rows, one chunk per host thread) and multiply in float32; int8 configs take (x @ bf16(q).T) * s in
+    float32 (BLAS on the host threads). Median of >= min_calls calls (more while under seconds_per_config)."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
     from oracle import gen as G
     from oracle import ref as R
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = max(1, min(threads, 16))
-    cfg = G.config(HEADLINE, seed=0)
-    (_, n, k, raw, xb), = cfg["projections"]
-    x = R.bf16_to_f32(xb)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        y = R.qmatmul_exact(x, raw, R.Q8_0, (n, k), threads=threads)
-        R.bf16_round(y)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    ab = algorithmic_bytes(8, 1, n, k)
-    try:
-        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
-    except OSError:
-        model = "?"
-    return {"value": round(ab / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 whole (Q8_0 W[17408,5120], x[1,5120]): {len(times)} calls of oracle.ref.qmatmul_exact "
-                      f"(float32 rebuild in 8 row chunks of 2176 + float32 dot, chunks on {threads} threads), "
-                      f"median {med * 1e3:.1f} ms/call; host CPU {model}"}
+    threads = _cpu_threads()
+    res = {}
+    for idx in configs:
+        cfg = G.config(idx, seed=0)
+        m = cfg["m"]
+        times = []
+        t_end = time.perf_counter() + seconds_per_config
+        while len(times) < min_calls or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            for name, n, k, w, xb in cfg["projections"]:
+                x = R.bf16_to_f32(xb)
+                if cfg["t"] == "int8":
+                    q, s = w
+                    with threadpool_limits(threads):
+                        y = R.int8_linear(x, q, s)
+                else:
+                    with threadpool_limits(1):                      # one BLAS thread per chunk, chunks on `threads`
+                        y = R.qmatmul_exact(x, w, cfg["t"], (n, k), threads=threads)
+                R.bf16_round(y)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        ab = sum(algorithmic_bytes(cfg["t"] if cfg["t"] == "int8" else int(cfg["t"]), m, n, k)
+                 for _, n, k, _, _ in cfg["projections"])
+        fl = sum(2 * m * n * k for _, n, k, _, _ in cfg["projections"])
+        res[f"c{idx}"] = {"us_per_step": round(med * 1e6, 1), "GBps": round(ab / med / 1e9, 3),
+                          "TFLOPs": round(fl / med / 1e12, 4), "calls": len(times)}
+        log(f"cpu baseline config {idx}: {med * 1e3:.1f} ms/step ({len(times)} calls, {threads} threads)")
+        del cfg
+    return res, threads
 
 
-def pmc_probe(launches=24, copy_mib=1024):
-    """the headline kernel alone, eagerly, for rocprofv3 --pmc: `launches` config-2 GEMV launches over rotating weight
-    copies, then a plain device copy of copy_mib MiB (read and written once) to calibrate the counters"""
+def cpu_baseline_line(per_config, threads):
+    """the contract's cpu_baseline object: config 2 (the headline) from cpu_baselines"""
+    c2 = per_config["c2"]
+    return {"value": c2["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 whole (Q8_0 W[17408,5120], x[1,5120], seed 0): {c2['calls']} calls of "
+                      f"oracle.ref.qmatmul_exact (float32 rebuild in 8 row chunks of 2176 + float32 dot, chunks on "
+                      f"{threads} threads), median {c2['us_per_step'] / 1e3:.1f} ms/call; host CPU {_cpu_model()}, "
+                      f"os.cpu_count() {os.cpu_count()}, torch threads {threads}"}
+
+
+# kernels of the matmul path (dispatches the pmc probe counts; repack, zero and dequant kernels excluded)
+MATMUL_KERNELS = ("gemv_kernel", "wsgemm_kernel", "kgemm_kernel", "sgemm_kernel", "gemm_kernel")
+
+
+def pmc_probe(configs=(1, 2, 3, 4, 5), launches=4, copy_mib=1024, rotate_mb=1024):
+    """for rocprofv3 --pmc: every projection of each config launched `launches` times eagerly over rotating weight
+    copies (the bench's inputs), in config and projection order, then a plain device copy of copy_mib MiB (read and
+    written once) 4 times to calibrate FETCH_SIZE / WRITE_SIZE"""
     import torch
     from mashbox_amd import synth
-    from mashbox_amd._lib import OUT_BF16, check, lib
+    from mashbox_amd._lib import check
 
-    L = lib()
-    dev = torch.device("cuda", 0)
-    t, M, ((_, N, K),) = synth.CONFIGS[HEADLINE]
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    x = synth.acts(M, K, seed=1000 * HEADLINE, device=dev)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    raw = synth.q8_0_raw(N, K, seed=1000 * HEADLINE + 7, device=dev)
-    pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
-    planes = torch.empty(pb, dtype=torch.uint8, device=dev)
-    check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st), "repack")
-    copies = [planes] + [planes.clone() for _ in range(11)]
-    for i in range(launches):
-        check(L.mbq_matmul(t, ctypes.c_void_p(copies[i % len(copies)].data_ptr()), 0, None, 1,
-                           ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st), "matmul")
-    src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
+    for idx in configs:
+        _, _, projs = synth.CONFIGS[idx]
+        for pi in range(len(projs)):
+            launch, copies, _, _, _ = setup_projection(idx, pi, rotate_mb << 20)
+            for i in range(launches):
+                check(launch((i + 1) % copies), "launch")
+            torch.cuda.synchronize()
+            del launch
+            torch.cuda.empty_cache()
+    src = torch.ones(copy_mib << 18, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(4):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_probe": {"launches": launches, "copy_bytes": copy_mib << 20,
-                                    "algorithmic_bytes": algorithmic_bytes(t, M, N, K)}}), flush=True)
+    print(json.dumps({"pmc_probe": {"configs": list(configs), "launches": launches, "copy_bytes": copy_mib << 20}}),
+          flush=True)
 
 
 def _counter_rows(d):
@@ -246,33 +318,99 @@ def _counter_rows(d):
     return rows
 
 
-def summarize_pmc(fetch_dir, write_dir, out, copy_mib=1024):
-    """profiles/traffic.json from the two rocprofv3 --pmc runs of --pmc-probe (FETCH_SIZE, then WRITE_SIZE): HBM bytes
-    per headline-kernel launch, each counter scaled by what it reads for the calibration copy"""
-    def per(rows, counter):
-        # headline-kernel dispatches, and the calibration copies: the probe's last 4 dispatches
-        rows = [r for r in rows if r["Counter_Name"] == counter]
-        last = sorted(int(r["Dispatch_Id"]) for r in rows)[-4:]
-        k = [float(r["Counter_Value"]) for r in rows if "gemv_kernel<8, 1," in r["Kernel_Name"]]
-        c = [float(r["Counter_Value"]) for r in rows if int(r["Dispatch_Id"]) in last]
-        return k, c
-    fk, fc = per(_counter_rows(fetch_dir), "FETCH_SIZE")
-    wk, wc = per(_counter_rows(write_dir), "WRITE_SIZE")
-    if not (fk and fc and wk and wc):
-        raise SystemExit(f"missing dispatches: gemv fetch {len(fk)} copy fetch {len(fc)} gemv write {len(wk)} copy write {len(wc)}")
+def _probe_dispatches(rows, counter):
+    """(matmul dispatches in launch order, the last 4 dispatches = the calibration copies) for one counter"""
+    rows = [r for r in rows if r["Counter_Name"] == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    mm = [r for r in rows if "mbq::" in r["Kernel_Name"] and any(k in r["Kernel_Name"] for k in MATMUL_KERNELS)]
+    return mm, rows[-4:]
+
+
+def summarize_pmc(fetch_dir, write_dir, out, configs=(1, 2, 3, 4, 5), launches=4, copy_mib=1024):
+    """profiles/traffic.json from two rocprofv3 --pmc runs of --pmc-probe (FETCH_SIZE, then WRITE_SIZE): HBM bytes per
+    step of each config (per projection the median of its probe launches after the first, each on a distinct weight
+    copy), each counter scaled by what it reads for the calibration copy"""
     import statistics as stt
+    from mashbox_amd import synth
+
+    fm, fc = _probe_dispatches(_counter_rows(fetch_dir), "FETCH_SIZE")
+    wm, wc = _probe_dispatches(_counter_rows(write_dir), "WRITE_SIZE")
+    plan = [(idx, name, n, k, synth.CONFIGS[idx][0], synth.CONFIGS[idx][1])
+            for idx in configs for name, n, k in synth.CONFIGS[idx][2]]
+    per = launches + 1                                      # setup_projection's eager check, then the probe's launches
+    if len(fm) != len(plan) * per or len(wm) != len(plan) * per:
+        raise SystemExit(f"expected {len(plan) * per} matmul dispatches, got fetch {len(fm)} write {len(wm)}")
     known_kib = (copy_mib << 20) / 1024.0
-    ff, fw = known_kib / stt.median(fc), known_kib / stt.median(wc)
-    fetch_b = stt.median(fk[1:] or fk) * ff * 1024.0       # the first launch also faults in code and tables
-    write_b = stt.median(wk[1:] or wk) * fw * 1024.0
-    rec = {"c2": {"hbm_bytes_per_launch": round(fetch_b + write_b), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
-                  "fetch_kib_raw": stt.median(fk), "write_kib_raw": stt.median(wk), "copy_fetch_kib_raw": stt.median(fc),
-                  "copy_write_kib_raw": stt.median(wc), "copy_kib": known_kib, "fetch_scale": round(ff, 4),
-                  "write_scale": round(fw, 4), "launches": len(fk),
-                  "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -f csv -- python3 bench.py --pmc-probe"}}
+    ff = known_kib / stt.median(float(r["Counter_Value"]) for r in fc)
+    fw = known_kib / stt.median(float(r["Counter_Value"]) for r in wc)
+    rec = {"fetch_scale": round(ff, 4), "write_scale": round(fw, 4), "copy_kib": known_kib,
+           "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -d DIR -o out --output-format csv -- "
+                      "python3 bench.py --pmc-probe; python3 bench.py --summarize-pmc FETCH_DIR WRITE_DIR"}
+    for idx in configs:
+        fetch_b = write_b = alg = 0.0
+        kernels = set()
+        for p, (ci, name, n, k, t, m) in enumerate(plan):
+            if ci != idx:
+                continue
+            # the eager check and the first probe launch also fault in code and tables: the later launches count
+            fk = [float(r["Counter_Value"]) for r in fm[p * per + 2:(p + 1) * per]]
+            wk = [float(r["Counter_Value"]) for r in wm[p * per + 2:(p + 1) * per]]
+            fetch_b += stt.median(fk) * ff * 1024.0
+            write_b += stt.median(wk) * fw * 1024.0
+            alg += algorithmic_bytes(t, m, n, k)
+            kernels.add(fm[p * per]["Kernel_Name"].split("(")[0])
+        rec[f"c{idx}"] = {"hbm_bytes_per_launch": round(fetch_b + write_b), "fetch_bytes": round(fetch_b),
+                          "write_bytes": round(write_b), "algorithmic_bytes": round(alg),
+                          "traffic_over_algorithmic": round((fetch_b + write_b) / alg, 4), "kernels": sorted(kernels)}
     with open(out, "w") as f:
         json.dump(rec, f, indent=1)
     print(json.dumps(rec), flush=True)
+
+
+def summarize_counters(d, kernel_substr=None, simds=1024, clock_ghz=2.17):
+    """markdown of rocprofv3 --pmc runs of --pmc-probe (one directory per pass under d): per matmul kernel, the mean
+    of each counter over its dispatches and derived shares. SQ_VALU_MFMA_BUSY_CYCLES is summed over the SIMDs (it
+    reads 16 per v_mfma_f32_16x16x32_bf16), so its share of the kernel is busy / (SIMDs x dispatch ns x clock); the
+    clock is the MFMA probe's (2.28 PF = 1024 SIMDs x 1024 flop/cycle x 2.17 GHz) and the dispatch time is the one the
+    profiler measured, on dispatches it serializes"""
+    import collections
+    import statistics as stt
+    rows = _counter_rows(d)
+    by = collections.defaultdict(lambda: collections.defaultdict(list))
+    dur = collections.defaultdict(list)
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "mbq::" not in name or not any(k in name for k in MATMUL_KERNELS):
+            continue
+        if kernel_substr and kernel_substr not in name:
+            continue
+        kern = name.split("(")[0]
+        by[kern][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        dur[(kern, r["Counter_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    for kern, cs in sorted(by.items()):
+        o = {k: sum(v) / len(v) for k, v in cs.items()}
+        ns = stt.median(dur[(kern, next(iter(cs)))])
+        print(f"\n`{kern}` ({len(next(iter(cs.values())))} dispatches per pass, median {ns / 1e3:.1f} us under the "
+              f"profiler)\n\n| counter | mean per dispatch |\n|---|---:|")
+        for k in sorted(o):
+            print(f"| {k} | {o[k]:.0f} |")
+        wc = o.get("SQ_WAVE_CYCLES")
+        if wc:
+            for k in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS"):
+                if k in o:
+                    print(f"| {k} / SQ_WAVE_CYCLES | {o[k] / wc:.3f} |")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in o:
+            busy = sum(cs["SQ_VALU_MFMA_BUSY_CYCLES"])
+            t_ns = sum(dur[(kern, "SQ_VALU_MFMA_BUSY_CYCLES")])
+            print(f"| MFMA busy share: SQ_VALU_MFMA_BUSY_CYCLES / ({simds} SIMDs x {clock_ghz} GHz x dispatch time) | "
+                  f"{busy / (simds * t_ns * clock_ghz):.3f} |")
+        if "SQ_VALU_MFMA_COEXEC_CYCLES" in o and "SQ_VALU_MFMA_BUSY_CYCLES" in o:
+            print(f"| SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES | "
+                  f"{o['SQ_VALU_MFMA_COEXEC_CYCLES'] / o['SQ_VALU_MFMA_BUSY_CYCLES']:.3f} |")
+        if "SQ_INSTS_VALU" in o and "SQ_INSTS_MFMA" in o and o["SQ_INSTS_MFMA"]:
+            print(f"| SQ_INSTS_VALU / SQ_INSTS_MFMA | {o['SQ_INSTS_VALU'] / o['SQ_INSTS_MFMA']:.2f} |")
+        if "SQ_LDS_BANK_CONFLICT" in o and "SQ_INSTS_LDS" in o and o["SQ_INSTS_LDS"]:
+            print(f"| SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS | {o['SQ_LDS_BANK_CONFLICT'] / o['SQ_INSTS_LDS']:.3f} |")
 
 
 def summarize_stats(csv_path, top=12):
@@ -295,19 +433,24 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="1,2,3,4,5,q6k_head")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE)")
-    ap.add_argument("--pmc-probe", action="store_true", help="only the headline kernel + a calibration copy (for --pmc)")
+    ap.add_argument("--pmc-probe", nargs="?", const="1,2,3,4,5", default=None, metavar="CONFIGS",
+                    help="only the configs' matmul launches + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write --traffic from the two --pmc runs of --pmc-probe")
+    ap.add_argument("--summarize-counters", nargs="+", metavar=("DIR", "KERNEL"),
+                    help="markdown of a --pmc run of --pmc-probe: counter means per matmul kernel")
     ap.add_argument("--summarize-stats", metavar="KERNEL_STATS_CSV", help="print a rocprofv3 --stats CSV as markdown")
     a = ap.parse_args()
     if a.summarize_pmc:
         return summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.traffic)
     if a.summarize_stats:
         return summarize_stats(a.summarize_stats)
+    if a.summarize_counters:
+        return summarize_counters(a.summarize_counters[0], a.summarize_counters[1] if len(a.summarize_counters) > 1 else None)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU: this path is measured on a single MI355X (its kernels shard by weight rows "
               "with no collective; see DESIGN.md). --gpus must be 1.", file=sys.stderr)
@@ -317,7 +460,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     if a.pmc_probe:
-        return pmc_probe()
+        return pmc_probe(tuple(int(c) for c in a.pmc_probe.split(",") if c), rotate_mb=a.rotate_mb)
     configs = [int(c) if c.isdigit() else c for c in a.configs.split(",") if c]
     if HEADLINE not in configs:
         configs.insert(0, HEADLINE)
@@ -326,12 +469,17 @@ def main():
         res[c] = run_config(c, a.steps, a.warmup, a.rotate_mb << 20)
     head = res[HEADLINE]
     proj = head["projections"]["w"]
-    traffic = None
     try:
         with open(a.traffic) as f:
-            traffic = json.load(f).get("c2", {}).get("hbm_bytes_per_launch")
+            tj = json.load(f)
     except (OSError, ValueError):
-        traffic = None
+        tj = {}
+    traffic = tj.get("c2", {}).get("hbm_bytes_per_launch")
+    for c, r in res.items():
+        tc = tj.get(f"c{c}" if isinstance(c, int) else str(c))
+        if tc and "hbm_bytes_per_launch" in tc:
+            r["hbm_traffic_bytes"] = tc["hbm_bytes_per_launch"]
+            r["traffic_over_algorithmic"] = round(tc["hbm_bytes_per_launch"] / r["algorithmic_bytes"], 4)
     line = {
         "metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(head["us_per_step"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
@@ -349,7 +497,11 @@ def main():
     }
     line["measured_peaks"] = measured_peaks()
     if not a.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+        per, threads = cpu_baselines(a.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline_line(per, threads)
+        line["cpu_baseline_configs"] = per | {"threads": threads, "cpu": _cpu_model(), "os_cpu_count": os.cpu_count(),
+                                              "kind": "port: oracle/ref.py restatement of mashbox's plain-JAX exact path",
+                                              "inputs": "oracle/gen.py seed 0, full BASELINE sizes"}
     print(json.dumps(line), flush=True)
 
 

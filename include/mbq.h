@@ -163,12 +163,17 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
+ *   MBQ_KERNEL_KGROUP  K-group kernel of tiled int8 planes (MBQ_I8T) at M <= 64: bm = 16, bn = weight rows per block
+ *                      (any count: N is cut into equal ranges that fill the CUs), splits = K ranges. The automatic
+ *                      plan of MBQ_I8T up to 64 rows.
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
- * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice).
+ * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice;
+ * MBQ_KERNEL_KGROUP takes bm = bn = 0 and chooses its rows per block for the forced splits, 0 = its own choice).
  * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
- * counters), allocated by the first such call on a device and kept until the process ends; GEMM calls on one device
- * that overlap in time must not both split K. That first call cannot run on a stream that is capturing a HIP graph: it
- * returns MBQ_E_ARG and launches nothing (make one eager call on the device before capturing). */
+ * counters) of uncached device memory, allocated by the first such call on a device and kept until the process ends;
+ * GEMM calls on one device that overlap in time must not both split K. That first call cannot run on a stream that is
+ * capturing a HIP graph: it returns MBQ_E_ARG and launches nothing (make one eager call on the device before
+ * capturing). */
 #define MBQ_KERNEL_AUTO 0
 #define MBQ_KERNEL_GEMV 0
 #define MBQ_KERNEL_STREAM 1
@@ -176,6 +181,15 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
 #define MBQ_KERNEL_KGROUP 3
 int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, int* bn, int* splits);
 int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits);
+
+/* Measurement probes (no counterpart in the reference): the peaks a benchmark reports beside the kernels' rates.
+ * mbq_probe_read reads every whole KiB of [p_dev, p_dev + bytes) once with 128-bit loads from a persistent grid (one
+ * block of 4 waves per CU) and writes at most one word to sink_dev: bytes / time is the HBM read rate a streaming kernel
+ * reaches. mbq_probe_mfma runs `iters` rounds of 8 independent v_mfma_f32_16x16x32_bf16 per wave, 8 waves per CU, and
+ * returns the launch's flop count in *flops: flops / time is the bf16 matrix-core rate at the clock the GPU holds under
+ * MFMA load. Both are stream-ordered and allocate nothing. */
+int mbq_probe_read(const void* p_dev, int64_t bytes, void* sink_dev, void* stream);
+int mbq_probe_mfma(int iters, void* sink_dev, int64_t* flops, void* stream);
 
 #ifdef __cplusplus
 }

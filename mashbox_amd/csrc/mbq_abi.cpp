@@ -322,4 +322,15 @@ int mbq_gemm_plan(int t, int64_t M, int64_t N, int64_t K, int* kernel, int* bm, 
 
 int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits) { return force_gemm_plan(kernel, bm, bn, splits); }
 
+int mbq_probe_read(const void* p_dev, int64_t bytes, void* sink_dev, void* stream) {
+    if (!p_dev || !sink_dev || bytes < 0) return set_error(MBQ_BAD_ARG, "read probe: NULL buffer or negative size");
+    return launch_probe_read(static_cast<const uint8_t*>(p_dev), bytes, static_cast<uint32_t*>(sink_dev),
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+int mbq_probe_mfma(int iters, void* sink_dev, int64_t* flops, void* stream) {
+    if (iters < 1 || !sink_dev || !flops) return set_error(MBQ_BAD_ARG, "MFMA probe: iters < 1 or NULL output");
+    return launch_probe_mfma(iters, static_cast<float*>(sink_dev), flops, reinterpret_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

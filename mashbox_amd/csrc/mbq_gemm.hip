@@ -448,6 +448,11 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 // from A stage l % 3 and B stage l % 2, each K substep's operands read during the one before. Both roles pass n
 // barriers in the same order.
 constexpr int SG_BM = 256, SG_BN = 192;
+// element offset of chunk c of row r in the specialized kernel's LDS tiles: rows of 64 bfloat16 (128 bytes, half of the
+// 64 four-byte banks), chunk c at c ^ ((r >> 1) & 7). A 32-lane pass of its operand reads (32 rows, one chunk) and of
+// its dequantized-weight writes (16 rows, two chunks each) then covers every bank twice, the least 512 bytes can; under
+// c ^ (r & 7) rows r and r + 8 shared banks (SQ_LDS_BANK_CONFLICT measured 3.3 cycles per LDS instruction).
+__device__ __forceinline__ int sg_off(int r, int c) { return r * GK + ((c ^ ((r >> 1) & 7)) << 3); }
 constexpr size_t SG_LDS = (size_t)(3 * SG_BM + 2 * SG_BN) * GK * sizeof(uint16_t);   // 144 KiB
 
 template <int T, bool KFULL>
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
             const uint16_t* Bs = B0 + (l & 1) * SG_BN * GK;
             // operand o of substep s: o < 4 A row tile o, else B column tile o - 4; chunk 2 s + (lane >> 5)
             auto rd = [&](int s, int o) {
-                const uint16_t* base = o < 4 ? As + lds_off(ar + 32 * o, 2 * s + lh) : Bs + lds_off(br + 32 * (o - 4), 2 * s + lh);
+                const uint16_t* base = o < 4 ? As + sg_off(ar + 32 * o, 2 * s + lh) : Bs + sg_off(br + 32 * (o - 4), 2 * s + lh);
                 return *reinterpret_cast<const bf16x8_t*>(base);
             };
             bf16x8_t op[2][7];
@@ -544,14 +549,14 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
     const rsrc_t wr = make_rsrc(base, (uint32_t)g.wbytes);
     const rsrc_t xr = make_rsrc(g.x, (uint32_t)((int64_t)M * K * 2));
     // x DMA: instruction i of producer wave w fills tile rows 8 (w + 4 i) .. +7 (8 instructions x 4 waves x 8 rows);
-    // lane l writes LDS slot l & 7 of row l >> 3, holding chunk (l & 7) ^ (row & 7) (the swizzle of lds_off)
+    // lane l writes LDS slot l & 7 of row l >> 3, holding chunk (l & 7) ^ ((row >> 1) & 7) (the swizzle of sg_off)
     constexpr int XD = SG_BM * GK * 2 / (4 * 64 * 16);              // 8
     static_assert(XD == 4 * 2, "the producer step interleaves one DMA instruction per dequantized chunk of 2 units");
     uint32_t xvo[XD];
     int xk[XD];
 #pragma unroll
     for (int i = 0; i < XD; ++i) {
-        const int r = 8 * (pw + 4 * i) + (lane >> 3), c = (lane & 7) ^ (lane >> 3);
+        const int r = 8 * (pw + 4 * i) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
         xvo[i] = m0 + r < M ? (uint32_t)(((int64_t)(m0 + r) * K + c * 8) * 2) : OOB_VOFF;     // rows past M: zero
         xk[i] = c * 8;
     }
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
             if (v == 1 && !two) break;                                // wave-uniform: waves 4-5 take two units
             const BScale sc = b_scale<T>(Rr[v], ((k0(l) >> 5) + bu[v]) & 7);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) st16(st + lds_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc, c));
+            for (int c = 0; c < 4; ++c) st16(st + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc, c));
         }
     };
     constexpr int NDW = XD, NWL = UPT * b_loads<T>();
@@ -626,7 +631,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
             for (int i = 0; i < XD; ++i) {
                 if (i > 0) dma_i(i);
                 const int v = i >> 2, c = i & 3;                      // chunk c of unit v
-                if (v == 0 || two) st16(bst + lds_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
+                if (v == 0 || two) st16(bst + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
             }
             wait_vm<NDW + NWL>();                                     // x(l + 1) has landed (loads complete in order)
             barrier_nofence();

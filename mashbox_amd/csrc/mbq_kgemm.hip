@@ -24,7 +24,9 @@
 // Lane layout (the weight-stream kernel's, mbq_wdirect.h): in K step s (32 values) of a chunk, lane l holds K values
 // 16 (l >> 4) + 8 s + e (e = 0..7) of x row 16 i + (l & 15) and of weight row (l & 15) of a tile; the MFMA sums over
 // K, so this K order is as good as any. x stage layout: 16 MT rows of 128 bytes, the 16-byte piece p of row r at slot
-// p ^ (r & 7); the DMA applies the swizzle through each lane's source address.
+// p ^ ((r >> 1) & 7); the DMA applies the swizzle through each lane's source address. With 64 four-byte banks a 128-byte
+// row is half the banks, so rows r and r + 8 of an A read (same r & 7, same half) would share banks under p ^ (r & 7):
+// SQ_LDS_BANK_CONFLICT measured 2.7-3 cycles per A read with it; (r >> 1) & 7 gives the 8 rows of each half 8 slots.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -123,12 +125,12 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         wo[j] = (row >= rq0 && row < rq1) ? (uint32_t)i8t_off(row, K, 0) + 16u * (uint32_t)lg : OOB_VOFF;
     }
     // x DMA: instruction i of this wave fills rows 8 (q + RG i) .. + 7 of the stage; lane l writes slot l % 8 of row
-    // l / 8, which holds piece (l % 8) ^ (row & 7); rows past M read zero
+    // l / 8, which holds piece (l % 8) ^ ((row >> 1) & 7); rows past M read zero
     uint32_t xvo[NX];
     int xk[NX];
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-        const int r = 8 * (q + RG * i) + (lane >> 3), p = (lane & 7) ^ (r & 7);
+        const int r = 8 * (q + RG * i) + (lane >> 3), p = (lane & 7) ^ ((r >> 1) & 7);
         xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + 8 * p) * 2) : OOB_VOFF;
         xk[i] = 8 * p;
     }
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     };
     // A operand: x row 16 i + (lane & 15), piece 2 (lane >> 4) + s of stage st
     auto a_op = [&](int st, int i, int s) __attribute__((always_inline)) {
-        const int r = 16 * i + r16, p = (2 * lg + s) ^ (r & 7);
+        const int r = 16 * i + r16, p = (2 * lg + s) ^ ((r >> 1) & 7);
         return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * 128 + (p << 4));
     };
 
