@@ -413,13 +413,16 @@ def summarize_counters(d, kernel_substr=None, simds=1024, clock_ghz=2.17):
             print(f"| SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS | {o['SQ_LDS_BANK_CONFLICT'] / o['SQ_INSTS_LDS']:.3f} |")
 
 
-def summarize_stats(csv_path, top=12):
-    """markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv"""
+def summarize_stats(csv_path, top_other=4):
+    """markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv: every mbq kernel, then the other kernels
+    (torch's input generation, copies) with the most time"""
     import csv
     rows = list(csv.DictReader(open(csv_path)))
     key = lambda r: float(r.get("TotalDurationNs", 0) or 0)
+    ours = [r for r in rows if "mbq::" in r["Name"]]
+    other = [r for r in rows if "mbq::" not in r["Name"]]
     print("| kernel | calls | avg us | min us | max us | % time |\n|---|---:|---:|---:|---:|---:|")
-    for r in sorted(rows, key=key, reverse=True)[:top]:
+    for r in sorted(ours, key=key, reverse=True) + sorted(other, key=key, reverse=True)[:top_other]:
         name = r["Name"]
         name = name[:90] + ("..." if len(name) > 90 else "")
         print(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
