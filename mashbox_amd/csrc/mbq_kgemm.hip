@@ -19,7 +19,8 @@
 //     S partials in split order, so the sum does not depend on arrival order. The partials sit in uncached device
 //     memory, or (mbq_matmul_noalloc) in the static scratch with an agent-scope release / acquire around the exchange.
 // Weights go from HBM (non-temporal loads) straight into B-operand registers, D chunks in flight per wave. After the
-// K loop the K groups of a row group add their accumulators through LDS in a fixed tree order.
+// K loop a reduce-scatter through LDS leaves each wave the sums of a share of the block's tiles (K groups added in a
+// fixed order), so the split exchange and the stores run on all 8 waves; the row scales are loaded at the start.
 //
 // Lane layout (the weight-stream kernel's, mbq_wdirect.h): in K step s (32 values) of a chunk, lane l holds K values
 // 16 (l >> 4) + 8 s + e (e = 0..7) of x row 16 i + (l & 15) and of weight row (l & 15) of a tile; the MFMA sums over
@@ -65,11 +66,13 @@ struct KgmArgs {
 // K groups and LDS stages per K group
 template <int RG> constexpr int kgm_kg() { return 8 / RG; }
 template <int RG> constexpr int kgm_depth() { return RG == 1 ? 2 : 3; }
-// dynamic LDS: the x rings, or the K-group reduction's buffer if larger
+// tiles per round of the K groups' reduce-scatter: 8 waves x TR tiles of 1 KiB in LDS at once (at most 80 KiB)
+template <int MT, int NTW> constexpr int kgm_round() { return MT * NTW < 10 ? MT * NTW : 10; }
+// dynamic LDS: the x rings, or the reduce-scatter's buffer if larger
 template <int MT, int RG, int NTW>
 constexpr size_t kgm_lds() {
     const size_t ring = (size_t)kgm_kg<RG>() * kgm_depth<RG>() * 16 * MT * 128;
-    const size_t red = (size_t)RG * (kgm_kg<RG>() / 2) * MT * NTW * 1024;
+    const size_t red = (size_t)8 * kgm_round<MT, NTW>() * 1024;
     return ring > red ? ring : red;
 }
 // floats of one block's partial tile: RG row groups x MT x NTW 16x16 tiles
@@ -123,6 +126,15 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     for (int j = 0; j < NTW; ++j) {
         const int row = 16 * (t0 + j) + r16;
         wo[j] = (row >= rq0 && row < rq1) ? (uint32_t)i8t_off(row, K, 0) + 16u * (uint32_t)lg : OOB_VOFF;
+    }
+    // the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their latency
+    // hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads)
+    float sc[(MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>()];
+#pragma unroll
+    for (int u = 0; u < (MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>(); ++u) {
+        const int tt = kg + kgm_kg<RG>() * u, j = tt % NTW, n = 16 * (t0 + j) + r16;
+        const bool live = ok && tt < MT * NTW && n >= rq0 && n < rq1;
+        sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, live ? (uint32_t)(g.sc_off + 4 * (int64_t)n) : OOB_VOFF, 0, 0));
     }
     // x DMA: instruction i of this wave fills rows 8 (q + RG i) .. + 7 of the stage; lane l writes slot l % 8 of row
     // l / 8, which holds piece (l % 8) ^ ((row >> 1) & 7); rows past M read zero
@@ -213,44 +225,53 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     }
     __syncthreads();
 
-    // K groups of a row group: kg in [h, 2h) hands its accumulators to kg - h through LDS, h = KG/2 .. 1
+    // Reduce-scatter of the K groups' accumulators through LDS, in rounds of TR tiles (a tile: one 16 x 16 float32
+    // MFMA result, 1 KiB over the wave): every wave writes its tiles of the round, and the wave that owns a tile (tile tt
+    // of row group q belongs to K group tt % KG) adds the KG copies in K-group order. Every wave then holds the block's
+    // sums of its TPW tiles, and the split exchange and the stores below run on all 8 waves at once.
+    constexpr int TT = MT * NTW, TR = kgm_round<MT, NTW>(), TPW = (TT + KG - 1) / KG;
     f32x4_t* red = reinterpret_cast<f32x4_t*>(kgm_lds_buf);
+    f32x4_t fin[TPW];
 #pragma unroll
-    for (int h = KG / 2; h >= 1; h /= 2) {
-        if (kg >= h && kg < 2 * h) {
-            f32x4_t* dst = red + ((size_t)(q * (KG / 2) + (kg - h)) * MT * NTW) * 64;
+    for (int u = 0; u < TPW; ++u) fin[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
+    for (int r0 = 0; r0 < TT; r0 += TR) {
 #pragma unroll
-                for (int j = 0; j < NTW; ++j) dst[(i * NTW + j) * 64 + lane] = acc[i][j];
-        }
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                const int tt = i * NTW + j;
+                if (tt >= r0 && tt < r0 + TR) red[((size_t)wave * TR + (tt - r0)) * 64 + lane] = acc[i][j];
+            }
         __syncthreads();
-        if (kg < h) {
-            const f32x4_t* src = red + ((size_t)(q * (KG / 2) + kg) * MT * NTW) * 64;
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
+        for (int u = 0; u < TPW; ++u) {
+            const int tt = kg + KG * u;
+            if (tt >= r0 && tt < r0 + TR && tt < TT) {                    // wave-uniform
+                const f32x4_t* src = red + ((size_t)(q * KG) * TR + (tt - r0)) * 64 + lane;
+                f32x4_t v = src[0];
 #pragma unroll
-                for (int j = 0; j < NTW; ++j) acc[i][j] += src[(i * NTW + j) * 64 + lane];
+                for (int k = 1; k < KG; ++k) v += src[(size_t)k * TR * 64];
+                fin[u] = v;
+            }
         }
         __syncthreads();
     }
 
-    // the K group 0 wave of each row group holds the block's sums of its rows
     constexpr int E = kgm_elems<MT, RG, NTW>();
     if (g.S > 1) {
+        // each wave stores its tiles of the block's partial, (range, split) -> E floats laid out [q][tile][lane]; the
+        // split that arrives last adds the S partials of each tile in split order (its own from registers)
         const rsrc_t pr = make_rsrc(g.ws, g.ws_bytes);
-        const uint32_t lofs = (uint32_t)(q * MT * NTW * 64 + lane) * 16u;
-        if (kg == 0) {
-            const uint32_t own = (uint32_t)(blockIdx.x * E) * 4u;
+        const uint32_t own = (uint32_t)(blockIdx.x * E) * 4u;
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int j = 0; j < NTW; ++j)
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), pr,
-                                                           lofs + (uint32_t)((i * NTW + j) * 64) * 16u, own, 16);
-            if (g.fenced) split_release();                                // the partial is visible at agent scope
-            else wait_vm<0>();
+        for (int u = 0; u < TPW; ++u) {
+            const int tt = kg + KG * u;
+            const uint32_t off = tt < TT ? (uint32_t)((q * TT + tt) * 64 + lane) * 16u : OOB_VOFF;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, fin[u]), pr, off, own, 16);
         }
+        if (g.fenced) split_release();                                    // the partial is visible at agent scope
+        else wait_vm<0>();
         __syncthreads();
         if (threadIdx.x == 0) {
             const int old = __hip_atomic_fetch_add(g.cnt + rr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -259,51 +280,60 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         }
         __syncthreads();
         if (!kgm_last) return;
-        if (g.fenced) split_acquire();                                              // the other blocks' partials, not stale lines
-        if (kg == 0) {
-            const uint32_t first = (uint32_t)(rr * g.S * E) * 4u;
-            for (int zz = 0; zz < g.S; ++zz) {                            // split order, whoever arrived last
-                f32x4_t v[MT][NTW];
+        if (g.fenced) split_acquire();                                    // the other blocks' partials, not stale lines
+        const uint32_t first = (uint32_t)(rr * g.S * E) * 4u;
+        f32x4_t sum[TPW] = {};
+        // the loads of ZC splits in flight at once (every split of a plan of up to 8 when TPW <= 3: one round trip),
+        // then their sums in split order
+        constexpr int ZC = 24 / TPW >= 8 ? 8 : (24 / TPW < 1 ? 1 : 24 / TPW);
+        for (int z0 = 0; z0 < g.S; z0 += ZC) {
+            f32x4_t v[ZC][TPW];
 #pragma unroll
-                for (int i = 0; i < MT; ++i)
+            for (int c = 0; c < ZC; ++c)
 #pragma unroll
-                    for (int j = 0; j < NTW; ++j)
-                        v[i][j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                      pr, lofs + (uint32_t)((i * NTW + j) * 64) * 16u, first + (uint32_t)(zz * E) * 4u, 16));
+                for (int u = 0; u < TPW; ++u) {
+                    const int zz = z0 + c, tt = kg + KG * u;
+                    const bool live = zz < g.S && zz != z && tt < TT;
+                    v[c][u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                  pr, live ? (uint32_t)((q * TT + tt) * 64 + lane) * 16u : OOB_VOFF,
+                                  live ? first + (uint32_t)(zz * E) * 4u : 0u, 16));
+                }
 #pragma unroll
-                for (int i = 0; i < MT; ++i)
+            for (int c = 0; c < ZC; ++c) {
+                const int zz = z0 + c;
+                if (zz < g.S) {
 #pragma unroll
-                    for (int j = 0; j < NTW; ++j) acc[i][j] = zz == 0 ? v[i][j] : acc[i][j] + v[i][j];
+                    for (int u = 0; u < TPW; ++u) {
+                        const f32x4_t t = zz == z ? fin[u] : v[c][u];
+                        sum[u] = zz == 0 ? t : sum[u] + t;
+                    }
+                }
             }
         }
-    }
-    if (kg != 0) return;
-    // every scale first (one wait), then the stores back to back: a store past M or outside [rq0, rq1) gets an offset
-    // out of y's range (no write), so the loop has no branches and no wait between stores
-    float sc[NTW];
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-        const int n = 16 * (t0 + j) + r16;
-        sc[j] = (ok && n >= rq0 && n < rq1) ? row_scale<T_I8T>(nullptr, wb, g.sc_off, n) : __builtin_nanf("");
+        for (int u = 0; u < TPW; ++u) fin[u] = sum[u];
     }
+
+    // stores: tile tt = i NTW + j of this wave's row group holds rows m = 16 i + 4 (lane >> 4) + r of x and column
+    // n = 16 (t0 + j) + (lane & 15) of y; a store past M or outside [rq0, rq1) gets an offset out of y's range (no
+    // write), so the stores run back to back with no branch and no wait between them
     const uint32_t esz = g.out_bf16 ? 2u : 4u;
     const rsrc_t yr = make_rsrc(g.y, (uint32_t)M * (uint32_t)N * esz);
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) {
+    for (int u = 0; u < TPW; ++u) {
+        const int tt = kg + KG * u, i = tt / NTW, j = tt - i * NTW;
         const int n = 16 * (t0 + j) + r16;
-        const bool col = n >= rq0 && n < rq1;
+        const bool col = tt < TT && n >= rq0 && n < rq1;
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = 16 * i + 4 * lg + r;
-                const uint32_t off = (col && m < M) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : OOB_VOFF;
-                const float v = acc[i][j][r] * sc[j];
-                if (g.out_bf16)
-                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)pack_bf16(v, 0.f), yr, off, 0, 0);
-                else
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, off, 0, 0);
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * i + 4 * lg + r;
+            const uint32_t off = (col && m < M) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : OOB_VOFF;
+            const float v = fin[u][r] * (ok ? sc[u] : __builtin_nanf(""));    // a layer outside the stack: NaN
+            if (g.out_bf16)
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)pack_bf16(v, 0.f), yr, off, 0, 0);
+            else
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, off, 0, 0);
+        }
     }
 }
 
