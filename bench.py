@@ -13,7 +13,9 @@ activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported b
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
 distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
 for K timed launches bracketed by torch.cuda.synchronize() and HIP events on the stream the kernels run on. The kernel's
-average launch duration is the event time / K. The CPU baseline is the oracle's restatement of mashbox's exact path
+average launch duration is the event time / K. Beside it, `eager_call_us` is the end-to-end time of back-to-back eager
+ctypes calls through the C ABI, timed on the host (argument checks, plan, launch and kernel; up to 50 calls). The CPU
+baseline is the oracle's restatement of mashbox's exact path
 (rebuild float32 weights per call, float32 dot; int8: float32 dot then the scales) on the host's cores, every config at
 full size (a few seconds each); `cpu_baseline` is config 2's.
 
@@ -125,6 +127,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
     t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
     out = {"projections": {}}
     total_us = 0.0
+    total_eager_us = 0.0
     total_bytes = 0
     total_flops = 0
     for pi, (name, N, K) in enumerate(projs):
@@ -149,11 +152,23 @@ def run_config(idx, steps, warmup, rotate_bytes):
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1000.0 / steps
+        # end to end through the C ABI: back-to-back eager ctypes calls timed on the host (argument checks, plan,
+        # launch, and the kernel), the caller's view when it does not capture a graph
+        ne = min(steps, 50)
+        rcs = 0
+        t0 = time.perf_counter()
+        for i in range(ne):
+            rcs |= launch(i % copies)
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) * 1e6 / ne
+        check(rcs, f"config {idx} {name} eager calls")
         ab = algorithmic_bytes(t, M, N, K)
         fl = 2 * M * N * K
         out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
-                                    "TFLOPs": round(fl / us / 1e6, 2), "rotation_copies": copies,
-                                    "rotation_MB": round(copies * wbytes / 1e6, 1), "plan": plan}
+                                    "TFLOPs": round(fl / us / 1e6, 2), "eager_call_us": round(eager_us, 2),
+                                    "rotation_copies": copies, "rotation_MB": round(copies * wbytes / 1e6, 1),
+                                    "plan": plan}
+        total_eager_us += eager_us
         total_us += us
         total_bytes += ab
         total_flops += fl
@@ -163,7 +178,8 @@ def run_config(idx, steps, warmup, rotate_bytes):
     tfl = total_flops / total_us / 1e6
     out.update({"type": {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}.get(t, t), "M": M, "us_per_step": round(total_us, 3),
                 "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "TFLOPs": round(tfl, 2),
-                "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4), "algorithmic_bytes": total_bytes, "flops": total_flops})
+                "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4), "eager_us_per_step": round(total_eager_us, 2),
+                "algorithmic_bytes": total_bytes, "flops": total_flops})
     if idx in synth.REF_TPU_US:
         out["reference_tpu_v6e_us"] = synth.REF_TPU_US[idx]
         out["speedup_vs_reference_tpu_v6e"] = round(synth.REF_TPU_US[idx] / total_us, 2)
