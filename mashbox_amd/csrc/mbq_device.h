@@ -180,6 +180,12 @@ __device__ __forceinline__ uint32_t bload2(rsrc_t r, uint32_t voff, uint32_t sof
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
+// 16 bytes per lane from global memory straight into LDS (buffer_load ... lds): lane l writes lds_wave + 16 l
+// (lds_wave wave-uniform); it counts in vmcnt like a load
+__device__ __forceinline__ void dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(N), expcnt and lgkmcnt not waited (gfx9 encoding: vmcnt bits 3:0 and 15:14)
 template <int N>
 __device__ __forceinline__ void wait_vm() {

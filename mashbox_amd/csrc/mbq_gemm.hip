@@ -43,11 +43,6 @@ constexpr int GK = 64, GT = 512;
 // element offset of chunk c (8 bfloat16) of row r in an LDS tile of 64-value rows
 __device__ __forceinline__ int lds_off(int r, int c) { return r * GK + ((c ^ (r & 7)) << 3); }
 
-// 16 bytes per lane from global memory straight into LDS: lane l writes lds_wave + 16 l (lds_wave wave-uniform)
-__device__ __forceinline__ void dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
-}
-
 // the raw bytes of one weight unit (32 values of one row), as loaded from the planes
 template <int T> struct BUnit;
 template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };

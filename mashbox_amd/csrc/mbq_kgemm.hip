@@ -155,7 +155,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         for (int i = 0; i < NX; ++i) {
             uint32_t v = live ? xvo[i] : OOB_VOFF;
             if constexpr (!KFULL) v = (64 * c + xk[i] < K) ? v : OOB_VOFF;
-            ws_dma16(xr, reinterpret_cast<uint16_t*>(ring + st * STAGE + 8 * (q + RG * i) * 128), v,
+            dma16(xr, reinterpret_cast<uint16_t*>(ring + st * STAGE + 8 * (q + RG * i) * 128), v,
                      live ? (uint32_t)c * 128u : 0u);
         }
     };

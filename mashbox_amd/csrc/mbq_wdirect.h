@@ -163,9 +163,4 @@ __device__ __forceinline__ bf16x8_t ws_bop(const WsRaw<T>& w, const WsScale& sc,
     return __builtin_bit_cast(bf16x8_t, o);
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane l writes lds_wave + 16 l (lds_wave wave-uniform)
-__device__ __forceinline__ void ws_dma16(rsrc_t r, uint16_t* lds_wave, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, voff, soff, 0, 0);
-}
-
 }  // namespace mbq

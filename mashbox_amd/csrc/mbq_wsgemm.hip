@@ -114,7 +114,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
         for (int i = 0; i < NDW; ++i) {
             uint32_t v = xvo[i];
             if constexpr (!KFULL) v = (kk + xk[i] < K) ? v : OOB_VOFF;      // past K: out of range, reads zero
-            ws_dma16(xr, ws_x + st * STAGE + RPI * (wave + 4 * i) * KI, v, (uint32_t)kk * 2u);
+            dma16(xr, ws_x + st * STAGE + RPI * (wave + 4 * i) * KI, v, (uint32_t)kk * 2u);
         }
     };
     auto load_w = [&](WsRaw<T>* W, int kk) {
