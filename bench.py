@@ -471,8 +471,9 @@ def main():
     if a.summarize_counters:
         return summarize_counters(a.summarize_counters[0], a.summarize_counters[1] if len(a.summarize_counters) > 1 else None)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py runs on one GPU: this path is measured on a single MI355X (its kernels shard by weight rows "
-              "with no collective; see DESIGN.md). --gpus must be 1.", file=sys.stderr)
+        print("bench.py runs on one GPU: this path is measured on a single MI355X, at one GPU's share of the weights "
+              "(column-parallel rows need no collective; row-parallel K splits add one reduce-scatter + all-gather "
+              "of the partials). --gpus must be 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
