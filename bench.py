@@ -1,14 +1,16 @@
 #!/usr/bin/env python
 """bench.py — the quantized-linear hot path on one MI355X against its roofline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,q6k_head] [--cpu-seconds S | --no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,q6k_head,m4_q4k,...] [--cpu-seconds S | --no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input of a BASELINE config: one kernel launch for the
 decode GEMV configs 1-3, the 7 projection launches of one 27B-class layer for configs 4-5. The headline (`value`) is
 config 2 (GGUF Q8_0 decode GEMV, x[1,5120] @ W[17408,5120]^T), in GB/s of algorithmic bytes (packed weight bytes +
 scales + x + y, never repack padding) per second, with the weights already in HBM. `q6k_head` is not a BASELINE
 config: it is the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one
-activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs.
+activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs, as are batched decode
+over the 27B-class layer at 4 and 16 activation rows (`m4_q4k`, `m16_q4k`, `m4_int8`, `m16_int8`: the reference
+engine's row buckets, Q4_K planes and int8 weights).
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
 distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
@@ -450,7 +452,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head")
+    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_int8,m16_int8")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")
