@@ -73,8 +73,9 @@ def setup_projection(idx, pi, rotate_bytes):
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     x = synth.acts(M, K, seed=seed, device=dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    if t == "int8" and M > 4:
-        # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes)
+    if t == "int8" and M > 1:
+        # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes; from 2 rows on they run
+        # faster than row-major weights: MI355X, 17408 x 5120 at 4 rows 19 vs 36 us)
         q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
         pb = check(L.mbq_plane_bytes(LIB.I8T, N, K), "int8 plane_bytes")
         planes = torch.empty(pb, dtype=torch.uint8, device=dev)
@@ -90,7 +91,7 @@ def setup_projection(idx, pi, rotate_bytes):
                                 M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
         plan = LIB.plan_str(LIB.I8T, M, N, K)
     elif t == "int8":
-        # decode int8: the reference's row-major weights, run by the decode GEMV
+        # decode int8 at one row: the reference's row-major weights, run by the decode GEMV
         q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
         wbytes = N * K + 4 * N
         copies = max(1, math.ceil(rotate_bytes / wbytes))
