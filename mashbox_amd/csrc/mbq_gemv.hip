@@ -47,10 +47,17 @@
 namespace mbq {
 
 constexpr int GV_WAVES = 8, GV_THREADS = 64 * GV_WAVES;
-// grid: one block per CU, two when every wave still gets at least GV_ROWS_2BPC rows (part rows) of a tall weight
-// (measured on MI355X: a 151936-row output head runs 10-14 % faster with two blocks per CU; weights of 5120-17408 rows
-// run slower, their waves then have only a few rows each)
-constexpr int GV_ROWS_2BPC = 16;
+// grid: one block per CU, two when every wave of the two still gets enough items (part rows): at least 16 at one
+// activation row, 8 at 2-4 rows, 3.5 with 3 parts per row (gv_two_blocks). Measured on MI355X, one block against two:
+// a 151936-row output head at one row 10-14 % faster with two; 17408 x 5120 at 2 rows (2 parts, 8.5 items per wave)
+// 0-7 % faster, at 3-4 rows (3 parts, 12.8) 12-14 %; 5120-6144 rows at 3-4 rows (3 parts, 3.8-4.5) 0-11 %; at 2-3
+// items per wave (2 parts: 4096-6144 rows at 2-3 rows) 5-10 % slower. With 3 parts a block's 8 waves take them 3 / 3 /
+// 2, so the waves of the third part carry half the rows each: a second block per CU fills in behind them.
+constexpr int GV_ITEMS_2BPC = 16, GV_ITEMS_2BPC_M = 8;
+inline bool gv_two_blocks(int64_t N, int S, int M, int cus) {
+    const int64_t items = N * S, waves2 = 2 * (int64_t)cus * GV_WAVES;   // part rows; waves of two blocks per CU
+    return items >= waves2 * GV_ITEMS_2BPC || (M > 1 && items >= waves2 * GV_ITEMS_2BPC_M) || (S == 3 && 2 * items >= waves2 * 7);
+}
 constexpr int GV_ITEM_CHUNKS = 3;     // parts of at most 3 chunks: items of 2-3 KiB (measured best on MI355X)
 
 template <int T> constexpr int gv_uw() { return unit32(T) ? 32 : 16; }   // values per 16-byte unit
@@ -432,7 +439,7 @@ static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
     int P = resident_blocks(kern, 4096);
     if (P < 1) return set_error(MBQ_LAUNCH_FAIL, "GEMV occupancy query failed");
-    const int bpc = a.N * S >= (int64_t)cus * 2 * GV_WAVES * GV_ROWS_2BPC ? 2 : 1;
+    const int bpc = gv_two_blocks(a.N, S, M, cus) ? 2 : 1;
     P = (int)std::min<int64_t>({(int64_t)P, (int64_t)cus * bpc, a.N});
     const int64_t rows_max = (a.N + P - 1) / P;
     const size_t lds = S > 1 ? (size_t)rows_max * S * M * 4 : 0;
