@@ -190,6 +190,11 @@ int mbq_force_gemm_plan(int kernel, int bm, int bn, int splits);
  * MFMA load. Both are stream-ordered and allocate nothing. */
 int mbq_probe_read(const void* p_dev, int64_t bytes, void* sink_dev, void* stream);
 int mbq_probe_mfma(int iters, void* sink_dev, int64_t* flops, void* stream);
+/* A check of the same family (no counterpart in the reference): every bfloat16 output value is converted from float32
+ * by one hardware instruction; mbq_probe_bf16 runs all 2^32 float32 bit patterns through it and through the integer
+ * round-to-nearest-even form (NaN kept quiet) and ADDS the count of inputs whose bits differ to the uint64 at diff_dev
+ * (the caller zeroes it). Zero on MI355X. Stream-ordered; allocates nothing. */
+int mbq_probe_bf16(void* diff_dev, void* stream);
 
 #ifdef __cplusplus
 }

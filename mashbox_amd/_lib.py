@@ -45,6 +45,7 @@ _SIGS = {
     "mbq_force_gemm_plan": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int]),
     "mbq_probe_read": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_void_p]),
     "mbq_probe_mfma": (_c.c_int, [_c.c_int, _c.c_void_p, _c.POINTER(_c.c_int64), _c.c_void_p]),
+    "mbq_probe_bf16": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
 }
 
 

@@ -328,6 +328,11 @@ int mbq_probe_read(const void* p_dev, int64_t bytes, void* sink_dev, void* strea
                              reinterpret_cast<hipStream_t>(stream));
 }
 
+int mbq_probe_bf16(void* diff_dev, void* stream) {
+    if (!diff_dev) return set_error(MBQ_BAD_ARG, "bf16 probe: NULL output");
+    return launch_probe_bf16(static_cast<unsigned long long*>(diff_dev), reinterpret_cast<hipStream_t>(stream));
+}
+
 int mbq_probe_mfma(int iters, void* sink_dev, int64_t* flops, void* stream) {
     if (iters < 1 || !sink_dev || !flops) return set_error(MBQ_BAD_ARG, "MFMA probe: iters < 1 or NULL output");
     return launch_probe_mfma(iters, static_cast<float*>(sink_dev), flops, reinterpret_cast<hipStream_t>(stream));

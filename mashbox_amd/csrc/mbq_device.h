@@ -21,11 +21,17 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 // fp16 bits -> float32, exact (subnormal, inf and NaN kept): reference src/mashbox/ops/reference.py:49-51
 __device__ __forceinline__ float f16f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu)); }
 
-// float32 -> bfloat16 bits, round to nearest even; NaN stays NaN (quiet)
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
+// float32 -> bfloat16 bits, round to nearest even; NaN stays NaN (quiet). One v_cvt_pk_bf16_f32: on every one of the
+// 2^32 inputs it gives the bits of the integer form bf16_bits_int (mbq_probe_bf16 checks that on the device at hand;
+// on MI355X no input differs), where the integer form's branch for NaN cost about 20 instructions per value.
+__device__ __forceinline__ uint32_t bf16_bits_int(float f) {
     const uint32_t u = __float_as_uint(f);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+    const bf16x2_t p = {(__bf16)f, (__bf16)0.f};
+    return __builtin_bit_cast(uint32_t, p) & 0xFFFFu;
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {

@@ -441,7 +441,7 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 // Step l, producers (after barrier l): DMA x(l + 2) into A stage (l + 2) % 3 (spread between the next item's chunks),
 // load weights (l + 3), dequantize weights (l + 1) into B stage (l + 1) % 2, wait for x(l + 1), barrier l + 1. Consumers: barrier l, then the 48 MFMAs of step l
 // from A stage l % 3 and B stage l % 2, each K substep's operands read during the one before. Both roles pass n
-// barriers in the same order.
+// barriers in the same order, and one more before bfloat16 outputs leave through LDS (the consumers' epilogue).
 constexpr int SG_BM = 256, SG_BN = 192;
 // element offset of chunk c of row r in the specialized kernel's LDS tiles: rows of 64 bfloat16 (128 bytes, half of the
 // 64 four-byte banks), chunk c at c ^ ((r >> 1) & 7). A 32-lane pass of its operand reads (32 rows, one chunk) and of
@@ -449,6 +449,10 @@ constexpr int SG_BM = 256, SG_BN = 192;
 // c ^ (r & 7) rows r and r + 8 shared banks (SQ_LDS_BANK_CONFLICT measured 3.3 cycles per LDS instruction).
 __device__ __forceinline__ int sg_off(int r, int c) { return r * GK + ((c ^ ((r >> 1) & 7)) << 3); }
 constexpr size_t SG_LDS = (size_t)(3 * SG_BM + 2 * SG_BN) * GK * sizeof(uint16_t);   // 144 KiB
+// row stride (elements) of a consumer wave's output quarter in LDS: 96 values and 8 of padding, so that the two rows a
+// two-byte write covers (4 apart) fall on different banks; 4 quarters of 128 rows take 104 KiB
+constexpr int SG_QS = 104;
+static_assert((size_t)4 * 128 * SG_QS * sizeof(uint16_t) <= SG_LDS && SG_QS % 8 == 0, "output quarters fit the LDS");
 
 template <int T, bool KFULL>
 __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
@@ -469,6 +473,8 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
     const int KT = (K + GK - 1) / GK, n = ok ? KT : 0;
     auto k0 = [&](int l) { return min(l, n - 1) * GK; };
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+    // bfloat16 output rows whose 8-value chunks are 16-byte aligned leave through LDS (the consumers' epilogue)
+    const bool vec = g.out_bf16 && (N & 7) == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15) == 0;
 
     if (wave < 4) {
         // ---------------------------------------------------------------------------------------------- consumer
@@ -519,6 +525,34 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         for (int j = 0; j < 3; ++j) {
             const int nn = n0 + br + 32 * j;
             scs[j] = nn < N ? row_scale<T>(g.srow, g.base + (ok ? lo : 0), g.sc_off, nn) : 0.f;
+        }
+        if (vec) {
+            // The wave's 128 x 96 quarter goes to a region of LDS of its own as bfloat16 rows, and from there to y in
+            // 16-byte chunks: 24 coalesced stores per lane instead of 192 two-byte ones (measured on MI355X: the
+            // two-byte stores kept a tile's waves busy for about a sixth of its time). The barrier pairs with the
+            // producers' last one: no stage is read any more and every DMA has landed.
+            barrier_nofence();
+            uint16_t* const stg = sg_lds + wave * (128 * SG_QS);
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            stg[(32 * i + 8 * e + 4 * lh + r) * SG_QS + 32 * j + (lane & 31)] =
+                                (uint16_t)bf16_bits(ok ? acc[i][j][4 * e + r] * scs[j] : __builtin_nanf(""));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");         // the wave reads back what its lanes wrote
+            uint16_t* const y = reinterpret_cast<uint16_t*>(g.y);
+#pragma unroll
+            for (int t = 0; t < 128 * 12 / 64; ++t) {                  // chunk q: row q / 12, 8 values from 8 (q % 12)
+                const int qd = 64 * t + lane, row = qd / 12, c = qd - 12 * row;
+                const int m = m0 + cm * 128 + row, nn = n0 + cn * 96 + 8 * c;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * SG_QS + 8 * c);
+                if (m < M && nn < N) *reinterpret_cast<u32x4*>(y + (int64_t)m * N + nn) = v;   // N % 8 == 0: whole chunks
+            }
+            return;
         }
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
@@ -644,6 +678,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         if (l + 1 < n - 1) pstep(I1{}, l + 1);
         wait_vm<0>();                                                 // no DMA may land after the block ends
     }
+    if (vec) barrier_nofence();                                       // the consumers may now write the output tile into LDS
 }
 
 // ------------------------------------------------------------------------------------------------- workspace

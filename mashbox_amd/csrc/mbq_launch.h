@@ -91,6 +91,7 @@ int launch_zero(uint8_t* p, int64_t n, hipStream_t s);   // n bytes at device ad
 // measurement probes (mbq_probe.hip)
 int launch_probe_read(const uint8_t* p, int64_t bytes, uint32_t* sink, hipStream_t s);
 int launch_probe_mfma(int iters, float* sink, int64_t* flops, hipStream_t s);
+int launch_probe_bf16(unsigned long long* diff, hipStream_t s);
 struct Layout;
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s);
 // tiled int8 planes from the (N, K) int8 quants and (N,) float32 scales (padding rows and columns written as zero)

@@ -4,6 +4,8 @@
 //         a streaming kernel can reach on this GPU
 //   mfma  v_mfma_f32_16x16x32_bf16 back to back on 8 independent accumulators per wave, 2 waves per SIMD: the bf16
 //         matrix-core rate at the clock the GPU holds under MFMA load
+//   bf16  every one of the 2^32 float32 bit patterns through bf16_bits (the conversion every bfloat16 output takes) and
+//         through its integer form: the inputs whose bits differ, counted (a check, not a rate)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -57,6 +59,17 @@ __global__ __launch_bounds__(512) void probe_mfma_kernel(int iters, float* sink)
     if (s == -1.f) sink[0] = s;              // keeps the MFMAs live; never taken (the sums are positive)
 }
 
+// grid-stride over the 2^32 patterns; each thread adds its count of differing inputs once
+__global__ __launch_bounds__(256) void probe_bf16_kernel(unsigned long long* diff) {
+    const uint64_t total = 1ull << 32, step = (uint64_t)gridDim.x * blockDim.x;
+    unsigned long long n = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        const float f = __uint_as_float((uint32_t)i);
+        n += bf16_bits(f) != bf16_bits_int(f);
+    }
+    if (n) atomicAdd(diff, n);
+}
+
 int launch_probe_read(const uint8_t* p, int64_t bytes, uint32_t* sink, hipStream_t s) {
     probe_read_kernel<<<cus_of_device(), 64 * PR_WAVES, 0, s>>>(p, bytes, sink);
     const hipError_t e = hipGetLastError();
@@ -69,6 +82,12 @@ int launch_probe_mfma(int iters, float* sink, int64_t* flops, hipStream_t s) {
     *flops = (int64_t)blocks * 8 * iters * 8 * 16 * 16 * 32 * 2;
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(MBQ_LAUNCH_FAIL, "MFMA probe launch: %s", hipGetErrorString(e));
+}
+
+int launch_probe_bf16(unsigned long long* diff, hipStream_t s) {
+    probe_bf16_kernel<<<4 * cus_of_device(), 256, 0, s>>>(diff);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(MBQ_LAUNCH_FAIL, "bf16 probe launch: %s", hipGetErrorString(e));
 }
 
 }  // namespace mbq
