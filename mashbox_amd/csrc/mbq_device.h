@@ -199,9 +199,16 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | 0x0F70 | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt not waited): a wave's own LDS writes have completed. A barrier does not wait
+// for them (the AMDGPU memory model releases LDS writes at workgroup scope with this wait), so a wave that writes LDS
+// for other waves waits for its writes before it passes the barrier they wait at (measured on MI355X: without it,
+// dequantized weight chunks written just before a barrier were read stale by the waves past it)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Workgroup barrier without the memory fence of __syncthreads, which waits for every load in flight (LDS DMA
 // included) and so empties a load pipeline at each step. The caller has waited (vmcnt) for the loads whose LDS writes
-// the other waves read after the barrier; the empty asm statements keep the compiler from moving memory accesses across.
+// the other waves read after the barrier, and (wait_lgkm0) for its own LDS writes that they read; the empty asm
+// statements keep the compiler from moving memory accesses across.
 __device__ __forceinline__ void barrier_nofence() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();

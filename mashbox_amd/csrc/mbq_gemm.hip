@@ -580,7 +580,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
     // x DMA: instruction i of producer wave w fills tile rows 8 (w + 4 i) .. +7 (8 instructions x 4 waves x 8 rows);
     // lane l writes LDS slot l & 7 of row l >> 3, holding chunk (l & 7) ^ ((row >> 1) & 7) (the swizzle of sg_off)
     constexpr int XD = SG_BM * GK * 2 / (4 * 64 * 16);              // 8
-    static_assert(XD == 4 * 2, "the producer step interleaves one DMA instruction per dequantized chunk of 2 units");
+    static_assert(XD == 8, "the producer step spreads its 8 DMA instructions among its 6 or 8 dequantized chunks");
     uint32_t xvo[XD];
     int xk[XD];
 #pragma unroll
@@ -599,20 +599,33 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
             dma16(xr, st + 8 * (pw + 4 * i) * GK, v, (uint32_t)kk * 2);
         }
     };
-    // weight units of a step: 2 per row (32 values each) = 384; producer thread t takes unit t and, for t < 128, unit
-    // t + 256 (row u >> 1, unit u & 1 of the step); rows past N are clamped (their outputs are never stored)
-    constexpr int UPT = 2;                                          // units per producer thread (the second for t < 128)
-    const bool two = pt < 2 * SG_BN - 256;
+    // Weight units of a step: 2 per row (32 values each) = 384 (row u >> 1, unit u & 1 of the step), 3 per pair of
+    // producer threads. Thread 2p dequantizes unit 3p whole and chunks 0-1 of unit 3p + 2, thread 2p + 1 unit 3p + 1
+    // whole and chunks 2-3 of unit 3p + 2: 6 chunks of 8 values per thread, so the four producer waves share the work
+    // evenly (with units 0-255 whole and 128 second units on two of the waves, those two set the step: measured on
+    // MI355X, the other two waited ≈ 700 of ≈ 2,300 cycles per step at the barrier). Both threads of a pair load the
+    // shared unit whole (the same bytes). Q6_K units take 8 registers each and the even split spills there, so Q6_K
+    // keeps that uneven one: thread t takes unit t whole and, for t < 128, unit t + 256. Rows past N are clamped
+    // (their outputs are never stored).
+    constexpr bool EVEN = T != T_Q6_K;
+    constexpr int UPT = 2;                                          // the thread's whole unit, then the shared (second) one
+    constexpr int NCH = EVEN ? 6 : 8;                               // chunks of 8 values per thread and step
+    const int ph = pt & 1;                                          // EVEN: which half of the shared unit
+    const bool two = EVEN || pt < 2 * SG_BN - 256;                  // uneven: the threads with a second unit
     BOff bo[UPT];
     int bu[UPT], brow[UPT];
 #pragma unroll
     for (int v = 0; v < UPT; ++v) {
-        const int u = v == 0 ? pt : pt + 256;
+        const int u = EVEN ? 3 * (pt >> 1) + (v == 0 ? ph : 2) : pt + 256 * v;
         brow[v] = u >> 1;
         bu[v] = u & 1;
         bo[v] = b_off<T>(g.sc_off, g.hi_off, g.d_off, min(n0 + brow[v], N - 1), K, bu[v]);
     }
-    if (!two) bo[1] = BOff{OOB_VOFF, OOB_VOFF, OOB_VOFF, OOB_VOFF};                      // no second unit: its loads read zero, no traffic
+    if (!two) bo[1] = BOff{OOB_VOFF, OOB_VOFF, OOB_VOFF, OOB_VOFF};   // no second unit: its loads read zero, no traffic
+    // chunk i of the thread: chunks 0-3 of its whole unit, then (EVEN) chunks 2 ph and 2 ph + 1 of the shared one or
+    // (uneven) chunks 0-3 of the second unit, which only threads with `two` have (wave-uniform)
+    auto chunk_v = [](int i) { return i < 4 ? 0 : 1; };
+    auto chunk_c = [&](int i) { return i < 4 ? i : EVEN ? 2 * ph + (i - 4) : i - 4; };
     BUnit<T> R[3][UPT];
     auto load_w = [&](BUnit<T>* Rr, int l) {
 #pragma unroll
@@ -620,12 +633,13 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
     };
     auto dequant = [&](const BUnit<T>* Rr, int l) {                   // weights of step l into B stage l % 2
         uint16_t* st = B0 + (l & 1) * SG_BN * GK;
+        BScale sc[UPT];
 #pragma unroll
-        for (int v = 0; v < UPT; ++v) {
-            if (v == 1 && !two) break;                                // wave-uniform: waves 4-5 take two units
-            const BScale sc = b_scale<T>(Rr[v], ((k0(l) >> 5) + bu[v]) & 7);
+        for (int v = 0; v < UPT; ++v) sc[v] = b_scale<T>(Rr[v], ((k0(l) >> 5) + bu[v]) & 7);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) st16(st + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc, c));
+        for (int i = 0; i < NCH; ++i) {
+            const int v = chunk_v(i), c = chunk_c(i);
+            if (v == 0 || two) st16(st + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
         }
     };
     constexpr int NDW = XD, NWL = UPT * b_loads<T>();
@@ -637,6 +651,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         load_w(R[2], 2);
         dequant(R[0], 0);
         wait_vm<NDW + 3 * NWL>();                                     // x(0) has landed
+        wait_lgkm0();                                                 // and the dequantized weights of step 0
         barrier_nofence();                                            // barrier 0
         // step l (l = 0 .. n - 2): x(l + 2), weights (l + 3), dequantize (l + 1), wait x(l + 1), barrier l + 1. The x
         // DMA's 8 instructions are spread between the dequantized chunks (a burst of them slows the consumers' reads).
@@ -659,10 +674,13 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < XD; ++i) {
                 if (i > 0) dma_i(i);
-                const int v = i >> 2, c = i & 3;                      // chunk c of unit v
-                if (v == 0 || two) st16(bst + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
+                if (i < NCH) {
+                    const int v = chunk_v(i), c = chunk_c(i);
+                    if (v == 0 || two) st16(bst + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
+                }
             }
             wait_vm<NDW + NWL>();                                     // x(l + 1) has landed (loads complete in order)
+            wait_lgkm0();                                             // and the dequantized weights of step l + 1
             barrier_nofence();
         };
         using I0 = std::integral_constant<int, 0>;
