@@ -414,6 +414,27 @@ def test_every_gemm_tile_shape_with_and_without_split(t, bm, bn, forced_plan, cu
     assert np.max(np.abs(outs[0] - outs[1])) <= 1e-4 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_specialized_gemm_bf16_output_tile_edges(t, forced_plan, cuda):
+    """the 256 x 192 tile without a split (the specialized-wave kernel) with bfloat16 output, whose tile leaves through
+    LDS in 16-byte chunks when N % 8 == 0: partial tiles on both edges (381 activation rows, 200 weight rows), against
+    the oracle, and bit for bit the same kernel's float32 output rounded to nearest even"""
+    rng = np.random.default_rng([t, 381, 200])
+    m, n, k = 381, 200, R.TYPES[t][1] * (24 if t in (R.Q4_0, R.Q8_0) else 3)
+    raw = G.RAW[t](rng, n, k)
+    xb = G.acts(rng, m, k)
+    planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+    x = _bf16_tensor(xb, cuda)
+    forced_plan(LIB.KERNEL_TILES, 256, 192, 1)
+    assert LIB.gemm_plan(t, m, n, k)[:4] == (LIB.KERNEL_TILES, 256, 192, 1)
+    print(f"case: {NAME[t]} {m} x {n} x {k}, tile 256 x 192, bf16 and f32 outputs", flush=True)
+    y = KQ.matmul(x, planes).cpu().numpy()
+    yb = KQ.matmul(x, planes, out_dtype=torch.bfloat16)
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    assert_product(y, ref, f"{NAME[t]} tile 256x192 f32")
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y))
+
+
 def _direct_case(t, m, n, k, rng, cuda):
     xb = G.acts(rng, m, k)
     x = _bf16_tensor(xb, cuda)
