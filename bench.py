@@ -104,18 +104,20 @@ def setup_projection(idx, pi, rotate_bytes):
         plan = LIB.plan_str(LIB.INT8, M, N, K)
     else:
         raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
-        pb = check(L.mbq_plane_bytes(t, N, K), "plane_bytes")
+        # batched Q4_K decode (2-64 rows): the blocks repacked once at load into 16-row tiles (MBQ_Q4KT planes), as int8
+        pt = LIB.Q4KT if t == 12 and 1 < M <= 64 else t
+        pb = check(L.mbq_plane_bytes(pt, N, K), "plane_bytes")
         planes = torch.empty(pb, dtype=torch.uint8, device=dev)
-        check(L.mbq_repack_dev(t, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st()), "repack")
+        check(L.mbq_repack_dev(pt, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st()), "repack")
         del raw
         wbytes = pb
         copies = max(1, math.ceil(rotate_bytes / wbytes))
         bufs = [planes] + [planes.clone() for _ in range(copies - 1)]
 
         def launch(c):
-            return L.mbq_matmul(t, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
+            return L.mbq_matmul(pt, ctypes.c_void_p(bufs[c].data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()),
                                 M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
-        plan = LIB.plan_str(t, M, N, K)
+        plan = LIB.plan_str(pt, M, N, K)
     torch.cuda.synchronize()
     check(launch(0), f"config {idx} {name}")          # eager call: argument errors surface here, not in a capture
     torch.cuda.synchronize()

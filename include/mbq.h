@@ -40,6 +40,16 @@ extern "C" {
 /* int8 per-output-channel weights repacked once at load into 16-row tiles (mbq_int8_repack_host / _dev): the planes
  * mbq_matmul, mbq_matmul_noalloc, mbq_plane_bytes, mbq_covers and mbq_gemm_plan take with this type id */
 #define MBQ_I8T (-9)
+/* Q4_K weights repacked once at load into 16-row tiles: mbq_repack_host / mbq_repack_dev / mbq_unpack_host with this
+ * type id take the same Q4_K file blocks (rows, row_bytes) and write (read) planes whose 16 rows x 128 values of a
+ * tile are one contiguous KiB, then the tiles' super-block headers (the Q4_K MFMA operand tile the K-group kernel
+ * loads); mbq_plane_bytes, mbq_covers, mbq_matmul, mbq_matmul_noalloc, mbq_dequant, mbq_dequant_rows and
+ * mbq_gemm_plan take them with this id, and give the results of the row-major MBQ_Q4_K planes (dequant bit for bit;
+ * matmul within the same bars, and bit for bit from 65 rows on, where both run the same plans). Not a ggml type:
+ * mbq_has_type and mbq_row_bytes refuse it. A layout of this library, with no counterpart in the reference: it serves
+ * decode batches of several rows (the engine's row buckets 4 and 16, reference src/mashbox/runtime/engine.py:424-428)
+ * better than the row-major planes. */
+#define MBQ_Q4KT (-12)
 
 #define MBQ_OUT_F32 0
 #define MBQ_OUT_BF16 1
@@ -163,9 +173,9 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
- *   MBQ_KERNEL_KGROUP  K-group kernel of tiled int8 planes (MBQ_I8T) at M <= 64: bm = 16, bn = weight rows per block
- *                      (any count: N is cut into equal ranges that fill the CUs), splits = K ranges. The automatic
- *                      plan of MBQ_I8T up to 64 rows.
+ *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T, MBQ_Q4KT) at M <= 64: bm = 16, bn = weight rows per
+ *                      block (any count: N is cut into equal ranges that fill the CUs), splits = K ranges. The
+ *                      automatic plan of tiled planes up to 64 rows (tiled planes have no GEMV or weight-stream plan).
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
  * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice;
  * MBQ_KERNEL_KGROUP takes bm = bn = 0 and chooses its rows per block for the forced splits, 0 = its own choice).

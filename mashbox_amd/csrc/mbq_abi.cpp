@@ -28,13 +28,18 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
-static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_0 || kquant(t); }
+// the ggml types with kernel planes
+static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+// plane types made from a ggml type's blocks: the ggml types' own, and Q4_K in 16-row tiles (T_Q4KT)
+static bool is_block_planes(int t) { return is_type(t) || t == T_Q4KT; }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// shape rules shared by every entry point of a ggml type
+// shape rules shared by every entry point of a ggml type's blocks (and of MBQ_Q4KT planes, made from Q4_K blocks)
 static int check_shape(int t, int64_t rows, int64_t cols) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14)", t);
+    if (!is_block_planes(t))
+        return set_error(MBQ_BAD_ARG, "type %d has no kernel planes (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, "
+                                      "tiled Q4_K = -12)", t);
     if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
     if (cols % block_values(t))
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
@@ -160,7 +165,7 @@ int mbq_repack_dev(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, ui
     if (!raw_dev || !planes_dev || !aligned16(planes_dev)) return set_error(MBQ_BAD_ARG, "NULL or misaligned buffer");
     const Layout L = layout(t, rows, cols);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // zero the alignment padding, then write every plane byte
+    // zero the alignment padding, then write every plane byte (T_Q4KT: the padding rows of the last tile too)
     int rc = 0;
     if (!for_each_gap(L, [&](int64_t off, int64_t n) { return (rc = launch_zero(planes_dev + off, n, s)) == 0; })) return rc;
     return launch_repack(t, raw_dev, rows, cols, planes_dev, L, s);
@@ -249,6 +254,7 @@ int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int3
 }
 
 int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream) {
+    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "dequant_raw takes a ggml type's blocks, not type %d", t);
     if (int rc = check_shape(t, rows, cols)) return rc;
     if (!raw_dev || !w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "raw is NULL or w is NULL / not 16-byte aligned");
     return launch_dequant_raw(t, raw_dev, rows, cols, w_dev, reinterpret_cast<hipStream_t>(stream));

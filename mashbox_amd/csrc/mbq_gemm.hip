@@ -46,6 +46,7 @@ __device__ __forceinline__ int lds_off(int r, int c) { return r * GK + ((c ^ (r 
 // the raw bytes of one weight unit (32 values of one row), as loaded from the planes
 template <int T> struct BUnit;
 template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
+template <> struct BUnit<T_Q4KT> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
@@ -65,6 +66,7 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     else if constexpr (T == T_Q5_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
+    else if constexpr (T == T_Q4KT) return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q4kt_meta_off(bn, K)), 0, 0};
     else if constexpr (T == T_Q4_0) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
     else if constexpr (T == T_I8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 32 * u), 0, 0, 0};   // 16-row tiles
     else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
@@ -79,6 +81,10 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, (uint32_t)k0 >> 2, 0));
         b.s = bload2(r, o.s, (uint32_t)k0 >> 4);
         b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 2);
+    } else if constexpr (T == T_Q4KT) {
+        // the step's 32 bytes of the row sit in the tile block of values 128 (k0 / 128) .., at byte (k0 / 2) % 64
+        b.q = bload16(r, o.q, ((uint32_t)k0 >> 7) * 1024u + (((uint32_t)k0 >> 1) & 63u));
+        b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 256);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
@@ -126,7 +132,7 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.b = 32.f * s.a;
         s.c = d * (float)(int8_t)((b.s >> 8) & 0xFFu);
         s.e = 32.f * s.c;
-    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    } else if constexpr (q4k_like(T) || T == T_Q5_K) {
         uint32_t sc, mn;
         q4k_scale_min_sel(b.meta[1], b.meta[2], b.meta[3], q4k_sel(j), &sc, &mn);
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
@@ -972,16 +978,17 @@ struct Choice { int kind, bm, bn, S; };   // K_STREAM: bn weight rows per block;
 
 static int choose(int t, const Args& a, Choice* c) {
     const int fk = g_force_kind.load();
-    // tiled int8 planes up to 64 rows: the K-group kernel (mbq_kgemm.hip), unless another kernel is forced
-    if (t == T_I8T && a.M <= WS_MAX_M && (fk == K_AUTO || fk == K_KGROUP)) {
+    // tiled planes up to 64 rows: the K-group kernel (mbq_kgemm.hip), unless another kernel is forced
+    if (tiled_type(t) && a.M <= WS_MAX_M && (fk == K_AUTO || fk == K_KGROUP)) {
         int R = 0, S = 0;
-        if (int rc = kgemm_plan(a, fk == K_KGROUP ? g_force_s.load() : 0, &R, &S)) return rc;
+        if (int rc = kgemm_plan(t, a, fk == K_KGROUP ? g_force_s.load() : 0, &R, &S)) return rc;
         *c = Choice{K_KGROUP, 16, R, S};
         return 0;
     }
     if (fk == K_KGROUP && a.M <= WS_MAX_M)
-        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled int8 planes (MBQ_I8T) only");
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q4KT) only");
     if (fk == K_STREAM) {
+        if (t == T_Q4KT) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled Q4_K planes");
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
@@ -1014,7 +1021,7 @@ static int launch_gemm_t(const Args& a, hipStream_t s) {
     Choice c;
     if (int rc = choose(T, a, &c)) return rc;
     if (c.kind == K_STREAM) return launch_wsgemm(T, a, c.bn, c.S, s);
-    if (c.kind == K_KGROUP) return launch_kgemm(a, c.S, s);
+    if (c.kind == K_KGROUP) return launch_kgemm(T, a, c.S, s);
     Plan p;
     if (int rc = pick<T>(a, &p)) return rc;
     Workspace w;
@@ -1053,6 +1060,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_Q6_K: rc = pick<T_Q6_K>(a, &p); if (!rc) *bm = CANDS<T_Q6_K>[p.idx].bm, *bn = CANDS<T_Q6_K>[p.idx].bn; break;
         case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
         case T_I8T: rc = pick<T_I8T>(a, &p); if (!rc) *bm = CANDS<T_I8T>[p.idx].bm, *bn = CANDS<T_I8T>[p.idx].bn; break;
+        case T_Q4KT: rc = pick<T_Q4KT>(a, &p); if (!rc) *bm = CANDS<T_Q4KT>[p.idx].bm, *bn = CANDS<T_Q4KT>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -1091,6 +1099,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_Q6_K: return launch_gemm_t<T_Q6_K>(a, s);
         case T_INT8: return launch_gemm_t<T_INT8>(a, s);
         case T_I8T: return launch_gemm_t<T_I8T>(a, s);
+        case T_Q4KT: return launch_gemm_t<T_Q4KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

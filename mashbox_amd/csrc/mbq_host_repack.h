@@ -1,5 +1,5 @@
-// Host repack of one weight into kernel planes, and its inverse (no HIP: also built alone, under the host
-// sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
+// Host repack of one weight into kernel planes (Q4_K also into 16-row tiles, T_Q4KT), and its inverse (no HIP: also
+// built alone, under the host sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
 // src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
 // int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
 #pragma once
@@ -42,6 +42,15 @@ inline uint32_t q6k_file_quant(const uint8_t* blk, int j, int i) {
     const uint32_t lo = (blk[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15u;
     const uint32_t hi = (blk[128 + 32 * g + i] >> (2 * r)) & 3u;
     return lo | (hi << 4);
+}
+
+// Q4_K planes (row-major, or T_Q4KT tiles): offset in the qs plane of byte b of row n's quants (b = value / 2; a
+// 16-byte unit never straddles a 64-byte tile row), and in the meta plane of super-block sb's header
+inline int64_t q4k_qs_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q4KT ? q4kt_off(n, K) + (b / 64) * 1024 + b % 64 : n * (K / 2) + b;
+}
+inline int64_t q4k_meta_at(int t, int64_t n, int64_t K, int64_t sb) {
+    return t == T_Q4KT ? q4kt_meta_off(n, K) + sb * 256 : (n * (K / 256) + sb) * 16;
 }
 
 inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
@@ -120,11 +129,10 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                 memcpy(q + b * 16, unit, 16);  // little-endian host, as the GPU
             }
         } else {
-            uint8_t* q = planes + L.qs_off + n * (K / 2);
-            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            // Q4_K, row-major or in 16-row tiles (T_Q4KT): the same units and headers at the layout's offsets
             for (int64_t b = 0; b < nb; ++b) {
                 const uint8_t* src = row + b * bb;
-                memcpy(meta + b * 16, src, 16);
+                memcpy(planes + L.sc_off + q4k_meta_at(t, n, K, b), src, 16);
                 const uint8_t* qs = src + 16;
                 for (int j = 0; j < 8; ++j) {
                     uint32_t unit[4] = {0, 0, 0, 0};
@@ -135,10 +143,18 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                         q4k_slot(i, &dw, &bit);
                         unit[dw] |= v << bit;
                     }
-                    memcpy(q + b * 128 + j * 16, unit, 16);  // little-endian host, as the GPU
+                    memcpy(planes + L.qs_off + q4k_qs_at(t, n, K, b * 128 + j * 16), unit, 16);  // little-endian host, as the GPU
                 }
             }
         }
+    }
+}
+
+// T_Q4KT: the rows of the last tile past N, zero (quants and headers)
+inline void q4kt_zero_pad_rows(int64_t N, int64_t K, uint8_t* planes, const Layout& L) {
+    for (int64_t n = N; n < (N + 15) / 16 * 16; ++n) {
+        for (int64_t b = 0; b < K / 2; b += 64) memset(planes + L.qs_off + q4k_qs_at(T_Q4KT, n, K, b), 0, 64);
+        for (int64_t sb = 0; sb < K / 256; ++sb) memset(planes + L.sc_off + q4k_meta_at(T_Q4KT, n, K, sb), 0, 16);
     }
 }
 
@@ -212,16 +228,14 @@ inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
                 }
             }
         } else {
-            const uint8_t* q = planes + L.qs_off + n * (K / 2);
-            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
             for (int64_t b = 0; b < nb; ++b) {
                 uint8_t* dst = row + b * bb;
-                memcpy(dst, meta + b * 16, 16);
+                memcpy(dst, planes + L.sc_off + q4k_meta_at(t, n, K, b), 16);
                 uint8_t* qs = dst + 16;
                 memset(qs, 0, 128);
                 for (int j = 0; j < 8; ++j) {
                     uint32_t unit[4];
-                    memcpy(unit, q + b * 128 + j * 16, 16);
+                    memcpy(unit, planes + L.qs_off + q4k_qs_at(t, n, K, b * 128 + j * 16), 16);
                     for (int i = 0; i < 32; ++i) {
                         int dw, bit;
                         q4k_slot(i, &dw, &bit);
@@ -285,6 +299,7 @@ inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, u
     const Layout L = layout(t, rows, cols);
     for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
+    if (t == T_Q4KT) q4kt_zero_pad_rows(rows, cols, planes, L);
 }
 
 inline void unpack_host(int t, const uint8_t* planes, int64_t rows, int64_t cols, uint8_t* raw, int threads) {

@@ -103,9 +103,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
-    } else if constexpr (T == T_Q4_K) {
-        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
-        const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
+    } else if constexpr (q4k_like(T)) {
+        const u32x4 q = T == T_Q4KT ? ld16(base + q4kt_off(n, K) + (u >> 2) * 1024 + (u & 3) * 16) : ld16(base + n * (K >> 1) + u * 16);
+        const u32x4 mt = T == T_Q4KT ? ld16(base + sc_off + q4kt_meta_off(n, K) + (u >> 3) * 256)
+                                     : ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
         uint32_t sc, mn;
         q4k_scale_min(mt[1], mt[2], mt[3], (int)(u & 7), &sc, &mn);
         const float dsc = f16f(mt[0]) * (float)sc;
@@ -236,12 +237,13 @@ template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
     const int bv = (T == T_Q8_0 || T == T_Q4_0) ? 32 : 256;
-    const int bb = (T == T_Q4_0) ? 18 : (T == T_Q8_0) ? 34 : (T == T_Q4_K) ? 144 : (T == T_Q5_K) ? 176 : 210;
+    const int bb = (T == T_Q4_0) ? 18 : (T == T_Q8_0) ? 34 : q4k_like(T) ? 144 : (T == T_Q5_K) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= (int64_t)N * nb) return;
+    const int64_t rows = T == T_Q4KT ? ((int64_t)N + 15) / 16 * 16 : N;     // T_Q4KT: the last tile's padding rows too
+    if (g >= rows * nb) return;
     const int64_t n = g / nb, b = g % nb;
-    const uint8_t* src = raw + n * nb * bb + b * bb;
+    const uint8_t* src = raw + (n < N ? n : 0) * nb * bb + b * bb;
     if constexpr (T == T_Q8_0) {
         uint8_t* q = planes + n * K + b * 32;
         for (int i = 0; i < 32; ++i) q[i] = src[2 + i];
@@ -301,6 +303,26 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
             for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
             hd[j * 2] = hw[0];
             hd[j * 2 + 1] = hw[1];
+        }
+    } else if constexpr (T == T_Q4KT) {
+        // the Q4_K units and header of row n at their tile offsets (mbq_layout.h); the rows of the last tile past the
+        // weight's own (n >= N, when the grid covers them) are written zero
+        const bool live = n < N;
+        uint8_t* meta = planes + sc_off + q4kt_meta_off(n, K) + b * 256;
+        for (int i = 0; i < 16; ++i) meta[i] = live ? src[i] : 0;
+        const uint8_t* qs = src + 16;
+        for (int j = 0; j < 8; ++j) {
+            uint32_t* dst = reinterpret_cast<uint32_t*>(planes + q4kt_off(n, K) + (2 * b + (j >> 2)) * 1024 + (j & 3) * 16);
+            for (int t = 0; t < 4; ++t) {
+                uint32_t v = 0;
+                for (int e = 0; e < 8 && live; ++e) {
+                    const int i = t * 8 + e;
+                    const uint32_t byte = qs[32 * (j >> 1) + i];
+                    const uint32_t q = (j & 1) ? (byte >> 4) : (byte & 15u);
+                    v |= q << (16 * (e & 1) + 4 * (e >> 1));
+                }
+                dst[t] = v;
+            }
         }
     } else {
         uint8_t* meta = planes + sc_off + (n * nb + b) * 16;
@@ -438,6 +460,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_Q6_K: return launch_t<T_Q6_K>(a, s);
         case T_INT8: return launch_t<T_INT8>(a, s);
         case T_I8T: return launch_t<T_I8T>(a, s);
+        case T_Q4KT: return launch_t<T_Q4KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
@@ -453,6 +476,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
     };
     if (t == T_Q4_0) run(dequant_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
+    else if (t == T_Q4KT) run(dequant_kernel<T_Q4KT>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -460,11 +484,12 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
 }
 
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
-    const int64_t blocks = N * (K / block_values(t));
+    const int64_t blocks = (t == T_Q4KT ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
     if (t == T_Q4_0) run(repack_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
+    else if (t == T_Q4KT) run(repack_kernel<T_Q4KT>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

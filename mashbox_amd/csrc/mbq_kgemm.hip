@@ -63,20 +63,33 @@ struct KgmArgs {
     int fenced;                    // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
-// K groups and LDS stages per K group
+// K values per chunk: one KiB of a 16-row weight tile (int8: 64 values; Q4_K: 128, four 32-value units per row)
+constexpr int kgm_cw(int t) { return t == T_Q4KT ? 128 : 64; }
+// bytes of one x stage: 16 MT rows of one chunk of bfloat16 values
+constexpr size_t kgm_stage(int t, int mt) { return (size_t)16 * mt * 2 * kgm_cw(t); }
+// most dynamic LDS a block may take (160 KiB per CU, less a little for the static variables)
+constexpr size_t KGM_LDS_MAX = 160 * 1024 - 256;
+// K groups and LDS stages per K group (3 with two row groups, when the rings fit)
 template <int RG> constexpr int kgm_kg() { return 8 / RG; }
-template <int RG> constexpr int kgm_depth() { return RG == 1 ? 2 : 3; }
+constexpr int kgm_depth(int t, int mt, int rg) { return rg == 1 ? 2 : ((size_t)(8 / rg) * 3 * kgm_stage(t, mt) <= KGM_LDS_MAX ? 3 : 2); }
+// bytes of the x rings of a block
+constexpr size_t kgm_ring(int t, int mt, int rg) { return (size_t)(8 / rg) * kgm_depth(t, mt, rg) * kgm_stage(t, mt); }
 // tiles per round of the K groups' reduce-scatter: 8 waves x TR tiles of 1 KiB in LDS at once (at most 80 KiB)
 template <int MT, int NTW> constexpr int kgm_round() { return MT * NTW < 10 ? MT * NTW : 10; }
 // dynamic LDS: the x rings, or the reduce-scatter's buffer if larger
-template <int MT, int RG, int NTW>
+template <int T, int MT, int RG, int NTW>
 constexpr size_t kgm_lds() {
-    const size_t ring = (size_t)kgm_kg<RG>() * kgm_depth<RG>() * 16 * MT * 128;
+    const size_t ring = kgm_ring(T, MT, RG);
     const size_t red = (size_t)8 * kgm_round<MT, NTW>() * 1024;
     return ring > red ? ring : red;
 }
 // floats of one block's partial tile: RG row groups x MT x NTW 16x16 tiles
 template <int MT, int RG, int NTW> constexpr int kgm_elems() { return RG * MT * NTW * 256; }
+
+// x stage swizzle: piece p of row r sits in slot p ^ kgm_swz(r). 128-byte rows (8 pieces): (r >> 1) & 7; 256-byte rows
+// (16 pieces, Q4_K chunks): r & 15, so the 16 rows an A-operand read of one lane group takes (one piece each) fall on
+// 16 different slots, every bank once
+template <int PCS> __device__ __forceinline__ int kgm_swz(int r) { return PCS == 8 ? (r >> 1) & 7 : r & 15; }
 
 // f(integral_constant<int, P>) for each P of the sequence, in order
 template <class F, int... P>
@@ -84,15 +97,23 @@ __device__ __forceinline__ void kgm_each(F&& f, std::integer_sequence<int, P...>
     (f(std::integral_constant<int, P>{}), ...);
 }
 
-template <int MT, int RG, int NTW, bool KFULL>
+template <int T, int MT, int RG, int NTW, bool KFULL>
 __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
     __shared__ int kgm_last;
-    constexpr int KG = kgm_kg<RG>(), D = kgm_depth<RG>();
-    constexpr int STAGE = 16 * MT * 128;                 // bytes of one x stage (16 MT rows x 64 values)
-    constexpr int NX = 2 * MT / RG;                      // x DMA instructions per wave per chunk (1 KiB each)
-    static_assert(NX * RG == 2 * MT, "the RG waves of a K group issue whole DMA instructions");
-    constexpr int VMT = (D - 1) * NTW + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
+    constexpr bool QK = T == T_Q4KT;                     // Q4_K tiles (else int8 tiles)
+    constexpr int CW = kgm_cw(T);                        // K values per chunk
+    constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
+    constexpr int PCS = XB / 16;                         // its 16-byte pieces
+    constexpr int RPI = 64 / PCS;                        // x rows per DMA instruction
+    constexpr int NS = CW / 32;                          // MFMA K steps per chunk
+    constexpr int KG = kgm_kg<RG>(), D = kgm_depth(T, MT, RG);
+    constexpr int STAGE = (int)kgm_stage(T, MT);         // bytes of one x stage (16 MT rows x CW values)
+    constexpr int NX = STAGE / 1024 / RG;                // x DMA instructions per wave per chunk (1 KiB each)
+    static_assert(NX * RG * 1024 == STAGE, "the RG waves of a K group issue whole DMA instructions");
+    static_assert(kgm_ring(T, MT, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
+    constexpr int NWL = QK ? 2 * NTW : NTW;              // weight loads per chunk (Q4_K: quants and headers)
+    constexpr int VMT = (D - 1) * NWL + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
     static_assert(VMT < 64, "vmcnt range");
     const int M = g.M, N = g.N, K = g.K;
     const int lane = threadIdx.x & 63, lg = lane >> 4, r16 = lane & 15;
@@ -114,35 +135,42 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 
     // chunks of this split: [c0, c1); K group kg takes c0 + kg + KG l for l < its count; every group walks `steps`
     // steps (the block's barrier keeps them together), a step past its count loads zero through the range check
-    const int KC = (K + 63) / 64;
+    const int KC = (K + CW - 1) / CW;
     const int c0 = z * g.kcs, c1 = min(KC, c0 + g.kcs);
     const int nch = ok ? max(0, c1 - c0) : 0;
     const int steps = (nch + KG - 1) / KG;
     const int mine = (nch - kg + KG - 1) / KG;           // chunks of this K group
 
-    // weight offsets: tile t0 + j, row r16, the lane group's 16 bytes; rows outside [rq0, rq1) read zero
-    uint32_t wo[NTW];
+    // weight offsets: tile t0 + j, row r16, the lane group's 16 bytes (of the chunk's KiB); Q4_K: also the row's
+    // super-block headers; rows outside [rq0, rq1) read zero
+    uint32_t wo[NTW], mo[NTW];
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
         const int row = 16 * (t0 + j) + r16;
-        wo[j] = (row >= rq0 && row < rq1) ? (uint32_t)i8t_off(row, K, 0) + 16u * (uint32_t)lg : OOB_VOFF;
+        const bool in = row >= rq0 && row < rq1;
+        wo[j] = in ? (uint32_t)(QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
+        mo[j] = in && QK ? (uint32_t)(g.sc_off + q4kt_meta_off(row, K)) : OOB_VOFF;
     }
-    // the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their latency
-    // hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads)
+    // int8: the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their
+    // latency hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads). Q4_K values
+    // carry their scales: 1.
     float sc[(MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>()];
 #pragma unroll
     for (int u = 0; u < (MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>(); ++u) {
         const int tt = kg + kgm_kg<RG>() * u, j = tt % NTW, n = 16 * (t0 + j) + r16;
         const bool live = ok && tt < MT * NTW && n >= rq0 && n < rq1;
-        sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, live ? (uint32_t)(g.sc_off + 4 * (int64_t)n) : OOB_VOFF, 0, 0));
+        if constexpr (QK)
+            sc[u] = 1.f;
+        else
+            sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, live ? (uint32_t)(g.sc_off + 4 * (int64_t)n) : OOB_VOFF, 0, 0));
     }
-    // x DMA: instruction i of this wave fills rows 8 (q + RG i) .. + 7 of the stage; lane l writes slot l % 8 of row
-    // l / 8, which holds piece (l % 8) ^ ((row >> 1) & 7); rows past M read zero
+    // x DMA: instruction i of this wave fills rows RPI (q + RG i) .. + RPI - 1 of the stage; lane l writes slot l % PCS
+    // of row l / PCS, which holds piece (l % PCS) ^ kgm_swz(row); rows past M read zero
     uint32_t xvo[NX];
     int xk[NX];
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-        const int r = 8 * (q + RG * i) + (lane >> 3), p = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = RPI * (q + RG * i) + lane / PCS, p = (lane % PCS) ^ kgm_swz<PCS>(r);
         xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + 8 * p) * 2) : OOB_VOFF;
         xk[i] = 8 * p;
     }
@@ -154,23 +182,28 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
             uint32_t v = live ? xvo[i] : OOB_VOFF;
-            if constexpr (!KFULL) v = (64 * c + xk[i] < K) ? v : OOB_VOFF;
-            dma16(xr, reinterpret_cast<uint16_t*>(ring + st * STAGE + 8 * (q + RG * i) * 128), v,
-                     live ? (uint32_t)c * 128u : 0u);
+            if constexpr (!KFULL) v = (CW * c + xk[i] < K) ? v : OOB_VOFF;
+            dma16(xr, reinterpret_cast<uint16_t*>(ring + st * STAGE + RPI * (q + RG * i) * XB), v,
+                     live ? (uint32_t)c * (uint32_t)XB : 0u);
         }
     };
-    auto load_w = [&](u32x4* W, int l) __attribute__((always_inline)) {
+    // the chunk's weights: a KiB per tile (non-temporal), and for Q4_K the 16-byte header of the super-block (chunk / 2)
+    auto load_w = [&](u32x4* W, u32x4* H, int l) __attribute__((always_inline)) {
         const int c = chunk_of(l);
         const bool live = l < mine;
 #pragma unroll
-        for (int j = 0; j < NTW; ++j)
+        for (int j = 0; j < NTW; ++j) {
             W[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? wo[j] : OOB_VOFF,
                                                                                   live ? (uint32_t)c * 1024u : 0u, 2));
+            if constexpr (QK)
+                H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
+                                                                                      live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
+        }
     };
-    // A operand: x row 16 i + (lane & 15), piece 2 (lane >> 4) + s of stage st
+    // A operand: x row 16 i + (lane & 15), piece NS (lane >> 4) + s of stage st (the K values the lane's weights hold)
     auto a_op = [&](int st, int i, int s) __attribute__((always_inline)) {
-        const int r = 16 * i + r16, p = (2 * lg + s) ^ ((r >> 1) & 7);
-        return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * 128 + (p << 4));
+        const int r = 16 * i + r16, p = (NS * lg + s) ^ kgm_swz<PCS>(r);
+        return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * XB + (p << 4));
     };
 
     f32x4_t acc[MT][NTW];
@@ -179,6 +212,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
         for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     u32x4 W[D][NTW];
+    u32x4 H[QK ? D : 1][NTW];                                             // Q4_K: the tiles' super-block headers
 
     // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
     // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
@@ -191,29 +225,43 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         __builtin_amdgcn_sched_barrier(0);
         dma_x((U + D - 1) % D, l + D - 1);
         __builtin_amdgcn_sched_barrier(0);
+        // Q4_K: the lane's 16 bytes are one 32-value unit of its row, sub-block 4 (chunk % 2) + lg of the super-block;
+        // its (d sc, dmin m) for the whole chunk
+        WsScale qs[QK ? NTW : 1];
+        if constexpr (QK) {
+            const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], H[U][j]}, j8);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
             bf16x8_t A[MT];
 #pragma unroll
             for (int i = 0; i < MT; ++i) A[i] = a_op(U, i, s);
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
-                const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
-                const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
-                const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
+                bf16x8_t B;
+                if constexpr (QK) {
+                    // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m rounded to bfloat16 (the LDS GEMM's operand)
+                    B = ws_bop<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], H[U][j]}, qs[j], s);
+                } else {
+                    const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
+                    const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
+                    B = __builtin_bit_cast(bf16x8_t, o);
+                }
 #pragma unroll
                 for (int i = 0; i < MT; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_w(W[U], l + D);
+        load_w(W[U], H[QK ? U : 0], l + D);
     };
 
     if (steps > 0) {                                                      // block-uniform
 #pragma unroll
         for (int p = 0; p < D; ++p) {
             if (p < D - 1) dma_x(p, p);
-            load_w(W[p], p);
+            load_w(W[p], H[QK ? p : 0], p);
         }
         int l = 0;
         for (; l + D <= steps; l += D)
@@ -341,6 +389,9 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 // A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
 struct KgmPlan { int S, R, RG, NTW; };
 constexpr int KGM_MAX_NTW = 6;
+// most tiles per wave of a type and batch: Q4_K at 33-64 rows holds its tiles' headers and units in 5 tiles' registers
+// (6 spill to scratch at 256 registers per lane)
+constexpr int kgm_max_ntw(int t, int mt) { return t == T_Q4KT && mt >= 3 ? 5 : KGM_MAX_NTW; }
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
 static int kgm_ntw(int64_t N, int64_t R, int RG) {
@@ -360,10 +411,14 @@ static int kgm_ntw(int64_t N, int64_t R, int RG) {
 // its partial tile written plus, for the last arriver, S partials read) plus the MFMA rows spent on rows outside the
 // block's range and the K groups left idle in a block's last step; the weights reflect MI355X timings of the 7
 // projections of a 27B-class layer at 64 rows against forced split counts, over S in {1, 2, 3, 4, 6, 8} (only `force_s` when
-// it is set) and RG in {1, 2}, with rows per block chosen so that the ranges fill the CUs once.
-static KgmPlan kgm_choose(int64_t M, int64_t N, int64_t K, int cus, int force_s) {
-    const int64_t KC = (K + 63) / 64;
+// it is set) and RG in {1, 2} (those whose x rings fit the LDS), with rows per block chosen so that the ranges fill
+// the CUs once. Q4_K tiles: a row's chunk is 64 bytes of quants and half a 16-byte header, and a tile row outside the
+// range costs its dequantization (the vector work of the whole row), not only its MFMA row.
+static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int force_s) {
+    const int CW = kgm_cw(t);
+    const int64_t KC = (K + CW - 1) / CW;
     const int MT = (int)((M + 15) / 16);
+    const double wpc = t == T_Q4KT ? 72.0 : 64.0, waste_w = t == T_Q4KT ? 1.5 : 0.5;
     KgmPlan best{0, 0, 0, 0};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
@@ -373,14 +428,15 @@ static KgmPlan kgm_choose(int64_t M, int64_t N, int64_t K, int cus, int force_s)
             const int64_t R = (N + ranges - 1) / ranges;
             for (int RG : {1, 2}) {
                 const int KG = 8 / RG;
+                if (kgm_ring(t, MT, RG) > KGM_LDS_MAX) continue;
                 const int ntw = kgm_ntw(N, R, RG);
-                if (ntw > KGM_MAX_NTW) continue;
+                if (ntw > kgm_max_ntw(t, MT)) continue;
                 const int64_t kcs = (KC + S - 1) / S;
-                const double w = (double)R * kcs * 64;                          // weight bytes
-                const double x = 0.5 * 16 * MT * 128 * kcs;                     // x bytes (L2 hits: half weight)
+                const double w = (double)R * kcs * wpc;                         // weight bytes
+                const double x = 0.5 * 16 * MT * 2 * CW * kcs;                  // x bytes (L2 hits: half weight)
                 // partial tile written, and S read by the last arriver at the end of its work (twice the weight)
                 const double part = S > 1 ? (double)RG * MT * ntw * 1024 * (1 + 2 * S) : 0.0;
-                const double waste = 0.5 * (double)std::max<int64_t>(0, RG * ntw * 16 - R) * kcs * 64;
+                const double waste = waste_w * (double)std::max<int64_t>(0, RG * ntw * 16 - R) * kcs * wpc;
                 const double idle = (double)((kcs + KG - 1) / KG * KG - kcs) / (double)kcs;
                 const double cost = (w + x + part + waste) * (1.0 + idle);
                 if (best.S == 0 || cost < best_cost) {
@@ -395,41 +451,55 @@ static KgmPlan kgm_choose(int64_t M, int64_t N, int64_t K, int cus, int force_s)
 }
 
 // ------------------------------------------------------------------------------------------------------ launchers
-template <int MT, int RG, int NTW, bool KFULL>
+template <int T, int MT, int RG, int NTW, bool KFULL>
 static int kgm_launch(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
-    auto kern = kgemm_kernel<MT, RG, NTW, KFULL>;
-    const size_t lds = kgm_lds<MT, RG, NTW>();
-    static std::atomic<uint64_t> lds_set{0};
-    if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
-        return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM: %zu bytes of LDS refused", lds);
-    const int64_t KC = (a.K + 63) / 64;
-    const int kcs = (int)((KC + p.S - 1) / p.S);
-    KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
-              a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
-    const int64_t ranges = (a.N + p.R - 1) / p.R;
-    kern<<<dim3((unsigned)(ranges * p.S)), KGM_THREADS, lds, s>>>(g);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM launch: %s", hipGetErrorString(e));
-    return 0;
+    if constexpr (kgm_ring(T, MT, RG) > KGM_LDS_MAX || NTW > kgm_max_ntw(T, MT)) {
+        return set_error(MBQ_BAD_ARG, "K-group GEMM: no kernel of %d row groups x %d tiles at %d activation rows", RG, NTW, 16 * MT);
+    } else {
+        auto kern = kgemm_kernel<T, MT, RG, NTW, KFULL>;
+        const size_t lds = kgm_lds<T, MT, RG, NTW>();
+        static std::atomic<uint64_t> lds_set{0};
+        if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
+            return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM: %zu bytes of LDS refused", lds);
+        const int64_t KC = (a.K + kgm_cw(T) - 1) / kgm_cw(T);
+        const int kcs = (int)((KC + p.S - 1) / p.S);
+        KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
+                  a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
+        const int64_t ranges = (a.N + p.R - 1) / p.R;
+        kern<<<dim3((unsigned)(ranges * p.S)), KGM_THREADS, lds, s>>>(g);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM launch: %s", hipGetErrorString(e));
+        return 0;
+    }
 }
 
-template <int MT, int RG, bool KFULL>
+template <int T, int MT, int RG, bool KFULL>
 static int kgm_launch_ntw(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
     switch (p.NTW) {
-        case 1: return kgm_launch<MT, RG, 1, KFULL>(a, p, w, s);
-        case 2: return kgm_launch<MT, RG, 2, KFULL>(a, p, w, s);
-        case 3: return kgm_launch<MT, RG, 3, KFULL>(a, p, w, s);
-        case 4: return kgm_launch<MT, RG, 4, KFULL>(a, p, w, s);
-        case 5: return kgm_launch<MT, RG, 5, KFULL>(a, p, w, s);
-        case 6: return kgm_launch<MT, RG, 6, KFULL>(a, p, w, s);
+        case 1: return kgm_launch<T, MT, RG, 1, KFULL>(a, p, w, s);
+        case 2: return kgm_launch<T, MT, RG, 2, KFULL>(a, p, w, s);
+        case 3: return kgm_launch<T, MT, RG, 3, KFULL>(a, p, w, s);
+        case 4: return kgm_launch<T, MT, RG, 4, KFULL>(a, p, w, s);
+        case 5: return kgm_launch<T, MT, RG, 5, KFULL>(a, p, w, s);
+        case 6: return kgm_launch<T, MT, RG, 6, KFULL>(a, p, w, s);
     }
     return set_error(MBQ_BAD_ARG, "K-group GEMM: %d tiles per wave", p.NTW);
 }
 
-template <int MT, bool KFULL>
+template <int T, int MT, bool KFULL>
 static int kgm_launch_rg(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
-    if (p.RG == 1) return kgm_launch_ntw<MT, 1, KFULL>(a, p, w, s);
-    return kgm_launch_ntw<MT, 2, KFULL>(a, p, w, s);
+    if (p.RG == 1) return kgm_launch_ntw<T, MT, 1, KFULL>(a, p, w, s);
+    return kgm_launch_ntw<T, MT, 2, KFULL>(a, p, w, s);
+}
+
+template <int T, bool KFULL>
+static int kgm_launch_mt(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
+    switch ((a.M + 15) / 16) {
+        case 1: return kgm_launch_rg<T, 1, KFULL>(a, p, w, s);
+        case 2: return kgm_launch_rg<T, 2, KFULL>(a, p, w, s);
+        case 3: return kgm_launch_rg<T, 3, KFULL>(a, p, w, s);
+        default: return kgm_launch_rg<T, 4, KFULL>(a, p, w, s);
+    }
 }
 
 // bytes of the partial tiles of a plan
@@ -439,8 +509,8 @@ static size_t kgm_ws_bytes(int64_t M, int64_t N, const KgmPlan& p) {
     return (size_t)ranges * p.S * p.RG * MT * p.NTW * 256 * 4;
 }
 
-int kgemm_plan(const Args& a, int force_s, int* rows_per_block, int* splits) {
-    const KgmPlan p = kgm_choose(a.M, a.N, a.K, cus_of_device(), force_s);
+int kgemm_plan(int t, const Args& a, int force_s, int* rows_per_block, int* splits) {
+    const KgmPlan p = kgm_choose(t, a.M, a.N, a.K, cus_of_device(), force_s);
     if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
                                    (long long)a.N, (long long)a.K, force_s);
     *rows_per_block = p.R;
@@ -448,11 +518,13 @@ int kgemm_plan(const Args& a, int force_s, int* rows_per_block, int* splits) {
     return 0;
 }
 
-int launch_kgemm(const Args& a, int force_s, hipStream_t s) {
+int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
+    if (t != T_I8T && t != T_Q4KT) return set_error(MBQ_BAD_ARG, "K-group GEMM: type %d is not a tiled plane type", t);
     if (a.M < 1 || a.M > 64) return set_error(MBQ_BAD_ARG, "K-group GEMM: M = %lld", (long long)a.M);
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES || a.M * a.N * 4 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "K-group GEMM operands over 2 GiB");
-    const KgmPlan p = kgm_choose(a.M, a.N, a.K, cus_of_device(), force_s);
+    if (t == T_Q4KT && a.K % 256) return set_error(MBQ_BAD_ARG, "K-group GEMM: Q4_K K = %lld", (long long)a.K);
+    const KgmPlan p = kgm_choose(t, a.M, a.N, a.K, cus_of_device(), force_s);
     if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
                                    (long long)a.N, (long long)a.K, force_s);
     Workspace w;
@@ -460,13 +532,8 @@ int launch_kgemm(const Args& a, int force_s, hipStream_t s) {
         const int64_t ranges = (a.N + p.R - 1) / p.R;
         if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.M, a.N, p), s, &w)) return rc;
     }
-    const bool kfull = a.K % 64 == 0;
-    switch ((a.M + 15) / 16) {
-        case 1: return kfull ? kgm_launch_rg<1, true>(a, p, w, s) : kgm_launch_rg<1, false>(a, p, w, s);
-        case 2: return kfull ? kgm_launch_rg<2, true>(a, p, w, s) : kgm_launch_rg<2, false>(a, p, w, s);
-        case 3: return kfull ? kgm_launch_rg<3, true>(a, p, w, s) : kgm_launch_rg<3, false>(a, p, w, s);
-        default: return kfull ? kgm_launch_rg<4, true>(a, p, w, s) : kgm_launch_rg<4, false>(a, p, w, s);
-    }
+    if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
+    return a.K % 64 == 0 ? kgm_launch_mt<T_I8T, true>(a, p, w, s) : kgm_launch_mt<T_I8T, false>(a, p, w, s);
 }
 
 }  // namespace mbq

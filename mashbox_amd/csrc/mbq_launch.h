@@ -75,10 +75,10 @@ constexpr int64_t WS_MAX_M = 64;
 int launch_wsgemm(int t, const Args& a, int rows_per_block, int splits, hipStream_t s);
 int wsgemm_plan(int t, const Args& a, int* rows_per_block, int* splits);
 void wsgemm_effective(int t, const Args& a, int* rows_per_block, int* splits);   // what a launch with these runs
-// K-group GEMM (mbq_kgemm.hip) of tiled int8 planes for GEMV_MAX_M < M <= WS_MAX_M (and M <= 4 where the GEMV has no
-// plan): splits = 0 chooses the K splits, else that many; the plan's rows per block and splits
-int launch_kgemm(const Args& a, int splits, hipStream_t s);
-int kgemm_plan(const Args& a, int splits, int* rows_per_block, int* chosen_splits);
+// K-group GEMM (mbq_kgemm.hip) of tiled planes (t = T_I8T or T_Q4KT) for M <= WS_MAX_M: splits = 0 chooses the K
+// splits, else that many; the plan's rows per block and splits
+int launch_kgemm(int t, const Args& a, int splits, hipStream_t s);
+int kgemm_plan(int t, const Args& a, int splits, int* rows_per_block, int* chosen_splits);
 // GEMM kernels (the values of MBQ_KERNEL_* in mbq.h)
 enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2, K_KGROUP = 3 };
 int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits);

@@ -41,6 +41,14 @@
 //     s    f32 (NP)                the per-row scales
 //   padding rows and columns are zero (scale 0)
 //
+//   Q4_K in 16-row tiles (MBQ_Q4KT planes, repacked once at load from the same Q4_K blocks; internal type T_Q4KT)
+//     qs   (NP / 16, K / 128) blocks of 1 KiB: block (rt, kc) holds rows 16 rt .. 16 rt + 15, 64 bytes each (the
+//                                  four Q4_K units of values 128 kc .. 128 kc + 127, as in the row-major qs plane), so
+//                                  a wave's 16-row MFMA B tile of 128 values is one contiguous KiB
+//     meta (NP / 16, K / 256) blocks of 256 bytes: block (rt, sb) holds the 16-byte super-block headers (d, dmin,
+//                                  12 scale bytes, as stored) of super-block sb of rows 16 rt .. 16 rt + 15
+//   padding rows are zero (d = dmin = 0: value 0)
+//
 // Every plane starts 256-byte aligned and the whole is rounded up to 256 bytes, so a stack of weights is a plain array
 // of these records (mbq_plane_bytes apart). The byte count is the file's plus at most 256 bytes of zero padding per
 // plane.
@@ -50,8 +58,8 @@
 namespace mbq {
 
 // T_INT8: the caller's row-major int8 weights (mbq_int8_linear); T_I8T: int8 weights repacked into 16-row tiles
-// (mbq_matmul with MBQ_INT8 planes)
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9 };
+// (mbq_matmul with MBQ_I8T planes); T_Q4KT: Q4_K blocks repacked into 16-row tiles (MBQ_Q4KT planes)
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9, T_Q4KT = -12 };
 // int8 types: 16-byte units of 16 values, a per-row float32 scale applied to the sum
 constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
 // T_I8T: bytes between consecutive 16-row tiles of the quant plane, and the byte offset of (row, K offset k0) (k0 a
@@ -59,13 +67,24 @@ constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
 constexpr int64_t i8t_tile_bytes(int64_t k) { return (k + 63) / 64 * 1024; }
 constexpr int64_t i8t_off(int64_t row, int64_t k, int64_t k0) { return (row >> 4) * i8t_tile_bytes(k) + (k0 >> 6) * 1024 + (row & 15) * 64; }
 
+// T_Q4KT: bytes between consecutive 16-row tiles of the quant plane, the byte offset of (row, value 0) in it (a value
+// k of the row-major qs plane's byte b = k / 2 sits at + (b / 64) * 1024 + b % 64), and the offset of (row, super-block
+// 0) in the meta plane (super-block sb at + 256 sb)
+constexpr int64_t q4kt_tile_bytes(int64_t k) { return k / 128 * 1024; }
+constexpr int64_t q4kt_off(int64_t row, int64_t k) { return (row >> 4) * q4kt_tile_bytes(k) + (row & 15) * 64; }
+constexpr int64_t q4kt_meta_off(int64_t row, int64_t k) { return (row >> 4) * (k / 256) * 256 + (row & 15) * 16; }
+// tiled plane types (16-row tiles, any number of rows)
+constexpr bool tiled_type(int t) { return t == T_I8T || t == T_Q4KT; }
+// the Q4_K value format, in row-major or tiled planes
+constexpr bool q4k_like(int t) { return t == T_Q4_K || t == T_Q4KT; }
+
 // the K-quants: 256-value super-blocks, kernel units of 32 values (16 bytes of low nibbles)
-constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q4KT; }
 // types whose kernel unit is 16 bytes of nibbles for 32 values (the K-quants and Q4_0); Q8_0 and int8 units are 16
 // bytes for 16 values
 constexpr bool unit32(int t) { return kquant(t) || t == T_Q4_0; }
 // Q4_0 and Q4_K: a unit's 16 bytes are the whole 4-bit quants, in the Q4_K order
-constexpr bool nib4(int t) { return t == T_Q4_K || t == T_Q4_0; }
+constexpr bool nib4(int t) { return q4k_like(t) || t == T_Q4_0; }
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
@@ -75,9 +94,10 @@ struct Layout {
     int64_t qs_off, qs_bytes, hi_off, hi_bytes, sc_off, sc_bytes, d_off, d_bytes, total;
 };
 
+// values and file bytes of one block (T_Q4KT planes are made from Q4_K blocks)
 inline int block_values(int t) { return (t == T_Q8_0 || t == T_Q4_0) ? 32 : kquant(t) ? 256 : 0; }
 inline int block_bytes(int t) {
-    return t == T_Q4_0 ? 18 : t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
+    return t == T_Q4_0 ? 18 : t == T_Q8_0 ? 34 : q4k_like(t) ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
 }
 
 inline Layout layout(int t, int64_t n, int64_t k) {
@@ -99,6 +119,10 @@ inline Layout layout(int t, int64_t n, int64_t k) {
         const int64_t np = (n + 15) / 16 * 16;
         L.qs_bytes = np * ((k + 63) / 64 * 64);
         L.sc_bytes = np * 4;
+    } else if (t == T_Q4KT) {
+        const int64_t np = (n + 15) / 16 * 16;
+        L.qs_bytes = np * (k / 2);
+        L.sc_bytes = np * (k / 256) * 16;
     } else {  // T_Q6_K
         L.qs_bytes = n * (k / 2);
         L.hi_bytes = n * (k / 4);

@@ -26,13 +26,16 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import INT8, OUT_BF16, OUT_F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, check, lib
+from ._lib import INT8, OUT_BF16, OUT_F32, Q4_0, Q4_K, Q4KT, Q5_K, Q6_K, Q8_0, check, lib
 
 # the types the reference's kernel package gives planes (reference src/mashbox/ops/bundle.py:39)
 TYPES = frozenset({Q4_0, Q8_0, Q4_K, Q5_K, Q6_K})
-NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q4KT: "Q4_K tiled"}
 # values and bytes per block (reference ops/reference.py:22-29)
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+# ggml types whose blocks also repack into 16-row tiles (repack(..., tiled=True)), and the plane type they take: every
+# wave-wide weight load of a 16-row MFMA tile is one contiguous KiB (the layout for decode batches of several rows)
+TILED = {Q4_K: Q4KT}
 picks_layer = True
 version = "0.1.0"
 
@@ -112,11 +115,20 @@ def _check_raw(t: int, raw_shape, shape):
     return t, rows, cols, tuple(int(v) for v in raw_shape[:-2])
 
 
-def repack_host(t: int, raw, shape, threads: int = 0) -> Planes:
+def _plane_type(t: int, tiled: bool) -> int:
+    if not tiled:
+        return t
+    if t not in TILED:
+        raise NotImplementedError(f"{NAMES.get(t, t)} has no tiled planes (tiled: {[NAMES[v] for v in TILED]})")
+    return TILED[t]
+
+
+def repack_host(t: int, raw, shape, threads: int = 0, tiled: bool = False) -> Planes:
     """host blocks (..., rows, row_bytes) uint8 -> host planes, on the host's cores (C++ threads)
-    (reference src/mashbox/ops/__init__.py:22-23,473-474)"""
+    (reference src/mashbox/ops/__init__.py:22-23,473-474); tiled=True: the 16-row tiles of TILED[t]"""
     raw = np.ascontiguousarray(np.asarray(raw), dtype=np.uint8)
     t, rows, cols, lead = _check_raw(t, raw.shape, shape)
+    t = _plane_type(t, tiled)
     pb = plane_bytes(t, (rows, cols))
     count = int(np.prod(lead, dtype=np.int64)) if lead else 1
     out = torch.empty(count * pb, dtype=torch.uint8)
@@ -128,13 +140,15 @@ def repack_host(t: int, raw, shape, threads: int = 0) -> Planes:
     return Planes(out, t, rows, cols, lead)
 
 
-def repack(t: int, raw: torch.Tensor, shape, stacked: bool = False) -> Planes:
+def repack(t: int, raw: torch.Tensor, shape, stacked: bool = False, tiled: bool = False) -> Planes:
     """device blocks (..., rows, row_bytes) uint8 (a torch tensor on the GPU) -> device planes, by the GPU
-    (reference src/mashbox/ops/__init__.py:16,475-485). `stacked` is accepted for the surface; leading axes are a stack."""
+    (reference src/mashbox/ops/__init__.py:16,475-485). `stacked` is accepted for the surface; leading axes are a stack.
+    tiled=True: the 16-row tiles of TILED[t]."""
     if not raw.is_cuda:
-        return repack_host(t, raw.numpy(), shape).to(torch.device("cuda", torch.cuda.current_device()))
+        return repack_host(t, raw.numpy(), shape, tiled=tiled).to(torch.device("cuda", torch.cuda.current_device()))
     raw = raw.contiguous()
     t, rows, cols, lead = _check_raw(t, tuple(raw.shape), shape)
+    t = _plane_type(t, tiled)
     pb = plane_bytes(t, (rows, cols))
     count = int(np.prod(lead, dtype=np.int64)) if lead else 1
     out = torch.empty(count * pb, dtype=torch.uint8, device=raw.device)
@@ -225,5 +239,5 @@ def take_rows(p: Planes, ids, layer=None) -> torch.Tensor:
     return w.reshape(tuple(ids.shape) + (p.K,))
 
 
-__all__ = ["TYPES", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers", "picks_layer",
-           "row_bytes", "INT8"]
+__all__ = ["TYPES", "TILED", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers",
+           "picks_layer", "row_bytes", "INT8", "Q4KT"]

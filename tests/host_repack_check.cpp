@@ -1,10 +1,11 @@
 // Host repack round trips, built alone under AddressSanitizer + UndefinedBehaviorSanitizer (and ThreadSanitizer) by
 // tests/test_host_sanitizers.py: every buffer is allocated at its exact size, so a read or write one byte past a
-// plane or a row is reported. For each GGUF type and the tiled int8 planes, at shapes that run on one host thread and
-// on several:
+// plane or a row is reported. For each GGUF type, Q4_K in 16-row tiles and the tiled int8 planes, at shapes that run
+// on one host thread and on several:
 //   * repack into a buffer full of 0xAB, unpack, and compare with the input bytes;
 //   * the alignment padding between planes (and the int8 tiles' padding rows and columns) reads zero;
-//   * the planes are the same bytes on 1 thread and on 5.
+//   * the planes are the same bytes on 1 thread and on 5 (written into buffers of different filler bytes: so every
+//     byte is written, the tiles' padding rows included).
 #include <stdint.h>
 #include <stdio.h>
 
@@ -87,7 +88,7 @@ static void int8_case(int64_t rows, int64_t cols) {
 }
 
 int main() {
-    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K};
+    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_Q4KT};
     const int64_t shapes[][2] = {{1, 256}, {3, 512}, {63, 768}, {64, 256}, {130, 1024}, {517, 256}};
     for (int t : types)
         for (const auto& sh : shapes) gguf_case(t, sh[0], sh[1]);

@@ -213,3 +213,39 @@ def test_int8_tiled_repack_is_lossless(n, k):
     assert np.array_equal(sc[:n].view(np.uint32), s.view(np.uint32)) and not sc[n:].any()
     assert L.lib().mbq_covers(L.I8T, n, k) == 1 and L.lib().mbq_covers(L.I8T, n, k + 8) == 0
     assert L.lib().mbq_dequant(L.I8T, None, 0, None, 1, n, k, None, None) < 0
+
+
+@pytest.mark.parametrize("n,kb", [(1, 1), (17, 2), (130, 3)])
+def test_q4_k_tiled_repack_is_lossless(n, kb):
+    """Q4_K blocks into 16-row tiles (MBQ_Q4KT) and back, exactly. The tiles hold the row-major planes' bytes: quant
+    block (rt, kc) row r = the 64 bytes at 64 kc of row 16 rt + r's qs plane, header block (rt, sb) row r = that row's
+    header sb; the rows of the last tile past n are zero; plane bytes = the two planes over 16-row-rounded rows, each
+    256-aligned"""
+    k = 256 * kb
+    rng = np.random.default_rng([n, kb, 12])
+    raw = rng.integers(0, 256, (n, R.row_bytes(R.Q4_K, k)), dtype=np.uint8)
+    p = KQ.repack_host(R.Q4_K, raw, (n, k), threads=3, tiled=True)
+    rm = KQ.repack_host(R.Q4_K, raw, (n, k))
+    assert p.t == L.Q4KT and rm.t == R.Q4_K
+    np16 = (n + 15) // 16 * 16
+    a256 = lambda v: (v + 255) // 256 * 256
+    assert p.stride == a256(a256(np16 * k // 2) + np16 * (k // 256) * 16)
+    buf, rmb = p.buf.numpy(), rm.buf.numpy()
+    full = np.zeros((np16, k // 2), np.uint8)
+    full[:n] = rmb[:n * k // 2].reshape(n, k // 2)
+    tiles = buf[:np16 * k // 2].reshape(np16 // 16, k // 128, 16, 64)
+    assert np.array_equal(tiles.transpose(0, 2, 1, 3).reshape(np16, k // 2), full)
+    mfull = np.zeros((np16, k // 256, 16), np.uint8)
+    mfull[:n] = rmb[a256(n * k // 2):a256(n * k // 2) + n * (k // 256) * 16].reshape(n, k // 256, 16)
+    mo = a256(np16 * k // 2)
+    heads = buf[mo:mo + np16 * (k // 256) * 16].reshape(np16 // 16, k // 256, 16, 16)
+    assert np.array_equal(heads.transpose(0, 2, 1, 3).reshape(np16, k // 256, 16), mfull)
+    back = np.zeros_like(raw)
+    assert L.lib().mbq_unpack_host(L.Q4KT, ctypes.c_void_p(p.buf.data_ptr()), n, k, back.ctypes.data_as(ctypes.c_void_p),
+                                   back.size) == 0
+    assert np.array_equal(back, raw)
+    assert L.lib().mbq_covers(L.Q4KT, n, k) == 1 and L.lib().mbq_covers(L.Q4KT, n, k + 32) == 0
+    assert L.lib().mbq_has_type(L.Q4KT) == 0 and L.lib().mbq_row_bytes(L.Q4KT, k) < 0     # not a ggml type
+    assert L.lib().mbq_dequant_raw(L.Q4KT, None, n, k, None, None) < 0                    # its blocks are Q4_K's
+    with pytest.raises(NotImplementedError):
+        KQ.repack_host(R.Q8_0, np.zeros((1, 34), np.uint8), (1, 32), tiled=True)
