@@ -243,7 +243,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                 bf16x8_t B;
                 if constexpr (QK) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m rounded to bfloat16 (the LDS GEMM's operand)
-                    B = ws_bop<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], H[U][j]}, qs[j], s);
+                    B = q4k_dword_bop(W[U][j][s], qs[j]);
                 } else {
                     const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
                     const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};

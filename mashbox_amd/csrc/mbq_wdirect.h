@@ -156,6 +156,20 @@ __device__ __forceinline__ uint32_t ws_bpair(const WsRaw<T>& w, const WsScale& s
     }
 }
 
+// The 8 values of one Q4_K unit dword (quant 2p in bits 4p..4p+3, quant 2p+1 in bits 16+4p..: mbq_layout.h) as the
+// bfloat16 B operand (d sc) q - dmin m, the values of ws_bop<T_Q4_K> bit for bit with two masks per dword instead of
+// four: v & 0x0F0F0F0F leaves bytes (q0, q4, q1, q5), v & 0xF0F0F0F0 bytes (16 q2, 16 q6, 16 q3, 16 q7), which take
+// the scale d sc / 16
+__device__ __forceinline__ bf16x8_t q4k_dword_bop(uint32_t v, const WsScale& sc) {
+    const uint32_t lo = opaque(v & 0x0F0F0F0Fu), hi = opaque(v & 0xF0F0F0F0u);
+    auto f = [](uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); };
+    const u32x4 o{pack_bf16(__builtin_fmaf(f(lo, 0), sc.a, -sc.b), __builtin_fmaf(f(lo, 2), sc.a, -sc.b)),
+                  pack_bf16(__builtin_fmaf(f(hi, 0), sc.c, -sc.b), __builtin_fmaf(f(hi, 2), sc.c, -sc.b)),
+                  pack_bf16(__builtin_fmaf(f(lo, 1), sc.a, -sc.b), __builtin_fmaf(f(lo, 3), sc.a, -sc.b)),
+                  pack_bf16(__builtin_fmaf(f(hi, 1), sc.c, -sc.b), __builtin_fmaf(f(hi, 3), sc.c, -sc.b))};
+    return __builtin_bit_cast(bf16x8_t, o);
+}
+
 // B operand of K step s: the 8 values of the lane's row, as bfloat16
 template <int T>
 __device__ __forceinline__ bf16x8_t ws_bop(const WsRaw<T>& w, const WsScale& sc, int s) {

@@ -28,6 +28,10 @@ warning. The exact path stays on the GPU: the file's blocks are rebuilt to float
 the reference dequantization), exact_chunk_rows rows at a time, and multiplied by a float32 GEMM. Nothing here computes
 on the host's CPU; without libmbq.so every call raises. The forced-failure switch is the reference's MASHBOX_FAULT
 (force:kernels-package, force:quant-kernel; reference src/mashbox/runtime/faults.py:14-16,57-61).
+
+Layout switch of this build (no counterpart in the reference): with env MBQ_TILES=1, weights of the types the kernel
+package can tile (its TILED map: Q4_K) load as 16-row tiles instead of row-major planes, the faster layout for decode
+batches of several rows; everything else is unchanged.
 """
 from __future__ import annotations
 
@@ -248,7 +252,8 @@ def device_nbytes(t: int, shape, nbytes: int, kernel_types=None) -> int:
     if size is None or weight_path(t, shape, kernel_types) != "kq":
         return int(nbytes)
     shape = tuple(int(v) for v in shape)
-    return int(np.prod(shape[:-2], dtype=np.int64)) * int(size(int(t), shape[-2:]))
+    pt = _KERNELS.module.TILED[int(t)] if _tiled(t) else int(t)
+    return int(np.prod(shape[:-2], dtype=np.int64)) * int(size(pt, shape[-2:]))
 
 
 # ---------------------------------------------------------------------------------------------------------- prepare
@@ -260,15 +265,22 @@ def _as_tensor(raw) -> torch.Tensor:
     return raw if isinstance(raw, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(raw, np.uint8)))
 
 
+def _tiled(t: int) -> bool:
+    """weights of type t load as the kernel package's 16-row tiles (env MBQ_TILES=1 and a type it can tile)"""
+    return os.environ.get("MBQ_TILES", "") == "1" and int(t) in getattr(_KERNELS.module, "TILED", {})
+
+
 def _planes_of(raw, t: int, shape):
-    """the kernel package's planes on the device: its host repack for host blocks when it has one, else its repack"""
+    """the kernel package's planes on the device: its host repack for host blocks when it has one, else its repack
+    (16-row tiles when _tiled(t))"""
     mod = _KERNELS.module
     if forced("quant-kernel"):
         raise RuntimeError("forced by MASHBOX_FAULT=force:quant-kernel")
+    kw = {"tiled": True} if _tiled(t) else {}
     if not isinstance(raw, torch.Tensor) and hasattr(mod, "repack_host"):
-        return mod.repack_host(t, np.asarray(raw), tuple(shape)).to(_device())
+        return mod.repack_host(t, np.asarray(raw), tuple(shape), **kw).to(_device())
     r = _as_tensor(raw).to(_device())
-    return mod.repack(t, r, tuple(shape), stacked=r.dim() > 2)
+    return mod.repack(t, r, tuple(shape), stacked=r.dim() > 2, **kw)
 
 
 def _preflight(planes, rows_cols, lead: int) -> None:

@@ -208,3 +208,27 @@ def test_kgroup_graph_replays(forced_plan, cuda):
         assert np.array_equal(y.cpu().numpy().view(np.uint32), eager.view(np.uint32))
         KQ.matmul(x2, p)
         torch.cuda.synchronize()
+
+
+def test_ops_prepare_loads_tiles(monkeypatch, cuda):
+    """with MBQ_TILES=1 the ops layer loads Q4_K weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
+    layer= in place and dequant against the oracle; device_nbytes counts the tiled planes"""
+    from mashbox_amd import ops
+    monkeypatch.setenv("MBQ_TILES", "1")
+    ops.load_kernels()
+    rng = np.random.default_rng(129)
+    n, k, L = 100, 512, 2
+    st = np.stack([G.q4_k_raw(rng, n, k) for _ in range(L)])
+    h = ops.prepare(st[0], R.Q4_K, (n, k))
+    hs = ops.prepare(st, R.Q4_K, (n, k))
+    assert isinstance(h, ops.Packed) and h.packed.t == LIB.Q4KT and hs.packed.t == LIB.Q4KT
+    assert ops.device_nbytes(R.Q4_K, (L, n, k), st.nbytes) == L * KQ.plane_bytes(LIB.Q4KT, (n, k))
+    w = [R.dequant(st[i], R.Q4_K, k) for i in range(L)]
+    assert diff_bits(ops.dequant(h).cpu().numpy(), w[0]) == 0
+    for m in (1, 4, 300):
+        xb, x = _x(rng, m, k, cuda)
+        xf = R.bf16_to_f32(xb).astype(np.float64)
+        assert_product(ops.qmatmul(x.float(), h).float().cpu().numpy(), xf @ w[0].astype(np.float64).T, f"prepare m={m}")
+        for i in range(L):
+            y = ops.qmatmul(x.float(), ops.At(hs.packed, i, R.Q4_K, (n, k))).float().cpu().numpy()
+            assert_product(y, xf @ w[i].astype(np.float64).T, f"prepare stack layer {i} m={m}")
