@@ -177,14 +177,15 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((hi >> 8) & 0xFFu), s.a, -s.b));
         o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(hi >> 24), s.a, -s.b));
     } else if constexpr (nib4(T)) {
-        // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h)
+        // dword t: quant 8t+2p in bits 4p..4p+3, quant 8t+2p+1 in bits 16+4p.. (mbq_layout.h); two masks leave bytes
+        // (q0, q4, q1, q5) and (16 q2, 16 q6, 16 q3, 16 q7), the latter taking the scale / 16
         const uint32_t w = sel4(b.q, t);
-        const uint32_t m0 = opaque(w & 0x000F000Fu), m1 = opaque(w & 0x00F000F0u);
-        const uint32_t m2 = opaque(w & 0x0F000F00u), m3 = opaque(w & 0xF000F000u);
-        o[0] = pack_bf16(__builtin_fmaf((float)(m0 & 0xFFu), s.a, -s.b), __builtin_fmaf((float)((m0 >> 16) & 0xFFu), s.a, -s.b));
-        o[1] = pack_bf16(__builtin_fmaf((float)(m1 & 0xFFu), s.c, -s.b), __builtin_fmaf((float)((m1 >> 16) & 0xFFu), s.c, -s.b));
-        o[2] = pack_bf16(__builtin_fmaf((float)((m2 >> 8) & 0xFFu), s.a, -s.b), __builtin_fmaf((float)(m2 >> 24), s.a, -s.b));
-        o[3] = pack_bf16(__builtin_fmaf((float)((m3 >> 8) & 0xFFu), s.c, -s.b), __builtin_fmaf((float)(m3 >> 24), s.c, -s.b));
+        const uint32_t lo = opaque(w & 0x0F0F0F0Fu), hi = opaque(w & 0xF0F0F0F0u);
+        auto f = [](uint32_t v, int by) { return (float)((v >> (8 * by)) & 0xFFu); };
+        o[0] = pack_bf16(__builtin_fmaf(f(lo, 0), s.a, -s.b), __builtin_fmaf(f(lo, 2), s.a, -s.b));
+        o[1] = pack_bf16(__builtin_fmaf(f(hi, 0), s.c, -s.b), __builtin_fmaf(f(hi, 2), s.c, -s.b));
+        o[2] = pack_bf16(__builtin_fmaf(f(lo, 1), s.a, -s.b), __builtin_fmaf(f(lo, 3), s.a, -s.b));
+        o[3] = pack_bf16(__builtin_fmaf(f(hi, 1), s.c, -s.b), __builtin_fmaf(f(hi, 3), s.c, -s.b));
     } else {
         // dwords 2t, 2t+1 of the unit's 8 (q0: 0..3, q1: 4..7)
         const uint32_t w0 = (t & 2) ? ((t & 1) ? b.q1[2] : b.q1[0]) : ((t & 1) ? b.q0[2] : b.q0[0]);
