@@ -313,7 +313,7 @@ def pmc_probe(configs=(1, 2, 3, 4, 5), launches=4, copy_mib=1024, rotate_mb=1024
     from mashbox_amd._lib import check
 
     for idx in configs:
-        _, _, projs = synth.CONFIGS[idx]
+        _, _, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
         for pi in range(len(projs)):
             launch, copies, _, _, _ = setup_projection(idx, pi, rotate_mb << 20)
             for i in range(launches):
@@ -485,7 +485,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     if a.pmc_probe:
-        return pmc_probe(tuple(int(c) for c in a.pmc_probe.split(",") if c), rotate_mb=a.rotate_mb)
+        return pmc_probe(tuple(int(c) if c.isdigit() else c for c in a.pmc_probe.split(",") if c), rotate_mb=a.rotate_mb)
     configs = [int(c) if c.isdigit() else c for c in a.configs.split(",") if c]
     if HEADLINE not in configs:
         configs.insert(0, HEADLINE)
