@@ -49,11 +49,12 @@ template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4KT> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4_0> { u32x4 q; uint32_t d; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
+template <> struct BUnit<T_Q8T> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
 template <> struct BUnit<T_I8T> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct BUnit<T_Q5_K> { u32x4 q, meta; uint32_t h; };
-template <int T> constexpr int b_loads() { return T == T_Q6_K ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
+template <int T> constexpr int b_loads() { return T == T_Q8T ? 5 : T == T_Q6_K ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
 
 // per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h: Q5_K, Q6_K; d: Q6_K
 struct BOff { uint32_t q, s, h, d; };
@@ -69,6 +70,7 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     else if constexpr (T == T_Q4KT) return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q4kt_meta_off(bn, K)), 0, 0};
     else if constexpr (T == T_Q4_0) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
     else if constexpr (T == T_I8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 32 * u), 0, 0, 0};   // 16-row tiles
+    else if constexpr (T == T_Q8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 8 * u), (uint32_t)(sc_off + q8t_d_off(bn, K) + 2 * u), 0, 0};
     else return BOff{(uint32_t)(bn * K + 32 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
 }
 
@@ -94,11 +96,21 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
         if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
     } else {
-        const uint32_t qk = T == T_I8T ? (uint32_t)k0 * 16u : (uint32_t)k0;     // T_I8T: a KiB per 64 values
-        b.q0 = bload16(r, o.q, qk);
-        b.q1 = bload16(r, o.q + 16, qk);
-        if constexpr (T == T_Q8_0) {
-            b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
+        const uint32_t qk = (T == T_I8T || T == T_Q8T) ? (uint32_t)k0 * 16u : (uint32_t)k0;   // tiles: a KiB per 64 values
+        if constexpr (T == T_Q8T) {
+            // the block's quants 8g .. 8g + 7 sit 16 g bytes apart (its other 8 bytes of each group: the other block)
+            u32x2 p[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                p[g] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.q + 16u * g, qk, 0));
+            b.q0 = u32x4{p[0][0], p[0][1], p[1][0], p[1][1]};
+            b.q1 = u32x4{p[2][0], p[2][1], p[3][0], p[3][1]};
+        } else {
+            b.q0 = bload16(r, o.q, qk);
+            b.q1 = bload16(r, o.q + 16, qk);
+        }
+        if constexpr (q8_like(T)) {
+            b.d = bload2(r, o.s, T == T_Q8T ? ((uint32_t)k0 >> 6) * 64u : ((uint32_t)k0 >> 5) * 2);
             if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
         }
     }
@@ -142,7 +154,7 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.a = f16f(b.d);
         s.b = 8.f * s.a;                                     // q d - 8 d = (q - 8) d, exact in float32
         s.c = s.a * 0.0625f;
-    } else if constexpr (T == T_Q8_0) {
+    } else if constexpr (q8_like(T)) {
         s.a = f16f(b.d);
         s.b = 128.f * s.a;
     }
@@ -191,8 +203,8 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         const uint32_t w0 = (t & 2) ? ((t & 1) ? b.q1[2] : b.q1[0]) : ((t & 1) ? b.q0[2] : b.q0[0]);
         const uint32_t w1 = (t & 2) ? ((t & 1) ? b.q1[3] : b.q1[1]) : ((t & 1) ? b.q0[3] : b.q0[1]);
         uint32_t r[4];
-        i8x4<T == T_Q8_0>(w0, s.a, s.b, &r[0]);
-        i8x4<T == T_Q8_0>(w1, s.a, s.b, &r[2]);
+        i8x4<q8_like(T)>(w0, s.a, s.b, &r[0]);
+        i8x4<q8_like(T)>(w1, s.a, s.b, &r[2]);
         o = u32x4{r[0], r[1], r[2], r[3]};
     }
     return o;
@@ -987,9 +999,9 @@ static int choose(int t, const Args& a, Choice* c) {
         return 0;
     }
     if (fk == K_KGROUP && a.M <= WS_MAX_M)
-        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q4KT) only");
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT) only");
     if (fk == K_STREAM) {
-        if (t == T_Q4KT) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled Q4_K planes");
+        if (t == T_Q4KT || t == T_Q8T) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
@@ -1062,6 +1074,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_INT8: rc = pick<T_INT8>(a, &p); if (!rc) *bm = CANDS<T_INT8>[p.idx].bm, *bn = CANDS<T_INT8>[p.idx].bn; break;
         case T_I8T: rc = pick<T_I8T>(a, &p); if (!rc) *bm = CANDS<T_I8T>[p.idx].bm, *bn = CANDS<T_I8T>[p.idx].bn; break;
         case T_Q4KT: rc = pick<T_Q4KT>(a, &p); if (!rc) *bm = CANDS<T_Q4KT>[p.idx].bm, *bn = CANDS<T_Q4KT>[p.idx].bn; break;
+        case T_Q8T: rc = pick<T_Q8T>(a, &p); if (!rc) *bm = CANDS<T_Q8T>[p.idx].bm, *bn = CANDS<T_Q8T>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -1101,6 +1114,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_INT8: return launch_gemm_t<T_INT8>(a, s);
         case T_I8T: return launch_gemm_t<T_I8T>(a, s);
         case T_Q4KT: return launch_gemm_t<T_Q4KT>(a, s);
+        case T_Q8T: return launch_gemm_t<T_Q8T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

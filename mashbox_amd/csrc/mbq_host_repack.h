@@ -1,4 +1,4 @@
-// Host repack of one weight into kernel planes (Q4_K also into 16-row tiles, T_Q4KT), and its inverse (no HIP: also
+// Host repack of one weight into kernel planes (Q4_K and Q8_0 also into 16-row tiles, T_Q4KT and T_Q8T), and its inverse (no HIP: also
 // built alone, under the host sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
 // src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
 // int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
@@ -53,6 +53,15 @@ inline int64_t q4k_meta_at(int t, int64_t n, int64_t K, int64_t sb) {
     return t == T_Q4KT ? q4kt_meta_off(n, K) + sb * 256 : (n * (K / 256) + sb) * 16;
 }
 
+// Q8_0 planes (row-major, or T_Q8T tiles): offset of block b of row n's first quant in the qs plane (T_Q8T: quants
+// 8g .. 8g + 7 of the block at + 16 g) and of its fp16 scale in the d plane
+inline int64_t q8_qs_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q8T ? i8t_off(n, K, (32 * b) & ~int64_t(63)) + q8t_byte((int)((32 * b) % 64)) : n * K + 32 * b;
+}
+inline int64_t q8_d_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q8T ? q8t_d_off(n, K) + (b / 2) * 64 + (b % 2) * 2 : (n * (K / 32) + b) * 2;
+}
+
 inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
@@ -104,12 +113,12 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                     }
                 }
             }
-        } else if (t == T_Q8_0) {
-            uint8_t* q = planes + L.qs_off + n * K;
-            uint8_t* d = planes + L.sc_off + n * nb * 2;
+        } else if (q8_like(t)) {
+            // Q8_0, row-major or in 16-row tiles (T_Q8T: a block's 32 quants in four 8-byte groups 16 bytes apart)
             for (int64_t b = 0; b < nb; ++b) {
-                memcpy(d + b * 2, row + b * bb, 2);
-                memcpy(q + b * 32, row + b * bb + 2, 32);
+                memcpy(planes + L.sc_off + q8_d_at(t, n, K, b), row + b * bb, 2);
+                for (int g = 0; g < (t == T_Q8T ? 4 : 1); ++g)
+                    memcpy(planes + L.qs_off + q8_qs_at(t, n, K, b) + 16 * g, row + b * bb + 2 + 8 * g, t == T_Q8T ? 8 : 32);
             }
         } else if (t == T_Q4_0) {
             // reference src/mashbox/ops/reference.py:66-70: value i (i < 16) is the low nibble of qs[i], value 16 + i
@@ -205,12 +214,11 @@ inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
                     }
                 }
             }
-        } else if (t == T_Q8_0) {
-            const uint8_t* q = planes + L.qs_off + n * K;
-            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+        } else if (q8_like(t)) {
             for (int64_t b = 0; b < nb; ++b) {
-                memcpy(row + b * bb, d + b * 2, 2);
-                memcpy(row + b * bb + 2, q + b * 32, 32);
+                memcpy(row + b * bb, planes + L.sc_off + q8_d_at(t, n, K, b), 2);
+                for (int g = 0; g < (t == T_Q8T ? 4 : 1); ++g)
+                    memcpy(row + b * bb + 2 + 8 * g, planes + L.qs_off + q8_qs_at(t, n, K, b) + 16 * g, t == T_Q8T ? 8 : 32);
             }
         } else if (t == T_Q4_0) {
             const uint8_t* q = planes + L.qs_off + n * (K / 2);
@@ -297,6 +305,7 @@ inline void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t
 // hardware thread). The caller checks the shape and the buffer sizes.
 inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
     const Layout L = layout(t, rows, cols);
+    if (t == T_Q8T) memset(planes, 0, (size_t)L.total);   // padding rows, the half-chunk past K, the gaps
     for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
     if (t == T_Q4KT) q4kt_zero_pad_rows(rows, cols, planes, L);

@@ -123,8 +123,17 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
     } else {
-        const u32x4 q = ld16(base + n * K + u * 16);
-        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + (n * (K >> 5) + (u >> 1)) * 2));
+        // Q8_0 (T_Q8T: unit u's two 8-byte groups at their tile offsets; the scale of block u / 2 in the tiled d plane)
+        u32x4 q;
+        if constexpr (T == T_Q8T) {
+            const uint8_t* c = base + i8t_off(n, K, (u >> 2) * 64) + q8t_byte((int)(u & 3) * 16);
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(c), hi = *reinterpret_cast<const u32x2*>(c + 16);
+            q = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+            q = ld16(base + n * K + u * 16);
+        }
+        const float d = f16f(*reinterpret_cast<const uint16_t*>(
+            base + sc_off + (T == T_Q8T ? q8t_d_off(n, K) + (u >> 2) * 64 + ((u >> 1) & 1) * 2 : (n * (K >> 5) + (u >> 1)) * 2)));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             float v[4];
@@ -236,15 +245,24 @@ int launch_zero(uint8_t* p, int64_t n, hipStream_t s) {
 template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    const int bv = (T == T_Q8_0 || T == T_Q4_0) ? 32 : 256;
-    const int bb = (T == T_Q4_0) ? 18 : (T == T_Q8_0) ? 34 : q4k_like(T) ? 144 : (T == T_Q5_K) ? 176 : 210;
+    const int bv = (q8_like(T) || T == T_Q4_0) ? 32 : 256;
+    const int bb = (T == T_Q4_0) ? 18 : q8_like(T) ? 34 : q4k_like(T) ? 144 : (T == T_Q5_K) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t rows = T == T_Q4KT ? ((int64_t)N + 15) / 16 * 16 : N;     // T_Q4KT: the last tile's padding rows too
-    if (g >= rows * nb) return;
-    const int64_t n = g / nb, b = g % nb;
-    const uint8_t* src = raw + (n < N ? n : 0) * nb * bb + b * bb;
-    if constexpr (T == T_Q8_0) {
+    // tiles: the last tile's padding rows too, and for T_Q8T the padding half-chunk past K (written zero)
+    const int64_t rows = tiled_type(T) ? ((int64_t)N + 15) / 16 * 16 : N;
+    const int64_t nbr = T == T_Q8T ? ((int64_t)K + 63) / 64 * 2 : nb;
+    if (g >= rows * nbr) return;
+    const int64_t n = g / nbr, b = g % nbr;
+    const bool live = n < N && b < nb;
+    const uint8_t* src = raw + (live ? n * nb * bb + b * bb : 0);
+    if constexpr (T == T_Q8T) {
+        uint8_t* q = planes + i8t_off(n, K, (32 * b) & ~int64_t(63));
+        for (int i = 0; i < 32; ++i) q[q8t_byte(32 * (int)(b & 1) + i)] = live ? src[2 + i] : 0;
+        uint8_t* d = planes + sc_off + q8t_d_off(n, K) + (b / 2) * 64 + (b % 2) * 2;
+        d[0] = live ? src[0] : 0;
+        d[1] = live ? src[1] : 0;
+    } else if constexpr (T == T_Q8_0) {
         uint8_t* q = planes + n * K + b * 32;
         for (int i = 0; i < 32; ++i) q[i] = src[2 + i];
         uint8_t* d = planes + sc_off + (n * nb + b) * 2;
@@ -306,8 +324,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         }
     } else if constexpr (T == T_Q4KT) {
         // the Q4_K units and header of row n at their tile offsets (mbq_layout.h); the rows of the last tile past the
-        // weight's own (n >= N, when the grid covers them) are written zero
-        const bool live = n < N;
+        // weight's own (n >= N) are written zero
         uint8_t* meta = planes + sc_off + q4kt_meta_off(n, K) + b * 256;
         for (int i = 0; i < 16; ++i) meta[i] = live ? src[i] : 0;
         const uint8_t* qs = src + 16;
@@ -461,6 +478,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_INT8: return launch_t<T_INT8>(a, s);
         case T_I8T: return launch_t<T_I8T>(a, s);
         case T_Q4KT: return launch_t<T_Q4KT>(a, s);
+        case T_Q8T: return launch_t<T_Q8T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
@@ -477,6 +495,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
     if (t == T_Q4_0) run(dequant_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
     else if (t == T_Q4KT) run(dequant_kernel<T_Q4KT>);
+    else if (t == T_Q8T) run(dequant_kernel<T_Q8T>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -484,12 +503,14 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
 }
 
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
-    const int64_t blocks = (t == T_Q4KT ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
+    const int64_t blocks = t == T_Q8T ? (N + 15) / 16 * 16 * ((K + 63) / 64 * 2)
+                                      : (t == T_Q4KT ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
     if (t == T_Q4_0) run(repack_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
     else if (t == T_Q4KT) run(repack_kernel<T_Q4KT>);
+    else if (t == T_Q8T) run(repack_kernel<T_Q8T>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

@@ -101,7 +101,8 @@ template <int T, int MT, int RG, int NTW, bool KFULL>
 __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
     __shared__ int kgm_last;
-    constexpr bool QK = T == T_Q4KT;                     // Q4_K tiles (else int8 tiles)
+    constexpr bool QK = T == T_Q4KT;                     // Q4_K tiles
+    constexpr bool Q8 = T == T_Q8T;                      // Q8_0 tiles (else int8 tiles)
     constexpr int CW = kgm_cw(T);                        // K values per chunk
     constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
     constexpr int PCS = XB / 16;                         // its 16-byte pieces
@@ -112,7 +113,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     constexpr int NX = STAGE / 1024 / RG;                // x DMA instructions per wave per chunk (1 KiB each)
     static_assert(NX * RG * 1024 == STAGE, "the RG waves of a K group issue whole DMA instructions");
     static_assert(kgm_ring(T, MT, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
-    constexpr int NWL = QK ? 2 * NTW : NTW;              // weight loads per chunk (Q4_K: quants and headers)
+    constexpr int NWL = QK || Q8 ? 2 * NTW : NTW;        // weight loads per chunk (Q4_K: quants and headers; Q8_0:
+                                                         // quants and the two block scales)
     constexpr int VMT = (D - 1) * NWL + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
     static_assert(VMT < 64, "vmcnt range");
     const int M = g.M, N = g.N, K = g.K;
@@ -149,17 +151,17 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         const int row = 16 * (t0 + j) + r16;
         const bool in = row >= rq0 && row < rq1;
         wo[j] = in ? (uint32_t)(QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
-        mo[j] = in && QK ? (uint32_t)(g.sc_off + q4kt_meta_off(row, K)) : OOB_VOFF;
+        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K))) : OOB_VOFF;
     }
     // int8: the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their
-    // latency hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads). Q4_K values
-    // carry their scales: 1.
+    // latency hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads). Q4_K and
+    // Q8_0 apply their block scales in the loop: 1.
     float sc[(MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>()];
 #pragma unroll
     for (int u = 0; u < (MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>(); ++u) {
         const int tt = kg + kgm_kg<RG>() * u, j = tt % NTW, n = 16 * (t0 + j) + r16;
         const bool live = ok && tt < MT * NTW && n >= rq0 && n < rq1;
-        if constexpr (QK)
+        if constexpr (QK || Q8)
             sc[u] = 1.f;
         else
             sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, live ? (uint32_t)(g.sc_off + 4 * (int64_t)n) : OOB_VOFF, 0, 0));
@@ -187,7 +189,9 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                      live ? (uint32_t)c * (uint32_t)XB : 0u);
         }
     };
-    // the chunk's weights: a KiB per tile (non-temporal), and for Q4_K the 16-byte header of the super-block (chunk / 2)
+    // the chunk's weights: a KiB per tile (non-temporal), and for Q4_K the 16-byte header of the super-block (chunk / 2).
+    // Q8_0: the lane's 16 bytes are its 8 quants of each of the chunk's two blocks (K step s = block s: values
+    // 32 s + 8 lg ..), then the row's two block scales
     auto load_w = [&](u32x4* W, u32x4* H, int l) __attribute__((always_inline)) {
         const int c = chunk_of(l);
         const bool live = l < mine;
@@ -195,14 +199,17 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         for (int j = 0; j < NTW; ++j) {
             W[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? wo[j] : OOB_VOFF,
                                                                                   live ? (uint32_t)c * 1024u : 0u, 2));
+            if constexpr (Q8)
+                H[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 64u : 0u, 0);
             if constexpr (QK)
                 H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
                                                                                       live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
         }
     };
-    // A operand: x row 16 i + (lane & 15), piece NS (lane >> 4) + s of stage st (the K values the lane's weights hold)
+    // A operand: x row 16 i + (lane & 15), piece NS (lane >> 4) + s of stage st (Q8_0: 4 s + (lane >> 4)), the K values
+    // the lane's weights hold
     auto a_op = [&](int st, int i, int s) __attribute__((always_inline)) {
-        const int r = 16 * i + r16, p = (NS * lg + s) ^ kgm_swz<PCS>(r);
+        const int r = 16 * i + r16, p = (Q8 ? 4 * s + lg : NS * lg + s) ^ kgm_swz<PCS>(r);
         return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * XB + (p << 4));
     };
 
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
         for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     u32x4 W[D][NTW];
-    u32x4 H[QK ? D : 1][NTW];                                             // Q4_K: the tiles' super-block headers
+    u32x4 H[QK || Q8 ? D : 1][NTW];                                       // Q4_K: super-block headers; Q8_0: scales
 
     // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
     // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
@@ -238,6 +245,29 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
             bf16x8_t A[MT];
 #pragma unroll
             for (int i = 0; i < MT; ++i) A[i] = a_op(U, i, s);
+            if constexpr (Q8 && MT <= 2) {
+                // Q8_0, one or two x row tiles: every MFMA of the step first (their block products in P), then the
+                // scale FMAs, so no FMA waits on the MFMA just issued
+                f32x4_t P[MT][NTW];
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
+                    const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
+                    const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+                        P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    const float ds = f16f(s == 0 ? H[U][j][0] : H[U][j][0] >> 16);
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(P[i][j][r], ds, acc[i][j][r]);
+                }
+                continue;
+            }
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
                 bf16x8_t B;
@@ -249,19 +279,30 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                     const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
                     B = __builtin_bit_cast(bf16x8_t, o);
                 }
+                if constexpr (Q8) {
+                    // K step s is block s of the chunk: its exact int8 product, then times the row's block scale
+                    const float ds = f16f(s == 0 ? H[U][j][0] : H[U][j][0] >> 16);
 #pragma unroll
-                for (int i = 0; i < MT; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < MT; ++i) {
+                        const f32x4_t p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(p[r], ds, acc[i][j][r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_w(W[U], H[QK ? U : 0], l + D);
+        load_w(W[U], H[QK || Q8 ? U : 0], l + D);
     };
 
     if (steps > 0) {                                                      // block-uniform
 #pragma unroll
         for (int p = 0; p < D; ++p) {
             if (p < D - 1) dma_x(p, p);
-            load_w(W[p], H[QK ? p : 0], p);
+            load_w(W[p], H[QK || Q8 ? p : 0], p);
         }
         int l = 0;
         for (; l + D <= steps; l += D)
@@ -418,7 +459,7 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
     const int MT = (int)((M + 15) / 16);
-    const double wpc = t == T_Q4KT ? 72.0 : 64.0, waste_w = t == T_Q4KT ? 1.5 : 0.5;
+    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q8T ? 68.0 : 64.0, waste_w = t == T_Q4KT ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
     KgmPlan best{0, 0, 0, 0};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
@@ -519,7 +560,7 @@ int kgemm_plan(int t, const Args& a, int force_s, int* rows_per_block, int* spli
 }
 
 int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
-    if (t != T_I8T && t != T_Q4KT) return set_error(MBQ_BAD_ARG, "K-group GEMM: type %d is not a tiled plane type", t);
+    if (!tiled_type(t)) return set_error(MBQ_BAD_ARG, "K-group GEMM: type %d is not a tiled plane type", t);
     if (a.M < 1 || a.M > 64) return set_error(MBQ_BAD_ARG, "K-group GEMM: M = %lld", (long long)a.M);
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES || a.M * a.N * 4 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "K-group GEMM operands over 2 GiB");
@@ -533,6 +574,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
         if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.M, a.N, p), s, &w)) return rc;
     }
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
+    if (t == T_Q8T) return a.K % 64 == 0 ? kgm_launch_mt<T_Q8T, true>(a, p, w, s) : kgm_launch_mt<T_Q8T, false>(a, p, w, s);
     return a.K % 64 == 0 ? kgm_launch_mt<T_I8T, true>(a, p, w, s) : kgm_launch_mt<T_I8T, false>(a, p, w, s);
 }
 

@@ -49,6 +49,14 @@
 //                                  12 scale bytes, as stored) of super-block sb of rows 16 rt .. 16 rt + 15
 //   padding rows are zero (d = dmin = 0: value 0)
 //
+//   Q8_0 in 16-row tiles (MBQ_Q8T planes, repacked once at load from the same Q8_0 blocks; internal type T_Q8T)
+//     qs   (NP / 16, KP / 64) blocks of 1 KiB (KP = K rounded up to 64): row r of block (rt, kc) holds the int8
+//                                  quants of values 64 kc .. 64 kc + 63 of row 16 rt + r, 16-byte group g = values
+//                                  8g .. 8g + 7 of the chunk's first 32-value block, then the same of its second, so
+//                                  that lane group g's one 128-bit load holds its 8 values of each block
+//     d    (NP / 16, KP / 64) blocks of 64 bytes: row r holds the fp16 scales of its two 32-value blocks of the chunk
+//   padding rows and the padding half-chunk past K are zero (scale 0)
+//
 // Every plane starts 256-byte aligned and the whole is rounded up to 256 bytes, so a stack of weights is a plain array
 // of these records (mbq_plane_bytes apart). The byte count is the file's plus at most 256 bytes of zero padding per
 // plane.
@@ -58,8 +66,10 @@
 namespace mbq {
 
 // T_INT8: the caller's row-major int8 weights (mbq_int8_linear); T_I8T: int8 weights repacked into 16-row tiles
-// (mbq_matmul with MBQ_I8T planes); T_Q4KT: Q4_K blocks repacked into 16-row tiles (MBQ_Q4KT planes)
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9, T_Q4KT = -12 };
+// (mbq_matmul with MBQ_I8T planes); T_Q4KT and T_Q8T: Q4_K and Q8_0 blocks repacked into 16-row tiles (MBQ_Q4KT and
+// MBQ_Q8T planes)
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9, T_Q8T = -10,
+             T_Q4KT = -12 };
 // int8 types: 16-byte units of 16 values, a per-row float32 scale applied to the sum
 constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
 // T_I8T: bytes between consecutive 16-row tiles of the quant plane, and the byte offset of (row, K offset k0) (k0 a
@@ -73,10 +83,16 @@ constexpr int64_t i8t_off(int64_t row, int64_t k, int64_t k0) { return (row >> 4
 constexpr int64_t q4kt_tile_bytes(int64_t k) { return k / 128 * 1024; }
 constexpr int64_t q4kt_off(int64_t row, int64_t k) { return (row >> 4) * q4kt_tile_bytes(k) + (row & 15) * 64; }
 constexpr int64_t q4kt_meta_off(int64_t row, int64_t k) { return (row >> 4) * (k / 256) * 256 + (row & 15) * 16; }
+// T_Q8T: offset of (row, chunk 0)'s two fp16 scales in the d plane (chunk kc of 64 values at + 64 kc); its quants sit
+// at i8t_off, value v (0..63) of a chunk row at byte q8t_byte(v)
+constexpr int64_t q8t_d_off(int64_t row, int64_t k) { return (row >> 4) * ((k + 63) / 64) * 64 + (row & 15) * 4; }
+constexpr int q8t_byte(int v) { return ((v & 31) >> 3) * 16 + (v >> 5) * 8 + (v & 7); }
 // tiled plane types (16-row tiles, any number of rows)
-constexpr bool tiled_type(int t) { return t == T_I8T || t == T_Q4KT; }
+constexpr bool tiled_type(int t) { return t == T_I8T || t == T_Q4KT || t == T_Q8T; }
 // the Q4_K value format, in row-major or tiled planes
 constexpr bool q4k_like(int t) { return t == T_Q4_K || t == T_Q4KT; }
+// the Q8_0 value format, in row-major or tiled planes
+constexpr bool q8_like(int t) { return t == T_Q8_0 || t == T_Q8T; }
 
 // the K-quants: 256-value super-blocks, kernel units of 32 values (16 bytes of low nibbles)
 constexpr bool kquant(int t) { return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q4KT; }
@@ -95,9 +111,9 @@ struct Layout {
 };
 
 // values and file bytes of one block (T_Q4KT planes are made from Q4_K blocks)
-inline int block_values(int t) { return (t == T_Q8_0 || t == T_Q4_0) ? 32 : kquant(t) ? 256 : 0; }
+inline int block_values(int t) { return (q8_like(t) || t == T_Q4_0) ? 32 : kquant(t) ? 256 : 0; }
 inline int block_bytes(int t) {
-    return t == T_Q4_0 ? 18 : t == T_Q8_0 ? 34 : q4k_like(t) ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
+    return t == T_Q4_0 ? 18 : q8_like(t) ? 34 : q4k_like(t) ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : 0;
 }
 
 inline Layout layout(int t, int64_t n, int64_t k) {
@@ -119,6 +135,10 @@ inline Layout layout(int t, int64_t n, int64_t k) {
         const int64_t np = (n + 15) / 16 * 16;
         L.qs_bytes = np * ((k + 63) / 64 * 64);
         L.sc_bytes = np * 4;
+    } else if (t == T_Q8T) {
+        const int64_t np = (n + 15) / 16 * 16, kp = (k + 63) / 64 * 64;
+        L.qs_bytes = np * kp;
+        L.sc_bytes = np * (kp / 16);
     } else if (t == T_Q4KT) {
         const int64_t np = (n + 15) / 16 * 16;
         L.qs_bytes = np * (k / 2);

@@ -248,4 +248,38 @@ def test_q4_k_tiled_repack_is_lossless(n, kb):
     assert L.lib().mbq_has_type(L.Q4KT) == 0 and L.lib().mbq_row_bytes(L.Q4KT, k) < 0     # not a ggml type
     assert L.lib().mbq_dequant_raw(L.Q4KT, None, n, k, None, None) < 0                    # its blocks are Q4_K's
     with pytest.raises(NotImplementedError):
-        KQ.repack_host(R.Q8_0, np.zeros((1, 34), np.uint8), (1, 32), tiled=True)
+        KQ.repack_host(R.Q6_K, np.zeros((1, 210), np.uint8), (1, 256), tiled=True)
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (17, 64), (33, 96), (130, 1056)])
+def test_q8_0_tiled_repack_is_lossless(n, k):
+    """Q8_0 blocks into 16-row tiles (MBQ_Q8T) and back, exactly. Quant block (rt, kc) row r = values 64 kc .. of row
+    16 rt + r, value v of the chunk at byte 16 ((v % 32) // 8) + 8 (v // 32) + v % 8 (lane group g's 16 bytes: its 8
+    values of each 32-value block); scale block (rt, kc) row r = that row's two fp16 block scales of the chunk; rows
+    past n and the half chunk past k are zero"""
+    rng = np.random.default_rng([n, k, 8])
+    raw = rng.integers(0, 256, (n, R.row_bytes(R.Q8_0, k)), dtype=np.uint8)
+    p = KQ.repack_host(R.Q8_0, raw, (n, k), threads=3, tiled=True)
+    assert p.t == L.Q8T
+    np16, kp = (n + 15) // 16 * 16, (k + 63) // 64 * 64
+    a256 = lambda v: (v + 255) // 256 * 256
+    assert p.stride == a256(a256(np16 * kp) + np16 * kp // 16)
+    buf = p.buf.numpy()
+    blocks = raw.reshape(n, k // 32, 34)
+    q = np.zeros((np16, kp), np.uint8)
+    q[:n, :k] = blocks[:, :, 2:].reshape(n, k)
+    d = np.zeros((np16, kp // 32, 2), np.uint8)
+    d[:n, :k // 32] = blocks[:, :, :2]
+    v = np.arange(64)
+    pos = 16 * ((v % 32) // 8) + 8 * (v // 32) + v % 8
+    assert sorted(pos) == list(range(64))
+    tiles = buf[:np16 * kp].reshape(np16 // 16, kp // 64, 16, 64)[..., pos]
+    assert np.array_equal(tiles.transpose(0, 2, 1, 3).reshape(np16, kp), q)
+    so = a256(np16 * kp)
+    ds = buf[so:so + np16 * kp // 16].reshape(np16 // 16, kp // 64, 16, 4)
+    assert np.array_equal(ds.transpose(0, 2, 1, 3).reshape(np16, kp // 32, 2), d)
+    back = np.zeros_like(raw)
+    assert L.lib().mbq_unpack_host(L.Q8T, ctypes.c_void_p(p.buf.data_ptr()), n, k, back.ctypes.data_as(ctypes.c_void_p),
+                                   back.size) == 0
+    assert np.array_equal(back, raw)
+    assert L.lib().mbq_covers(L.Q8T, n, k) == 1 and L.lib().mbq_covers(L.Q8T, n, k + 16) == 0

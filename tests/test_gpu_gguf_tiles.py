@@ -1,11 +1,11 @@
-"""GPU parity of Q4_K weights repacked at load into 16-row tiles (kernels.repack(..., tiled=True), libmbq's MBQ_Q4KT
-planes) against the reference's Q4_K dequantization (reference src/mashbox/ops/reference.py:132-149) and its
-dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
+"""GPU parity of Q4_K and Q8_0 weights repacked at load into 16-row tiles (kernels.repack(..., tiled=True), libmbq's
+MBQ_Q4KT and MBQ_Q8T planes) against the reference's dequantization (reference src/mashbox/ops/reference.py:132-149,
+:101-103) and its dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
 
 Oracle: oracle.ref's dequantization of the same blocks (bit for bit for dequant, take_rows and the repack) and the
 float64 product of those weights (tests/_check.py bars). Batches of 1-64 rows run the K-group kernel (mbq_kgemm.hip),
-which reads only tiled planes; batches past 64 rows run the same LDS-tile plans as row-major Q4_K planes, so there the
-two layouts give the same bits.
+which reads only tiled planes; batches past 64 rows run the same LDS-tile plans as row-major planes, so there the two
+layouts give the same bits.
 """
 import ctypes
 
@@ -21,6 +21,8 @@ from mashbox_amd import _lib as LIB
 from mashbox_amd import kernels as KQ
 
 pytestmark = pytest.mark.gpu
+TYPES = [R.Q4_K, R.Q8_0]
+NAME = {R.Q4_K: "Q4_K", R.Q8_0: "Q8_0"}
 
 
 def _x(rng, m, k, dev):
@@ -34,75 +36,90 @@ def forced_plan():
     LIB.force_gemm_plan()
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("n,k", [(1, 256), (17, 512), (100, 768), (130, 4096)])
-def test_device_repack_equals_host_repack(n, k, cuda):
+def test_device_repack_equals_host_repack(t, n, k, cuda):
     """the GPU repack writes the host repack's bytes, every byte (into a buffer full of 0xAB), the padding rows of the
     last tile included"""
     rng = np.random.default_rng([n, k, 120])
-    raw = G.q4_k_raw(rng, n, k)
-    host = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True)
-    dev = KQ.repack(R.Q4_K, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
-    assert dev.t == LIB.Q4KT and torch.equal(dev.buf.cpu(), host.buf)
+    raw = G.RAW[t](rng, n, k)
+    host = KQ.repack_host(t, raw, (n, k), tiled=True)
+    dev = KQ.repack(t, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
+    assert dev.t == KQ.TILED[t] and torch.equal(dev.buf.cpu(), host.buf)
     dirty = torch.full((host.buf.numel(),), 0xAB, dtype=torch.uint8, device=cuda)
     rd = torch.from_numpy(raw).to(cuda)
-    assert LIB.lib().mbq_repack_dev(LIB.Q4KT, ctypes.c_void_p(rd.data_ptr()), n, k, ctypes.c_void_p(dirty.data_ptr()),
+    assert LIB.lib().mbq_repack_dev(KQ.TILED[t], ctypes.c_void_p(rd.data_ptr()), n, k, ctypes.c_void_p(dirty.data_ptr()),
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
     assert torch.equal(dirty.cpu(), host.buf)
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("n,k", [(1, 256), (33, 512), (130, 2304)])
-def test_dequant_and_rows_bit_exact(n, k, cuda):
+def test_dequant_and_rows_bit_exact(t, n, k, cuda):
     """dequant and take_rows of tiled planes: bit for bit the oracle's dequantization (random bytes: NaN and infinite
     scales included)"""
     rng = np.random.default_rng([n, k, 121])
-    raw = rng.integers(0, 256, (n, R.row_bytes(R.Q4_K, k)), dtype=np.uint8)
-    p = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True).to(cuda)
-    want = R.dequant(raw, R.Q4_K, k)
+    raw = rng.integers(0, 256, (n, R.row_bytes(t, k)), dtype=np.uint8)
+    p = KQ.repack_host(t, raw, (n, k), tiled=True).to(cuda)
+    want = R.dequant(raw, t, k)
     assert diff_bits(KQ.dequant(p).cpu().numpy(), want) == 0
     ids = rng.integers(-n, n, 9)
     assert diff_bits(KQ.take_rows(p, torch.from_numpy(ids)).cpu().numpy(), want[ids]) == 0
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("n,k", [(33, 256), (100, 512), (1000, 2304), (4500, 1024)])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16, 17, 32, 33, 48, 64, 65, 130])
-def test_matmul_matches_reference(n, k, m, cuda):
+def test_matmul_matches_reference(t, n, k, m, cuda):
+    _matmul_case(t, n, k, m, cuda)
+
+
+@pytest.mark.parametrize("n,k", [(33, 96), (100, 1056), (7, 32)])
+@pytest.mark.parametrize("m", [1, 4, 16, 33, 64, 65, 130])
+def test_q8_0_ragged_k(n, k, m, cuda):
+    """Q8_0 rows of an odd number of 32-value blocks: the tiles' last chunk is half padding (zero quants, zero scale)"""
+    _matmul_case(R.Q8_0, n, k, m, cuda)
+
+
+def _matmul_case(t, n, k, m, cuda):
     rng = np.random.default_rng([n, k, m, 122])
-    raw = G.q4_k_raw(rng, n, k)
+    raw = G.RAW[t](rng, n, k)
     xb, x = _x(rng, m, k, cuda)
-    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, R.Q4_K, k).astype(np.float64).T
-    p = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True).to(cuda)
-    plan = LIB.plan_str(LIB.Q4KT, m, n, k)
-    print(f"q4k tiles m={m} n={n} k={k} {plan}", flush=True)
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    p = KQ.repack_host(t, raw, (n, k), tiled=True).to(cuda)
+    plan = LIB.plan_str(KQ.TILED[t], m, n, k)
+    print(f"{NAME[t]} tiles m={m} n={n} k={k} {plan}", flush=True)
     y = KQ.matmul(x, p).cpu().numpy()
-    assert_product(y, ref, f"q4k tiles m={m} n={n} k={k} ({plan})")
+    assert_product(y, ref, f"{NAME[t]} tiles m={m} n={n} k={k} ({plan})")
     yb = KQ.matmul(x, p, out_dtype=torch.bfloat16)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y))
     if m <= 64:
-        assert LIB.gemm_plan(LIB.Q4KT, m, n, k)[0] == LIB.KERNEL_KGROUP
+        assert LIB.gemm_plan(KQ.TILED[t], m, n, k)[0] == LIB.KERNEL_KGROUP
     else:                                                       # the row-major planes' plan: the same bits
-        assert plan == LIB.plan_str(R.Q4_K, m, n, k)
-        rm = KQ.repack_host(R.Q4_K, raw, (n, k)).to(cuda)
+        assert plan == LIB.plan_str(t, m, n, k)
+        rm = KQ.repack_host(t, raw, (n, k)).to(cuda)
         assert np.array_equal(y.view(np.uint32), KQ.matmul(x, rm).cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("m", [1, 4, 16, 17, 33, 64])
 @pytest.mark.parametrize("n,k", [(1000, 256 * 9), (4500, 1024), (70, 768)])
-def test_kgroup_every_split_count(m, n, k, forced_plan, cuda):
-    """the K-group kernel on tiled Q4_K planes at every split count the planner can take (each fixes rows per block, row
+def test_kgroup_every_split_count(t, m, n, k, forced_plan, cuda):
+    """the K-group kernel on tiled planes at every split count the planner can take (each fixes rows per block, row
     groups and tiles per wave), on row counts whose block ranges start and end inside 16-row tiles and K ranges whose
     splits end inside super-blocks (a chunk is half a super-block), against the float64 product; a split K repeats bit
     for bit"""
     rng = np.random.default_rng([m, n, k, 123])
-    raw = G.q4_k_raw(rng, n, k)
+    raw = G.RAW[t](rng, n, k)
     xb, x = _x(rng, m, k, cuda)
-    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, R.Q4_K, k).astype(np.float64).T
-    p = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True).to(cuda)
+    ref = R.bf16_to_f32(xb).astype(np.float64) @ R.dequant(raw, t, k).astype(np.float64).T
+    p = KQ.repack_host(t, raw, (n, k), tiled=True).to(cuda)
     for splits in (0, 1, 2, 3, 4, 6, 8):
         if splits > k // 128:
             continue
         forced_plan(LIB.KERNEL_KGROUP, 0, 0, splits)
         try:
-            plan = LIB.gemm_plan(LIB.Q4KT, m, n, k)
+            plan = LIB.gemm_plan(KQ.TILED[t], m, n, k)
         except LIB.MbqError as e:
             # a forced split count whose row ranges need more tiles per wave than the kernel holds (Q4_K at 33-64 rows:
             # 5) has no plan; the call is refused the same way, with nothing launched. The automatic plan always runs.
@@ -110,38 +127,40 @@ def test_kgroup_every_split_count(m, n, k, forced_plan, cuda):
             with pytest.raises(LIB.MbqError):
                 KQ.matmul(x, p)
             continue
-        plan = LIB.gemm_plan(LIB.Q4KT, m, n, k)
+        plan = LIB.gemm_plan(KQ.TILED[t], m, n, k)
         assert plan[0] == LIB.KERNEL_KGROUP and (splits == 0 or plan[3] == splits), plan
-        print(f"q4k tiles kgroup m={m} n={n} k={k} plan {plan}", flush=True)
+        print(f"{NAME[t]} tiles kgroup m={m} n={n} k={k} plan {plan}", flush=True)
         y = KQ.matmul(x, p).cpu().numpy()
-        assert_product(y, ref, f"q4k tiles kgroup m={m} n={n} k={k} plan {plan}")
+        assert_product(y, ref, f"{NAME[t]} tiles kgroup m={m} n={n} k={k} plan {plan}")
         assert np.array_equal(KQ.matmul(x, p).cpu().numpy().view(np.uint32), y.view(np.uint32))
 
 
-def test_stream_plan_refused(forced_plan, cuda):
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_stream_plan_refused(t, forced_plan, cuda):
     """the weight-stream kernel reads row-major planes only: a forced stream plan on tiled planes is an error, not a
     launch"""
     rng = np.random.default_rng(124)
-    raw = G.q4_k_raw(rng, 64, 512)
-    p = KQ.repack_host(R.Q4_K, raw, (64, 512), tiled=True).to(cuda)
+    raw = G.RAW[t](rng, 64, 512)
+    p = KQ.repack_host(t, raw, (64, 512), tiled=True).to(cuda)
     _, x = _x(rng, 8, 512, cuda)
     forced_plan(LIB.KERNEL_STREAM, 16, 64, 1)
     with pytest.raises(LIB.MbqError):
         KQ.matmul(x, p)
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("m", [1, 4, 64, 300])
-def test_stack_read_in_place(m, cuda):
+def test_stack_read_in_place(t, m, cuda):
     """a stack of 3 weights repacked at once; layer= as an int and as a device int32 reads one in place; a device layer
     outside the stack gives NaN"""
     rng = np.random.default_rng([m, 125])
     n, k, L = 70, 768, 3
-    st = np.stack([G.q4_k_raw(rng, n, k) for _ in range(L)])
-    p = KQ.repack(R.Q4_K, torch.from_numpy(st).to(cuda), (n, k), tiled=True)
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(L)])
+    p = KQ.repack(t, torch.from_numpy(st).to(cuda), (n, k), tiled=True)
     xb, x = _x(rng, m, k, cuda)
     xf = R.bf16_to_f32(xb).astype(np.float64)
     for layer in range(L):
-        ref = xf @ R.dequant(st[layer], R.Q4_K, k).astype(np.float64).T
+        ref = xf @ R.dequant(st[layer], t, k).astype(np.float64).T
         assert_product(KQ.matmul(x, p, layer=layer).cpu().numpy(), ref, f"layer {layer}")
         got = KQ.matmul(x, p, layer=torch.tensor(layer, dtype=torch.int32, device=cuda)).cpu().numpy()
         assert_product(got, ref, f"device layer {layer}")
@@ -150,50 +169,53 @@ def test_stack_read_in_place(m, cuda):
     assert np.all(np.isnan(bad))
 
 
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 @pytest.mark.parametrize("m", [4, 16])
-def test_27b_layer_at_decode_buckets(m, cuda):
+def test_27b_layer_at_decode_buckets(t, m, cuda):
     """the 7 projections of a 27B-class layer at the engine's row buckets 4 and 16 (reference
     src/mashbox/runtime/engine.py:424-428): every output against the float64 product (on the GPU) of the oracle's
     dequantization"""
     rng = np.random.default_rng([m, 126])
     for name, (n, k) in G.LAYER_27B.items():
-        raw = G.q4_k_raw(rng, n, k)
+        raw = G.RAW[t](rng, n, k)
         xb, x = _x(rng, m, k, cuda)
-        p = KQ.repack(R.Q4_K, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
-        print(f"q4k tiles 27B {name} m={m} ({LIB.plan_str(LIB.Q4KT, m, n, k)})", flush=True)
+        p = KQ.repack(t, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
+        print(f"{NAME[t]} tiles 27B {name} m={m} ({LIB.plan_str(KQ.TILED[t], m, n, k)})", flush=True)
         y = KQ.matmul(x, p)
-        w64 = torch.from_numpy(R.dequant(raw, R.Q4_K, k)).to(cuda).to(torch.float64)
-        assert_product_dev(y, x.to(torch.float64) @ w64.T, f"27B {name} m={m} ({LIB.plan_str(LIB.Q4KT, m, n, k)})")
+        w64 = torch.from_numpy(R.dequant(raw, t, k)).to(cuda).to(torch.float64)
+        assert_product_dev(y, x.to(torch.float64) @ w64.T, f"27B {name} m={m} ({LIB.plan_str(KQ.TILED[t], m, n, k)})")
         del w64, y
         torch.cuda.empty_cache()
 
 
-def test_noalloc_equals_matmul(forced_plan, cuda):
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_noalloc_equals_matmul(t, forced_plan, cuda):
     """mbq_matmul_noalloc on tiled planes (split-K partials in the static scratch) gives mbq_matmul's bits, on two calls
     in a row, the second smaller"""
     rng = np.random.default_rng(127)
     n, k = 1024, 5120
-    raw = G.q4_k_raw(rng, n, k)
-    p = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True).to(cuda)
+    raw = G.RAW[t](rng, n, k)
+    p = KQ.repack_host(t, raw, (n, k), tiled=True).to(cuda)
     forced_plan(LIB.KERNEL_KGROUP, 0, 0, 4)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for m in (16, 5):
         _, x = _x(rng, m, k, cuda)
         want = KQ.matmul(x, p)
         got = torch.empty_like(want)
-        assert LIB.lib().mbq_matmul_noalloc(LIB.Q4KT, ctypes.c_void_p(p.buf.data_ptr()), 0, None, 1,
+        assert LIB.lib().mbq_matmul_noalloc(KQ.TILED[t], ctypes.c_void_p(p.buf.data_ptr()), 0, None, 1,
                                             ctypes.c_void_p(x.data_ptr()), m, n, k, ctypes.c_void_p(got.data_ptr()),
                                             LIB.OUT_F32, stream) == 0
         assert torch.equal(got.view(torch.int32), want.view(torch.int32))
 
 
-def test_kgroup_graph_replays(forced_plan, cuda):
-    """a split-K K-group call on tiled Q4_K planes recorded into a HIP graph replays bit for bit equal to the eager call,
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_kgroup_graph_replays(t, forced_plan, cuda):
+    """a split-K K-group call on tiled planes recorded into a HIP graph replays bit for bit equal to the eager call,
     with eager calls of the same kernel in between"""
     rng = np.random.default_rng(128)
     m, n, k = 16, 1024, 5120
-    raw = G.q4_k_raw(rng, n, k)
-    p = KQ.repack_host(R.Q4_K, raw, (n, k), tiled=True).to(cuda)
+    raw = G.RAW[t](rng, n, k)
+    p = KQ.repack_host(t, raw, (n, k), tiled=True).to(cuda)
     _, x = _x(rng, m, k, cuda)
     _, x2 = _x(rng, m, k, cuda)
     forced_plan(LIB.KERNEL_KGROUP, 0, 0, 4)
@@ -210,25 +232,26 @@ def test_kgroup_graph_replays(forced_plan, cuda):
         torch.cuda.synchronize()
 
 
-def test_ops_prepare_loads_tiles(monkeypatch, cuda):
-    """with MBQ_TILES=1 the ops layer loads Q4_K weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_ops_prepare_loads_tiles(t, monkeypatch, cuda):
+    """with MBQ_TILES=1 the ops layer loads Q4_K and Q8_0 weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
     layer= in place and dequant against the oracle; device_nbytes counts the tiled planes"""
     from mashbox_amd import ops
     monkeypatch.setenv("MBQ_TILES", "1")
     ops.load_kernels()
     rng = np.random.default_rng(129)
     n, k, L = 100, 512, 2
-    st = np.stack([G.q4_k_raw(rng, n, k) for _ in range(L)])
-    h = ops.prepare(st[0], R.Q4_K, (n, k))
-    hs = ops.prepare(st, R.Q4_K, (n, k))
-    assert isinstance(h, ops.Packed) and h.packed.t == LIB.Q4KT and hs.packed.t == LIB.Q4KT
-    assert ops.device_nbytes(R.Q4_K, (L, n, k), st.nbytes) == L * KQ.plane_bytes(LIB.Q4KT, (n, k))
-    w = [R.dequant(st[i], R.Q4_K, k) for i in range(L)]
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(L)])
+    h = ops.prepare(st[0], t, (n, k))
+    hs = ops.prepare(st, t, (n, k))
+    assert isinstance(h, ops.Packed) and h.packed.t == KQ.TILED[t] and hs.packed.t == KQ.TILED[t]
+    assert ops.device_nbytes(t, (L, n, k), st.nbytes) == L * KQ.plane_bytes(KQ.TILED[t], (n, k))
+    w = [R.dequant(st[i], t, k) for i in range(L)]
     assert diff_bits(ops.dequant(h).cpu().numpy(), w[0]) == 0
     for m in (1, 4, 300):
         xb, x = _x(rng, m, k, cuda)
         xf = R.bf16_to_f32(xb).astype(np.float64)
         assert_product(ops.qmatmul(x.float(), h).float().cpu().numpy(), xf @ w[0].astype(np.float64).T, f"prepare m={m}")
         for i in range(L):
-            y = ops.qmatmul(x.float(), ops.At(hs.packed, i, R.Q4_K, (n, k))).float().cpu().numpy()
+            y = ops.qmatmul(x.float(), ops.At(hs.packed, i, t, (n, k))).float().cpu().numpy()
             assert_product(y, xf @ w[i].astype(np.float64).T, f"prepare stack layer {i} m={m}")
