@@ -53,8 +53,9 @@ template <> struct BUnit<T_Q8T> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
 template <> struct BUnit<T_I8T> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
+template <> struct BUnit<T_Q6KT> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct BUnit<T_Q5_K> { u32x4 q, meta; uint32_t h; };
-template <int T> constexpr int b_loads() { return T == T_Q8T ? 5 : T == T_Q6_K ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
+template <int T> constexpr int b_loads() { return T == T_Q8T ? 5 : q6k_like(T) ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
 
 // per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h: Q5_K, Q6_K; d: Q6_K
 struct BOff { uint32_t q, s, h, d; };
@@ -64,6 +65,9 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     if constexpr (T == T_Q6_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 4) + 2 * u),
                     (uint32_t)(hi_off + bn * (K >> 2) + 8 * u), (uint32_t)(d_off + bn * (K >> 7))};
+    else if constexpr (T == T_Q6KT)
+        return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q6kt_s_off(bn, K) + 2 * u),
+                    (uint32_t)(hi_off + q6kt_h_off(bn, K) + 8 * u), (uint32_t)(d_off + q6kt_d_off(bn, K))};
     else if constexpr (T == T_Q5_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
@@ -83,6 +87,12 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, (uint32_t)k0 >> 2, 0));
         b.s = bload2(r, o.s, (uint32_t)k0 >> 4);
         b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 2);
+    } else if constexpr (T == T_Q6KT) {
+        // the step's half of the chunk (values 128 (k0 / 128) + 64 ((k0 / 64) % 2) ..) in each tiled plane
+        b.q = bload16(r, o.q, ((uint32_t)k0 >> 7) * 1024u + (((uint32_t)k0 >> 1) & 63u));
+        b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, ((uint32_t)k0 >> 7) * 512u + (((uint32_t)k0 >> 2) & 31u), 0));
+        b.s = bload2(r, o.s, ((uint32_t)k0 >> 7) * 128u + (((uint32_t)k0 >> 4) & 7u));
+        b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 32u);
     } else if constexpr (T == T_Q4KT) {
         // the step's 32 bytes of the row sit in the tile block of values 128 (k0 / 128) .., at byte (k0 / 2) % 64
         b.q = bload16(r, o.q, ((uint32_t)k0 >> 7) * 1024u + (((uint32_t)k0 >> 1) & 63u));
@@ -138,7 +148,7 @@ struct BScale { float a, b, c, e; };
 template <int T>
 __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
     BScale s{1.f, 128.f, 0.f, 0.f};
-    if constexpr (T == T_Q6_K) {
+    if constexpr (q6k_like(T)) {
         const float d = f16f(b.d);
         s.a = d * (float)(int8_t)(b.s & 0xFFu);           // exact
         s.b = 32.f * s.a;
@@ -171,7 +181,7 @@ __device__ __forceinline__ uint32_t sel4(const u32x4& v, int i) {
 template <int T>
 __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int t) {
     u32x4 o;
-    if constexpr (T == T_Q6_K) {
+    if constexpr (q6k_like(T)) {
         // the quants of values 8t .. 8t+3 and 8t+4 .. 8t+7 as bytes; (q - 32) * (d sc) is one exact FMA
         uint32_t lo, hi;
         q6k_bytes(sel4(b.q, t), (t & 2) ? b.h[1] : b.h[0], t, &lo, &hi);
@@ -626,7 +636,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
     // shared unit whole (the same bytes). Q6_K units take 8 registers each and the even split spills there, so Q6_K
     // keeps that uneven one: thread t takes unit t whole and, for t < 128, unit t + 256. Rows past N are clamped
     // (their outputs are never stored).
-    constexpr bool EVEN = T != T_Q6_K;
+    constexpr bool EVEN = !q6k_like(T);
     constexpr int UPT = 2;                                          // the thread's whole unit, then the shared (second) one
     constexpr int NCH = EVEN ? 6 : 8;                               // chunks of 8 values per thread and step
     const int ph = pt & 1;                                          // EVEN: which half of the shared unit
@@ -999,9 +1009,9 @@ static int choose(int t, const Args& a, Choice* c) {
         return 0;
     }
     if (fk == K_KGROUP && a.M <= WS_MAX_M)
-        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT) only");
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q6KT) only");
     if (fk == K_STREAM) {
-        if (t == T_Q4KT || t == T_Q8T) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
+        if (t == T_Q4KT || t == T_Q8T || t == T_Q6KT) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
@@ -1075,6 +1085,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_I8T: rc = pick<T_I8T>(a, &p); if (!rc) *bm = CANDS<T_I8T>[p.idx].bm, *bn = CANDS<T_I8T>[p.idx].bn; break;
         case T_Q4KT: rc = pick<T_Q4KT>(a, &p); if (!rc) *bm = CANDS<T_Q4KT>[p.idx].bm, *bn = CANDS<T_Q4KT>[p.idx].bn; break;
         case T_Q8T: rc = pick<T_Q8T>(a, &p); if (!rc) *bm = CANDS<T_Q8T>[p.idx].bm, *bn = CANDS<T_Q8T>[p.idx].bn; break;
+        case T_Q6KT: rc = pick<T_Q6KT>(a, &p); if (!rc) *bm = CANDS<T_Q6KT>[p.idx].bm, *bn = CANDS<T_Q6KT>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -1115,6 +1126,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_I8T: return launch_gemm_t<T_I8T>(a, s);
         case T_Q4KT: return launch_gemm_t<T_Q4KT>(a, s);
         case T_Q8T: return launch_gemm_t<T_Q8T>(a, s);
+        case T_Q6KT: return launch_gemm_t<T_Q6KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

@@ -1,4 +1,4 @@
-// Host repack of one weight into kernel planes (Q4_K and Q8_0 also into 16-row tiles, T_Q4KT and T_Q8T), and its inverse (no HIP: also
+// Host repack of one weight into kernel planes (Q4_K, Q6_K and Q8_0 also into 16-row tiles, T_Q4KT, T_Q6KT and T_Q8T), and its inverse (no HIP: also
 // built alone, under the host sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
 // src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
 // int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
@@ -62,6 +62,26 @@ inline int64_t q8_d_at(int t, int64_t n, int64_t K, int64_t b) {
     return t == T_Q8T ? q8t_d_off(n, K) + (b / 2) * 64 + (b % 2) * 2 : (n * (K / 32) + b) * 2;
 }
 
+// Q6_K planes (row-major, or T_Q6KT tiles) of row n: unit j of super-block b in the qs and qh planes, half h (8 bytes)
+// of the super-block's 16 sub-block scales, and its fp16 scale
+struct Q6kAt {
+    int t;
+    int64_t n, K;
+    uint8_t* p;
+    const Layout& L;
+    bool tiled() const { return t == T_Q6KT; }
+    uint8_t* q(int64_t b, int j) const {
+        return p + L.qs_off + (tiled() ? q4kt_off(n, K) + (2 * b + (j >> 2)) * 1024 + (j & 3) * 16 : n * (K / 2) + b * 128 + j * 16);
+    }
+    uint8_t* h(int64_t b, int j) const {
+        return p + L.hi_off + (tiled() ? q6kt_h_off(n, K) + (2 * b + (j >> 2)) * 512 + (j & 3) * 8 : n * (K / 4) + b * 64 + j * 8);
+    }
+    uint8_t* sc(int64_t b, int hf) const {
+        return p + L.sc_off + (tiled() ? q6kt_s_off(n, K) + (2 * b + hf) * 128 : n * (K / 16) + b * 16 + 8 * hf);
+    }
+    uint8_t* d(int64_t b) const { return p + L.d_off + (tiled() ? q6kt_d_off(n, K) + b * 32 : (n * (K / 256) + b) * 2); }
+};
+
 inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, const Layout& L, int64_t r0, int64_t r1) {
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
@@ -90,18 +110,17 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                     }
                 }
             }
-        } else if (t == T_Q6_K) {
-            uint8_t* q = planes + L.qs_off + n * (K / 2);
-            uint8_t* h = planes + L.hi_off + n * (K / 4);
-            uint8_t* sc = planes + L.sc_off + n * (K / 16);
-            uint8_t* d = planes + L.d_off + n * nb * 2;
+        } else if (q6k_like(t)) {
+            // Q6_K, row-major or in 16-row tiles (T_Q6KT): the same bytes of each plane at the layout's offsets
+            const Q6kAt at{t, n, K, planes, L};
             for (int64_t b = 0; b < nb; ++b) {
                 const uint8_t* src = row + b * bb;
-                memcpy(sc + b * 16, src + 192, 16);
-                memcpy(d + b * 2, src + 208, 2);
+                memcpy(at.sc(b, 0), src + 192, 8);
+                memcpy(at.sc(b, 1), src + 200, 8);
+                memcpy(at.d(b), src + 208, 2);
                 for (int j = 0; j < 8; ++j) {
-                    uint8_t* qu = q + b * 128 + j * 16;
-                    uint8_t* hu = h + b * 64 + j * 8;
+                    uint8_t* qu = at.q(b, j);
+                    uint8_t* hu = at.h(b, j);
                     memset(qu, 0, 16);
                     memset(hu, 0, 8);
                     for (int i = 0; i < 32; ++i) {
@@ -191,19 +210,17 @@ inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
                     }
                 }
             }
-        } else if (t == T_Q6_K) {
-            const uint8_t* q = planes + L.qs_off + n * (K / 2);
-            const uint8_t* h = planes + L.hi_off + n * (K / 4);
-            const uint8_t* sc = planes + L.sc_off + n * (K / 16);
-            const uint8_t* d = planes + L.d_off + n * nb * 2;
+        } else if (q6k_like(t)) {
+            const Q6kAt at{t, n, K, const_cast<uint8_t*>(planes), L};
             for (int64_t b = 0; b < nb; ++b) {
                 uint8_t* dst = row + b * bb;
                 memset(dst, 0, 192);
-                memcpy(dst + 192, sc + b * 16, 16);
-                memcpy(dst + 208, d + b * 2, 2);
+                memcpy(dst + 192, at.sc(b, 0), 8);
+                memcpy(dst + 200, at.sc(b, 1), 8);
+                memcpy(dst + 208, at.d(b), 2);
                 for (int j = 0; j < 8; ++j) {
-                    const uint8_t* qu = q + b * 128 + j * 16;
-                    const uint8_t* hu = h + b * 64 + j * 8;
+                    const uint8_t* qu = at.q(b, j);
+                    const uint8_t* hu = at.h(b, j);
                     const int g = j >> 2, r = j & 3;
                     for (int i = 0; i < 32; ++i) {
                         int lb, lbit, hb, hbit;
@@ -305,7 +322,7 @@ inline void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t
 // hardware thread). The caller checks the shape and the buffer sizes.
 inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
     const Layout L = layout(t, rows, cols);
-    if (t == T_Q8T) memset(planes, 0, (size_t)L.total);   // padding rows, the half-chunk past K, the gaps
+    if (t == T_Q8T || t == T_Q6KT) memset(planes, 0, (size_t)L.total);   // padding rows (Q8_0: the half chunk past K)
     for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
     if (t == T_Q4KT) q4kt_zero_pad_rows(rows, cols, planes, L);

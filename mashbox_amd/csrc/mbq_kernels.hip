@@ -48,11 +48,13 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         for (int i = 0; i < uw; ++i) out[i] = __builtin_nanf("");
         return;
     }
-    if constexpr (T == T_Q6_K) {
-        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
-        const u32x2 h = *reinterpret_cast<const u32x2*>(base + hi_off + n * (K >> 2) + u * 8);
-        const uint16_t scp = *reinterpret_cast<const uint16_t*>(base + sc_off + n * (K >> 4) + u * 2);
-        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + d_off + (n * (K >> 8) + (u >> 3)) * 2));
+    if constexpr (q6k_like(T)) {
+        // T_Q6KT: unit u of chunk u / 4 in each tiled plane
+        constexpr bool TL = T == T_Q6KT;
+        const u32x4 q = ld16(base + (TL ? q4kt_off(n, K) + (u >> 2) * 1024 + (u & 3) * 16 : n * (K >> 1) + u * 16));
+        const u32x2 h = *reinterpret_cast<const u32x2*>(base + hi_off + (TL ? q6kt_h_off(n, K) + (u >> 2) * 512 + (u & 3) * 8 : n * (K >> 2) + u * 8));
+        const uint16_t scp = *reinterpret_cast<const uint16_t*>(base + sc_off + (TL ? q6kt_s_off(n, K) + (u >> 2) * 128 + (u & 3) * 2 : n * (K >> 4) + u * 2));
+        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + d_off + (TL ? q6kt_d_off(n, K) + (u >> 3) * 32 : (n * (K >> 8) + (u >> 3)) * 2)));
         const float ds0 = d * (float)(int8_t)(scp & 0xFFu), ds1 = d * (float)(int8_t)(scp >> 8);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -299,18 +301,20 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
             for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
             hd[j] = hw;
         }
-    } else if constexpr (T == T_Q6_K) {
-        uint8_t* sc = planes + sc_off + n * (K >> 4) + b * 16;
-        for (int i = 0; i < 16; ++i) sc[i] = src[192 + i];
-        uint8_t* d = planes + d_off + (n * nb + b) * 2;
-        d[0] = src[208];
-        d[1] = src[209];
-        uint32_t* qd = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 128);
-        uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + n * (K >> 2) + b * 64);
+    } else if constexpr (q6k_like(T)) {
+        // T_Q6KT: every plane's bytes at their tile offsets; the last tile's rows past N written zero
+        constexpr bool TL = T == T_Q6KT;
+        for (int i = 0; i < 16; ++i)
+            planes[sc_off + (TL ? q6kt_s_off(n, K) + (2 * b + (i >> 3)) * 128 + (i & 7) : n * (K >> 4) + b * 16 + i)] = live ? src[192 + i] : 0;
+        uint8_t* d = planes + d_off + (TL ? q6kt_d_off(n, K) + b * 32 : (n * nb + b) * 2);
+        d[0] = live ? src[208] : 0;
+        d[1] = live ? src[209] : 0;
         for (int j = 0; j < 8; ++j) {
+            uint32_t* qd = reinterpret_cast<uint32_t*>(planes + (TL ? q4kt_off(n, K) + (2 * b + (j >> 2)) * 1024 + (j & 3) * 16 : n * (K >> 1) + b * 128 + j * 16));
+            uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + (TL ? q6kt_h_off(n, K) + (2 * b + (j >> 2)) * 512 + (j & 3) * 8 : n * (K >> 2) + b * 64 + j * 8));
             const int g = j >> 2, r = j & 3;
             uint32_t qw[4] = {0, 0, 0, 0}, hw[2] = {0, 0};
-            for (int i = 0; i < 32; ++i) {
+            for (int i = 0; i < 32 && live; ++i) {
                 const uint32_t lo = (src[64 * g + 32 * (r & 1) + i] >> (4 * (r >> 1))) & 15u;
                 const uint32_t hi = (src[128 + 32 * g + i] >> (2 * r)) & 3u;
                 // slots of mbq_layout.h: low nibble dword i/8, byte i%4, bits 4 ((i/4)%2); high bits dword i/16,
@@ -318,9 +322,9 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
                 qw[i >> 3] |= lo << (8 * (i & 3) + 4 * ((i >> 2) & 1));
                 hw[i >> 4] |= hi << (8 * (i & 3) + 2 * ((i >> 2) & 3));
             }
-            for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
-            hd[j * 2] = hw[0];
-            hd[j * 2 + 1] = hw[1];
+            for (int t = 0; t < 4; ++t) qd[t] = qw[t];
+            hd[0] = hw[0];
+            hd[1] = hw[1];
         }
     } else if constexpr (T == T_Q4KT) {
         // the Q4_K units and header of row n at their tile offsets (mbq_layout.h); the rows of the last tile past the
@@ -479,6 +483,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_I8T: return launch_t<T_I8T>(a, s);
         case T_Q4KT: return launch_t<T_Q4KT>(a, s);
         case T_Q8T: return launch_t<T_Q8T>(a, s);
+        case T_Q6KT: return launch_t<T_Q6KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
@@ -496,6 +501,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
     else if (t == T_Q4_K) run(dequant_kernel<T_Q4_K>);
     else if (t == T_Q4KT) run(dequant_kernel<T_Q4KT>);
     else if (t == T_Q8T) run(dequant_kernel<T_Q8T>);
+    else if (t == T_Q6KT) run(dequant_kernel<T_Q6KT>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -504,13 +510,14 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
 
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
     const int64_t blocks = t == T_Q8T ? (N + 15) / 16 * 16 * ((K + 63) / 64 * 2)
-                                      : (t == T_Q4KT ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
+                                      : (tiled_type(t) ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
     if (t == T_Q4_0) run(repack_kernel<T_Q4_0>);
     else if (t == T_Q4_K) run(repack_kernel<T_Q4_K>);
     else if (t == T_Q4KT) run(repack_kernel<T_Q4KT>);
     else if (t == T_Q8T) run(repack_kernel<T_Q8T>);
+    else if (t == T_Q6KT) run(repack_kernel<T_Q6KT>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

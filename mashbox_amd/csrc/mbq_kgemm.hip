@@ -51,6 +51,7 @@ struct KgmArgs {
     const int32_t* layer_dev;
     int nlayers;
     int64_t sc_off, wbytes;
+    int64_t hi_off, d_off;         // Q6_K tiles: the high-bit and super-block scale planes
     const uint16_t* x;
     int M, N, K;
     void* y;
@@ -63,8 +64,9 @@ struct KgmArgs {
     int fenced;                    // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
-// K values per chunk: one KiB of a 16-row weight tile (int8: 64 values; Q4_K: 128, four 32-value units per row)
-constexpr int kgm_cw(int t) { return t == T_Q4KT ? 128 : 64; }
+// K values per chunk: one KiB of a 16-row weight tile (int8, Q8_0: 64 values; Q4_K, Q6_K: 128, four 32-value units per
+// row of low nibbles)
+constexpr int kgm_cw(int t) { return (t == T_Q4KT || t == T_Q6KT) ? 128 : 64; }
 // bytes of one x stage: 16 MT rows of one chunk of bfloat16 values
 constexpr size_t kgm_stage(int t, int mt) { return (size_t)16 * mt * 2 * kgm_cw(t); }
 // most dynamic LDS a block may take (160 KiB per CU, less a little for the static variables)
@@ -86,6 +88,10 @@ constexpr size_t kgm_lds() {
 // floats of one block's partial tile: RG row groups x MT x NTW 16x16 tiles
 template <int MT, int RG, int NTW> constexpr int kgm_elems() { return RG * MT * NTW * 256; }
 
+// a Q6_K tile unit as the weight-direct helpers take it: low nibbles, then (high bits, sub-block scales, super-block
+// scale) as loaded into one 4-dword register set
+__device__ __forceinline__ WsRaw<T_Q6_K> q6raw(const u32x4& q, const u32x4& h) { return WsRaw<T_Q6_K>{q, u32x2{h[0], h[1]}, h[2], h[3]}; }
+
 // x stage swizzle: piece p of row r sits in slot p ^ kgm_swz(r). 128-byte rows (8 pieces): (r >> 1) & 7; 256-byte rows
 // (16 pieces, Q4_K chunks): r & 15, so the 16 rows an A-operand read of one lane group takes (one piece each) fall on
 // 16 different slots, every bank once
@@ -101,7 +107,8 @@ template <int T, int MT, int RG, int NTW, bool KFULL>
 __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
     __shared__ int kgm_last;
-    constexpr bool QK = T == T_Q4KT;                     // Q4_K tiles
+    constexpr bool Q6 = T == T_Q6KT;                     // Q6_K tiles (the Q4_K tiles' chunks and lane units)
+    constexpr bool QK = T == T_Q4KT || Q6;               // Q4_K or Q6_K tiles
     constexpr bool Q8 = T == T_Q8T;                      // Q8_0 tiles (else int8 tiles)
     constexpr int CW = kgm_cw(T);                        // K values per chunk
     constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
@@ -113,8 +120,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     constexpr int NX = STAGE / 1024 / RG;                // x DMA instructions per wave per chunk (1 KiB each)
     static_assert(NX * RG * 1024 == STAGE, "the RG waves of a K group issue whole DMA instructions");
     static_assert(kgm_ring(T, MT, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
-    constexpr int NWL = QK || Q8 ? 2 * NTW : NTW;        // weight loads per chunk (Q4_K: quants and headers; Q8_0:
-                                                         // quants and the two block scales)
+    constexpr int NWL = Q6 ? 4 * NTW : QK || Q8 ? 2 * NTW : NTW;   // weight loads per chunk (Q4_K: quants and headers;
+                                                                   // Q6_K: the four planes; Q8_0: quants, scales)
     constexpr int VMT = (D - 1) * NWL + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
     static_assert(VMT < 64, "vmcnt range");
     const int M = g.M, N = g.N, K = g.K;
@@ -145,13 +152,16 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 
     // weight offsets: tile t0 + j, row r16, the lane group's 16 bytes (of the chunk's KiB); Q4_K: also the row's
     // super-block headers; rows outside [rq0, rq1) read zero
-    uint32_t wo[NTW], mo[NTW];
+    uint32_t wo[NTW], mo[NTW], ho[NTW], dq[NTW];
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
         const int row = 16 * (t0 + j) + r16;
         const bool in = row >= rq0 && row < rq1;
         wo[j] = in ? (uint32_t)(QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
-        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K))) : OOB_VOFF;
+        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg : QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K)))
+                                 : OOB_VOFF;
+        ho[j] = in && Q6 ? (uint32_t)(g.hi_off + q6kt_h_off(row, K) + 8 * lg) : OOB_VOFF;
+        dq[j] = in && Q6 ? (uint32_t)(g.d_off + q6kt_d_off(row, K)) : OOB_VOFF;
     }
     // int8: the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their
     // latency hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads). Q4_K and
@@ -201,9 +211,16 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                                                                                   live ? (uint32_t)c * 1024u : 0u, 2));
             if constexpr (Q8)
                 H[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 64u : 0u, 0);
-            if constexpr (QK)
+            if constexpr (Q6) {
+                // the unit's 8 bytes of high bits, its two sub-block scales, the super-block scale
+                const u32x2 h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                    wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 512u : 0u, 2));
+                H[j] = u32x4{h[0], h[1], bload2(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u),
+                             bload2(wr, live ? dq[j] : OOB_VOFF, live ? (uint32_t)(c >> 1) * 32u : 0u)};
+            } else if constexpr (QK) {
                 H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
                                                                                       live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
+            }
         }
     };
     // A operand: x row 16 i + (lane & 15), piece NS (lane >> 4) + s of stage st (Q8_0: 4 s + (lane >> 4)), the K values
@@ -235,7 +252,10 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         // Q4_K: the lane's 16 bytes are one 32-value unit of its row, sub-block 4 (chunk % 2) + lg of the super-block;
         // its (d sc, dmin m) for the whole chunk
         WsScale qs[QK ? NTW : 1];
-        if constexpr (QK) {
+        if constexpr (Q6) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q6_K>(q6raw(W[U][j], H[U][j]), 0);
+        } else if constexpr (QK) {
             const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
             for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], H[U][j]}, j8);
@@ -271,7 +291,10 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
                 bf16x8_t B;
-                if constexpr (QK) {
+                if constexpr (Q6) {
+                    // values 8 s .. 8 s + 7 of the unit, (d sc) (q - 32) rounded to bfloat16 (the LDS GEMM's operand)
+                    B = ws_bop<T_Q6_K>(q6raw(W[U][j], H[U][j]), qs[j], s);
+                } else if constexpr (QK) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m rounded to bfloat16 (the LDS GEMM's operand)
                     B = q4k_dword_bop(W[U][j][s], qs[j]);
                 } else {
@@ -430,9 +453,11 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 // A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
 struct KgmPlan { int S, R, RG, NTW; };
 constexpr int KGM_MAX_NTW = 6;
-// most tiles per wave of a type and batch: Q4_K at 33-64 rows holds its tiles' headers and units in 5 tiles' registers
-// (6 spill to scratch at 256 registers per lane)
-constexpr int kgm_max_ntw(int t, int mt) { return t == T_Q4KT && mt >= 3 ? 5 : KGM_MAX_NTW; }
+// most tiles per wave of a type and batch: Q4_K at 33-64 rows and Q6_K from 17 rows hold their tiles' units and scales
+// in 5 tiles' registers (6 spill to scratch at 256 registers per lane)
+constexpr int kgm_max_ntw(int t, int mt) {
+    return (t == T_Q4KT && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
+}
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
 static int kgm_ntw(int64_t N, int64_t R, int RG) {
@@ -459,7 +484,8 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
     const int MT = (int)((M + 15) / 16);
-    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q8T ? 68.0 : 64.0, waste_w = t == T_Q4KT ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
+    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
+    const double waste_w = (t == T_Q4KT || t == T_Q6KT) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
     KgmPlan best{0, 0, 0, 0};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
@@ -504,7 +530,7 @@ static int kgm_launch(const Args& a, const KgmPlan& p, const Workspace& w, hipSt
             return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM: %zu bytes of LDS refused", lds);
         const int64_t KC = (a.K + kgm_cw(T) - 1) / kgm_cw(T);
         const int kcs = (int)((KC + p.S - 1) / p.S);
-        KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
+        KgmArgs g{a.base, a.stride, a.layer_dev, a.nlayers, a.sc_off, a.wbytes, a.hi_off, a.d_off, a.x, (int)a.M, (int)a.N, (int)a.K, a.y,
                   a.out_bf16, p.R, p.S, kcs, w.ws, w.cnt, (uint32_t)w.bytes, w.fenced};
         const int64_t ranges = (a.N + p.R - 1) / p.R;
         kern<<<dim3((unsigned)(ranges * p.S)), KGM_THREADS, lds, s>>>(g);
@@ -564,7 +590,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     if (a.M < 1 || a.M > 64) return set_error(MBQ_BAD_ARG, "K-group GEMM: M = %lld", (long long)a.M);
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES || a.M * a.N * 4 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "K-group GEMM operands over 2 GiB");
-    if (t == T_Q4KT && a.K % 256) return set_error(MBQ_BAD_ARG, "K-group GEMM: Q4_K K = %lld", (long long)a.K);
+    if ((t == T_Q4KT || t == T_Q6KT) && a.K % 256) return set_error(MBQ_BAD_ARG, "K-group GEMM: K-quant K = %lld", (long long)a.K);
     const KgmPlan p = kgm_choose(t, a.M, a.N, a.K, cus_of_device(), force_s);
     if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
                                    (long long)a.N, (long long)a.K, force_s);
@@ -574,6 +600,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
         if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.M, a.N, p), s, &w)) return rc;
     }
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
+    if (t == T_Q6KT) return kgm_launch_mt<T_Q6KT, true>(a, p, w, s);
     if (t == T_Q8T) return a.K % 64 == 0 ? kgm_launch_mt<T_Q8T, true>(a, p, w, s) : kgm_launch_mt<T_Q8T, false>(a, p, w, s);
     return a.K % 64 == 0 ? kgm_launch_mt<T_I8T, true>(a, p, w, s) : kgm_launch_mt<T_I8T, false>(a, p, w, s);
 }

@@ -102,8 +102,9 @@ CONFIGS = {
 # the reference's largest published per-call number: a Q6_K output head, 151936 x 2560, one activation row
 # (reference CORE-CHANGES.md:73, 369.8 us on TPU v6e-1)
 # batched decode over one 27B-class layer at the reference engine's row buckets 4 and 16 (runtime/engine.py:424-428):
-# Q4_K, Q8_0 and int8 weights, each repacked into 16-row tiles (as config 4 takes int8)
+# Q4_K, Q8_0, Q6_K and int8 weights, each repacked into 16-row tiles (as config 4 takes int8)
 EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          "m4_q4k": (12, 4, LAYER_27B), "m16_q4k": (12, 16, LAYER_27B), "m4_q8": (8, 4, LAYER_27B), "m16_q8": (8, 16, LAYER_27B),
+         "m4_q6k": (14, 4, LAYER_27B), "m16_q6k": (14, 16, LAYER_27B),
          "m4_int8": ("int8", 4, LAYER_27B), "m16_int8": ("int8", 16, LAYER_27B)}
 REF_TPU_US = {"q6k_head": 369.8}

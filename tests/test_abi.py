@@ -248,7 +248,28 @@ def test_q4_k_tiled_repack_is_lossless(n, kb):
     assert L.lib().mbq_has_type(L.Q4KT) == 0 and L.lib().mbq_row_bytes(L.Q4KT, k) < 0     # not a ggml type
     assert L.lib().mbq_dequant_raw(L.Q4KT, None, n, k, None, None) < 0                    # its blocks are Q4_K's
     with pytest.raises(NotImplementedError):
-        KQ.repack_host(R.Q6_K, np.zeros((1, 210), np.uint8), (1, 256), tiled=True)
+        KQ.repack_host(R.Q5_K, np.zeros((1, 176), np.uint8), (1, 256), tiled=True)
+
+
+@pytest.mark.parametrize("n,kb", [(1, 1), (17, 2), (130, 3)])
+def test_q6_k_tiled_repack_is_lossless(n, kb):
+    """Q6_K blocks into 16-row tiles (MBQ_Q6KT) and back, exactly; the low-nibble tiles hold the row-major planes' bytes
+    (16 rows x 64 bytes per 128-value chunk, as MBQ_Q4KT's); rows of the last tile past n are zero"""
+    k = 256 * kb
+    rng = np.random.default_rng([n, kb, 14])
+    raw = rng.integers(0, 256, (n, R.row_bytes(R.Q6_K, k)), dtype=np.uint8)
+    p = KQ.repack_host(R.Q6_K, raw, (n, k), threads=3, tiled=True)
+    rm = KQ.repack_host(R.Q6_K, raw, (n, k))
+    assert p.t == L.Q6KT
+    np16 = (n + 15) // 16 * 16
+    full = np.zeros((np16, k // 2), np.uint8)
+    full[:n] = rm.buf.numpy()[:n * k // 2].reshape(n, k // 2)
+    tiles = p.buf.numpy()[:np16 * k // 2].reshape(np16 // 16, k // 128, 16, 64)
+    assert np.array_equal(tiles.transpose(0, 2, 1, 3).reshape(np16, k // 2), full)
+    back = np.zeros_like(raw)
+    assert L.lib().mbq_unpack_host(L.Q6KT, ctypes.c_void_p(p.buf.data_ptr()), n, k, back.ctypes.data_as(ctypes.c_void_p),
+                                   back.size) == 0
+    assert np.array_equal(back, raw)
 
 
 @pytest.mark.parametrize("n,k", [(1, 32), (17, 64), (33, 96), (130, 1056)])
