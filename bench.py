@@ -9,9 +9,9 @@ config 2 (GGUF Q8_0 decode GEMV, x[1,5120] @ W[17408,5120]^T), in GB/s of algori
 scales + x + y, never repack padding) per second, with the weights already in HBM. `q6k_head` is not a BASELINE
 config: it is the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one
 activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs, as are batched decode
-over the 27B-class layer at 4 and 16 activation rows (`m4_q4k`, `m16_q4k`, `m4_q8`, `m16_q8`, `m4_q6k`,
-`m16_q6k`, `m4_int8`, `m16_int8`: the reference engine's row buckets; Q4_K, Q8_0, Q6_K and int8 weights in 16-row
-tiles).
+over the 27B-class layer at 4 and 16 activation rows (`m4_q4k`, `m16_q4k`, `m4_q8`, `m16_q8`, `m4_q5k`,
+`m16_q5k`, `m4_q6k`, `m16_q6k`, `m4_int8`, `m16_int8`: the reference engine's row buckets; Q4_K, Q8_0, Q5_K, Q6_K and
+int8 weights in 16-row tiles).
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
 distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
@@ -49,7 +49,7 @@ def algorithmic_bytes(t, m, n, k):
     if t == "int8":
         w = n * k + 4 * n
     else:
-        bs, ts = {8: (32, 34), 12: (256, 144), 14: (256, 210)}[t]
+        bs, ts = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}[t]
         w = n * (k // bs) * ts
     return w + 2 * m * k + 2 * m * n
 
@@ -104,10 +104,10 @@ def setup_projection(idx, pi, rotate_bytes):
                                      ctypes.c_void_p(x.data_ptr()), M, N, K, ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
         plan = LIB.plan_str(LIB.INT8, M, N, K)
     else:
-        raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
-        # batched Q4_K / Q8_0 / Q6_K decode (2-64 rows): the blocks repacked once at load into 16-row tiles (MBQ_Q4KT,
-        # MBQ_Q8T, MBQ_Q6KT planes), as int8
-        pt = {12: LIB.Q4KT, 8: LIB.Q8T, 14: LIB.Q6KT}.get(t, t) if 1 < M <= 64 else t
+        raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 13: synth.q5_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
+        # batched GGUF decode (2-64 rows): the blocks repacked once at load into 16-row tiles (MBQ_Q4KT, MBQ_Q5KT,
+        # MBQ_Q6KT, MBQ_Q8T planes), as int8
+        pt = {12: LIB.Q4KT, 8: LIB.Q8T, 13: LIB.Q5KT, 14: LIB.Q6KT}.get(t, t) if 1 < M <= 64 else t
         pb = check(L.mbq_plane_bytes(pt, N, K), "plane_bytes")
         planes = torch.empty(pb, dtype=torch.uint8, device=dev)
         check(L.mbq_repack_dev(pt, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st()), "repack")
@@ -457,7 +457,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q6k,m16_q6k,m4_int8,m16_int8")
+    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,m4_int8,m16_int8")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -59,6 +59,9 @@ extern "C" {
  * nibbles, high bits, sub-block scales, super-block scales) tiled by 16 rows x 128 values, the low nibbles' KiB
  * holding one 32-value unit per lane of a wave-wide load. Dequant bit for bit, matmul the same bars. Not a ggml type. */
 #define MBQ_Q6KT (-14)
+/* Q5_K weights in 16-row tiles, as MBQ_Q4KT (low nibbles and super-block headers tiled the same way) plus the high-bit
+ * words tiled by 16 rows x 128 values. Dequant bit for bit, matmul the same bars. Not a ggml type. */
+#define MBQ_Q5KT (-13)
 
 #define MBQ_OUT_F32 0
 #define MBQ_OUT_BF16 1
@@ -182,10 +185,10 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
- *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q6KT) at M <= 64: bm = 16,
- *                      bn = weight rows per block (any count: N is cut into equal ranges that fill the CUs), splits =
- *                      K ranges. The automatic plan of tiled planes up to 64 rows (they have no GEMV or weight-stream
- *                      plan).
+ *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT) at M <= 64:
+ *                      bm = 16, bn = weight rows per block (any count: N is cut into equal ranges that fill the
+ *                      CUs), splits = K ranges. The automatic plan of tiled planes up to 64 rows (they have no
+ *                      GEMV or weight-stream plan).
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
  * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice;
  * MBQ_KERNEL_KGROUP takes bm = bn = 0 and chooses its rows per block for the forced splits, 0 = its own choice).

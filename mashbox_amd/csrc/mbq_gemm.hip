@@ -55,7 +55,8 @@ template <> struct BUnit<T_I8T> { u32x4 q0, q1; };
 template <> struct BUnit<T_Q6_K> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct BUnit<T_Q6KT> { u32x4 q; u32x2 h; uint32_t s, d; };
 template <> struct BUnit<T_Q5_K> { u32x4 q, meta; uint32_t h; };
-template <int T> constexpr int b_loads() { return T == T_Q8T ? 5 : q6k_like(T) ? 4 : (T == T_Q8_0 || T == T_Q5_K) ? 3 : 2; }   // buffer loads per unit
+template <> struct BUnit<T_Q5KT> { u32x4 q, meta; uint32_t h; };
+template <int T> constexpr int b_loads() { return T == T_Q8T ? 5 : q6k_like(T) ? 4 : (T == T_Q8_0 || q5k_like(T)) ? 3 : 2; }   // buffer loads per unit
 
 // per-thread byte offsets of a weight unit's planes (the K step's part goes in the scalar offset); h: Q5_K, Q6_K; d: Q6_K
 struct BOff { uint32_t q, s, h, d; };
@@ -68,6 +69,8 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
     else if constexpr (T == T_Q6KT)
         return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q6kt_s_off(bn, K) + 2 * u),
                     (uint32_t)(hi_off + q6kt_h_off(bn, K) + 8 * u), (uint32_t)(d_off + q6kt_d_off(bn, K))};
+    else if constexpr (T == T_Q5KT)
+        return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q4kt_meta_off(bn, K)), (uint32_t)(hi_off + q5kt_h_off(bn, K) + 4 * u), 0};
     else if constexpr (T == T_Q5_K)
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
@@ -93,10 +96,12 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.h = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.h, ((uint32_t)k0 >> 7) * 512u + (((uint32_t)k0 >> 2) & 31u), 0));
         b.s = bload2(r, o.s, ((uint32_t)k0 >> 7) * 128u + (((uint32_t)k0 >> 4) & 7u));
         b.d = bload2(r, o.d, ((uint32_t)k0 >> 8) * 32u);
-    } else if constexpr (T == T_Q4KT) {
+    } else if constexpr (T == T_Q4KT || T == T_Q5KT) {
         // the step's 32 bytes of the row sit in the tile block of values 128 (k0 / 128) .., at byte (k0 / 2) % 64
         b.q = bload16(r, o.q, ((uint32_t)k0 >> 7) * 1024u + (((uint32_t)k0 >> 1) & 63u));
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 256);
+        if constexpr (T == T_Q5KT)
+            b.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, o.h, ((uint32_t)k0 >> 7) * 256u + (((uint32_t)k0 >> 3) & 15u), 0);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
@@ -154,7 +159,7 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.b = 32.f * s.a;
         s.c = d * (float)(int8_t)((b.s >> 8) & 0xFFu);
         s.e = 32.f * s.c;
-    } else if constexpr (q4k_like(T) || T == T_Q5_K) {
+    } else if constexpr (q4k_like(T) || q5k_like(T)) {
         uint32_t sc, mn;
         q4k_scale_min_sel(b.meta[1], b.meta[2], b.meta[3], q4k_sel(j), &sc, &mn);
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
@@ -190,7 +195,7 @@ __device__ __forceinline__ u32x4 b_chunk(const BUnit<T>& b, const BScale& s, int
         o[1] = pack_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(lo >> 24), ds, -m));
         o[2] = pack_bf16(__builtin_fmaf((float)(hi & 0xFFu), ds, -m), __builtin_fmaf((float)((hi >> 8) & 0xFFu), ds, -m));
         o[3] = pack_bf16(__builtin_fmaf((float)((hi >> 16) & 0xFFu), ds, -m), __builtin_fmaf((float)(hi >> 24), ds, -m));
-    } else if constexpr (T == T_Q5_K) {
+    } else if constexpr (q5k_like(T)) {
         // the quants of values 8t .. 8t+3 and 8t+4 .. 8t+7 as bytes; (d sc) q - dmin m is one FMA with one rounding
         uint32_t lo, hi;
         q5k_bytes(sel4(b.q, t), b.h, t, &lo, &hi);
@@ -1009,9 +1014,9 @@ static int choose(int t, const Args& a, Choice* c) {
         return 0;
     }
     if (fk == K_KGROUP && a.M <= WS_MAX_M)
-        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q6KT) only");
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT) only");
     if (fk == K_STREAM) {
-        if (t == T_Q4KT || t == T_Q8T || t == T_Q6KT) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
+        if (tiled_type(t) && t != T_I8T) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
         if (a.M > WS_MAX_M)
             return set_error(MBQ_BAD_ARG, "a forced weight-stream plan needs M <= %lld", (long long)WS_MAX_M);
         *c = Choice{K_STREAM, 16, g_force_bn.load(), std::max(1, g_force_s.load())};
@@ -1086,6 +1091,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_Q4KT: rc = pick<T_Q4KT>(a, &p); if (!rc) *bm = CANDS<T_Q4KT>[p.idx].bm, *bn = CANDS<T_Q4KT>[p.idx].bn; break;
         case T_Q8T: rc = pick<T_Q8T>(a, &p); if (!rc) *bm = CANDS<T_Q8T>[p.idx].bm, *bn = CANDS<T_Q8T>[p.idx].bn; break;
         case T_Q6KT: rc = pick<T_Q6KT>(a, &p); if (!rc) *bm = CANDS<T_Q6KT>[p.idx].bm, *bn = CANDS<T_Q6KT>[p.idx].bn; break;
+        case T_Q5KT: rc = pick<T_Q5KT>(a, &p); if (!rc) *bm = CANDS<T_Q5KT>[p.idx].bm, *bn = CANDS<T_Q5KT>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -1127,6 +1133,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_Q4KT: return launch_gemm_t<T_Q4KT>(a, s);
         case T_Q8T: return launch_gemm_t<T_Q8T>(a, s);
         case T_Q6KT: return launch_gemm_t<T_Q6KT>(a, s);
+        case T_Q5KT: return launch_gemm_t<T_Q5KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

@@ -1,4 +1,4 @@
-// Host repack of one weight into kernel planes (Q4_K, Q6_K and Q8_0 also into 16-row tiles, T_Q4KT, T_Q6KT and T_Q8T), and its inverse (no HIP: also
+// Host repack of one weight into kernel planes (Q4_K, Q5_K, Q6_K and Q8_0 also into 16-row tiles), and its inverse (no HIP: also
 // built alone, under the host sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
 // src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
 // int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
@@ -62,6 +62,18 @@ inline int64_t q8_d_at(int t, int64_t n, int64_t K, int64_t b) {
     return t == T_Q8T ? q8t_d_off(n, K) + (b / 2) * 64 + (b % 2) * 2 : (n * (K / 32) + b) * 2;
 }
 
+// Q5_K planes (row-major, or T_Q5KT tiles) of row n: unit j of super-block b in the qs and qh planes, and the
+// super-block's header
+inline int64_t q5k_q_at(int t, int64_t n, int64_t K, int64_t b, int j) {
+    return t == T_Q5KT ? q4kt_off(n, K) + (2 * b + (j >> 2)) * 1024 + (j & 3) * 16 : n * (K / 2) + b * 128 + j * 16;
+}
+inline int64_t q5k_h_at(int t, int64_t n, int64_t K, int64_t b, int j) {
+    return t == T_Q5KT ? q5kt_h_off(n, K) + (2 * b + (j >> 2)) * 256 + (j & 3) * 4 : n * (K / 8) + b * 32 + j * 4;
+}
+inline int64_t q5k_meta_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q5KT ? q4kt_meta_off(n, K) + b * 256 : (n * (K / 256) + b) * 16;
+}
+
 // Q6_K planes (row-major, or T_Q6KT tiles) of row n: unit j of super-block b in the qs and qh planes, half h (8 bytes)
 // of the super-block's 16 sub-block scales, and its fp16 scale
 struct Q6kAt {
@@ -86,18 +98,15 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         const uint8_t* row = raw + n * rb;
-        if (t == T_Q5_K) {
+        if (q5k_like(t)) {
             // reference src/mashbox/ops/reference.py:150-159: value 32j + i takes nibble j % 2 of qs[32 (j / 2) + i]
-            // (qs at byte 48) and bit j of qh[i] (qh at byte 16)
-            uint8_t* q = planes + L.qs_off + n * (K / 2);
-            uint8_t* h = planes + L.hi_off + n * (K / 8);
-            uint8_t* meta = planes + L.sc_off + n * nb * 16;
+            // (qs at byte 48) and bit j of qh[i] (qh at byte 16); T_Q5KT: at the tile offsets
             for (int64_t b = 0; b < nb; ++b) {
                 const uint8_t* src = row + b * bb;
-                memcpy(meta + b * 16, src, 16);
+                memcpy(planes + L.sc_off + q5k_meta_at(t, n, K, b), src, 16);
                 for (int j = 0; j < 8; ++j) {
-                    uint8_t* qu = q + b * 128 + j * 16;
-                    uint8_t* hu = h + b * 32 + j * 4;
+                    uint8_t* qu = planes + L.qs_off + q5k_q_at(t, n, K, b, j);
+                    uint8_t* hu = planes + L.hi_off + q5k_h_at(t, n, K, b, j);
                     memset(qu, 0, 16);
                     memset(hu, 0, 4);
                     for (int i = 0; i < 32; ++i) {
@@ -190,17 +199,14 @@ inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
     const int64_t nb = K / block_values(t), bb = block_bytes(t), rb = nb * bb;
     for (int64_t n = r0; n < r1; ++n) {
         uint8_t* row = raw + n * rb;
-        if (t == T_Q5_K) {
-            const uint8_t* q = planes + L.qs_off + n * (K / 2);
-            const uint8_t* h = planes + L.hi_off + n * (K / 8);
-            const uint8_t* meta = planes + L.sc_off + n * nb * 16;
+        if (q5k_like(t)) {
             for (int64_t b = 0; b < nb; ++b) {
                 uint8_t* dst = row + b * bb;
-                memcpy(dst, meta + b * 16, 16);
+                memcpy(dst, planes + L.sc_off + q5k_meta_at(t, n, K, b), 16);
                 memset(dst + 16, 0, 160);
                 for (int j = 0; j < 8; ++j) {
-                    const uint8_t* qu = q + b * 128 + j * 16;
-                    const uint8_t* hu = h + b * 32 + j * 4;
+                    const uint8_t* qu = planes + L.qs_off + q5k_q_at(t, n, K, b, j);
+                    const uint8_t* hu = planes + L.hi_off + q5k_h_at(t, n, K, b, j);
                     for (int i = 0; i < 32; ++i) {
                         int lb, lbit, hb, hbit;
                         q5k_slot(i, &lb, &lbit, &hb, &hbit);
@@ -322,7 +328,7 @@ inline void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t
 // hardware thread). The caller checks the shape and the buffer sizes.
 inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
     const Layout L = layout(t, rows, cols);
-    if (t == T_Q8T || t == T_Q6KT) memset(planes, 0, (size_t)L.total);   // padding rows (Q8_0: the half chunk past K)
+    if (t == T_Q8T || t == T_Q6KT || t == T_Q5KT) memset(planes, 0, (size_t)L.total);   // padding rows (Q8_0: the half chunk past K)
     for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
     if (t == T_Q4KT) q4kt_zero_pad_rows(rows, cols, planes, L);

@@ -70,10 +70,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
-    } else if constexpr (T == T_Q5_K) {
-        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
-        const uint32_t h = *reinterpret_cast<const uint32_t*>(base + hi_off + n * (K >> 3) + u * 4);
-        const u32x4 mt = ld16(base + sc_off + (n * (K >> 8) + (u >> 3)) * 16);
+    } else if constexpr (q5k_like(T)) {
+        constexpr bool TL = T == T_Q5KT;                         // unit u of chunk u / 4 in each tiled plane
+        const u32x4 q = ld16(base + (TL ? q4kt_off(n, K) + (u >> 2) * 1024 + (u & 3) * 16 : n * (K >> 1) + u * 16));
+        const uint32_t h = *reinterpret_cast<const uint32_t*>(base + hi_off + (TL ? q5kt_h_off(n, K) + (u >> 2) * 256 + (u & 3) * 4 : n * (K >> 3) + u * 4));
+        const u32x4 mt = ld16(base + sc_off + (TL ? q4kt_meta_off(n, K) + (u >> 3) * 256 : (n * (K >> 8) + (u >> 3)) * 16));
         uint32_t sc, mn;
         q4k_scale_min(mt[1], mt[2], mt[3], (int)(u & 7), &sc, &mn);
         const float dsc = f16f(mt[0]) * (float)sc;
@@ -248,7 +249,7 @@ template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
     const int bv = (q8_like(T) || T == T_Q4_0) ? 32 : 256;
-    const int bb = (T == T_Q4_0) ? 18 : q8_like(T) ? 34 : q4k_like(T) ? 144 : (T == T_Q5_K) ? 176 : 210;
+    const int bb = (T == T_Q4_0) ? 18 : q8_like(T) ? 34 : q4k_like(T) ? 144 : q5k_like(T) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     // tiles: the last tile's padding rows too, and for T_Q8T the padding half-chunk past K (written zero)
@@ -283,14 +284,16 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
             }
             dst[t] = v;
         }
-    } else if constexpr (T == T_Q5_K) {
-        uint8_t* meta = planes + sc_off + (n * nb + b) * 16;
-        for (int i = 0; i < 16; ++i) meta[i] = src[i];
-        uint32_t* qd = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 128);
-        uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + n * (K >> 3) + b * 32);
+    } else if constexpr (q5k_like(T)) {
+        // T_Q5KT: at the tile offsets; the last tile's rows past N written zero
+        constexpr bool TL = T == T_Q5KT;
+        uint8_t* meta = planes + sc_off + (TL ? q4kt_meta_off(n, K) + b * 256 : (n * nb + b) * 16);
+        for (int i = 0; i < 16; ++i) meta[i] = live ? src[i] : 0;
         for (int j = 0; j < 8; ++j) {
+            uint32_t* qd = reinterpret_cast<uint32_t*>(planes + (TL ? q4kt_off(n, K) + (2 * b + (j >> 2)) * 1024 + (j & 3) * 16 : n * (K >> 1) + b * 128 + j * 16));
+            uint32_t* hd = reinterpret_cast<uint32_t*>(planes + hi_off + (TL ? q5kt_h_off(n, K) + (2 * b + (j >> 2)) * 256 + (j & 3) * 4 : n * (K >> 3) + b * 32 + j * 4));
             uint32_t qw[4] = {0, 0, 0, 0}, hw = 0;
-            for (int i = 0; i < 32; ++i) {
+            for (int i = 0; i < 32 && live; ++i) {
                 const uint32_t lo = (src[48 + 32 * (j >> 1) + i] >> (4 * (j & 1))) & 15u;
                 const uint32_t hi = (src[16 + i] >> j) & 1u;
                 // slots of mbq_layout.h: low nibble dword i/8, byte i%4, bits 4 ((i/4)%2); high bit byte i%4,
@@ -298,8 +301,8 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
                 qw[i >> 3] |= lo << (8 * (i & 3) + 4 * ((i >> 2) & 1));
                 hw |= hi << (8 * (i & 3) + 2 * (i >> 3) + ((i >> 2) & 1));
             }
-            for (int t = 0; t < 4; ++t) qd[j * 4 + t] = qw[t];
-            hd[j] = hw;
+            for (int t = 0; t < 4; ++t) qd[t] = qw[t];
+            hd[0] = hw;
         }
     } else if constexpr (q6k_like(T)) {
         // T_Q6KT: every plane's bytes at their tile offsets; the last tile's rows past N written zero
@@ -484,6 +487,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_Q4KT: return launch_t<T_Q4KT>(a, s);
         case T_Q8T: return launch_t<T_Q8T>(a, s);
         case T_Q6KT: return launch_t<T_Q6KT>(a, s);
+        case T_Q5KT: return launch_t<T_Q5KT>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
@@ -502,6 +506,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
     else if (t == T_Q4KT) run(dequant_kernel<T_Q4KT>);
     else if (t == T_Q8T) run(dequant_kernel<T_Q8T>);
     else if (t == T_Q6KT) run(dequant_kernel<T_Q6KT>);
+    else if (t == T_Q5KT) run(dequant_kernel<T_Q5KT>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -518,6 +523,7 @@ int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* plan
     else if (t == T_Q4KT) run(repack_kernel<T_Q4KT>);
     else if (t == T_Q8T) run(repack_kernel<T_Q8T>);
     else if (t == T_Q6KT) run(repack_kernel<T_Q6KT>);
+    else if (t == T_Q5KT) run(repack_kernel<T_Q5KT>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

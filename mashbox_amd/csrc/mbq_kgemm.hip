@@ -64,9 +64,9 @@ struct KgmArgs {
     int fenced;                    // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
-// K values per chunk: one KiB of a 16-row weight tile (int8, Q8_0: 64 values; Q4_K, Q6_K: 128, four 32-value units per
-// row of low nibbles)
-constexpr int kgm_cw(int t) { return (t == T_Q4KT || t == T_Q6KT) ? 128 : 64; }
+// K values per chunk: one KiB of a 16-row weight tile (int8, Q8_0: 64 values; the K-quants: 128, four 32-value units
+// per row of low nibbles)
+constexpr int kgm_cw(int t) { return (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT) ? 128 : 64; }
 // bytes of one x stage: 16 MT rows of one chunk of bfloat16 values
 constexpr size_t kgm_stage(int t, int mt) { return (size_t)16 * mt * 2 * kgm_cw(t); }
 // most dynamic LDS a block may take (160 KiB per CU, less a little for the static variables)
@@ -108,7 +108,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
     __shared__ int kgm_last;
     constexpr bool Q6 = T == T_Q6KT;                     // Q6_K tiles (the Q4_K tiles' chunks and lane units)
-    constexpr bool QK = T == T_Q4KT || Q6;               // Q4_K or Q6_K tiles
+    constexpr bool Q5 = T == T_Q5KT;                     // Q5_K tiles (Q4_K's, plus a high-bit word per unit)
+    constexpr bool QK = T == T_Q4KT || Q5 || Q6;         // K-quant tiles
     constexpr bool Q8 = T == T_Q8T;                      // Q8_0 tiles (else int8 tiles)
     constexpr int CW = kgm_cw(T);                        // K values per chunk
     constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
@@ -120,8 +121,9 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     constexpr int NX = STAGE / 1024 / RG;                // x DMA instructions per wave per chunk (1 KiB each)
     static_assert(NX * RG * 1024 == STAGE, "the RG waves of a K group issue whole DMA instructions");
     static_assert(kgm_ring(T, MT, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
-    constexpr int NWL = Q6 ? 4 * NTW : QK || Q8 ? 2 * NTW : NTW;   // weight loads per chunk (Q4_K: quants and headers;
-                                                                   // Q6_K: the four planes; Q8_0: quants, scales)
+    constexpr int NWL = Q6 ? 4 * NTW : Q5 ? 3 * NTW : QK || Q8 ? 2 * NTW : NTW;   // weight loads per chunk (Q4_K:
+                                                         // quants, headers; Q5_K: and high bits; Q6_K: the four
+                                                         // planes; Q8_0: quants, scales)
     constexpr int VMT = (D - 1) * NWL + (D - 2) * NX;    // loads issued after a chunk's last load (see the loop)
     static_assert(VMT < 64, "vmcnt range");
     const int M = g.M, N = g.N, K = g.K;
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         wo[j] = in ? (uint32_t)(QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
         mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg : QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K)))
                                  : OOB_VOFF;
-        ho[j] = in && Q6 ? (uint32_t)(g.hi_off + q6kt_h_off(row, K) + 8 * lg) : OOB_VOFF;
+        ho[j] = in && (Q5 || Q6) ? (uint32_t)(g.hi_off + (Q6 ? q6kt_h_off(row, K) + 8 * lg : q5kt_h_off(row, K) + 4 * lg)) : OOB_VOFF;
         dq[j] = in && Q6 ? (uint32_t)(g.d_off + q6kt_d_off(row, K)) : OOB_VOFF;
     }
     // int8: the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     // the chunk's weights: a KiB per tile (non-temporal), and for Q4_K the 16-byte header of the super-block (chunk / 2).
     // Q8_0: the lane's 16 bytes are its 8 quants of each of the chunk's two blocks (K step s = block s: values
     // 32 s + 8 lg ..), then the row's two block scales
-    auto load_w = [&](u32x4* W, u32x4* H, int l) __attribute__((always_inline)) {
+    auto load_w = [&](u32x4* W, u32x4* H, uint32_t* Hb, int l) __attribute__((always_inline)) {
         const int c = chunk_of(l);
         const bool live = l < mine;
 #pragma unroll
@@ -220,6 +222,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
             } else if constexpr (QK) {
                 H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
                                                                                       live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
+                if constexpr (Q5)                                 // the unit's high-bit word
+                    Hb[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 256u : 0u, 2);
             }
         }
     };
@@ -236,7 +240,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
         for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     u32x4 W[D][NTW];
-    u32x4 H[QK || Q8 ? D : 1][NTW];                                       // Q4_K: super-block headers; Q8_0: scales
+    u32x4 H[QK || Q8 ? D : 1][NTW];                                       // K-quants: headers / scales; Q8_0: scales
+    uint32_t Hb[Q5 ? D : 1][NTW];                                         // Q5_K: high-bit words
 
     // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
     // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
@@ -255,6 +260,10 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         if constexpr (Q6) {
 #pragma unroll
             for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q6_K>(q6raw(W[U][j], H[U][j]), 0);
+        } else if constexpr (Q5) {
+            const int j8 = 4 * (chunk_of(l) & 1) + lg;
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], H[U][j], Hb[U][j]}, j8);
         } else if constexpr (QK) {
             const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
@@ -294,6 +303,9 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                 if constexpr (Q6) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) (q - 32) rounded to bfloat16 (the LDS GEMM's operand)
                     B = ws_bop<T_Q6_K>(q6raw(W[U][j], H[U][j]), qs[j], s);
+                } else if constexpr (Q5) {
+                    // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m (one rounding) rounded to bfloat16
+                    B = ws_bop<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], H[U][j], Hb[U][j]}, qs[j], s);
                 } else if constexpr (QK) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m rounded to bfloat16 (the LDS GEMM's operand)
                     B = q4k_dword_bop(W[U][j][s], qs[j]);
@@ -318,14 +330,14 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_w(W[U], H[QK || Q8 ? U : 0], l + D);
+        load_w(W[U], H[QK || Q8 ? U : 0], Hb[Q5 ? U : 0], l + D);
     };
 
     if (steps > 0) {                                                      // block-uniform
 #pragma unroll
         for (int p = 0; p < D; ++p) {
             if (p < D - 1) dma_x(p, p);
-            load_w(W[p], H[QK || Q8 ? p : 0], p);
+            load_w(W[p], H[QK || Q8 ? p : 0], Hb[Q5 ? p : 0], p);
         }
         int l = 0;
         for (; l + D <= steps; l += D)
@@ -453,10 +465,11 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 // A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
 struct KgmPlan { int S, R, RG, NTW; };
 constexpr int KGM_MAX_NTW = 6;
-// most tiles per wave of a type and batch: Q4_K at 33-64 rows and Q6_K from 17 rows hold their tiles' units and scales
-// in 5 tiles' registers (6 spill to scratch at 256 registers per lane)
+// most tiles per wave of a type and batch whose units and scales fit the registers without spilling at 256 per lane:
+// Q4_K at 33-64 rows and Q6_K from 17 rows 5; Q5_K 5 at 17-32 and 49-64 rows, 4 at 33-48 (three stages deep)
 constexpr int kgm_max_ntw(int t, int mt) {
-    return (t == T_Q4KT && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
+    return t == T_Q5KT ? (mt == 1 ? KGM_MAX_NTW : mt == 3 ? 4 : 5)
+                       : (t == T_Q4KT && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
 }
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
@@ -484,8 +497,8 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
     const int MT = (int)((M + 15) / 16);
-    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
-    const double waste_w = (t == T_Q4KT || t == T_Q6KT) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
+    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q5KT ? 88.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
+    const double waste_w = (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
     KgmPlan best{0, 0, 0, 0};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
@@ -590,7 +603,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     if (a.M < 1 || a.M > 64) return set_error(MBQ_BAD_ARG, "K-group GEMM: M = %lld", (long long)a.M);
     if (a.wbytes > BUF_MAX_BYTES || a.M * a.K * 2 > BUF_MAX_BYTES || a.M * a.N * 4 > BUF_MAX_BYTES)
         return set_error(MBQ_BAD_ARG, "K-group GEMM operands over 2 GiB");
-    if ((t == T_Q4KT || t == T_Q6KT) && a.K % 256) return set_error(MBQ_BAD_ARG, "K-group GEMM: K-quant K = %lld", (long long)a.K);
+    if ((t == T_Q4KT || t == T_Q5KT || t == T_Q6KT) && a.K % 256) return set_error(MBQ_BAD_ARG, "K-group GEMM: K-quant K = %lld", (long long)a.K);
     const KgmPlan p = kgm_choose(t, a.M, a.N, a.K, cus_of_device(), force_s);
     if (p.S == 0) return set_error(MBQ_BAD_ARG, "K-group GEMM: no plan for %lld x %lld x %lld (%d splits)", (long long)a.M,
                                    (long long)a.N, (long long)a.K, force_s);
@@ -601,6 +614,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     }
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
     if (t == T_Q6KT) return kgm_launch_mt<T_Q6KT, true>(a, p, w, s);
+    if (t == T_Q5KT) return kgm_launch_mt<T_Q5KT, true>(a, p, w, s);
     if (t == T_Q8T) return a.K % 64 == 0 ? kgm_launch_mt<T_Q8T, true>(a, p, w, s) : kgm_launch_mt<T_Q8T, false>(a, p, w, s);
     return a.K % 64 == 0 ? kgm_launch_mt<T_I8T, true>(a, p, w, s) : kgm_launch_mt<T_I8T, false>(a, p, w, s);
 }

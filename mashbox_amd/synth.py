@@ -66,6 +66,16 @@ def q4_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> 
     return torch.cat([d, dmin, s.to(torch.uint8), qs.to(torch.uint8)], dim=-1).reshape(n, nb * 144)
 
 
+def q5_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:
+    """(n, k/256*176) uint8 Q5_K super-blocks: the Q4_K header (d, dmin, 12 packed 6-bit scales and mins), 32 bytes of
+    high bits, 128 bytes of low nibbles, both uniform random bytes (5-bit quants uniform in [0, 31])"""
+    g = _gen(seed, device)
+    nb = k // 256
+    head = q4_k_raw(n, k, seed=seed, device=device, lo=lo, hi=hi).reshape(n, nb, 144)[:, :, :16]
+    bits = torch.randint(0, 256, (n, nb, 160), generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+    return torch.cat([head, bits], dim=-1).reshape(n, nb * 176)
+
+
 def q6_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:
     """(n, k/256*210) uint8 Q6_K super-blocks: ql (low nibbles), qh (2-bit highs), 16 int8 scales, fp16 d
     (reference src/mashbox/ops/reference.py:164-173: value 128g + 32r + i takes nibble r // 2 of ql[64g + 32 (r % 2) + i]
@@ -102,9 +112,10 @@ CONFIGS = {
 # the reference's largest published per-call number: a Q6_K output head, 151936 x 2560, one activation row
 # (reference CORE-CHANGES.md:73, 369.8 us on TPU v6e-1)
 # batched decode over one 27B-class layer at the reference engine's row buckets 4 and 16 (runtime/engine.py:424-428):
-# Q4_K, Q8_0, Q6_K and int8 weights, each repacked into 16-row tiles (as config 4 takes int8)
+# Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, each repacked into 16-row tiles (as config 4 takes int8)
 EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          "m4_q4k": (12, 4, LAYER_27B), "m16_q4k": (12, 16, LAYER_27B), "m4_q8": (8, 4, LAYER_27B), "m16_q8": (8, 16, LAYER_27B),
+         "m4_q5k": (13, 4, LAYER_27B), "m16_q5k": (13, 16, LAYER_27B),
          "m4_q6k": (14, 4, LAYER_27B), "m16_q6k": (14, 16, LAYER_27B),
          "m4_int8": ("int8", 4, LAYER_27B), "m16_int8": ("int8", 16, LAYER_27B)}
 REF_TPU_US = {"q6k_head": 369.8}

@@ -1,6 +1,6 @@
 // Host repack round trips, built alone under AddressSanitizer + UndefinedBehaviorSanitizer (and ThreadSanitizer) by
 // tests/test_host_sanitizers.py: every buffer is allocated at its exact size, so a read or write one byte past a
-// plane or a row is reported. For each GGUF type, Q4_K, Q6_K and Q8_0 in 16-row tiles and the tiled int8 planes, at shapes that run
+// plane or a row is reported. For each GGUF type, Q4_K, Q5_K, Q6_K and Q8_0 in 16-row tiles and the tiled int8 planes, at shapes that run
 // on one host thread and on several:
 //   * repack into a buffer full of 0xAB, unpack, and compare with the input bytes;
 //   * the alignment padding between planes (and the int8 tiles' padding rows and columns) reads zero;
@@ -88,7 +88,7 @@ static void int8_case(int64_t rows, int64_t cols) {
 }
 
 int main() {
-    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_Q4KT, T_Q8T, T_Q6KT};
+    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_Q4KT, T_Q8T, T_Q6KT, T_Q5KT};
     const int64_t shapes[][2] = {{1, 256}, {3, 512}, {63, 768}, {64, 256}, {130, 1024}, {517, 256}};
     for (int t : types)
         for (const auto& sh : shapes) gguf_case(t, sh[0], sh[1]);

@@ -1,6 +1,6 @@
-"""GPU parity of Q4_K, Q8_0 and Q6_K weights repacked at load into 16-row tiles (kernels.repack(..., tiled=True),
-libmbq's MBQ_Q4KT, MBQ_Q8T and MBQ_Q6KT planes) against the reference's dequantization (reference
-src/mashbox/ops/reference.py:132-149, :101-103, :164-173) and its dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
+"""GPU parity of Q4_K, Q8_0, Q6_K and Q5_K weights repacked at load into 16-row tiles (kernels.repack(..., tiled=True),
+libmbq's MBQ_Q4KT, MBQ_Q8T, MBQ_Q6KT and MBQ_Q5KT planes) against the reference's dequantization (reference
+src/mashbox/ops/reference.py:132-149, :101-103, :164-173, :150-159) and its dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
 
 Oracle: oracle.ref's dequantization of the same blocks (bit for bit for dequant, take_rows and the repack) and the
 float64 product of those weights (tests/_check.py bars). Batches of 1-64 rows run the K-group kernel (mbq_kgemm.hip),
@@ -21,8 +21,8 @@ from mashbox_amd import _lib as LIB
 from mashbox_amd import kernels as KQ
 
 pytestmark = pytest.mark.gpu
-TYPES = [R.Q4_K, R.Q8_0, R.Q6_K]
-NAME = {R.Q4_K: "Q4_K", R.Q8_0: "Q8_0", R.Q6_K: "Q6_K"}
+TYPES = [R.Q4_K, R.Q8_0, R.Q6_K, R.Q5_K]
+NAME = {R.Q4_K: "Q4_K", R.Q8_0: "Q8_0", R.Q6_K: "Q6_K", R.Q5_K: "Q5_K"}
 
 
 def _x(rng, m, k, dev):
@@ -234,7 +234,7 @@ def test_kgroup_graph_replays(t, forced_plan, cuda):
 
 @pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 def test_ops_prepare_loads_tiles(t, monkeypatch, cuda):
-    """with MBQ_TILES=1 the ops layer loads Q4_K, Q8_0 and Q6_K weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
+    """with MBQ_TILES=1 the ops layer loads Q4_K, Q8_0, Q6_K and Q5_K weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
     layer= in place and dequant against the oracle; device_nbytes counts the tiled planes"""
     from mashbox_amd import ops
     monkeypatch.setenv("MBQ_TILES", "1")
