@@ -62,6 +62,9 @@ extern "C" {
 /* Q5_K weights in 16-row tiles, as MBQ_Q4KT (low nibbles and super-block headers tiled the same way) plus the high-bit
  * words tiled by 16 rows x 128 values. Dequant bit for bit, matmul the same bars. Not a ggml type. */
 #define MBQ_Q5KT (-13)
+/* Q4_0 weights in 16-row tiles, as MBQ_Q4KT (16 rows x 128 values of 16-byte units per KiB), the blocks' fp16 scales
+ * tiled beside them; K a multiple of 32 (the last chunk's blocks past K are zero padding). Not a ggml type. */
+#define MBQ_Q40T (-11)
 
 #define MBQ_OUT_F32 0
 #define MBQ_OUT_BF16 1
@@ -185,7 +188,7 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
- *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT) at M <= 64:
+ *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T and the tiled GGUF types) at M <= 64:
  *                      bm = 16, bn = weight rows per block (any count: N is cut into equal ranges that fill the
  *                      CUs), splits = K ranges. The automatic plan of tiled planes up to 64 rows (they have no
  *                      GEMV or weight-stream plan).

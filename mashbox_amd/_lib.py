@@ -9,7 +9,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("MBQ_LIB", os.path.join(HERE, "libmbq.so"))
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, INT8, I8T = 2, 8, 12, 13, 14, -8, -9
-Q8T, Q4KT, Q5KT, Q6KT = -10, -12, -13, -14   # Q8_0 and K-quant planes in 16-row tiles (MBQ_Q8T, MBQ_Q4KT, ...)
+Q8T, Q40T, Q4KT, Q5KT, Q6KT = -10, -11, -12, -13, -14   # the GGUF types' planes in 16-row tiles (MBQ_Q8T, ...)
 OUT_F32, OUT_BF16 = 0, 1
 
 # every symbol include/mbq.h declares, with its ctypes signature

@@ -30,8 +30,8 @@ int set_error(int code, const char* fmt, ...) {
 
 // the ggml types with kernel planes
 static bool is_type(int t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
-// plane types made from a ggml type's blocks: the ggml types' own, and the K-quants and Q8_0 in 16-row tiles
-static bool is_block_planes(int t) { return is_type(t) || t == T_Q4KT || t == T_Q8T || t == T_Q6KT || t == T_Q5KT; }
+// plane types made from a ggml type's blocks: the ggml types' own, and each in 16-row tiles
+static bool is_block_planes(int t) { return is_type(t) || t == T_Q4KT || t == T_Q8T || t == T_Q6KT || t == T_Q5KT || t == T_Q40T; }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -40,7 +40,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 static int check_shape(int t, int64_t rows, int64_t cols) {
     if (!is_block_planes(t))
         return set_error(MBQ_BAD_ARG, "type %d has no kernel planes (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, "
-                                      "tiled Q8_0 = -10, tiled Q4_K = -12, tiled Q5_K = -13, tiled Q6_K = -14)", t);
+                                      "tiled Q8_0 = -10, tiled Q4_0 = -11, tiled Q4_K = -12, tiled Q5_K = -13, tiled Q6_K = -14)", t);
     if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
     if (cols % block_values(t))
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,

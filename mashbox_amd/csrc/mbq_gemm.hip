@@ -48,6 +48,7 @@ template <int T> struct BUnit;
 template <> struct BUnit<T_Q4_K> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4KT> { u32x4 q, meta; };
 template <> struct BUnit<T_Q4_0> { u32x4 q; uint32_t d; };
+template <> struct BUnit<T_Q40T> { u32x4 q; uint32_t d; };
 template <> struct BUnit<T_Q8_0> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_Q8T> { u32x4 q0, q1; uint32_t d; };
 template <> struct BUnit<T_INT8> { u32x4 q0, q1; };
@@ -75,6 +76,7 @@ __device__ __forceinline__ BOff b_off(int64_t sc_off, int64_t hi_off, int64_t d_
         return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), (uint32_t)(hi_off + bn * (K >> 3) + 4 * u), 0};
     else if constexpr (T == T_Q4_K) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 8) * 16), 0, 0};
     else if constexpr (T == T_Q4KT) return BOff{(uint32_t)(q4kt_off(bn, K) + 16 * u), (uint32_t)(sc_off + q4kt_meta_off(bn, K)), 0, 0};
+    else if constexpr (T == T_Q40T) return BOff{(uint32_t)(q40t_off(bn, K) + 16 * u), (uint32_t)(sc_off + q40t_d_off(bn, K) + 2 * u), 0, 0};
     else if constexpr (T == T_Q4_0) return BOff{(uint32_t)(bn * (K >> 1) + 16 * u), (uint32_t)(sc_off + bn * (K >> 5) * 2 + 2 * u), 0, 0};
     else if constexpr (T == T_I8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 32 * u), 0, 0, 0};   // 16-row tiles
     else if constexpr (T == T_Q8T) return BOff{(uint32_t)(i8t_off(bn, K, 0) + 8 * u), (uint32_t)(sc_off + q8t_d_off(bn, K) + 2 * u), 0, 0};
@@ -106,9 +108,10 @@ __device__ __forceinline__ void b_load(BUnit<T>& b, rsrc_t r, const BOff& o, int
         b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
         b.meta = bload16(r, o.s, ((uint32_t)k0 >> 8) * 16);
         if constexpr (T == T_Q5_K) b.h = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, o.h, (uint32_t)k0 >> 3, 0);
-    } else if constexpr (T == T_Q4_0) {
-        b.q = bload16(r, o.q, (uint32_t)k0 >> 1);
-        b.d = bload2(r, o.s, ((uint32_t)k0 >> 5) * 2);
+    } else if constexpr (q40_like(T)) {
+        // T_Q40T: the step's two units in the tile block of values 128 (k0 / 128) .., and their scales beside
+        b.q = bload16(r, o.q, T == T_Q40T ? ((uint32_t)k0 >> 7) * 1024u + (((uint32_t)k0 >> 1) & 63u) : (uint32_t)k0 >> 1);
+        b.d = bload2(r, o.s, T == T_Q40T ? ((uint32_t)k0 >> 7) * 128u + (((uint32_t)k0 >> 5) & 3u) * 2u : ((uint32_t)k0 >> 5) * 2);
         if constexpr (!KFULL) b.d = (k0 + 32 * u < K) ? b.d : 0u;
     } else {
         const uint32_t qk = (T == T_I8T || T == T_Q8T) ? (uint32_t)k0 * 16u : (uint32_t)k0;   // tiles: a KiB per 64 values
@@ -165,7 +168,7 @@ __device__ __forceinline__ BScale b_scale(const BUnit<T>& b, int j) {
         s.a = f16f(b.meta[0]) * (float)sc;                   // exact
         s.b = f16f(b.meta[0] >> 16) * (float)mn;             // exact
         s.c = s.a * 0.0625f;                                 // exact: a power-of-two scale
-    } else if constexpr (T == T_Q4_0) {
+    } else if constexpr (q40_like(T)) {
         s.a = f16f(b.d);
         s.b = 8.f * s.a;                                     // q d - 8 d = (q - 8) d, exact in float32
         s.c = s.a * 0.0625f;
@@ -1014,7 +1017,7 @@ static int choose(int t, const Args& a, Choice* c) {
         return 0;
     }
     if (fk == K_KGROUP && a.M <= WS_MAX_M)
-        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T, MBQ_Q8T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT) only");
+        return set_error(MBQ_BAD_ARG, "the K-group kernel runs tiled planes (MBQ_I8T and the tiled GGUF types) only");
     if (fk == K_STREAM) {
         if (tiled_type(t) && t != T_I8T) return set_error(MBQ_BAD_ARG, "the weight-stream GEMM does not read tiled GGUF planes");
         if (a.M > WS_MAX_M)
@@ -1092,6 +1095,7 @@ int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits) 
         case T_Q8T: rc = pick<T_Q8T>(a, &p); if (!rc) *bm = CANDS<T_Q8T>[p.idx].bm, *bn = CANDS<T_Q8T>[p.idx].bn; break;
         case T_Q6KT: rc = pick<T_Q6KT>(a, &p); if (!rc) *bm = CANDS<T_Q6KT>[p.idx].bm, *bn = CANDS<T_Q6KT>[p.idx].bn; break;
         case T_Q5KT: rc = pick<T_Q5KT>(a, &p); if (!rc) *bm = CANDS<T_Q5KT>[p.idx].bm, *bn = CANDS<T_Q5KT>[p.idx].bn; break;
+        case T_Q40T: rc = pick<T_Q40T>(a, &p); if (!rc) *bm = CANDS<T_Q40T>[p.idx].bm, *bn = CANDS<T_Q40T>[p.idx].bn; break;
         default: return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
     }
     if (rc) return rc;
@@ -1134,6 +1138,7 @@ int launch_gemm(int t, const Args& a, hipStream_t s) {
         case T_Q8T: return launch_gemm_t<T_Q8T>(a, s);
         case T_Q6KT: return launch_gemm_t<T_Q6KT>(a, s);
         case T_Q5KT: return launch_gemm_t<T_Q5KT>(a, s);
+        case T_Q40T: return launch_gemm_t<T_Q40T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no GEMM for type %d", t);
 }

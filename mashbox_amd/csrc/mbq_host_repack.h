@@ -1,4 +1,4 @@
-// Host repack of one weight into kernel planes (Q4_K, Q5_K, Q6_K and Q8_0 also into 16-row tiles), and its inverse (no HIP: also
+// Host repack of one weight into kernel planes (every GGUF type also into 16-row tiles), and its inverse (no HIP: also
 // built alone, under the host sanitizers, by tests/test_host_sanitizers.py). Plane layouts: mbq_layout.h; file blocks: reference
 // src/mashbox/ops/reference.py:66-70 (Q4_0), :101-103 (Q8_0), :132-149 (Q4_K), :150-159 (Q5_K), :164-173 (Q6_K);
 // int8 per-channel weights: reference src/mashbox/models/qwen3_8_27b/model.py:72-82.
@@ -60,6 +60,14 @@ inline int64_t q8_qs_at(int t, int64_t n, int64_t K, int64_t b) {
 }
 inline int64_t q8_d_at(int t, int64_t n, int64_t K, int64_t b) {
     return t == T_Q8T ? q8t_d_off(n, K) + (b / 2) * 64 + (b % 2) * 2 : (n * (K / 32) + b) * 2;
+}
+
+// Q4_0 planes (row-major, or T_Q40T tiles): block b of row n's 16-byte unit in the qs plane, and its fp16 scale
+inline int64_t q40_q_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q40T ? q40t_off(n, K) + (b >> 2) * 1024 + (b & 3) * 16 : n * (K / 2) + b * 16;
+}
+inline int64_t q40_d_at(int t, int64_t n, int64_t K, int64_t b) {
+    return t == T_Q40T ? q40t_d_off(n, K) + (b >> 2) * 128 + (b & 3) * 2 : (n * (K / 32) + b) * 2;
 }
 
 // Q5_K planes (row-major, or T_Q5KT tiles) of row n: unit j of super-block b in the qs and qh planes, and the
@@ -148,14 +156,12 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                 for (int g = 0; g < (t == T_Q8T ? 4 : 1); ++g)
                     memcpy(planes + L.qs_off + q8_qs_at(t, n, K, b) + 16 * g, row + b * bb + 2 + 8 * g, t == T_Q8T ? 8 : 32);
             }
-        } else if (t == T_Q4_0) {
+        } else if (q40_like(t)) {
             // reference src/mashbox/ops/reference.py:66-70: value i (i < 16) is the low nibble of qs[i], value 16 + i
-            // its high nibble (qs at byte 2)
-            uint8_t* q = planes + L.qs_off + n * (K / 2);
-            uint8_t* d = planes + L.sc_off + n * nb * 2;
+            // its high nibble (qs at byte 2); T_Q40T: at the tile offsets
             for (int64_t b = 0; b < nb; ++b) {
                 const uint8_t* src = row + b * bb;
-                memcpy(d + b * 2, src, 2);
+                memcpy(planes + L.sc_off + q40_d_at(t, n, K, b), src, 2);
                 uint32_t unit[4] = {0, 0, 0, 0};
                 for (int i = 0; i < 32; ++i) {
                     const uint32_t v = (src[2 + (i & 15)] >> (4 * (i >> 4))) & 15u;
@@ -163,7 +169,7 @@ inline void repack_rows(int t, const uint8_t* raw, int64_t K, uint8_t* planes, c
                     q4k_slot(i, &dw, &bit);
                     unit[dw] |= v << bit;
                 }
-                memcpy(q + b * 16, unit, 16);  // little-endian host, as the GPU
+                memcpy(planes + L.qs_off + q40_q_at(t, n, K, b), unit, 16);  // little-endian host, as the GPU
             }
         } else {
             // Q4_K, row-major or in 16-row tiles (T_Q4KT): the same units and headers at the layout's offsets
@@ -243,15 +249,13 @@ inline void unpack_rows(int t, const uint8_t* planes, int64_t K, uint8_t* raw, c
                 for (int g = 0; g < (t == T_Q8T ? 4 : 1); ++g)
                     memcpy(row + b * bb + 2 + 8 * g, planes + L.qs_off + q8_qs_at(t, n, K, b) + 16 * g, t == T_Q8T ? 8 : 32);
             }
-        } else if (t == T_Q4_0) {
-            const uint8_t* q = planes + L.qs_off + n * (K / 2);
-            const uint8_t* d = planes + L.sc_off + n * nb * 2;
+        } else if (q40_like(t)) {
             for (int64_t b = 0; b < nb; ++b) {
                 uint8_t* dst = row + b * bb;
-                memcpy(dst, d + b * 2, 2);
+                memcpy(dst, planes + L.sc_off + q40_d_at(t, n, K, b), 2);
                 memset(dst + 2, 0, 16);
                 uint32_t unit[4];
-                memcpy(unit, q + b * 16, 16);
+                memcpy(unit, planes + L.qs_off + q40_q_at(t, n, K, b), 16);
                 for (int i = 0; i < 32; ++i) {
                     int dw, bit;
                     q4k_slot(i, &dw, &bit);
@@ -328,7 +332,7 @@ inline void i8t_unpack_tiles(const uint8_t* planes, int64_t N, int64_t K, int8_t
 // hardware thread). The caller checks the shape and the buffer sizes.
 inline void repack_host(int t, const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* planes, int threads) {
     const Layout L = layout(t, rows, cols);
-    if (t == T_Q8T || t == T_Q6KT || t == T_Q5KT) memset(planes, 0, (size_t)L.total);   // padding rows (Q8_0: the half chunk past K)
+    if (t == T_Q8T || t == T_Q6KT || t == T_Q5KT || t == T_Q40T) memset(planes, 0, (size_t)L.total);   // padding rows (Q8_0: the half chunk past K)
     for_each_gap(L, [&](int64_t off, int64_t n) { memset(planes + off, 0, (size_t)n); return true; });
     parallel_rows(rows, threads, [&](int64_t a, int64_t b) { repack_rows(t, raw, cols, planes, L, a, b); });
     if (t == T_Q4KT) q4kt_zero_pad_rows(rows, cols, planes, L);

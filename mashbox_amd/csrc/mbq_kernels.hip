@@ -92,9 +92,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
             st16(out + t * 8, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])});
             st16(out + t * 8 + 4, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])});
         }
-    } else if constexpr (T == T_Q4_0) {
-        const u32x4 q = ld16(base + n * (K >> 1) + u * 16);
-        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + (n * (K >> 5) + u) * 2));
+    } else if constexpr (q40_like(T)) {
+        constexpr bool TL = T == T_Q40T;                         // block u: unit u % 4 of chunk u / 4 in the tiles
+        const u32x4 q = ld16(base + (TL ? q40t_off(n, K) + (u >> 2) * 1024 + (u & 3) * 16 : n * (K >> 1) + u * 16));
+        const float d = f16f(*reinterpret_cast<const uint16_t*>(base + sc_off + (TL ? q40t_d_off(n, K) + (u >> 2) * 128 + (u & 3) * 2 : (n * (K >> 5) + u) * 2)));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             float v[8];
@@ -248,13 +249,13 @@ int launch_zero(uint8_t* p, int64_t n, hipStream_t s) {
 template <int T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ raw, int N, int K, uint8_t* __restrict__ planes,
                                                      int64_t sc_off, int64_t hi_off, int64_t d_off) {
-    const int bv = (q8_like(T) || T == T_Q4_0) ? 32 : 256;
-    const int bb = (T == T_Q4_0) ? 18 : q8_like(T) ? 34 : q4k_like(T) ? 144 : q5k_like(T) ? 176 : 210;
+    const int bv = (q8_like(T) || q40_like(T)) ? 32 : 256;
+    const int bb = q40_like(T) ? 18 : q8_like(T) ? 34 : q4k_like(T) ? 144 : q5k_like(T) ? 176 : 210;
     const int64_t nb = K / bv;
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    // tiles: the last tile's padding rows too, and for T_Q8T the padding half-chunk past K (written zero)
+    // tiles: the last tile's padding rows too, and for T_Q8T / T_Q40T the padding blocks of the last chunk (written zero)
     const int64_t rows = tiled_type(T) ? ((int64_t)N + 15) / 16 * 16 : N;
-    const int64_t nbr = T == T_Q8T ? ((int64_t)K + 63) / 64 * 2 : nb;
+    const int64_t nbr = T == T_Q8T ? ((int64_t)K + 63) / 64 * 2 : T == T_Q40T ? ((int64_t)K + 127) / 128 * 4 : nb;
     if (g >= rows * nbr) return;
     const int64_t n = g / nbr, b = g % nbr;
     const bool live = n < N && b < nb;
@@ -271,14 +272,16 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
         uint8_t* d = planes + sc_off + (n * nb + b) * 2;
         d[0] = src[0];
         d[1] = src[1];
-    } else if constexpr (T == T_Q4_0) {
-        uint8_t* d = planes + sc_off + (n * nb + b) * 2;
-        d[0] = src[0];
-        d[1] = src[1];
-        uint32_t* dst = reinterpret_cast<uint32_t*>(planes + n * (K >> 1) + b * 16);
+    } else if constexpr (q40_like(T)) {
+        // T_Q40T: at the tile offsets; rows past N and blocks past K (the last chunk's padding) written zero
+        constexpr bool TL = T == T_Q40T;
+        uint8_t* d = planes + sc_off + (TL ? q40t_d_off(n, K) + (b >> 2) * 128 + (b & 3) * 2 : (n * nb + b) * 2);
+        d[0] = live ? src[0] : 0;
+        d[1] = live ? src[1] : 0;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(planes + (TL ? q40t_off(n, K) + (b >> 2) * 1024 + (b & 3) * 16 : n * (K >> 1) + b * 16));
         for (int t = 0; t < 4; ++t) {
             uint32_t v = 0;
-            for (int e = 0; e < 8; ++e) {
+            for (int e = 0; e < 8 && live; ++e) {
                 const int i = t * 8 + e;                               // slot of mbq_layout.h: dword i/8, bits 16 (e&1) + 4 (e/2)
                 v |= ((uint32_t)(src[2 + (i & 15)] >> (4 * (i >> 4))) & 15u) << (16 * (e & 1) + 4 * (e >> 1));
             }
@@ -488,6 +491,7 @@ int launch_matmul(int t, const Args& a, hipStream_t s) {
         case T_Q8T: return launch_t<T_Q8T>(a, s);
         case T_Q6KT: return launch_t<T_Q6KT>(a, s);
         case T_Q5KT: return launch_t<T_Q5KT>(a, s);
+        case T_Q40T: return launch_t<T_Q40T>(a, s);
     }
     return set_error(MBQ_BAD_ARG, "no kernel for type %d", t);
 }
@@ -507,6 +511,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
     else if (t == T_Q8T) run(dequant_kernel<T_Q8T>);
     else if (t == T_Q6KT) run(dequant_kernel<T_Q6KT>);
     else if (t == T_Q5KT) run(dequant_kernel<T_Q5KT>);
+    else if (t == T_Q40T) run(dequant_kernel<T_Q40T>);
     else if (t == T_Q5_K) run(dequant_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(dequant_kernel<T_Q6_K>);
     else run(dequant_kernel<T_Q8_0>);
@@ -515,6 +520,7 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
 
 int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* planes, const Layout& L, hipStream_t s) {
     const int64_t blocks = t == T_Q8T ? (N + 15) / 16 * 16 * ((K + 63) / 64 * 2)
+                           : t == T_Q40T ? (N + 15) / 16 * 16 * ((K + 127) / 128 * 4)
                                       : (tiled_type(t) ? (N + 15) / 16 * 16 : N) * (K / block_values(t));
     const dim3 grid((unsigned)((blocks + 255) / 256));
     auto run = [&](auto kern) { kern<<<grid, 256, 0, s>>>(raw, (int)N, (int)K, planes, L.sc_off, L.hi_off, L.d_off); };
@@ -524,6 +530,7 @@ int launch_repack(int t, const uint8_t* raw, int64_t N, int64_t K, uint8_t* plan
     else if (t == T_Q8T) run(repack_kernel<T_Q8T>);
     else if (t == T_Q6KT) run(repack_kernel<T_Q6KT>);
     else if (t == T_Q5KT) run(repack_kernel<T_Q5KT>);
+    else if (t == T_Q40T) run(repack_kernel<T_Q40T>);
     else if (t == T_Q5_K) run(repack_kernel<T_Q5_K>);
     else if (t == T_Q6_K) run(repack_kernel<T_Q6_K>);
     else run(repack_kernel<T_Q8_0>);

@@ -64,9 +64,9 @@ struct KgmArgs {
     int fenced;                    // S > 1: ws is cached memory: release / acquire around the exchange
 };
 
-// K values per chunk: one KiB of a 16-row weight tile (int8, Q8_0: 64 values; the K-quants: 128, four 32-value units
-// per row of low nibbles)
-constexpr int kgm_cw(int t) { return (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT) ? 128 : 64; }
+// K values per chunk: one KiB of a 16-row weight tile (int8, Q8_0: 64 values; the K-quants and Q4_0: 128, four 32-value
+// units per row of nibbles)
+constexpr int kgm_cw(int t) { return (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT || t == T_Q40T) ? 128 : 64; }
 // bytes of one x stage: 16 MT rows of one chunk of bfloat16 values
 constexpr size_t kgm_stage(int t, int mt) { return (size_t)16 * mt * 2 * kgm_cw(t); }
 // most dynamic LDS a block may take (160 KiB per CU, less a little for the static variables)
@@ -109,7 +109,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     __shared__ int kgm_last;
     constexpr bool Q6 = T == T_Q6KT;                     // Q6_K tiles (the Q4_K tiles' chunks and lane units)
     constexpr bool Q5 = T == T_Q5KT;                     // Q5_K tiles (Q4_K's, plus a high-bit word per unit)
-    constexpr bool QK = T == T_Q4KT || Q5 || Q6;         // K-quant tiles
+    constexpr bool Q40 = T == T_Q40T;                    // Q4_0 tiles (Q4_K's units, one fp16 scale per unit)
+    constexpr bool QK = T == T_Q4KT || Q5 || Q6 || Q40;  // nibble-unit tiles
     constexpr bool Q8 = T == T_Q8T;                      // Q8_0 tiles (else int8 tiles)
     constexpr int CW = kgm_cw(T);                        // K values per chunk
     constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
@@ -159,8 +160,9 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     for (int j = 0; j < NTW; ++j) {
         const int row = 16 * (t0 + j) + r16;
         const bool in = row >= rq0 && row < rq1;
-        wo[j] = in ? (uint32_t)(QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
-        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg : QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K)))
+        wo[j] = in ? (uint32_t)(Q40 ? q40t_off(row, K) : QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
+        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg : Q40 ? q40t_d_off(row, K) + 2 * lg
+                                                         : QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K)))
                                  : OOB_VOFF;
         ho[j] = in && (Q5 || Q6) ? (uint32_t)(g.hi_off + (Q6 ? q6kt_h_off(row, K) + 8 * lg : q5kt_h_off(row, K) + 4 * lg)) : OOB_VOFF;
         dq[j] = in && Q6 ? (uint32_t)(g.d_off + q6kt_d_off(row, K)) : OOB_VOFF;
@@ -219,6 +221,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                                     wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 512u : 0u, 2));
                 H[j] = u32x4{h[0], h[1], bload2(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u),
                              bload2(wr, live ? dq[j] : OOB_VOFF, live ? (uint32_t)(c >> 1) * 32u : 0u)};
+            } else if constexpr (Q40) {
+                H[j][0] = bload2(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u);   // the unit's block scale
             } else if constexpr (QK) {
                 H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
                                                                                       live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
@@ -260,6 +264,12 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         if constexpr (Q6) {
 #pragma unroll
             for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q6_K>(q6raw(W[U][j], H[U][j]), 0);
+        } else if constexpr (Q40) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                const float d = f16f(H[U][j][0]);
+                qs[j] = WsScale{d, 8.f * d, d * 0.0625f, 0.f};          // d q - 8 d = (q - 8) d, exact in float32
+            }
         } else if constexpr (Q5) {
             const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
@@ -469,7 +479,7 @@ constexpr int KGM_MAX_NTW = 6;
 // Q4_K at 33-64 rows and Q6_K from 17 rows 5; Q5_K 5 at 17-32 and 49-64 rows, 4 at 33-48 (three stages deep)
 constexpr int kgm_max_ntw(int t, int mt) {
     return t == T_Q5KT ? (mt == 1 ? KGM_MAX_NTW : mt == 3 ? 4 : 5)
-                       : (t == T_Q4KT && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
+                       : ((t == T_Q4KT || t == T_Q40T) && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
 }
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
@@ -497,8 +507,8 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
     const int MT = (int)((M + 15) / 16);
-    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q5KT ? 88.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
-    const double waste_w = (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
+    const double wpc = t == T_Q4KT ? 72.0 : t == T_Q40T ? 72.0 : t == T_Q5KT ? 88.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
+    const double waste_w = (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT || t == T_Q40T) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
     KgmPlan best{0, 0, 0, 0};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
@@ -615,6 +625,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
     if (t == T_Q6KT) return kgm_launch_mt<T_Q6KT, true>(a, p, w, s);
     if (t == T_Q5KT) return kgm_launch_mt<T_Q5KT, true>(a, p, w, s);
+    if (t == T_Q40T) return a.K % 128 == 0 ? kgm_launch_mt<T_Q40T, true>(a, p, w, s) : kgm_launch_mt<T_Q40T, false>(a, p, w, s);
     if (t == T_Q8T) return a.K % 64 == 0 ? kgm_launch_mt<T_Q8T, true>(a, p, w, s) : kgm_launch_mt<T_Q8T, false>(a, p, w, s);
     return a.K % 64 == 0 ? kgm_launch_mt<T_I8T, true>(a, p, w, s) : kgm_launch_mt<T_I8T, false>(a, p, w, s);
 }

@@ -49,6 +49,12 @@
 //                                  12 scale bytes, as stored) of super-block sb of rows 16 rt .. 16 rt + 15
 //   padding rows are zero (d = dmin = 0: value 0)
 //
+//   Q4_0 in 16-row tiles (MBQ_Q40T planes, repacked once at load from the same Q4_0 blocks; internal type T_Q40T)
+//     qs   (NP / 16, KP / 128) blocks of 1 KiB (KP = K rounded up to 128): row r at 64 r, the four units of the chunk
+//                                  (the row-major qs plane's bytes), as MBQ_Q4KT's
+//     d    (NP / 16, KP / 128) blocks of 128 B: row r at 8 r, the fp16 scales of the chunk's four blocks
+//   rows past N and blocks past K are zero (scale 0)
+//
 //   Q5_K in 16-row tiles (MBQ_Q5KT planes, repacked once at load from the same Q5_K blocks; internal type T_Q5KT): the
 //   low nibbles and the super-block headers as MBQ_Q4KT's, and the high bits in (NP / 16, K / 128) blocks of 256 B
 //   (row r at 16 r: the chunk's four units' 4-byte words); rows past N zero
@@ -77,10 +83,10 @@
 namespace mbq {
 
 // T_INT8: the caller's row-major int8 weights (mbq_int8_linear); T_I8T: int8 weights repacked into 16-row tiles
-// (mbq_matmul with MBQ_I8T planes); T_Q4KT, T_Q5KT, T_Q6KT and T_Q8T: Q4_K, Q5_K, Q6_K and Q8_0 blocks repacked into
-// 16-row tiles (MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT and MBQ_Q8T planes)
+// (mbq_matmul with MBQ_I8T planes); T_Q40T, T_Q4KT, T_Q5KT, T_Q6KT and T_Q8T: the GGUF types' blocks repacked into
+// 16-row tiles (MBQ_Q40T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT and MBQ_Q8T planes)
 enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9, T_Q8T = -10,
-             T_Q4KT = -12, T_Q5KT = -13, T_Q6KT = -14 };
+             T_Q40T = -11, T_Q4KT = -12, T_Q5KT = -13, T_Q6KT = -14 };
 // int8 types: 16-byte units of 16 values, a per-row float32 scale applied to the sum
 constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
 // T_I8T: bytes between consecutive 16-row tiles of the quant plane, and the byte offset of (row, K offset k0) (k0 a
@@ -104,7 +110,12 @@ constexpr int64_t q6kt_h_off(int64_t row, int64_t k) { return (row >> 4) * (k / 
 constexpr int64_t q6kt_s_off(int64_t row, int64_t k) { return (row >> 4) * (k / 128) * 128 + (row & 15) * 8; }
 constexpr int64_t q6kt_d_off(int64_t row, int64_t k) { return (row >> 4) * (k / 256) * 32 + (row & 15) * 2; }
 // tiled plane types (16-row tiles, any number of rows)
-constexpr bool tiled_type(int t) { return t == T_I8T || t == T_Q4KT || t == T_Q8T || t == T_Q6KT || t == T_Q5KT; }
+constexpr bool tiled_type(int t) { return t == T_I8T || t == T_Q4KT || t == T_Q8T || t == T_Q6KT || t == T_Q5KT || t == T_Q40T; }
+// T_Q40T: offsets of (row, chunk 0) in the qs plane (chunk kc of 128 values at + 1024 kc) and the d plane (+ 128 kc)
+constexpr int64_t q40t_off(int64_t row, int64_t k) { return (row >> 4) * ((k + 127) / 128) * 1024 + (row & 15) * 64; }
+constexpr int64_t q40t_d_off(int64_t row, int64_t k) { return (row >> 4) * ((k + 127) / 128) * 128 + (row & 15) * 8; }
+// the Q4_0 value format, in row-major or tiled planes
+constexpr bool q40_like(int t) { return t == T_Q4_0 || t == T_Q40T; }
 // T_Q5KT: offset of (row, chunk 0) in the high-bit plane (chunk kc at + 256 kc); low nibbles and headers as T_Q4KT's
 constexpr int64_t q5kt_h_off(int64_t row, int64_t k) { return (row >> 4) * (k / 128) * 256 + (row & 15) * 16; }
 // the Q5_K value format, in row-major or tiled planes
@@ -122,9 +133,9 @@ constexpr bool kquant(int t) {
 }
 // types whose kernel unit is 16 bytes of nibbles for 32 values (the K-quants and Q4_0); Q8_0 and int8 units are 16
 // bytes for 16 values
-constexpr bool unit32(int t) { return kquant(t) || t == T_Q4_0; }
+constexpr bool unit32(int t) { return kquant(t) || q40_like(t); }
 // Q4_0 and Q4_K: a unit's 16 bytes are the whole 4-bit quants, in the Q4_K order
-constexpr bool nib4(int t) { return q4k_like(t) || t == T_Q4_0; }
+constexpr bool nib4(int t) { return q4k_like(t) || q40_like(t); }
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
@@ -135,9 +146,9 @@ struct Layout {
 };
 
 // values and file bytes of one block (T_Q4KT planes are made from Q4_K blocks)
-inline int block_values(int t) { return (q8_like(t) || t == T_Q4_0) ? 32 : kquant(t) ? 256 : 0; }
+inline int block_values(int t) { return (q8_like(t) || q40_like(t)) ? 32 : kquant(t) ? 256 : 0; }
 inline int block_bytes(int t) {
-    return t == T_Q4_0 ? 18 : q8_like(t) ? 34 : q4k_like(t) ? 144 : q5k_like(t) ? 176 : q6k_like(t) ? 210 : 0;
+    return q40_like(t) ? 18 : q8_like(t) ? 34 : q4k_like(t) ? 144 : q5k_like(t) ? 176 : q6k_like(t) ? 210 : 0;
 }
 
 inline Layout layout(int t, int64_t n, int64_t k) {
@@ -162,6 +173,10 @@ inline Layout layout(int t, int64_t n, int64_t k) {
     } else if (t == T_Q8T) {
         const int64_t np = (n + 15) / 16 * 16, kp = (k + 63) / 64 * 64;
         L.qs_bytes = np * kp;
+        L.sc_bytes = np * (kp / 16);
+    } else if (t == T_Q40T) {
+        const int64_t np = (n + 15) / 16 * 16, kp = (k + 127) / 128 * 128;
+        L.qs_bytes = np * (kp / 2);
         L.sc_bytes = np * (kp / 16);
     } else if (t == T_Q5KT) {
         const int64_t np = (n + 15) / 16 * 16;

@@ -26,17 +26,17 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import INT8, OUT_BF16, OUT_F32, Q4_0, Q4_K, Q4KT, Q5_K, Q5KT, Q6_K, Q6KT, Q8_0, Q8T, check, lib
+from ._lib import INT8, OUT_BF16, OUT_F32, Q4_0, Q40T, Q4_K, Q4KT, Q5_K, Q5KT, Q6_K, Q6KT, Q8_0, Q8T, check, lib
 
 # the types the reference's kernel package gives planes (reference src/mashbox/ops/bundle.py:39)
 TYPES = frozenset({Q4_0, Q8_0, Q4_K, Q5_K, Q6_K})
 NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", Q4KT: "Q4_K tiled", Q8T: "Q8_0 tiled",
-         Q5KT: "Q5_K tiled", Q6KT: "Q6_K tiled"}
+         Q5KT: "Q5_K tiled", Q6KT: "Q6_K tiled", Q40T: "Q4_0 tiled"}
 # values and bytes per block (reference ops/reference.py:22-29)
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 # ggml types whose blocks also repack into 16-row tiles (repack(..., tiled=True)), and the plane type they take: every
 # wave-wide weight load of a 16-row MFMA tile is one contiguous KiB (the layout for decode batches of several rows)
-TILED = {Q4_K: Q4KT, Q8_0: Q8T, Q5_K: Q5KT, Q6_K: Q6KT}
+TILED = {Q4_0: Q40T, Q4_K: Q4KT, Q8_0: Q8T, Q5_K: Q5KT, Q6_K: Q6KT}
 picks_layer = True
 version = "0.1.0"
 
@@ -241,4 +241,4 @@ def take_rows(p: Planes, ids, layer=None) -> torch.Tensor:
 
 
 __all__ = ["TYPES", "TILED", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers",
-           "picks_layer", "row_bytes", "INT8", "Q4KT", "Q8T", "Q5KT", "Q6KT"]
+           "picks_layer", "row_bytes", "INT8", "Q4KT", "Q8T", "Q5KT", "Q6KT", "Q40T"]

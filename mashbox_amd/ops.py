@@ -30,7 +30,7 @@ on the host's CPU; without libmbq.so every call raises. The forced-failure switc
 (force:kernels-package, force:quant-kernel; reference src/mashbox/runtime/faults.py:14-16,57-61).
 
 Layout switch of this build (no counterpart in the reference): with env MBQ_TILES=1, weights of the types the kernel
-package can tile (its TILED map: Q4_K, Q5_K, Q6_K and Q8_0) load as 16-row tiles instead of row-major planes, the faster layout for decode
+package can tile (its TILED map: every GGUF type it serves) load as 16-row tiles instead of row-major planes, the faster layout for decode
 batches of several rows; everything else is unchanged.
 """
 from __future__ import annotations

@@ -1,6 +1,6 @@
 // Host repack round trips, built alone under AddressSanitizer + UndefinedBehaviorSanitizer (and ThreadSanitizer) by
 // tests/test_host_sanitizers.py: every buffer is allocated at its exact size, so a read or write one byte past a
-// plane or a row is reported. For each GGUF type, Q4_K, Q5_K, Q6_K and Q8_0 in 16-row tiles and the tiled int8 planes, at shapes that run
+// plane or a row is reported. For each GGUF type, every GGUF type in 16-row tiles and the tiled int8 planes, at shapes that run
 // on one host thread and on several:
 //   * repack into a buffer full of 0xAB, unpack, and compare with the input bytes;
 //   * the alignment padding between planes (and the int8 tiles' padding rows and columns) reads zero;
@@ -88,11 +88,11 @@ static void int8_case(int64_t rows, int64_t cols) {
 }
 
 int main() {
-    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_Q4KT, T_Q8T, T_Q6KT, T_Q5KT};
+    const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_Q4KT, T_Q8T, T_Q6KT, T_Q5KT, T_Q40T};
     const int64_t shapes[][2] = {{1, 256}, {3, 512}, {63, 768}, {64, 256}, {130, 1024}, {517, 256}};
     for (int t : types)
         for (const auto& sh : shapes) gguf_case(t, sh[0], sh[1]);
-    for (int64_t c : {32, 96}) gguf_case(T_Q8_0, 200, c), gguf_case(T_Q8T, 200, c), gguf_case(T_Q4_0, 200, c);
+    for (int64_t c : {32, 96}) gguf_case(T_Q8_0, 200, c), gguf_case(T_Q8T, 200, c), gguf_case(T_Q4_0, 200, c), gguf_case(T_Q40T, 200, c);
     const int64_t i8[][2] = {{1, 16}, {15, 48}, {16, 64}, {17, 80}, {100, 4112}, {1040, 128}, {33, 1000 * 16}};
     for (const auto& sh : i8) int8_case(sh[0], sh[1]);
     if (g_fail) {

@@ -248,7 +248,7 @@ def test_q4_k_tiled_repack_is_lossless(n, kb):
     assert L.lib().mbq_has_type(L.Q4KT) == 0 and L.lib().mbq_row_bytes(L.Q4KT, k) < 0     # not a ggml type
     assert L.lib().mbq_dequant_raw(L.Q4KT, None, n, k, None, None) < 0                    # its blocks are Q4_K's
     with pytest.raises(NotImplementedError):
-        KQ.repack_host(R.Q4_0, np.zeros((1, 18), np.uint8), (1, 32), tiled=True)
+        KQ.repack_host(99, np.zeros((1, 18), np.uint8), (1, 32), tiled=True)
 
 
 @pytest.mark.parametrize("n,kb", [(1, 1), (17, 2), (130, 3)])

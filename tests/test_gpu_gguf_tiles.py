@@ -1,4 +1,4 @@
-"""GPU parity of Q4_K, Q8_0, Q6_K and Q5_K weights repacked at load into 16-row tiles (kernels.repack(..., tiled=True),
+"""GPU parity of every GGUF type's weights (Q4_K, Q8_0, Q6_K, Q5_K, Q4_0) repacked at load into 16-row tiles (kernels.repack(..., tiled=True),
 libmbq's MBQ_Q4KT, MBQ_Q8T, MBQ_Q6KT and MBQ_Q5KT planes) against the reference's dequantization (reference
 src/mashbox/ops/reference.py:132-149, :101-103, :164-173, :150-159) and its dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
 
@@ -21,8 +21,8 @@ from mashbox_amd import _lib as LIB
 from mashbox_amd import kernels as KQ
 
 pytestmark = pytest.mark.gpu
-TYPES = [R.Q4_K, R.Q8_0, R.Q6_K, R.Q5_K]
-NAME = {R.Q4_K: "Q4_K", R.Q8_0: "Q8_0", R.Q6_K: "Q6_K", R.Q5_K: "Q5_K"}
+TYPES = [R.Q4_K, R.Q8_0, R.Q6_K, R.Q5_K, R.Q4_0]
+NAME = {R.Q4_K: "Q4_K", R.Q8_0: "Q8_0", R.Q6_K: "Q6_K", R.Q5_K: "Q5_K", R.Q4_0: "Q4_0"}
 
 
 def _x(rng, m, k, dev):
@@ -74,11 +74,13 @@ def test_matmul_matches_reference(t, n, k, m, cuda):
     _matmul_case(t, n, k, m, cuda)
 
 
+@pytest.mark.parametrize("t", [R.Q8_0, R.Q4_0], ids=NAME.get)
 @pytest.mark.parametrize("n,k", [(33, 96), (100, 1056), (7, 32)])
 @pytest.mark.parametrize("m", [1, 4, 16, 33, 64, 65, 130])
-def test_q8_0_ragged_k(n, k, m, cuda):
-    """Q8_0 rows of an odd number of 32-value blocks: the tiles' last chunk is half padding (zero quants, zero scale)"""
-    _matmul_case(R.Q8_0, n, k, m, cuda)
+def test_ragged_k(t, n, k, m, cuda):
+    """Q8_0 and Q4_0 rows whose blocks do not fill the tiles' last chunk (64 values for Q8_0, 128 for Q4_0): its
+    remaining blocks are padding (zero quants, zero scale)"""
+    _matmul_case(t, n, k, m, cuda)
 
 
 def _matmul_case(t, n, k, m, cuda):
