@@ -13,14 +13,20 @@ over the 27B-class layer at 4 and 16 activation rows (`m4_q4k`, `m16_q4k`, `m4_q
 `m16_q5k`, `m4_q6k`, `m16_q6k`, `m4_int8`, `m16_int8`: the reference engine's row buckets; Q4_K, Q8_0, Q5_K, Q6_K and
 int8 weights in 16-row tiles).
 
-Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) that cycles through >= 1 GiB of
-distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for W warmup launches, then once
-for K timed launches bracketed by torch.cuda.synchronize() and HIP events on the stream the kernels run on. The kernel's
-average launch duration is the event time / K. Beside it, `eager_call_us` is the end-to-end time of back-to-back eager
-ctypes calls through the C ABI, timed on the host (argument checks, plan, launch and kernel; up to 50 calls). The CPU
+Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) of K launches that cycles through
+>= 1 GiB of distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for warmup, then R
+times (R >= 5 and R * K >= 100), each replay bracketed by torch.cuda.synchronize() and timed with HIP events on the
+stream the kernels run on. A projection's launch time is the median over the R replays of (replay time / K), so every
+figure is the median of >= 100 timed launches whatever K is; `mean_us` beside it is the mean over all of them. Beside
+it, `eager_call_us` is the end-to-end time of back-to-back eager ctypes calls through the C ABI, timed on the host
+(argument checks, plan, launch and kernel; up to 50 calls). Rows `c2_ops`, `c5_ops` and `m4_q4k_ops` time the same
+work through mashbox_amd.ops.qmatmul (prepare's default layout, the result in x's dtype), the caller's path. The CPU
 baseline is the oracle's restatement of mashbox's exact path
 (rebuild float32 weights per call, float32 dot; int8: float32 dot then the scales) on the host's cores, every config at
 full size (a few seconds each); `cpu_baseline` is config 2's.
+
+The one JSON line on stdout carries the contract's fields and one short summary per config (well under the 8,000
+characters a driver keeps); the per-projection detail goes to --detail (default gpurun_out/bench_detail.json).
 
 Profiling modes (rocprofv3 runs of committed files; summaries in profiles/): --pmc-probe [CONFIGS] launches each
 config's projections a few times plus a calibration copy; --summarize-pmc turns a FETCH_SIZE and a WRITE_SIZE run of
@@ -58,9 +64,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# rows timed through mashbox_amd.ops.qmatmul (the caller's path) instead of the C ABI: row -> the config it repeats
+OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k"}
+
+
+def config_of(idx):
+    from mashbox_amd import synth
+    idx = OPS_ROWS.get(idx, idx)
+    return synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
+
+
 def setup_projection(idx, pi, rotate_bytes):
     """one projection of a config, ready to launch: seeded synthetic weights in HBM (repacked as a load would), cycled
-    over >= rotate_bytes of distinct copies -> (launch(copy) -> rc, copies, weight bytes, plan text, (t, M, N, K))"""
+    over >= rotate_bytes of distinct copies -> (launch(copy) -> rc, copies, weight bytes, plan text, (t, M, N, K)).
+    An OPS_ROWS entry loads the GGUF blocks with ops.prepare and launches ops.qmatmul."""
     import torch
     from mashbox_amd import synth
     from mashbox_amd import _lib as LIB
@@ -68,13 +85,34 @@ def setup_projection(idx, pi, rotate_bytes):
 
     L = lib()
     dev = torch.device("cuda", 0)
-    t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
+    via_ops = idx in OPS_ROWS
+    base = OPS_ROWS.get(idx, idx)
+    t, M, projs = config_of(idx)
     name, N, K = projs[pi]
-    seed = (1000 * idx if isinstance(idx, int) else 9000) + pi
+    seed = (1000 * base if isinstance(base, int) else 9000) + pi
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     x = synth.acts(M, K, seed=seed, device=dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    if t == "int8" and M > 1:
+    if via_ops:
+        from mashbox_amd import kernels as KQ
+        from mashbox_amd import ops
+        if ops.kernel_types() == frozenset():
+            ops.load_kernels()
+        raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 13: synth.q5_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
+        h = ops.prepare(raw, t, (N, K))
+        if not isinstance(h, ops.Packed):
+            raise RuntimeError(f"{idx} {name}: ops.prepare gave {h!r}, not kernel planes")
+        del raw
+        p = h.packed
+        wbytes = p.buf.numel()
+        copies = max(1, math.ceil(rotate_bytes / wbytes))
+        hs = [h] + [ops.Packed(KQ.Planes(p.buf.clone(), p.t, p.N, p.K, p.lead), h.t, h.shape) for _ in range(copies - 1)]
+
+        def launch(c):
+            ops.qmatmul(x, hs[c])
+            return 0
+        plan = "ops.qmatmul " + LIB.plan_str(p.t, M, N, K)
+    elif t == "int8" and M > 1:
         # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes; from 2 rows on they run
         # faster than row-major weights: MI355X, 17408 x 5120 at 4 rows 19 vs 36 us)
         q, s = synth.int8_weights(N, K, seed=seed + 7, device=dev)
@@ -126,17 +164,40 @@ def setup_projection(idx, pi, rotate_bytes):
     return launch, copies, wbytes, plan, (t, M, N, K)
 
 
+def time_graph(g, launches, replays):
+    """-> (median, mean) microseconds per launch over `replays` replays of graph g (each holds `launches` launches),
+    each replay bracketed by torch.cuda.synchronize() and timed with HIP events on the current stream"""
+    import statistics
+    import torch
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    per = []
+    for _ in range(replays):
+        torch.cuda.synchronize()
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1000.0 / launches)
+    return statistics.median(per), sum(per) / len(per)
+
+
+def replays_for(steps, min_launches=100, min_replays=5):
+    return max(min_replays, math.ceil(min_launches / max(1, steps)))
+
+
 def run_config(idx, steps, warmup, rotate_bytes):
     import torch
     from mashbox_amd import synth
     from mashbox_amd._lib import check
 
-    t, M, projs = synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
+    t, M, projs = config_of(idx)
+    base = OPS_ROWS.get(idx, idx)
     out = {"projections": {}}
-    total_us = 0.0
-    total_eager_us = 0.0
+    total_us = total_mean_us = total_eager_us = 0.0
     total_bytes = 0
     total_flops = 0
+    replays = replays_for(steps)
     for pi, (name, N, K) in enumerate(projs):
         launch, copies, wbytes, plan, _ = setup_projection(idx, pi, rotate_bytes)
 
@@ -151,18 +212,12 @@ def run_config(idx, steps, warmup, rotate_bytes):
             gw = capture(warmup)
             gw.replay()
         g = capture(steps)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / steps
+        us, mean_us = time_graph(g, steps, replays)
         # end to end through the C ABI: back-to-back eager ctypes calls timed on the host (argument checks, plan,
         # launch, and the kernel), the caller's view when it does not capture a graph
         ne = min(steps, 50)
         rcs = 0
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(ne):
             rcs |= launch(i % copies)
@@ -171,27 +226,29 @@ def run_config(idx, steps, warmup, rotate_bytes):
         check(rcs, f"config {idx} {name} eager calls")
         ab = algorithmic_bytes(t, M, N, K)
         fl = 2 * M * N * K
-        out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "GBps": round(ab / us / 1e3, 1),
-                                    "TFLOPs": round(fl / us / 1e6, 2), "eager_call_us": round(eager_us, 2),
-                                    "rotation_copies": copies, "rotation_MB": round(copies * wbytes / 1e6, 1),
-                                    "plan": plan}
+        out["projections"][name] = {"M": M, "N": N, "K": K, "us": round(us, 3), "mean_us": round(mean_us, 3),
+                                    "GBps": round(ab / us / 1e3, 1), "TFLOPs": round(fl / us / 1e6, 2),
+                                    "eager_call_us": round(eager_us, 2), "rotation_copies": copies,
+                                    "rotation_MB": round(copies * wbytes / 1e6, 1), "plan": plan}
         total_eager_us += eager_us
         total_us += us
+        total_mean_us += mean_us
         total_bytes += ab
         total_flops += fl
         del launch, g
         torch.cuda.empty_cache()
     gbs = total_bytes / total_us / 1e3
     tfl = total_flops / total_us / 1e6
-    out.update({"type": {8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}.get(t, t), "M": M, "us_per_step": round(total_us, 3),
-                "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "TFLOPs": round(tfl, 2),
-                "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4), "eager_us_per_step": round(total_eager_us, 2),
-                "algorithmic_bytes": total_bytes, "flops": total_flops})
-    if idx in synth.REF_TPU_US:
-        out["reference_tpu_v6e_us"] = synth.REF_TPU_US[idx]
-        out["speedup_vs_reference_tpu_v6e"] = round(synth.REF_TPU_US[idx] / total_us, 2)
-    log(f"config {idx}: {out['us_per_step']:.2f} us/step  {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% HBM)  "
-        f"{tfl:.1f} TFLOP/s ({100 * tfl / PEAK_BF16_TFLOPS:.1f}% MFMA)")
+    out.update({"type": {8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}.get(t, t), "M": M,
+                "us_per_step": round(total_us, 3), "mean_us_per_step": round(total_mean_us, 3),
+                "launches_timed": replays * steps, "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                "TFLOPs": round(tfl, 2), "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+                "eager_us_per_step": round(total_eager_us, 2), "algorithmic_bytes": total_bytes, "flops": total_flops})
+    if base in synth.REF_TPU_US:
+        out["reference_tpu_v6e_us"] = synth.REF_TPU_US[base]
+        out["speedup_vs_reference_tpu_v6e"] = round(synth.REF_TPU_US[base] / total_us, 2)
+    log(f"{idx}: {total_us:.2f} us  {gbs:.0f} GB/s {100 * gbs / PEAK_HBM_GBS:.1f}%HBM  "
+        f"{tfl:.1f} TF/s {100 * tfl / PEAK_BF16_TFLOPS:.1f}%MFMA")
     return out
 
 
@@ -457,10 +514,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,m4_int8,m16_int8")
+    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,"
+                                          "m4_int8,m16_int8,c2_ops,c5_ops,m4_q4k_ops")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--detail", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
+                    help="per-projection detail (JSON file; '' = none)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE)")
     ap.add_argument("--pmc-probe", nargs="?", const="1,2,3,4,5", default=None, metavar="CONFIGS",
@@ -494,42 +554,77 @@ def main():
     res = {}
     for c in configs:
         res[c] = run_config(c, a.steps, a.warmup, a.rotate_mb << 20)
-    head = res[HEADLINE]
-    proj = head["projections"]["w"]
     try:
         with open(a.traffic) as f:
             tj = json.load(f)
     except (OSError, ValueError):
         tj = {}
-    traffic = tj.get("c2", {}).get("hbm_bytes_per_launch")
+    peaks = measured_peaks()
+    cpu = None
+    if not a.no_cpu:
+        per, threads = cpu_baselines(a.cpu_seconds)
+        cpu = (per, threads)
+    line, detail = make_line(res, tj, peaks, cpu, a.steps, a.warmup, a.detail)
+    if a.detail:
+        os.makedirs(os.path.dirname(os.path.abspath(a.detail)), exist_ok=True)
+        with open(a.detail, "w") as f:
+            json.dump(detail, f, indent=1)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+
+
+def _key(c):
+    return f"c{c}" if isinstance(c, int) else str(c)
+
+
+def summary(r):
+    """one config's short summary for the JSON line: microseconds per step, the rate of its bound and its fraction"""
+    o = {"us": round(r["us_per_step"], 2)}
+    if r["mfma_frac"] >= 0.1:                      # the prefill GEMM and config 4: MFMA rate beside the HBM rate
+        o.update(TFLOPs=round(r["TFLOPs"], 1), mfma=round(r["mfma_frac"], 3))
+    o.update(GBps=round(r["GBps"]), hbm=round(r["hbm_frac"], 3))
+    if "traffic_over_algorithmic" in r:
+        o["traffic_x"] = round(r["traffic_over_algorithmic"], 3)
+    return o
+
+
+def make_line(res, traffic, peaks, cpu, steps, warmup, detail_path=None):
+    """-> (the one JSON line of the contract, the per-projection detail). res: run_config results by config; traffic:
+    profiles/traffic.json; cpu: (cpu_baselines per config, threads) or None"""
+    head = res[HEADLINE]
+    proj = head["projections"]["w"]
     for c, r in res.items():
-        tc = tj.get(f"c{c}" if isinstance(c, int) else str(c))
+        tc = traffic.get(_key(c))
         if tc and "hbm_bytes_per_launch" in tc:
             r["hbm_traffic_bytes"] = tc["hbm_bytes_per_launch"]
             r["traffic_over_algorithmic"] = round(tc["hbm_bytes_per_launch"] / r["algorithmic_bytes"], 4)
     line = {
-        "metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(head["us_per_step"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded, BASELINE config value ranges, generated on the GPU)",
         "config": {"workload": "config 2: GGUF Q8_0 decode GEMV x bf16[1,5120] @ W[17408,5120]^T, fp32 accumulate, "
                                "bf16 out", "M": 1, "N": 17408, "K": 5120, "weight_type": "Q8_0",
                    "rotation_MB": proj["rotation_MB"]},
+        "timing": f"per launch: median over {replays_for(steps)} graph replays of {steps} launches "
+                  f"({head['launches_timed']} launches), HIP events on the launching stream",
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "frac": round(head["GBps"] / PEAK_HBM_GBS, 4), "traffic": traffic.get("c2", {}).get("hbm_bytes_per_launch"),
                      "kernel": "mbq::gemv_kernel (Q8_0, 1 activation row)", "kernel_us": proj["us"],
-                     "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
-        "configs": {(f"c{c}" if isinstance(c, int) else c): {k: v for k, v in r.items() if k != "projections"}
-                    | {"projections": r["projections"]} for c, r in res.items()},
+                     "kernel_mean_us": proj["mean_us"], "algorithmic_bytes_per_launch": head["algorithmic_bytes"]},
+        "configs": {_key(c): summary(r) for c, r in res.items()},
+        "measured_peaks": {k: v for k, v in peaks.items() if k != "how"},
     }
-    line["measured_peaks"] = measured_peaks()
-    if not a.no_cpu:
-        per, threads = cpu_baselines(a.cpu_seconds)
+    detail = {"configs": {_key(c): r for c, r in res.items()}, "measured_peaks": peaks}
+    if cpu is not None:
+        per, threads = cpu
         line["cpu_baseline"] = cpu_baseline_line(per, threads)
-        line["cpu_baseline_configs"] = per | {"threads": threads, "cpu": _cpu_model(), "os_cpu_count": os.cpu_count(),
-                                              "kind": "port: oracle/ref.py restatement of mashbox's plain-JAX exact path",
-                                              "inputs": "oracle/gen.py seed 0, full BASELINE sizes"}
-    print(json.dumps(line), flush=True)
+        line["cpu_baseline_us"] = {c: v["us_per_step"] for c, v in per.items()}
+        detail["cpu_baseline_configs"] = per | {"threads": threads, "cpu": _cpu_model(), "os_cpu_count": os.cpu_count(),
+                                                "kind": "port: oracle/ref.py restatement of mashbox's plain-JAX exact path",
+                                                "inputs": "oracle/gen.py seed 0, full BASELINE sizes"}
+    if detail_path:
+        line["detail"] = os.path.relpath(os.path.abspath(detail_path), ROOT)
+    return line, detail
 
 
 if __name__ == "__main__":

@@ -8,9 +8,9 @@
  * Conventions
  *   - Plain pointers and sizes only. "dev" pointers are device (HBM) addresses owned by the caller; "host" pointers are
  *     host memory. Every device entry point is stream-ordered on `stream` (a hipStream_t; NULL = the default stream)
- *     and returns before the work finishes; none allocates, except the GEMM's one-time split-K workspace of
- *     mbq_matmul and mbq_int8_linear (see mbq_gemm_plan; mbq_matmul_noalloc never allocates), and none holds a host
- *     lock.
+ *     and returns before the work finishes; none allocates, except the GEMM's split-K workspaces of mbq_matmul
+ *     and mbq_int8_linear, once per stream (see mbq_gemm_plan; mbq_matmul_noalloc never allocates), and none waits on
+ *     the GPU except for that allocation.
  *   - Matrices are row-major. Activations x are bfloat16 bits (uint16) of shape (M, K); results y are (M, N) as
  *     float32 (out_dtype MBQ_OUT_F32) or bfloat16 bits rounded to nearest even (MBQ_OUT_BF16).
  *   - Weights have N rows (outputs) and K columns (inputs), as the GGUF reader orders them (reference
@@ -195,11 +195,14 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
  * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice;
  * MBQ_KERNEL_KGROUP takes bm = bn = 0 and chooses its rows per block for the forced splits, 0 = its own choice).
- * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB per-device workspace (plus 256 KiB of
- * counters) of uncached device memory, allocated by the first such call on a device and kept until the process ends;
- * GEMM calls on one device that overlap in time must not both split K. That first call cannot run on a stream that is
- * capturing a HIP graph: it returns MBQ_E_ARG and launches nothing (make one eager call on the device before
- * capturing). */
+ * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB workspace (plus 256 KiB of counters) of
+ * uncached device memory, one per (device, stream), so split-K calls that overlap in time on two streams never share
+ * partials or counters. A stream's workspace is allocated by its first eager split-K call and kept until the process
+ * ends (at most 31 streams per device). Every eager split-K call also keeps one spare workspace per device, which the
+ * first split-K call recorded into a HIP graph on a stream without a workspace of its own takes; a recorded call that
+ * finds neither (no eager split-K call on the device yet, or the spare taken by another capturing stream since the last
+ * eager call) returns MBQ_E_ARG and launches nothing. Graphs recorded on one stream share its workspace: their replays
+ * must not overlap in time. */
 #define MBQ_KERNEL_AUTO 0
 #define MBQ_KERNEL_GEMV 0
 #define MBQ_KERNEL_STREAM 1

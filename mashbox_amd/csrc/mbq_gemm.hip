@@ -737,39 +737,75 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------- workspace
-// Split-K partials and arrival counters, one set per device, allocated (and the counters cleared) by the first GEMM
-// call that splits K on that device and kept until the process ends. GEMM calls on one device that overlap in time
-// (two streams) must not both split K; the dispatcher sizes splits to fit the fixed size. The allocation cannot be
-// recorded into a HIP graph: a first split-K call on a stream that is capturing is refused with an error (nothing is
-// launched), so that a caller makes one eager call before capturing.
+// Split-K partials and arrival counters: one set per (device, stream), so that split-K calls overlapping in time on two
+// streams of a device (a server's prefill and decode streams) never share partials or counters. A stream's set is
+// allocated (its counters cleared) by the first split-K call made on it eagerly, and kept until the process ends.
+//
+// An allocation cannot be recorded into a HIP graph, so each eager split-K call also makes sure the device holds one
+// spare set: the first split-K call recorded on a stream that has no set of its own (torch.cuda.graph records on a side
+// stream) takes the spare, which is then that stream's for good. A call under capture that finds neither (no eager
+// split-K call yet on the device, or the spare taken by another capturing stream since the last eager call) is refused
+// with an error and launches nothing. Graphs recorded on one stream share its set: replays of two such graphs must not
+// overlap in time. A destroyed stream's set is kept (a later stream at the same handle reuses it).
+constexpr int WS_MAX_STREAMS = 32;            // sets per device (each WS_BYTES + WS_TILES counters), spare included
+
+static int ws_alloc(Workspace* w, int dev) {
+    // Uncached device memory: no L2 holds its lines, so a partial one XCD stores is what another XCD loads after the
+    // arrival count, with no cache write-back or invalidation between (the exchange of every split-K kernel). Never
+    // freed, also on a failed set-up.
+    void *p = nullptr, *c = nullptr;
+    if (hipExtMallocWithFlags(&p, WS_BYTES, hipDeviceMallocUncached) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation on device %d failed", dev);
+    // the counters are zeroed on the null stream and waited for here, once: the first kernel that uses them may run on
+    // a non-blocking stream, which does not wait for the null stream
+    if (hipExtMallocWithFlags(&c, WS_TILES * sizeof(int), hipDeviceMallocUncached) != hipSuccess ||
+        hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess)
+        return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K counter allocation on device %d failed", dev);
+    w->ws = static_cast<float*>(p);
+    w->cnt = static_cast<int*>(c);
+    w->bytes = WS_BYTES;
+    w->tiles = WS_TILES;
+    w->fenced = 0;
+    return 0;
+}
+
 int workspace(Workspace* out, hipStream_t s) {
-    static Workspace per_dev[64];
+    struct Dev { hipStream_t stream[WS_MAX_STREAMS]; Workspace set[WS_MAX_STREAMS]; int n = 0; Workspace spare; };
+    static Dev per_dev[64];
     static std::mutex mu;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MBQ_LAUNCH_FAIL, "GEMM: no device");
     std::lock_guard<std::mutex> lk(mu);
-    Workspace& w = per_dev[dev];
-    if (!w.ws) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return set_error(MBQ_BAD_ARG, "GEMM: the first split-K call on device %d allocates its workspace, which a "
-                                          "stream being captured into a graph cannot do: make one eager call first", dev);
-        // Uncached device memory: no L2 holds its lines, so a partial one XCD stores is what another XCD loads after the
-        // arrival count, with no cache write-back or invalidation between (the exchange of every split-K kernel). It is
-        // kept until the process ends (never freed, also on a failed set-up).
-        void *p = nullptr, *c = nullptr;
-        if (hipExtMallocWithFlags(&p, WS_BYTES, hipDeviceMallocUncached) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K workspace allocation failed");
-        // the counters are zeroed on the null stream and waited for here, once: the first kernel that uses them may run
-        // on a non-blocking stream, which does not wait for the null stream
-        if (hipExtMallocWithFlags(&c, WS_TILES * sizeof(int), hipDeviceMallocUncached) != hipSuccess ||
-            hipMemset(c, 0, WS_TILES * sizeof(int)) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess)
-            return set_error(MBQ_LAUNCH_FAIL, "GEMM: split-K counter allocation failed");
-        w.ws = static_cast<float*>(p);
-        w.cnt = static_cast<int*>(c);
-        w.bytes = WS_BYTES;
-        w.tiles = WS_TILES;
+    Dev& d = per_dev[dev];
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+    // sets held: d.n streams' and the spare, at most WS_MAX_STREAMS; the spare is refilled by eager calls (best effort:
+    // a failed refill only means that a later first capture on a new stream is refused)
+    auto refill = [&] { if (!capturing && !d.spare.ws && d.n < WS_MAX_STREAMS) ws_alloc(&d.spare, dev); };
+    for (int i = 0; i < d.n; ++i)
+        if (d.stream[i] == s) {
+            *out = d.set[i];
+            refill();
+            return 0;
+        }
+    if (!capturing && d.n + (d.spare.ws ? 1 : 0) >= WS_MAX_STREAMS)
+        return set_error(MBQ_BAD_ARG, "GEMM: split-K calls on more than %d streams of device %d (one workspace each)",
+                         WS_MAX_STREAMS - 1, dev);
+    Workspace w;
+    if (capturing) {
+        if (!d.spare.ws)
+            return set_error(MBQ_BAD_ARG, "GEMM: the first split-K call on this stream of device %d needs a workspace, "
+                                          "which a stream being captured into a graph cannot allocate: make one eager "
+                                          "call first", dev);
+        w = d.spare;
+        d.spare = Workspace{};
+    } else {
+        if (int rc = ws_alloc(&w, dev)) return rc;
     }
+    d.stream[d.n] = s;
+    d.set[d.n] = w;
+    ++d.n;
+    refill();
     *out = w;
     return 0;
 }

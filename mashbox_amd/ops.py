@@ -177,6 +177,7 @@ class _Package:
         self.error = None
         self.preflight = {}
         self.layer_preflight = {}
+        self._out_dtype = None
 
     def __getitem__(self, key):
         if key not in ("module", "types", "name", "error"):
@@ -188,6 +189,16 @@ class _Package:
         if test is None or len(tuple(shape)) < 2:
             return True
         return bool(test(int(t), tuple(int(v) for v in tuple(shape)[-2:])))
+
+    def out_dtype(self) -> bool:
+        """the package's matmul takes out_dtype= (a result written in the activation dtype by the kernel itself)"""
+        if self._out_dtype is None:
+            mm = getattr(self.module, "matmul", None)
+            try:
+                self._out_dtype = mm is not None and "out_dtype" in inspect.signature(mm).parameters
+            except (TypeError, ValueError):
+                self._out_dtype = False
+        return self._out_dtype
 
     def picks_layer(self) -> bool:
         flag = getattr(self.module, "picks_layer", None)
@@ -410,14 +421,23 @@ def _on_pick(h: Pick, fn):
 
 
 # ----------------------------------------------------------------------------------------------------- the calls
+def _kernel_matmul(x: torch.Tensor, planes, **kw) -> torch.Tensor:
+    """the package's matmul with the result in x's dtype. A bfloat16 x gets a bfloat16 result written by the kernel
+    (its float32 sums rounded to nearest even, the same bits as a float32 result cast afterwards) when the package takes
+    out_dtype=; other dtypes, and packages without it, take the float32 result and a cast."""
+    if x.dtype == torch.bfloat16 and _KERNELS.out_dtype():
+        return _KERNELS.module.matmul(x, planes, out_dtype=torch.bfloat16, **kw)
+    return _KERNELS.module.matmul(x, planes, **kw).to(x.dtype)
+
+
 def qmatmul(x: torch.Tensor, h) -> torch.Tensor:
     """x (..., cols) @ W.T -> (..., rows): float32 accumulation, result in x's dtype (reference ops/__init__.py:594-632)"""
     if isinstance(h, Pick):
         return _on_pick(h, lambda one: qmatmul(x, one))
     if isinstance(h, At):
-        return _KERNELS.module.matmul(x, h.packed, layer=h.layer).to(x.dtype)
+        return _kernel_matmul(x, h.packed, layer=h.layer)
     if isinstance(h, Packed):
-        return _KERNELS.module.matmul(x, h.packed).to(x.dtype)
+        return _kernel_matmul(x, h.packed)
     if isinstance(h, Raw):
         if h.raw.dim() > 2:
             raise ValueError(f"{h}: a stack is multiplied one layer at a time (index the stack)")

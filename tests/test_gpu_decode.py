@@ -7,9 +7,10 @@ the six weight types runs M in {1, 2, 3, 4, 8, 16} over the seven projections of
 the decode GEMV's registers hold at 1-4 rows for Q8_0 / int8, and at 3-4 rows for every type, so the weight stream runs
 it).
 
-Oracle: the weights come from the oracle's seeded generators; the kernel's dequantization is compared bit for bit with
-the oracle's on a row sample (first, last and 60 seeded rows), and every output of every product is compared with the
-float64 product of those exact weights (computed on the GPU), within the product bars of tests/_check.py.
+Oracle: the weights come from the oracle's seeded generators; every output of every product is compared with the
+float64 product (computed on the GPU) of the oracle's dequantization of every row, within the product bars of
+tests/_check.py; the kernel's own dequantization is compared bit for bit with the oracle's on a row sample (first, last
+and 60 seeded rows).
 """
 import numpy as np
 import pytest
@@ -50,11 +51,15 @@ def test_decode_batches_on_every_layer_shape(t, cuda):
             assert KQ.kq_covers(t, (n, k)), f"{name} {n}x{k} must be covered"
             raw = G.RAW[t](rng, n, k)
             planes = KQ.repack_host(t, raw, (n, k)).to(cuda)
+            # the reference weights are the oracle's dequantization of every row (not the kernel's own); the kernel's
+            # dequantization is checked against it bit for bit on a row sample, as a separate assertion
+            w_or = R.dequant(raw, t, k)
             wd = KQ.dequant(planes)
             rows = np.unique(np.concatenate([[0, 1, n - 2, n - 1], rng.choice(n, 60, replace=False)]))
-            assert diff_bits(wd[torch.from_numpy(rows).to(cuda)].cpu().numpy(), R.dequant(raw[rows], t, k)) == 0
-            w64 = wd.to(torch.float64)
+            assert diff_bits(wd[torch.from_numpy(rows).to(cuda)].cpu().numpy(), w_or[rows]) == 0
             del wd
+            w64 = torch.from_numpy(w_or).to(cuda).to(torch.float64)
+            del w_or
         for m in DECODE_M:
             xb = G.acts(rng, m, k)
             x = _bf16(xb, cuda)

@@ -95,6 +95,36 @@ def test_kernel_and_exact_paths_match_the_oracle(t, cuda):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("t", [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K])
+def test_qmatmul_writes_bf16_directly(t, cuda):
+    """qmatmul of bfloat16 activations returns the kernel's own bfloat16 output (no float32 result and cast): bit for
+    bit kernels.matmul(..., out_dtype=bfloat16), which is the float32 result rounded to nearest even; for a handle, a
+    layer of a held stack (At), and float32 activations (float32 result, then a cast to float32: the same values)"""
+    import torch
+    ops.load_kernels()
+    rng = np.random.default_rng(900 + t)
+    n, k = 200, R.TYPES[t][1] * 8
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(2)])
+    h = ops.prepare(st[0], t, (n, k))
+    hs = ops.prepare(st, t, (n, k))
+    for m in (1, 4, 16, 80):
+        _, x = _x(rng, m, k, cuda)
+        y = ops.qmatmul(x, h)
+        assert y.dtype == torch.bfloat16
+        direct = KQ.matmul(x, h.packed, out_dtype=torch.bfloat16)
+        f32 = KQ.matmul(x, h.packed)
+        assert torch.equal(y.view(torch.int16), direct.view(torch.int16)), f"m={m}: not the kernel's bf16 output"
+        assert torch.equal(y.view(torch.int16), f32.to(torch.bfloat16).view(torch.int16)), f"m={m}: not RNE of f32"
+        held, xs = ops.scan_split({"w": hs})
+        w = ops.scan_join(held, xs, torch.tensor(1, dtype=torch.int32, device=cuda))["w"]
+        ya = ops.qmatmul(x, w)
+        assert torch.equal(ya.view(torch.int16),
+                           KQ.matmul(x, hs.packed, layer=1, out_dtype=torch.bfloat16).view(torch.int16))
+    xf = x.float()
+    assert torch.equal(ops.qmatmul(xf, h), KQ.matmul(xf, h.packed))
+
+
+@pytest.mark.gpu
 def test_exact_path_chunks_large_weights(cuda, monkeypatch):
     """a weight over EXACT_CHUNK values is rebuilt a chunk of rows at a time: same values as one rebuild"""
     ops.load_kernels(module="off")

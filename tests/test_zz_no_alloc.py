@@ -111,3 +111,64 @@ def test_noalloc_int8_planes_split_k():
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), f"int8 case {i}: noalloc differs"
         assert_product_dev(y, ref, f"int8 planes case {i}")
+
+
+CAPTURE_SCRIPT = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import torch
+from oracle import gen as G
+from oracle import ref as R
+from mashbox_amd import _lib as LIB
+
+dev = torch.device("cuda", 0)
+L = LIB.lib()
+t, m, n, k = R.Q4_K, 16, 1024, 5120
+print(f"case: Q4_K {m} x {n} x {k}, first split-K call = mbq_matmul_noalloc under capture", flush=True)
+assert LIB.gemm_plan(t, m, n, k)[3] > 1, "the case must split K"
+rng = np.random.default_rng(11)
+raw = G.q4_k_raw(rng, n, k)
+pb = LIB.check(L.mbq_plane_bytes(t, n, k), "plane_bytes")
+host = torch.empty(pb, dtype=torch.uint8)
+LIB.check(L.mbq_repack_host(t, raw.ctypes.data_as(ctypes.c_void_p), n, k, ctypes.c_void_p(host.data_ptr()), pb, 0), "repack")
+planes = host.to(dev)
+x = torch.from_numpy(G.acts(rng, m, k).astype(np.int16)).view(torch.bfloat16).to(dev)
+y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+def call(fn, out):
+    return fn(t, ctypes.c_void_p(planes.data_ptr()), 0, None, 1, ctypes.c_void_p(x.data_ptr()), m, n, k,
+              ctypes.c_void_p(out.data_ptr()), LIB.OUT_F32, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    LIB.check(call(L.mbq_matmul_noalloc, y), "mbq_matmul_noalloc under capture")
+torch.cuda.synchronize()
+eager = torch.full_like(y, float("nan"))
+for i in range(4):
+    g.replay()
+    torch.cuda.synchronize()
+    if i == 0:
+        LIB.check(call(L.mbq_matmul, eager), "mbq_matmul")        # the allocating entry point, after the capture
+        torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), eager.view(torch.int32)), f"replay {i} differs from mbq_matmul"
+    y.fill_(float("nan"))
+    other = torch.empty_like(y)
+    LIB.check(call(L.mbq_matmul_noalloc, other), "eager mbq_matmul_noalloc between replays")
+    torch.cuda.synchronize()
+    assert torch.equal(other.view(torch.int32), eager.view(torch.int32)), "eager noalloc differs"
+print("noalloc capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """in a fresh process (no workspace or scratch set up yet), the first split-K call is mbq_matmul_noalloc recorded
+    into a HIP graph: it needs no allocation, so it records; every replay equals mbq_matmul's eager result bit for bit,
+    with eager noalloc calls between the replays"""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=240)
+    sys.stdout.write(r.stdout)
+    sys.stderr.write(r.stderr[-4000:])
+    assert r.returncode == 0 and "noalloc capture ok" in r.stdout
