@@ -6,12 +6,13 @@
 A step is one pass of the hot path over one batch of synthetic input of a BASELINE config: one kernel launch for the
 decode GEMV configs 1-3, the 7 projection launches of one 27B-class layer for configs 4-5. The headline (`value`) is
 config 2 (GGUF Q8_0 decode GEMV, x[1,5120] @ W[17408,5120]^T), in GB/s of algorithmic bytes (packed weight bytes +
-scales + x + y, never repack padding) per second, with the weights already in HBM. `q6k_head` is not a BASELINE
-config: it is the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one
-activation row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs, as are batched decode
-over the 27B-class layer at 4 and 16 activation rows (`m4_q4k`, `m16_q4k`, `m4_q8`, `m16_q8`, `m4_q5k`,
-`m16_q5k`, `m4_q6k`, `m16_q6k`, `m4_int8`, `m16_int8`: the reference engine's row buckets; Q4_K, Q8_0, Q5_K, Q6_K and
-int8 weights in 16-row tiles).
+scales + x + y, never repack padding) per second, with the weights already in HBM. Weights are repacked once at load
+as a load would (north star 3): single-row configs into the row-major planes of the decode GEMV, batched configs (4
+int8, 5 Q4_K) into 16-row tiles, the layout ops.prepare loads by default. `q6k_head` is not a BASELINE config: it is
+the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one activation
+row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs, as are one 27B-class layer at 1,
+4 and 16 activation rows (`m1_q4k` row-major, `m1_q4k_tiles`, `m4_*`, `m16_*`: the reference engine's row buckets;
+Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, tiles from 2 rows on) and config 5 on row-major planes (`c5_rm`).
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) of K launches that cycles through
 >= 1 GiB of distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for warmup, then R
@@ -19,8 +20,9 @@ times (R >= 5 and R * K >= 100), each replay bracketed by torch.cuda.synchronize
 stream the kernels run on. A projection's launch time is the median over the R replays of (replay time / K), so every
 figure is the median of >= 100 timed launches whatever K is; `mean_us` beside it is the mean over all of them. Beside
 it, `eager_call_us` is the end-to-end time of back-to-back eager ctypes calls through the C ABI, timed on the host
-(argument checks, plan, launch and kernel; up to 50 calls). Rows `c2_ops`, `c5_ops` and `m4_q4k_ops` time the same
-work through mashbox_amd.ops.qmatmul (prepare's default layout, the result in x's dtype), the caller's path. The CPU
+(argument checks, plan, launch and kernel; up to 50 calls). Rows `c2_ops`, `m1_q4k_ops`, `m4_q4k_ops` and `c5_ops`
+time the same work through mashbox_amd.ops.qmatmul (prepare's default layout, the result in x's dtype), the caller's
+path. The CPU
 baseline is the oracle's restatement of mashbox's exact path
 (rebuild float32 weights per call, float32 dot; int8: float32 dot then the scales) on the host's cores, every config at
 full size (a few seconds each); `cpu_baseline` is config 2's.
@@ -65,7 +67,7 @@ def log(*a):
 
 
 # rows timed through mashbox_amd.ops.qmatmul (the caller's path) instead of the C ABI: row -> the config it repeats
-OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k"}
+OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k", "m1_q4k_ops": "m1_q4k"}
 
 
 def config_of(idx):
@@ -143,9 +145,10 @@ def setup_projection(idx, pi, rotate_bytes):
         plan = LIB.plan_str(LIB.INT8, M, N, K)
     else:
         raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 13: synth.q5_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
-        # batched GGUF decode (2-64 rows): the blocks repacked once at load into 16-row tiles (MBQ_Q4KT, MBQ_Q5KT,
-        # MBQ_Q6KT, MBQ_Q8T planes), as int8
-        pt = {12: LIB.Q4KT, 8: LIB.Q8T, 13: LIB.Q5KT, 14: LIB.Q6KT}.get(t, t) if 1 < M <= 64 else t
+        # batched GGUF configs (2 rows and more) load the blocks as 16-row tiles, ops.prepare's default layout;
+        # single-row configs keep the row-major planes of the decode GEMV; "_rm" / "_tiles" rows force one
+        tiles = (M > 1 and not str(idx).endswith("_rm")) or str(idx).endswith("_tiles")
+        pt = {12: LIB.Q4KT, 8: LIB.Q8T, 13: LIB.Q5KT, 14: LIB.Q6KT}.get(t, t) if tiles else t
         pb = check(L.mbq_plane_bytes(pt, N, K), "plane_bytes")
         planes = torch.empty(pb, dtype=torch.uint8, device=dev)
         check(L.mbq_repack_dev(pt, ctypes.c_void_p(raw.data_ptr()), N, K, ctypes.c_void_p(planes.data_ptr()), st()), "repack")
@@ -514,8 +517,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,"
-                                          "m4_int8,m16_int8,c2_ops,c5_ops,m4_q4k_ops")
+    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m1_q4k,m1_q4k_tiles,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,"
+                                          "m16_q5k,m4_q6k,m16_q6k,m4_int8,m16_int8,c5_rm,c2_ops,m1_q4k_ops,m4_q4k_ops,c5_ops")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")

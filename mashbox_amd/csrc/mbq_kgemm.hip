@@ -103,25 +103,101 @@ __device__ __forceinline__ void kgm_each(F&& f, std::integer_sequence<int, P...>
     (f(std::integral_constant<int, P>{}), ...);
 }
 
+// ---------------------------------------------------------------------------------- factored sub-block products
+// Nibble tiles (Q4_K, Q5_K, Q4_0) at up to 32 activation rows take the scales out of the MFMA operands. A lane's 16
+// bytes of a chunk are one 32-value unit (sub-block) of its row, so in the loaded order the four lane groups hold four
+// different sub-blocks. Two v_permlane32_swap and two v_permlane16_swap transpose the four units' dwords across the
+// lane groups (kgm_lg_transpose), after which dword u of lane group g is dword g of unit u: K step u of the chunk is then
+// sub-block u alone, and its B operand is the exact bfloat16 pairs 128 + q, one AND-OR (Q4_K, Q4_0) or one byte permute
+// (Q5_K) per pair. With x's sum X over the sub-block,
+//     sum_k x_k ((d sc) q_k - dmin m) = (d sc) * sum_k x_k (128 + q_k) - (128 d sc + dmin m) * X,
+// so each K step's MFMA product is scaled by its sub-block's d sc (4 FMAs per x row tile), and the offsets of the
+// chunk's four sub-blocks are one v_mfma_f32_16x16x4_f32 of the x sums (16 x rows x 4 sub-blocks, from MFMAs of the x
+// operand against ones) and the offsets (4 sub-blocks x 16 weight rows: each lane's own sub-block). Q4_0 is the case
+// d sc = d, offset 136 d. The dequantization's ~3.2 VALU per weight value become ~1.1; from 33 rows on the per-value
+// form shares its dequantization over 3-4 x row tiles and needs fewer instructions, so it stays there.
+// chunks per wave the register-x path holds (its plans keep every wave's chunk count within this)
+constexpr int kgm_rx_chunks() { return 5; }
+// register-x path: chunks of weights in flight per wave (two: three or four were slower on MI355X, e.g. a 17408 x 5120
+// Q4_K gate at one row 15.4 -> 17.1 us, the 5120 x 17408 down 17.0 -> 18.6 us)
+constexpr int kgm_rx_depth(int) { return 2; }
+
+template <int T, int MT> constexpr bool kgm_factored() { return (T == T_Q4KT || T == T_Q5KT || T == T_Q40T) && MT >= 1 && MT <= 2; }
+
+// in: lane group g holds dwords 0..3 of unit g (of its row); out: lane group g holds dword g of units 0..3
+__device__ __forceinline__ u32x4 kgm_lg_transpose(const u32x4& w) {
+    const u32x2 a = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false));
+    const u32x2 b = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false));
+    const u32x2 c = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false));
+    const u32x2 d = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false));
+    return u32x4{c[0], c[1], d[0], d[1]};
+}
+
+// the sum over the four lane groups (rows of 16 lanes) of v, in every lane: one v_permlane32_swap and one
+// v_permlane16_swap, each with an add
+__device__ __forceinline__ float kgm_lg_sum(float v) {
+    const u32x2 a = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false));
+    const float h = __uint_as_float(a[0]) + __uint_as_float(a[1]);                  // groups 0 + 2, 1 + 3
+    const u32x2 b = __builtin_bit_cast(u32x2, __builtin_amdgcn_permlane16_swap(__float_as_uint(h), __float_as_uint(h), false, false));
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// a row's 16-byte Q4_K / Q5_K header in every lane of the row, from lane group g's dword g of it (a transpose of four
+// copies: dword u of the result comes from lane group u)
+__device__ __forceinline__ u32x4 kgm_hdr(uint32_t v) { return kgm_lg_transpose(u32x4{v, v, v, v}); }
+
+// Q4_K / Q5_K: d sc of sub-blocks 4 h + u (u = 0..3) of the lane's row, from its super-block header meta (d and dmin,
+// then the 12 scale bytes s0 s1 s2 as dwords 1-3; reference src/mashbox/ops/reference.py:132-139), all four 6-bit
+// scales (and mins) unpacked at once, one per byte; *on = -(128 d sc + dmin m) of the lane's own sub-block 4 h + lg.
+// Without branches: sub-blocks 0-3 (h = 0) take the low 6 bits of s0 (scales) and s1 (mins); sub-blocks 4-7 the low
+// (high) nibbles of s2 with bits 6-7 of s0 (s1) as their bits 4-5. km = h ? 0x0F0F0F0F : 0x3F3F3F3F and
+// hm = h ? 0x30303030 : 0 are the wave's masks.
+__device__ __forceinline__ void kgm_kq_scales(const u32x4& meta, bool h, uint32_t km, uint32_t hm, int lg, float s[4],
+                                              float* on) {
+    const float d = f16f(meta[0]), dm = f16f(meta[0] >> 16);
+    const uint32_t scv = ((h ? meta[3] : meta[1]) & km) | ((meta[1] >> 2) & hm);
+    const uint32_t mnv = ((h ? meta[3] >> 4 : meta[2]) & km) | ((meta[2] >> 2) & hm);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s[u] = d * (float)((scv >> (8 * u)) & 0xFFu);         // exact
+    const float sg = d * (float)__builtin_amdgcn_ubfe(scv, 8u * (uint32_t)lg, 8u);
+    const float mg = dm * (float)__builtin_amdgcn_ubfe(mnv, 8u * (uint32_t)lg, 8u);
+    *on = -__builtin_fmaf(128.f, sg, mg);
+}
+
+// Q4_0: the four blocks' scales d (fp16 pairs dd[0] = blocks 0, 1 and dd[1] = blocks 2, 3 of the chunk) and
+// *on = -136 d of the lane's own block (d (q - 8) = d (128 + q) - 136 d; 136 d is exact)
+__device__ __forceinline__ void kgm_q40_scales(uint32_t d01, uint32_t d23, int lg, float s[4], float* on) {
+    s[0] = f16f(d01);
+    s[1] = f16f(d01 >> 16);
+    s[2] = f16f(d23);
+    s[3] = f16f(d23 >> 16);
+    *on = -136.f * f16f(__builtin_amdgcn_ubfe(lg < 2 ? d01 : d23, 16u * (uint32_t)(lg & 1), 16u));
+}
+
 template <int T, int MT, int RG, int NTW, bool KFULL>
 __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t kgm_lds_buf[];
+    constexpr bool DIAG = MT < 0;                        // sub-block-diagonal x tiles (M <= 4 |MT|, see kgm_mt)
+    constexpr int MX = DIAG ? -MT : MT;                  // 16-row x tiles of a stage (and accumulator tiles per tile)
+    constexpr bool RX = MT == -1;                        // x in registers, no LDS stages (kgm_rx_chunks)
+    constexpr int CHX = kgm_rx_chunks();                 // RX: most chunks per wave
     __shared__ int kgm_last;
     constexpr bool Q6 = T == T_Q6KT;                     // Q6_K tiles (the Q4_K tiles' chunks and lane units)
     constexpr bool Q5 = T == T_Q5KT;                     // Q5_K tiles (Q4_K's, plus a high-bit word per unit)
     constexpr bool Q40 = T == T_Q40T;                    // Q4_0 tiles (Q4_K's units, one fp16 scale per unit)
     constexpr bool QK = T == T_Q4KT || Q5 || Q6 || Q40;  // nibble-unit tiles
     constexpr bool Q8 = T == T_Q8T;                      // Q8_0 tiles (else int8 tiles)
+    constexpr bool FACT = kgm_factored<T, MT>();         // factored sub-block products (above)
     constexpr int CW = kgm_cw(T);                        // K values per chunk
     constexpr int XB = 2 * CW;                           // bytes of one x row of a chunk
     constexpr int PCS = XB / 16;                         // its 16-byte pieces
     constexpr int RPI = 64 / PCS;                        // x rows per DMA instruction
     constexpr int NS = CW / 32;                          // MFMA K steps per chunk
-    constexpr int KG = kgm_kg<RG>(), D = kgm_depth(T, MT, RG);
-    constexpr int STAGE = (int)kgm_stage(T, MT);         // bytes of one x stage (16 MT rows x CW values)
+    constexpr int KG = kgm_kg<RG>(), D = RX ? kgm_rx_depth(NTW) : kgm_depth(T, MX, RG);
+    constexpr int STAGE = (int)kgm_stage(T, MX);         // bytes of one x stage (16 MX rows x CW values)
     constexpr int NX = STAGE / 1024 / RG;                // x DMA instructions per wave per chunk (1 KiB each)
     static_assert(NX * RG * 1024 == STAGE, "the RG waves of a K group issue whole DMA instructions");
-    static_assert(kgm_ring(T, MT, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
+    static_assert(kgm_ring(T, MX, RG) <= KGM_LDS_MAX, "the x rings fit the LDS");
     constexpr int NWL = Q6 ? 4 * NTW : Q5 ? 3 * NTW : QK || Q8 ? 2 * NTW : NTW;   // weight loads per chunk (Q4_K:
                                                          // quants, headers; Q5_K: and high bits; Q6_K: the four
                                                          // planes; Q8_0: quants, scales)
@@ -161,20 +237,23 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         const int row = 16 * (t0 + j) + r16;
         const bool in = row >= rq0 && row < rq1;
         wo[j] = in ? (uint32_t)(Q40 ? q40t_off(row, K) : QK ? q4kt_off(row, K) : i8t_off(row, K, 0)) + 16u * (uint32_t)lg : OOB_VOFF;
-        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg : Q40 ? q40t_d_off(row, K) + 2 * lg
+        // factored Q4_0 / Q5_K: every lane loads its row's four block scales / high-bit words of the chunk
+        mo[j] = in && (QK || Q8) ? (uint32_t)(g.sc_off + (Q6 ? q6kt_s_off(row, K) + 2 * lg
+                                                         : Q40 ? q40t_d_off(row, K) + (FACT ? 0 : 2 * lg)
                                                          : QK ? q4kt_meta_off(row, K) : q8t_d_off(row, K)))
                                  : OOB_VOFF;
-        ho[j] = in && (Q5 || Q6) ? (uint32_t)(g.hi_off + (Q6 ? q6kt_h_off(row, K) + 8 * lg : q5kt_h_off(row, K) + 4 * lg)) : OOB_VOFF;
+        ho[j] = in && (Q5 || Q6) ? (uint32_t)(g.hi_off + (Q6 ? q6kt_h_off(row, K) + 8 * lg : q5kt_h_off(row, K) + (FACT ? 0 : 4 * lg)))
+                                 : OOB_VOFF;
         dq[j] = in && Q6 ? (uint32_t)(g.d_off + q6kt_d_off(row, K)) : OOB_VOFF;
     }
     // int8: the row scales of the tiles this wave finishes (see the reduce-scatter below), loaded first so that their
     // latency hides behind the K loop; the first step's vmcnt wait covers them (they are the oldest loads). Q4_K and
     // Q8_0 apply their block scales in the loop: 1.
-    float sc[(MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>()];
+    float sc[(MX * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>()];
 #pragma unroll
-    for (int u = 0; u < (MT * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>(); ++u) {
+    for (int u = 0; u < (MX * NTW + kgm_kg<RG>() - 1) / kgm_kg<RG>(); ++u) {
         const int tt = kg + kgm_kg<RG>() * u, j = tt % NTW, n = 16 * (t0 + j) + r16;
-        const bool live = ok && tt < MT * NTW && n >= rq0 && n < rq1;
+        const bool live = ok && tt < MX * NTW && n >= rq0 && n < rq1;
         if constexpr (QK || Q8)
             sc[u] = 1.f;
         else
@@ -187,7 +266,14 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
         const int r = RPI * (q + RG * i) + lane / PCS, p = (lane % PCS) ^ kgm_swz<PCS>(r);
-        xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + 8 * p) * 2) : OOB_VOFF;
+        if constexpr (DIAG) {
+            // stage row r = 16 t + 4 u + e holds x row 4 t + e in the pieces of sub-block u (4 u .. 4 u + 3) and zeros
+            // in the others
+            const int xr = 4 * (r >> 4) + (r & 3);
+            xvo[i] = xr < M && (p >> 2) == ((r >> 2) & 3) ? (uint32_t)(((int64_t)xr * K + 8 * p) * 2) : OOB_VOFF;
+        } else {
+            xvo[i] = r < M ? (uint32_t)(((int64_t)r * K + 8 * p) * 2) : OOB_VOFF;
+        }
         xk[i] = 8 * p;
     }
     uint8_t* ring = kgm_lds_buf + (size_t)kg * D * STAGE;
@@ -206,7 +292,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
     // the chunk's weights: a KiB per tile (non-temporal), and for Q4_K the 16-byte header of the super-block (chunk / 2).
     // Q8_0: the lane's 16 bytes are its 8 quants of each of the chunk's two blocks (K step s = block s: values
     // 32 s + 8 lg ..), then the row's two block scales
-    auto load_w = [&](u32x4* W, u32x4* H, uint32_t* Hb, int l) __attribute__((always_inline)) {
+    auto load_w = [&](u32x4* W, u32x4* H, u32x4* Hb, int l) __attribute__((always_inline)) {
         const int c = chunk_of(l);
         const bool live = l < mine;
 #pragma unroll
@@ -221,13 +307,23 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                                     wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 512u : 0u, 2));
                 H[j] = u32x4{h[0], h[1], bload2(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u),
                              bload2(wr, live ? dq[j] : OOB_VOFF, live ? (uint32_t)(c >> 1) * 32u : 0u)};
+            } else if constexpr (Q40 && FACT) {                   // the four blocks' scales
+                const u32x2 d = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                    wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u, 0));
+                H[j][0] = d[0];
+                H[j][1] = d[1];
             } else if constexpr (Q40) {
                 H[j][0] = bload2(wr, live ? mo[j] : OOB_VOFF, live ? (uint32_t)c * 128u : 0u);   // the unit's block scale
             } else if constexpr (QK) {
-                H[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? mo[j] : OOB_VOFF,
-                                                                                      live ? (uint32_t)(c >> 1) * 256u : 0u, 0));
-                if constexpr (Q5)                                 // the unit's high-bit word
-                    Hb[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 256u : 0u, 2);
+                // Q4_K / Q5_K: dword lg of the row's 16-byte super-block header (the four lane groups of a row load its
+                // four dwords, 256 B per wave instead of a KiB; kgm_hdr gives every lane all four)
+                H[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? mo[j] + 4u * (uint32_t)lg : OOB_VOFF,
+                                                                         live ? (uint32_t)(c >> 1) * 256u : 0u, 0);
+                if constexpr (Q5 && FACT)                         // the four units' high-bit words
+                    Hb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 256u : 0u, 2));
+                else if constexpr (Q5)                            // the unit's high-bit word
+                    Hb[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, live ? ho[j] : OOB_VOFF, live ? (uint32_t)c * 256u : 0u, 2);
             }
         }
     };
@@ -238,14 +334,14 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         return *reinterpret_cast<const bf16x8_t*>(ring + st * STAGE + r * XB + (p << 4));
     };
 
-    f32x4_t acc[MT][NTW];
+    f32x4_t acc[MX][NTW];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MX; ++i)
 #pragma unroll
         for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     u32x4 W[D][NTW];
     u32x4 H[QK || Q8 ? D : 1][NTW];                                       // K-quants: headers / scales; Q8_0: scales
-    uint32_t Hb[Q5 ? D : 1][NTW];                                         // Q5_K: high-bit words
+    u32x4 Hb[Q5 ? D : 1][NTW];                                            // Q5_K: high-bit word(s)
 
     // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
     // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
@@ -258,6 +354,132 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         __builtin_amdgcn_sched_barrier(0);
         dma_x((U + D - 1) % D, l + D - 1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (DIAG) {
+            // the chunk's four K steps chain into one product per tile: output row 4 u + e of x tile i is x row 4 i + e
+            // times sub-block u (the lane group's unit, whose scale the lane holds); the x sums by the same chain
+            // against ones; then the lane's (d sc, offset) once per chunk
+            const int j8 = 4 * (chunk_of(l) & 1) + lg;
+            const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{BF16_ONES, BF16_ONES, BF16_ONES, BF16_ONES});
+            f32x4_t P[MX][NTW], DX[MX];
+#pragma unroll
+            for (int i = 0; i < MX; ++i) {
+                DX[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) P[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                bf16x8_t A[MX];
+#pragma unroll
+                for (int i = 0; i < MX; ++i) {
+                    A[i] = a_op(U, i, s);
+                    DX[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], ones, DX[i], 0, 0, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    const uint32_t w = W[U][j][s];
+                    u32x4 o;
+                    if constexpr (Q5) {
+                        uint32_t lo, hi;
+                        q5k_bytes(w, Hb[U][j][0], s, &lo, &hi);
+                        const uint32_t c43 = in_vgpr(0x43434343u);
+                        o = u32x4{b128_pair(lo, c43, 0), b128_pair(lo, c43, 1), b128_pair(hi, c43, 0), b128_pair(hi, c43, 1)};
+                    } else {
+                        const uint32_t m = in_vgpr(0x000F000Fu), e = in_vgpr(0x43004300u);
+                        o = u32x4{(w & m) | e, ((w >> 4) & m) | e, ((w >> 8) & m) | e, ((w >> 12) & m) | e};
+                    }
+                    const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
+#pragma unroll
+                    for (int i = 0; i < MX; ++i) P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, P[i][j], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                float a, on;
+                if constexpr (Q40) {
+                    a = f16f(H[U][j][0]);
+                    on = -136.f * a;                                             // d (q - 8) = d (128 + q) - 136 d
+                } else {
+                    const u32x4 hd = kgm_hdr(H[U][j][0]);
+                    const WsScale c = Q5 ? ws_scale<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], hd, Hb[U][j][0]}, j8)
+                                         : ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], hd}, j8);
+                    a = c.a;
+                    on = -__builtin_fmaf(128.f, c.a, c.b);                       // -(128 d sc + dmin m)
+                }
+#pragma unroll
+                for (int i = 0; i < MX; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[i][j][r] = __builtin_fmaf(on, DX[i][r], __builtin_fmaf(a, P[i][j][r], acc[i][j][r]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
+            return;
+        }
+        if constexpr (FACT) {
+            // K step u = sub-block u of the chunk: lane group lg's x values are values 8 lg .. 8 lg + 7 of it (piece
+            // 4 u + lg); the x sums of the four sub-blocks by MFMAs against ones, with x as the B operand, so that
+            // lane l holds row 16 i + (l & 15)'s sum (the f32 MFMA's A operand takes sub-block lg's)
+            // the super-block half of the chunk: c0 + kg + KG l has the parity of c0 + kg (KG is even)
+            static_assert(KG % 2 == 0, "a K group's chunks keep their parity");
+            const bool h = ((c0 + kg) & 1) != 0;
+            const uint32_t km = h ? 0x0F0F0F0Fu : 0x3F3F3F3Fu, hm = h ? 0x30303030u : 0u;
+            const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{BF16_ONES, BF16_ONES, BF16_ONES, BF16_ONES});
+            bf16x8_t A[4][MX];
+            float xs[MX];
+#pragma unroll
+            for (int i = 0; i < MX; ++i) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int r = 16 * i + r16, p = (4 * u + lg) ^ kgm_swz<PCS>(r);
+                    A[u][i] = *reinterpret_cast<const bf16x8_t*>(ring + U * STAGE + r * XB + (p << 4));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, A[u][i], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    xs[i] = u == 0 ? t[0] : (lg == u ? t[0] : xs[i]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) {
+                const u32x4 w = kgm_lg_transpose(W[U][j]);                 // dword u: values 8 lg .. of sub-block u
+                float sc4[4], on;
+                if constexpr (Q40)
+                    kgm_q40_scales(H[U][j][0], H[U][j][1], lg, sc4, &on);
+                else
+                    kgm_kq_scales(kgm_hdr(H[U][j][0]), h, km, hm, lg, sc4, &on);
+                f32x4_t P[4][MX];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    u32x4 o;
+                    if constexpr (Q5) {
+                        uint32_t lo, hi;
+                        q5k_bytes(w[u], Hb[U][j][u], lg, &lo, &hi);
+                        const uint32_t c43 = in_vgpr(0x43434343u);
+                        o = u32x4{b128_pair(lo, c43, 0), b128_pair(lo, c43, 1), b128_pair(hi, c43, 0), b128_pair(hi, c43, 1)};
+                    } else {
+                        // ((w >> 4p) & 0x000F000F) | 0x43004300: one v_and_or_b32 with both constants in registers
+                        const uint32_t m = in_vgpr(0x000F000Fu), e = in_vgpr(0x43004300u);
+                        o = u32x4{(w[u] & m) | e, ((w[u] >> 4) & m) | e, ((w[u] >> 8) & m) | e, ((w[u] >> 12) & m) | e};
+                    }
+                    const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
+#pragma unroll
+                    for (int i = 0; i < MX; ++i)
+                        P[u][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[u][i], B, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int i = 0; i < MX; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(sc4[u], P[u][i][r], acc[i][j][r]);
+#pragma unroll
+                for (int i = 0; i < MX; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[i], on, acc[i][j], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
+            return;
+        }
         // Q4_K: the lane's 16 bytes are one 32-value unit of its row, sub-block 4 (chunk % 2) + lg of the super-block;
         // its (d sc, dmin m) for the whole chunk
         WsScale qs[QK ? NTW : 1];
@@ -273,35 +495,35 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         } else if constexpr (Q5) {
             const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
-            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], H[U][j], Hb[U][j]}, j8);
+            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], kgm_hdr(H[U][j][0]), Hb[U][j][0]}, j8);
         } else if constexpr (QK) {
             const int j8 = 4 * (chunk_of(l) & 1) + lg;
 #pragma unroll
-            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], H[U][j]}, j8);
+            for (int j = 0; j < NTW; ++j) qs[j] = ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], kgm_hdr(H[U][j][0])}, j8);
         }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            bf16x8_t A[MT];
+            bf16x8_t A[MX];
 #pragma unroll
-            for (int i = 0; i < MT; ++i) A[i] = a_op(U, i, s);
-            if constexpr (Q8 && MT <= 2) {
+            for (int i = 0; i < MX; ++i) A[i] = a_op(U, i, s);
+            if constexpr (Q8 && MX <= 2) {
                 // Q8_0, one or two x row tiles: every MFMA of the step first (their block products in P), then the
                 // scale FMAs, so no FMA waits on the MFMA just issued
-                f32x4_t P[MT][NTW];
+                f32x4_t P[MX][NTW];
 #pragma unroll
                 for (int j = 0; j < NTW; ++j) {
                     const uint32_t a = hide(W[U][j][2 * s]), b = hide(W[U][j][2 * s + 1]);
                     const u32x4 o{i8_pair(a, 0), i8_pair(a, 1), i8_pair(b, 0), i8_pair(b, 1)};
                     const bf16x8_t B = __builtin_bit_cast(bf16x8_t, o);
 #pragma unroll
-                    for (int i = 0; i < MT; ++i)
+                    for (int i = 0; i < MX; ++i)
                         P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 }
 #pragma unroll
                 for (int j = 0; j < NTW; ++j) {
                     const float ds = f16f(s == 0 ? H[U][j][0] : H[U][j][0] >> 16);
 #pragma unroll
-                    for (int i = 0; i < MT; ++i)
+                    for (int i = 0; i < MX; ++i)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(P[i][j][r], ds, acc[i][j][r]);
                 }
@@ -315,7 +537,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                     B = ws_bop<T_Q6_K>(q6raw(W[U][j], H[U][j]), qs[j], s);
                 } else if constexpr (Q5) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m (one rounding) rounded to bfloat16
-                    B = ws_bop<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], H[U][j], Hb[U][j]}, qs[j], s);
+                    B = ws_bop<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], H[U][j], Hb[U][j][0]}, qs[j], s);
                 } else if constexpr (QK) {
                     // values 8 s .. 8 s + 7 of the unit, (d sc) q - dmin m rounded to bfloat16 (the LDS GEMM's operand)
                     B = q4k_dword_bop(W[U][j][s], qs[j]);
@@ -328,14 +550,14 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                     // K step s is block s of the chunk: its exact int8 product, then times the row's block scale
                     const float ds = f16f(s == 0 ? H[U][j][0] : H[U][j][0] >> 16);
 #pragma unroll
-                    for (int i = 0; i < MT; ++i) {
+                    for (int i = 0; i < MX; ++i) {
                         const f32x4_t p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(p[r], ds, acc[i][j][r]);
                     }
                 } else {
 #pragma unroll
-                    for (int i = 0; i < MT; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < MX; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B, acc[i][j], 0, 0, 0);
                 }
             }
         }
@@ -343,7 +565,76 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         load_w(W[U], H[QK || Q8 ? U : 0], Hb[Q5 ? U : 0], l + D);
     };
 
-    if (steps > 0) {                                                      // block-uniform
+    if constexpr (RX) {
+        // The wave's chunks' A operands stay in registers for the whole kernel (the diagonal mapping: lane (lg, r16)
+        // holds x row r16 & 3's values of unit lg of the chunk when lg == r16 >> 2, else zero), so the K loop has no
+        // LDS stage, DMA or barrier; weights run D chunks ahead. A chunk past the wave's count loads nothing (OOB).
+        bf16x8_t AX[CHX][NS];
+        {
+            const int xrow = r16 & 3;
+            const bool lv = lg == (r16 >> 2) && xrow < M;
+#pragma unroll
+            for (int ci = 0; ci < CHX; ++ci) {
+                const bool live = lv && ci < mine && (KFULL || CW * chunk_of(ci) + 32 * lg < K);
+                const uint32_t off = live ? (uint32_t)(((int64_t)xrow * K + CW * chunk_of(ci) + 32 * lg) * 2) : OOB_VOFF;
+#pragma unroll
+                for (int u = 0; u < NS; ++u)
+                    AX[ci][u] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, live ? 16u * u : 0u, 0));
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < D; ++p) load_w(W[p], H[p], Hb[Q5 ? p : 0], p);
+        wait_vm<D * NWL>();                                               // the x loads (issued first) have landed
+        const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{BF16_ONES, BF16_ONES, BF16_ONES, BF16_ONES});
+        f32x4_t DX[CHX];
+#pragma unroll
+        for (int ci = 0; ci < CHX; ++ci) {
+            DX[ci] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < NS; ++u) DX[ci] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AX[ci][u], ones, DX[ci], 0, 0, 0);
+        }
+        kgm_each([&](auto CI) __attribute__((always_inline)) {
+            constexpr int ci = decltype(CI)::value, U = ci % D;
+            if (ci < mine) {                                              // wave-uniform; later chunks are dead too
+                wait_vm<(D - 1 < CHX - 1 - ci ? D - 1 : CHX - 1 - ci) * NWL>();
+                const int j8 = 4 * (chunk_of(ci) & 1) + lg;
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    f32x4_t P = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int u = 0; u < NS; ++u) {
+                        const uint32_t w = W[U][j][u];
+                        u32x4 o;
+                        if constexpr (Q5) {
+                            uint32_t lo, hi;
+                            q5k_bytes(w, Hb[U][j][0], u, &lo, &hi);
+                            const uint32_t c43 = in_vgpr(0x43434343u);
+                            o = u32x4{b128_pair(lo, c43, 0), b128_pair(lo, c43, 1), b128_pair(hi, c43, 0), b128_pair(hi, c43, 1)};
+                        } else {
+                            const uint32_t m = in_vgpr(0x000F000Fu), e = in_vgpr(0x43004300u);
+                            o = u32x4{(w & m) | e, ((w >> 4) & m) | e, ((w >> 8) & m) | e, ((w >> 12) & m) | e};
+                        }
+                        P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AX[ci][u], __builtin_bit_cast(bf16x8_t, o), P, 0, 0, 0);
+                    }
+                    float a, on;
+                    if constexpr (Q40) {
+                        a = f16f(H[U][j][0]);
+                        on = -136.f * a;
+                    } else {
+                        const u32x4 hd = kgm_hdr(H[U][j][0]);
+                        const WsScale c = Q5 ? ws_scale<T_Q5_K>(WsRaw<T_Q5_K>{W[U][j], hd, Hb[U][j][0]}, j8)
+                                             : ws_scale<T_Q4_K>(WsRaw<T_Q4_K>{W[U][j], hd}, j8);
+                        a = c.a;
+                        on = -__builtin_fmaf(128.f, c.a, c.b);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[0][j][r] = __builtin_fmaf(on, DX[ci][r], __builtin_fmaf(a, P[r], acc[0][j][r]));
+                }
+                if constexpr (ci + D < CHX) load_w(W[U], H[U], Hb[Q5 ? U : 0], ci + D);
+            }
+        }, std::make_integer_sequence<int, CHX>{});
+        wait_vm<0>();
+    } else if (steps > 0) {                                               // block-uniform
 #pragma unroll
         for (int p = 0; p < D; ++p) {
             if (p < D - 1) dma_x(p, p);
@@ -357,13 +648,22 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         }, std::make_integer_sequence<int, D - 1>{});
         wait_vm<0>();                                                     // no DMA may land after the rings are reused
     }
+    if constexpr (DIAG) {
+        // lane group g holds sub-block g's share of each output: their sum, in lane group 0's rows 0-3 of each tile
+#pragma unroll
+        for (int i = 0; i < MX; ++i)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][j][r] = kgm_lg_sum(acc[i][j][r]);
+    }
     __syncthreads();
 
     // Reduce-scatter of the K groups' accumulators through LDS, in rounds of TR tiles (a tile: one 16 x 16 float32
     // MFMA result, 1 KiB over the wave): every wave writes its tiles of the round, and the wave that owns a tile (tile tt
     // of row group q belongs to K group tt % KG) adds the KG copies in K-group order. Every wave then holds the block's
     // sums of its TPW tiles, and the split exchange and the stores below run on all 8 waves at once.
-    constexpr int TT = MT * NTW, TR = kgm_round<MT, NTW>(), TPW = (TT + KG - 1) / KG;
+    constexpr int TT = MX * NTW, TR = kgm_round<MX, NTW>(), TPW = (TT + KG - 1) / KG;
     f32x4_t* red = reinterpret_cast<f32x4_t*>(kgm_lds_buf);
     f32x4_t fin[TPW];
 #pragma unroll
@@ -371,7 +671,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 #pragma unroll
     for (int r0 = 0; r0 < TT; r0 += TR) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+        for (int i = 0; i < MX; ++i)
 #pragma unroll
             for (int j = 0; j < NTW; ++j) {
                 const int tt = i * NTW + j;
@@ -392,7 +692,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         __syncthreads();
     }
 
-    constexpr int E = kgm_elems<MT, RG, NTW>();
+    constexpr int E = kgm_elems<MX, RG, NTW>();
     if (g.S > 1) {
         // each wave stores its tiles of the block's partial, (range, split) -> E floats laid out [q][tile][lane]; the
         // split that arrives last adds the S partials of each tile in split order (its own from registers)
@@ -460,7 +760,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         const bool col = tt < TT && n >= rq0 && n < rq1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int m = 16 * i + 4 * lg + r;
+            // diagonal x tiles: x row 4 i + r, stored by lane group 0 (every group holds the same sums)
+            const int m = DIAG ? (lg == 0 ? 4 * i + r : M) : 16 * i + 4 * lg + r;
             const uint32_t off = (col && m < M) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : OOB_VOFF;
             const float v = fin[u][r] * (ok ? sc[u] : __builtin_nanf(""));    // a layer outside the stack: NaN
             if (g.out_bf16)
@@ -475,12 +776,31 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 // A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
 struct KgmPlan { int S, R, RG, NTW; };
 constexpr int KGM_MAX_NTW = 6;
-// most tiles per wave of a type and batch whose units and scales fit the registers without spilling at 256 per lane:
-// Q4_K at 33-64 rows and Q6_K from 17 rows 5; Q5_K 5 at 17-32 and 49-64 rows, 4 at 33-48 (three stages deep)
-constexpr int kgm_max_ntw(int t, int mt) {
-    return t == T_Q5KT ? (mt == 1 ? KGM_MAX_NTW : mt == 3 ? 4 : 5)
-                       : ((t == T_Q4KT || t == T_Q40T) && mt >= 3) || (t == T_Q6KT && mt >= 2) ? 5 : KGM_MAX_NTW;
+// most tiles per wave of a type, x-tile parameter (kgm_mt) and row-group count whose units and scales fit the registers
+// without spilling at 256 per lane (two row groups keep three stages of weights in flight, one group two); from the
+// compiler's register counts of every instance:
+//   per-value dequantization: Q4_K / Q4_0 at 33-64 rows 5, Q6_K from 17 rows 5, Q5_K 5 (4 at 33-48 rows);
+//   factored products (9-32 rows): Q4_K / Q4_0 6 (5 at 17-32 rows with two row groups); Q5_K one row group 6 (4 at
+//   17-32 rows), two row groups 4 (3);
+//   diagonal x tiles: at 1-4 rows (x in registers, one row group) 6; at 5-8 rows Q4_K / Q4_0 6 (with two row groups
+//   4 / 5), Q5_K 5 (4).
+constexpr int kgm_max_ntw(int t, int mt, int rg) {
+    const bool q5 = t == T_Q5KT, q4 = t == T_Q4KT || t == T_Q40T;
+    if (mt == -1) return rg == 1 ? KGM_MAX_NTW : 0;                        // x in registers: one row group only
+    if (mt < 0) return q5 ? (rg == 1 ? 5 : 4) : rg == 1 ? KGM_MAX_NTW : (t == T_Q4KT ? 4 : 5);
+    const bool fact = (q4 || q5) && mt <= 2;
+    if (q5) return fact ? (rg == 1 ? (mt == 1 ? KGM_MAX_NTW : 4) : (mt == 1 ? 4 : 3)) : (mt == 3 ? 4 : 5);
+    if (q4) return fact ? (mt == 2 && rg == 2 ? 5 : KGM_MAX_NTW) : 5;
+    if (t == T_Q6KT) return mt >= 2 ? 5 : KGM_MAX_NTW;
+    return KGM_MAX_NTW;
 }
+
+// the kernel's x-tile parameter for M activation rows: 16-row x tiles (1-4), or for the nibble tiles at up to 8 rows
+// -1 / -2: one or two sub-block-diagonal x tiles of 4 rows each (the kernel's DIAG path)
+constexpr int kgm_mt(int t, int64_t M) {
+    return (t == T_Q4KT || t == T_Q5KT || t == T_Q40T) && M <= 8 ? (M <= 4 ? -1 : -2) : (int)((M + 15) / 16);
+}
+constexpr int kgm_abs(int v) { return v < 0 ? -v : v; }
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
 static int kgm_ntw(int64_t N, int64_t R, int RG) {
@@ -506,7 +826,7 @@ static int kgm_ntw(int64_t N, int64_t R, int RG) {
 static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int force_s) {
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
-    const int MT = (int)((M + 15) / 16);
+    const int MTS = kgm_mt(t, M), MT = kgm_abs(MTS);
     const double wpc = t == T_Q4KT ? 72.0 : t == T_Q40T ? 72.0 : t == T_Q5KT ? 88.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
     const double waste_w = (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT || t == T_Q40T) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
     KgmPlan best{0, 0, 0, 0};
@@ -520,12 +840,16 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
                 const int KG = 8 / RG;
                 if (kgm_ring(t, MT, RG) > KGM_LDS_MAX) continue;
                 const int ntw = kgm_ntw(N, R, RG);
-                if (ntw > kgm_max_ntw(t, MT)) continue;
+                if (ntw > kgm_max_ntw(t, MTS, RG)) continue;
                 const int64_t kcs = (KC + S - 1) / S;
+                if (MTS == -1 && (kcs + KG - 1) / KG > kgm_rx_chunks()) continue;       // the chunks x registers hold
                 const double w = (double)R * kcs * wpc;                         // weight bytes
-                const double x = 0.5 * 16 * MT * 2 * CW * kcs;                  // x bytes (L2 hits: half weight)
-                // partial tile written, and S read by the last arriver at the end of its work (twice the weight)
-                const double part = S > 1 ? (double)RG * MT * ntw * 1024 * (1 + 2 * S) : 0.0;
+                // x bytes (L2 hits: half weight); diagonal x tiles move only the batch's rows
+                const double x = 0.5 * (MTS < 0 ? (double)M : 16.0 * MT) * 2 * CW * kcs;
+                // partial tile written, and S read by the last arriver at the end of its work (twice the weight), and
+                // the exchange's dependent round trips (store and wait, arrival count, partial loads): about 4 us at
+                // 1-16 rows, a CU's share of 96 KB (MI355X, K-group plans of a 27B-class layer forced to 1-8 splits)
+                const double part = S > 1 ? (double)RG * MT * ntw * 1024 * (1 + 2 * S) + (M <= 16 ? 96e3 : 0.0) : 0.0;
                 const double waste = waste_w * (double)std::max<int64_t>(0, RG * ntw * 16 - R) * kcs * wpc;
                 const double idle = (double)((kcs + KG - 1) / KG * KG - kcs) / (double)kcs;
                 const double cost = (w + x + part + waste) * (1.0 + idle);
@@ -543,11 +867,12 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
 // ------------------------------------------------------------------------------------------------------ launchers
 template <int T, int MT, int RG, int NTW, bool KFULL>
 static int kgm_launch(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
-    if constexpr (kgm_ring(T, MT, RG) > KGM_LDS_MAX || NTW > kgm_max_ntw(T, MT)) {
-        return set_error(MBQ_BAD_ARG, "K-group GEMM: no kernel of %d row groups x %d tiles at %d activation rows", RG, NTW, 16 * MT);
+    if constexpr (kgm_ring(T, kgm_abs(MT), RG) > KGM_LDS_MAX || NTW > kgm_max_ntw(T, MT, RG)) {
+        return set_error(MBQ_BAD_ARG, "K-group GEMM: no kernel of %d row groups x %d tiles at %d activation rows", RG, NTW,
+                         MT < 0 ? -4 * MT : 16 * MT);
     } else {
         auto kern = kgemm_kernel<T, MT, RG, NTW, KFULL>;
-        const size_t lds = kgm_lds<T, MT, RG, NTW>();
+        const size_t lds = kgm_lds<T, kgm_abs(MT), RG, NTW>();
         static std::atomic<uint64_t> lds_set{0};
         if (set_lds_limit((const void*)kern, lds, lds_set) != hipSuccess)
             return set_error(MBQ_LAUNCH_FAIL, "K-group GEMM: %zu bytes of LDS refused", lds);
@@ -584,6 +909,10 @@ static int kgm_launch_rg(const Args& a, const KgmPlan& p, const Workspace& w, hi
 
 template <int T, bool KFULL>
 static int kgm_launch_mt(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
+    if constexpr (T == T_Q4KT || T == T_Q5KT || T == T_Q40T) {
+        if (a.M <= 4) return kgm_launch_rg<T, -1, KFULL>(a, p, w, s);
+        if (a.M <= 8) return kgm_launch_rg<T, -2, KFULL>(a, p, w, s);
+    }
     switch ((a.M + 15) / 16) {
         case 1: return kgm_launch_rg<T, 1, KFULL>(a, p, w, s);
         case 2: return kgm_launch_rg<T, 2, KFULL>(a, p, w, s);
@@ -593,8 +922,8 @@ static int kgm_launch_mt(const Args& a, const KgmPlan& p, const Workspace& w, hi
 }
 
 // bytes of the partial tiles of a plan
-static size_t kgm_ws_bytes(int64_t M, int64_t N, const KgmPlan& p) {
-    const int MT = (int)((M + 15) / 16);
+static size_t kgm_ws_bytes(int t, int64_t M, int64_t N, const KgmPlan& p) {
+    const int MT = kgm_abs(kgm_mt(t, M));
     const int64_t ranges = (N + p.R - 1) / p.R;
     return (size_t)ranges * p.S * p.RG * MT * p.NTW * 256 * 4;
 }
@@ -620,7 +949,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     Workspace w;
     if (p.S > 1) {
         const int64_t ranges = (a.N + p.R - 1) / p.R;
-        if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.M, a.N, p), s, &w)) return rc;
+        if (int rc = split_workspace(a, ranges, kgm_ws_bytes(t, a.M, a.N, p), s, &w)) return rc;
     }
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
     if (t == T_Q6KT) return kgm_launch_mt<T_Q6KT, true>(a, p, w, s);

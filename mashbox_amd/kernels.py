@@ -69,13 +69,21 @@ def kq_covers(t: int, shape) -> bool:
     return bool(lib().mbq_covers(int(t), rows, cols))
 
 
+# weight layouts repack can produce: the row-major planes, the 16-row tiles of TILED[t], or both (tiles, with the
+# row-major planes of the same weights beside them for single-row calls)
+LAYOUTS = ("rowmajor", "tiles", "both")
+
+
 class Planes:
     """The kernel planes of one (rows, cols) weight or a stack of them: `buf` is a flat uint8 tensor of
-    prod(lead) * plane_bytes bytes (host or device), weight i of the stack at byte i * plane_bytes."""
+    prod(lead) * plane_bytes bytes (host or device), weight i of the stack at byte i * plane_bytes. `alt`, when set, is
+    the row-major planes of the same weights (layout "both"): matmul runs single-row calls on it (the decode GEMV) and
+    everything else on these planes."""
 
-    def __init__(self, buf: torch.Tensor, t: int, n: int, k: int, lead=()):
+    def __init__(self, buf: torch.Tensor, t: int, n: int, k: int, lead=(), alt: "Planes | None" = None):
         self.buf, self.t, self.N, self.K, self.lead = buf, int(t), int(n), int(k), tuple(int(v) for v in lead)
         self.stride = plane_bytes(self.t, (self.N, self.K))
+        self.alt = alt
 
     @property
     def count(self) -> int:
@@ -84,8 +92,14 @@ class Planes:
             c *= v
         return c
 
+    @property
+    def nbytes(self) -> int:
+        """bytes the planes take (both layouts' with `alt`)"""
+        return self.buf.numel() + (self.alt.nbytes if self.alt is not None else 0)
+
     def to(self, device) -> "Planes":
-        return Planes(self.buf.to(device), self.t, self.N, self.K, self.lead)
+        return Planes(self.buf.to(device), self.t, self.N, self.K, self.lead,
+                      None if self.alt is None else self.alt.to(device))
 
     def __getitem__(self, i) -> "Planes":
         """one weight (or sub-stack) of a stack along the first stacked axis: a view, no copy"""
@@ -99,10 +113,12 @@ class Planes:
             raise IndexError(i)
         i %= self.lead[0]
         size = inner * self.stride
-        return Planes(self.buf[i * size:(i + 1) * size], self.t, self.N, self.K, self.lead[1:])
+        return Planes(self.buf[i * size:(i + 1) * size], self.t, self.N, self.K, self.lead[1:],
+                      None if self.alt is None else self.alt[i])
 
     def __repr__(self):
-        return f"Planes({NAMES.get(self.t, self.t)}, lead={self.lead}, ({self.N}, {self.K}), {self.buf.device})"
+        extra = " + row-major" if self.alt is not None else ""
+        return f"Planes({NAMES.get(self.t, self.t)}{extra}, lead={self.lead}, ({self.N}, {self.K}), {self.buf.device})"
 
 
 def _check_raw(t: int, raw_shape, shape):
@@ -116,6 +132,17 @@ def _check_raw(t: int, raw_shape, shape):
     return t, rows, cols, tuple(int(v) for v in raw_shape[:-2])
 
 
+def _layout_of(t: int, tiled: bool, layout) -> str:
+    """the layout of a repack call: `layout` when given (one of LAYOUTS), else tiles when tiled=True"""
+    if layout is None:
+        return "tiles" if tiled else "rowmajor"
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout {layout!r} is not one of {LAYOUTS}")
+    if layout != "rowmajor" and int(t) not in TILED:
+        raise NotImplementedError(f"{NAMES.get(int(t), t)} has no tiled planes (tiled: {[NAMES[v] for v in TILED]})")
+    return layout
+
+
 def _plane_type(t: int, tiled: bool) -> int:
     if not tiled:
         return t
@@ -124,9 +151,16 @@ def _plane_type(t: int, tiled: bool) -> int:
     return TILED[t]
 
 
-def repack_host(t: int, raw, shape, threads: int = 0, tiled: bool = False) -> Planes:
+def repack_host(t: int, raw, shape, threads: int = 0, tiled: bool = False, layout=None) -> Planes:
     """host blocks (..., rows, row_bytes) uint8 -> host planes, on the host's cores (C++ threads)
-    (reference src/mashbox/ops/__init__.py:22-23,473-474); tiled=True: the 16-row tiles of TILED[t]"""
+    (reference src/mashbox/ops/__init__.py:22-23,473-474); tiled=True (or layout="tiles"): the 16-row tiles of TILED[t];
+    layout="both": the tiles with the row-major planes as `alt`"""
+    lay = _layout_of(t, tiled, layout)
+    if lay == "both":
+        p = repack_host(t, raw, shape, threads, layout="tiles")
+        p.alt = repack_host(t, raw, shape, threads)
+        return p
+    tiled = lay == "tiles"
     raw = np.ascontiguousarray(np.asarray(raw), dtype=np.uint8)
     t, rows, cols, lead = _check_raw(t, raw.shape, shape)
     t = _plane_type(t, tiled)
@@ -141,12 +175,19 @@ def repack_host(t: int, raw, shape, threads: int = 0, tiled: bool = False) -> Pl
     return Planes(out, t, rows, cols, lead)
 
 
-def repack(t: int, raw: torch.Tensor, shape, stacked: bool = False, tiled: bool = False) -> Planes:
+def repack(t: int, raw: torch.Tensor, shape, stacked: bool = False, tiled: bool = False, layout=None) -> Planes:
     """device blocks (..., rows, row_bytes) uint8 (a torch tensor on the GPU) -> device planes, by the GPU
     (reference src/mashbox/ops/__init__.py:16,475-485). `stacked` is accepted for the surface; leading axes are a stack.
-    tiled=True: the 16-row tiles of TILED[t]."""
+    tiled=True (or layout="tiles"): the 16-row tiles of TILED[t]; layout="both": the tiles with the row-major planes as
+    `alt`."""
+    lay = _layout_of(t, tiled, layout)
     if not raw.is_cuda:
-        return repack_host(t, raw.numpy(), shape, tiled=tiled).to(torch.device("cuda", torch.cuda.current_device()))
+        return repack_host(t, raw.numpy(), shape, layout=lay).to(torch.device("cuda", torch.cuda.current_device()))
+    if lay == "both":
+        p = repack(t, raw, shape, stacked, layout="tiles")
+        p.alt = repack(t, raw, shape, stacked)
+        return p
+    tiled = lay == "tiles"
     raw = raw.contiguous()
     t, rows, cols, lead = _check_raw(t, tuple(raw.shape), shape)
     t = _plane_type(t, tiled)
@@ -188,6 +229,8 @@ def matmul(x: torch.Tensor, p: Planes, layer=None, out_dtype=torch.float32) -> t
     empty result without a launch. layer= reads weight `layer` of a one-axis stack in place."""
     if not p.buf.is_cuda:
         raise ValueError(f"{p} is on the host: move the planes to the GPU (planes.to('cuda'))")
+    if p.alt is not None and x.numel() == x.shape[-1]:
+        p = p.alt                                     # one activation row: the row-major planes' decode GEMV
     p, lh, ld, nl = _layer_args(p, layer)
     lead = tuple(x.shape[:-1])
     if x.shape[-1] != p.K:
@@ -240,5 +283,5 @@ def take_rows(p: Planes, ids, layer=None) -> torch.Tensor:
     return w.reshape(tuple(ids.shape) + (p.K,))
 
 
-__all__ = ["TYPES", "TILED", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers",
+__all__ = ["TYPES", "TILED", "LAYOUTS", "take_rows", "Planes", "repack_host", "repack", "matmul", "dequant", "plane_bytes", "kq_covers",
            "picks_layer", "row_bytes", "INT8", "Q4KT", "Q8T", "Q5KT", "Q6KT", "Q40T"]

@@ -29,9 +29,12 @@ the reference dequantization), exact_chunk_rows rows at a time, and multiplied b
 on the host's CPU; without libmbq.so every call raises. The forced-failure switch is the reference's MASHBOX_FAULT
 (force:kernels-package, force:quant-kernel; reference src/mashbox/runtime/faults.py:14-16,57-61).
 
-Layout switch of this build (no counterpart in the reference): with env MBQ_TILES=1, weights of the types the kernel
-package can tile (its TILED map: every GGUF type it serves) load as 16-row tiles instead of row-major planes, the faster layout for decode
-batches of several rows; everything else is unchanged.
+Weight layout (no counterpart in the reference, whose kernel package has one): weights of the types the kernel package
+can tile (its TILED map: every GGUF type it serves) load as its 16-row tiles, the layout its K-group kernel runs at
+2-64 activation rows and its prefill GEMM runs fastest on (MI355X, a 27B-class Q4_K layer: 4 rows 87 us against 122 us
+on row-major planes, 16 rows 98 against 137, 2048 rows 1339 against 1398); at one row the row-major planes' decode
+GEMV is faster (64 against 84 us). Env MBQ_LAYOUT picks another: "rowmajor", or "both" (the tiles plus the row-major
+planes of the same weights, twice the bytes: every batch size gets its faster kernel).
 """
 from __future__ import annotations
 
@@ -263,8 +266,13 @@ def device_nbytes(t: int, shape, nbytes: int, kernel_types=None) -> int:
     if size is None or weight_path(t, shape, kernel_types) != "kq":
         return int(nbytes)
     shape = tuple(int(v) for v in shape)
-    pt = _KERNELS.module.TILED[int(t)] if _tiled(t) else int(t)
-    return int(np.prod(shape[:-2], dtype=np.int64)) * int(size(pt, shape[-2:]))
+    lay = _layout(t)
+    one = 0
+    if lay in ("tiles", "both"):
+        one += int(size(_KERNELS.module.TILED[int(t)], shape[-2:]))
+    if lay in ("rowmajor", "both"):
+        one += int(size(int(t), shape[-2:]))
+    return int(np.prod(shape[:-2], dtype=np.int64)) * one
 
 
 # ---------------------------------------------------------------------------------------------------------- prepare
@@ -276,18 +284,28 @@ def _as_tensor(raw) -> torch.Tensor:
     return raw if isinstance(raw, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(raw, np.uint8)))
 
 
-def _tiled(t: int) -> bool:
-    """weights of type t load as the kernel package's 16-row tiles (env MBQ_TILES=1 and a type it can tile)"""
-    return os.environ.get("MBQ_TILES", "") == "1" and int(t) in getattr(_KERNELS.module, "TILED", {})
+LAYOUTS = ("tiles", "rowmajor", "both")
+
+
+def _layout(t: int) -> str:
+    """the layout weights of type t load in: env MBQ_LAYOUT ("tiles" by default, "rowmajor" or "both") for a type the
+    kernel package tiles (its TILED map), else "rowmajor" (the package's only planes)"""
+    if int(t) not in getattr(_KERNELS.module, "TILED", {}):
+        return "rowmajor"
+    lay = os.environ.get("MBQ_LAYOUT", "tiles") or "tiles"
+    if lay not in LAYOUTS:
+        raise ValueError(f"MBQ_LAYOUT={lay!r} is not one of {LAYOUTS}")
+    return lay
 
 
 def _planes_of(raw, t: int, shape):
     """the kernel package's planes on the device: its host repack for host blocks when it has one, else its repack
-    (16-row tiles when _tiled(t))"""
+    (in the layout _layout(t) names)"""
     mod = _KERNELS.module
     if forced("quant-kernel"):
         raise RuntimeError("forced by MASHBOX_FAULT=force:quant-kernel")
-    kw = {"tiled": True} if _tiled(t) else {}
+    lay = _layout(t)
+    kw = {"layout": lay} if lay != "rowmajor" else {}
     if not isinstance(raw, torch.Tensor) and hasattr(mod, "repack_host"):
         return mod.repack_host(t, np.asarray(raw), tuple(shape), **kw).to(_device())
     r = _as_tensor(raw).to(_device())

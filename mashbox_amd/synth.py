@@ -117,5 +117,9 @@ EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          "m4_q4k": (12, 4, LAYER_27B), "m16_q4k": (12, 16, LAYER_27B), "m4_q8": (8, 4, LAYER_27B), "m16_q8": (8, 16, LAYER_27B),
          "m4_q5k": (13, 4, LAYER_27B), "m16_q5k": (13, 16, LAYER_27B),
          "m4_q6k": (14, 4, LAYER_27B), "m16_q6k": (14, 16, LAYER_27B),
-         "m4_int8": ("int8", 4, LAYER_27B), "m16_int8": ("int8", 16, LAYER_27B)}
+         "m4_int8": ("int8", 4, LAYER_27B), "m16_int8": ("int8", 16, LAYER_27B),
+         # single-row decode of the same layer: row-major planes (decode GEMV) and the same weights as 16-row tiles
+         "m1_q4k": (12, 1, LAYER_27B), "m1_q4k_tiles": (12, 1, LAYER_27B),
+         # config 5's prefill on the row-major planes (config 5 itself loads the weights as 16-row tiles)
+         "c5_rm": (12, 2048, LAYER_27B)}
 REF_TPU_US = {"q6k_head": 369.8}

@@ -236,10 +236,10 @@ def test_kgroup_graph_replays(t, forced_plan, cuda):
 
 @pytest.mark.parametrize("t", TYPES, ids=NAME.get)
 def test_ops_prepare_loads_tiles(t, monkeypatch, cuda):
-    """with MBQ_TILES=1 the ops layer loads Q4_K, Q8_0, Q6_K and Q5_K weights (one and a stack) as tiles: qmatmul at 1, 4 and 300 rows,
-    layer= in place and dequant against the oracle; device_nbytes counts the tiled planes"""
+    """by default the ops layer loads every GGUF type's weights (one and a stack) as tiles: qmatmul at 1, 4 and 300
+    rows, layer= in place and dequant against the oracle; device_nbytes counts the tiled planes"""
     from mashbox_amd import ops
-    monkeypatch.setenv("MBQ_TILES", "1")
+    monkeypatch.delenv("MBQ_LAYOUT", raising=False)
     ops.load_kernels()
     rng = np.random.default_rng(129)
     n, k, L = 100, 512, 2
@@ -257,3 +257,39 @@ def test_ops_prepare_loads_tiles(t, monkeypatch, cuda):
         for i in range(L):
             y = ops.qmatmul(x.float(), ops.At(hs.packed, i, t, (n, k))).float().cpu().numpy()
             assert_product(y, xf @ w[i].astype(np.float64).T, f"prepare stack layer {i} m={m}")
+
+
+@pytest.mark.parametrize("t", TYPES, ids=NAME.get)
+def test_default_prepare_at_decode_buckets(t, monkeypatch, cuda):
+    """the ops layer's default prepare (no environment switch) serves a decoding server's row buckets 1, 4 and 16
+    (reference src/mashbox/runtime/engine.py:424-428) from one load: every output against the float64 product of the
+    oracle's dequantization, for one weight and for a layer of a stack read in place; layout "both" holds the
+    row-major planes beside the tiles and runs one row on them (the decode GEMV's bits) and 4 and 16 rows on the tiles
+    (the K-group kernel's bits)"""
+    from mashbox_amd import ops
+    monkeypatch.delenv("MBQ_LAYOUT", raising=False)
+    ops.load_kernels()
+    rng = np.random.default_rng([t, 130])
+    n, k, L = 1000, 2048, 2
+    st = np.stack([G.RAW[t](rng, n, k) for _ in range(L)])
+    h = ops.prepare(st[1], t, (n, k))
+    hs = ops.prepare(st, t, (n, k))
+    assert h.packed.t == KQ.TILED[t] and h.packed.alt is None
+    w64 = torch.from_numpy(R.dequant(st[1], t, k)).to(cuda).to(torch.float64)
+    monkeypatch.setenv("MBQ_LAYOUT", "both")
+    hb = ops.prepare(st[1], t, (n, k))
+    assert hb.packed.t == KQ.TILED[t] and hb.packed.alt is not None and hb.packed.alt.t == t
+    assert ops.device_nbytes(t, (n, k), st[1].nbytes) == KQ.plane_bytes(KQ.TILED[t], (n, k)) + KQ.plane_bytes(t, (n, k))
+    rm = KQ.repack_host(t, st[1], (n, k)).to(cuda)
+    for m in (1, 4, 16):
+        xb, x = _x(rng, m, k, cuda)
+        ref = x.to(torch.float64) @ w64.T
+        print(f"{NAME[t]} default prepare m={m} ({LIB.plan_str(KQ.TILED[t], m, n, k)})", flush=True)
+        y = ops.qmatmul(x, h)
+        assert y.dtype == torch.bfloat16
+        assert_product_dev(y, ref, f"{NAME[t]} default m={m}")
+        ya = ops.qmatmul(x, ops.At(hs.packed, 1, t, (n, k)))
+        assert torch.equal(ya.view(torch.int16), y.view(torch.int16)), f"{NAME[t]} stack layer m={m}"
+        yb = ops.qmatmul(x, hb)
+        want = KQ.matmul(x, rm if m == 1 else h.packed, out_dtype=torch.bfloat16)
+        assert torch.equal(yb.view(torch.int16), want.view(torch.int16)), f"{NAME[t]} both m={m}"

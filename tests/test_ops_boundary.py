@@ -24,7 +24,8 @@ def _reset():
 
 
 # ------------------------------------------------------------------------------------------------ CPU: routing
-def test_weight_path_and_device_bytes():
+def test_weight_path_and_device_bytes(monkeypatch):
+    monkeypatch.delenv("MBQ_LAYOUT", raising=False)
     assert ops.load_kernels() == frozenset({2, 8, 12, 13, 14})
     assert ops.weight_path(12, (5120, 17408)) == "kq" and ops.weight_path(8, (17408, 5120)) == "kq"
     assert ops.weight_path(14, (256, 256)) == "kq"
@@ -32,10 +33,20 @@ def test_weight_path_and_device_bytes():
     assert ops.weight_path(12, (5, 100)) == "exact"                      # kq_covers: not whole super-blocks
     assert ops.weight_path(12, (256, 256), kernel_types=frozenset()) == "exact"
     nb = 5120 * R.row_bytes(12, 17408)
-    assert ops.device_nbytes(12, (5120, 17408), nb) == KQ.plane_bytes(12, (5120, 17408))
-    assert ops.device_nbytes(12, (3, 5120, 17408), 3 * nb) == 3 * KQ.plane_bytes(12, (5120, 17408))
+    # the default layout is the kernel package's 16-row tiles; MBQ_LAYOUT picks row-major planes or both
+    tiles, rm = KQ.plane_bytes(KQ.TILED[12], (5120, 17408)), KQ.plane_bytes(12, (5120, 17408))
+    assert ops.device_nbytes(12, (5120, 17408), nb) == tiles
+    assert ops.device_nbytes(12, (3, 5120, 17408), 3 * nb) == 3 * tiles
     assert ops.device_nbytes(14, (256, 256), 12345, kernel_types=frozenset({8, 12})) == 12345
-    assert ops.device_nbytes(14, (256, 256), 12345) == KQ.plane_bytes(14, (256, 256))
+    assert ops.device_nbytes(14, (256, 256), 12345) == KQ.plane_bytes(KQ.TILED[14], (256, 256))
+    monkeypatch.setenv("MBQ_LAYOUT", "rowmajor")
+    assert ops.device_nbytes(12, (3, 5120, 17408), 3 * nb) == 3 * rm
+    monkeypatch.setenv("MBQ_LAYOUT", "both")
+    assert ops.device_nbytes(12, (3, 5120, 17408), 3 * nb) == 3 * (rm + tiles)
+    monkeypatch.setenv("MBQ_LAYOUT", "diagonal")
+    with pytest.raises(ValueError):
+        ops.device_nbytes(12, (5120, 17408), nb)
+    monkeypatch.delenv("MBQ_LAYOUT")
     ops.load_kernels(module="off")
     assert ops.weight_path(12, (256, 256)) == "exact"
 
