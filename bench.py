@@ -487,7 +487,7 @@ def summarize_counters(d, kernel_substr=None, simds=1024, clock_ghz=2.17):
             t_ns = sum(dur[(kern, "SQ_VALU_MFMA_BUSY_CYCLES")])
             print(f"| MFMA busy share: SQ_VALU_MFMA_BUSY_CYCLES / ({simds} SIMDs x {clock_ghz} GHz x dispatch time) | "
                   f"{busy / (simds * t_ns * clock_ghz):.3f} |")
-        if "SQ_VALU_MFMA_COEXEC_CYCLES" in o and "SQ_VALU_MFMA_BUSY_CYCLES" in o:
+        if "SQ_VALU_MFMA_COEXEC_CYCLES" in o and o.get("SQ_VALU_MFMA_BUSY_CYCLES"):
             print(f"| SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES | "
                   f"{o['SQ_VALU_MFMA_COEXEC_CYCLES'] / o['SQ_VALU_MFMA_BUSY_CYCLES']:.3f} |")
         if "SQ_INSTS_VALU" in o and "SQ_INSTS_MFMA" in o and o["SQ_INSTS_MFMA"]:
