@@ -15,7 +15,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmbq.so")
-SOURCES = ["mbq_kernels.hip", "mbq_gemv.hip", "mbq_gemm.hip", "mbq_wsgemm.hip", "mbq_kgemm.hip", "mbq_probe.hip", "mbq_abi.cpp"]
+SOURCES = ["mbq_kernels.hip", "mbq_gemv.hip", "mbq_tgemv.hip", "mbq_gemm.hip", "mbq_wsgemm.hip", "mbq_kgemm.hip", "mbq_probe.hip", "mbq_abi.cpp"]
 ARCH = os.environ.get("MBQ_OFFLOAD_ARCH", "gfx950")
 
 

@@ -1014,6 +1014,7 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
 
 // forced plan (tests, tuning): kernel, tile rows, tile columns, splits; kernel 0 = automatic
 static std::atomic<int> g_force_kind{0}, g_force_bm{0}, g_force_bn{0}, g_force_s{0};
+int forced_gemm_kernel() { return g_force_kind.load(); }
 
 template <int T>
 static int find_cand(int bm, int bn) {

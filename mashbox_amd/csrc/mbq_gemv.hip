@@ -515,6 +515,7 @@ static int launch_gemv_t(const Args& a, hipStream_t s) {
 }
 
 int launch_gemv(int t, const Args& a, hipStream_t s) {
+    if (tiled_type(t)) return launch_tgemv(t, a, s);   // one row on 16-row tiles (mbq_tgemv.hip)
     switch (t) {
         case T_Q4_0: return launch_gemv_t<T_Q4_0>(a, s);
         case T_Q8_0: return launch_gemv_t<T_Q8_0>(a, s);
@@ -539,6 +540,7 @@ static bool gemv_runs_t(const Args& a) {
 }
 
 bool gemv_runs(int t, const Args& a) {
+    if (tiled_type(t)) return tgemv_runs(t, a);
     switch (t) {
         case T_Q4_0: return gemv_runs_t<T_Q4_0>(a);
         case T_Q8_0: return gemv_runs_t<T_Q8_0>(a);

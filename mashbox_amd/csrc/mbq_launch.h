@@ -69,6 +69,10 @@ int cus_of_device();
 int launch_matmul(int t, const Args& a, hipStream_t s);
 int launch_gemv(int t, const Args& a, hipStream_t s);   // M <= GEMV_MAX_M (mbq_gemv.hip)
 bool gemv_runs(int t, const Args& a);                   // the GEMV has a plan for this call (else the weight stream runs it)
+// decode GEMV on 16-row tile planes (mbq_tgemv.hip), one activation row: launch_gemv and gemv_runs route tiled types
+// there; it does not run while a GEMM kernel is forced (force_gemm_plan)
+int launch_tgemv(int t, const Args& a, hipStream_t s);
+bool tgemv_runs(int t, const Args& a);
 int launch_gemm(int t, const Args& a, hipStream_t s);   // M > GEMV_MAX_M
 // weight-stream GEMM (mbq_wsgemm.hip) for GEMV_MAX_M < M <= WS_MAX_M: rows_per_block 32 or 64, splits >= 1
 constexpr int64_t WS_MAX_M = 64;
@@ -83,6 +87,7 @@ int kgemm_plan(int t, const Args& a, int splits, int* rows_per_block, int* chose
 enum : int { K_AUTO = 0, K_GEMV = 0, K_STREAM = 1, K_TILES = 2, K_KGROUP = 3 };
 int gemm_plan(int t, const Args& a, int* kernel, int* bm, int* bn, int* splits);
 int force_gemm_plan(int kernel, int bm, int bn, int splits);
+int forced_gemm_kernel();                                 // the forced kernel, or K_AUTO
 int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t out_rows, hipStream_t s);   // rows: a row gather, or nullptr
 int launch_int8_embed(const int8_t* q, const float* s, int64_t N, int64_t D, const int32_t* toks, int64_t T, void* y,
                       int out_bf16, hipStream_t st);

@@ -3,9 +3,9 @@ libmbq's MBQ_Q4KT, MBQ_Q8T, MBQ_Q6KT and MBQ_Q5KT planes) against the reference'
 src/mashbox/ops/reference.py:132-149, :101-103, :164-173, :150-159) and its dequantize-then-matmul (reference src/mashbox/ops/__init__.py:594-632).
 
 Oracle: oracle.ref's dequantization of the same blocks (bit for bit for dequant, take_rows and the repack) and the
-float64 product of those weights (tests/_check.py bars). Batches of 1-64 rows run the K-group kernel (mbq_kgemm.hip),
-which reads only tiled planes; batches past 64 rows run the same LDS-tile plans as row-major planes, so there the two
-layouts give the same bits.
+float64 product of those weights (tests/_check.py bars). One row runs the tile GEMV (mbq_tgemv.hip) and 2-64 rows the
+K-group kernel (mbq_kgemm.hip), which read only tiled planes; batches past 64 rows run the same LDS-tile plans as
+row-major planes, so there the two layouts give the same bits.
 """
 import ctypes
 
@@ -95,7 +95,9 @@ def _matmul_case(t, n, k, m, cuda):
     assert_product(y, ref, f"{NAME[t]} tiles m={m} n={n} k={k} ({plan})")
     yb = KQ.matmul(x, p, out_dtype=torch.bfloat16)
     assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y))
-    if m <= 64:
+    if m == 1:
+        assert LIB.gemm_plan(KQ.TILED[t], m, n, k)[0] == LIB.KERNEL_GEMV
+    elif m <= 64:
         assert LIB.gemm_plan(KQ.TILED[t], m, n, k)[0] == LIB.KERNEL_KGROUP
     else:                                                       # the row-major planes' plan: the same bits
         assert plan == LIB.plan_str(t, m, n, k)
@@ -172,11 +174,11 @@ def test_stack_read_in_place(t, m, cuda):
 
 
 @pytest.mark.parametrize("t", TYPES, ids=NAME.get)
-@pytest.mark.parametrize("m", [4, 16])
+@pytest.mark.parametrize("m", [1, 4, 16])
 def test_27b_layer_at_decode_buckets(t, m, cuda):
-    """the 7 projections of a 27B-class layer at the engine's row buckets 4 and 16 (reference
-    src/mashbox/runtime/engine.py:424-428): every output against the float64 product (on the GPU) of the oracle's
-    dequantization"""
+    """the 7 projections of a 27B-class layer at the engine's row buckets 1, 4 and 16 (reference
+    src/mashbox/runtime/engine.py:424-428; one row: the tile GEMV, 4 and 16: the K-group kernel): every output against
+    the float64 product (on the GPU) of the oracle's dequantization"""
     rng = np.random.default_rng([m, 126])
     for name, (n, k) in G.LAYER_27B.items():
         raw = G.RAW[t](rng, n, k)
@@ -293,3 +295,24 @@ def test_default_prepare_at_decode_buckets(t, monkeypatch, cuda):
         yb = ops.qmatmul(x, hb)
         want = KQ.matmul(x, rm if m == 1 else h.packed, out_dtype=torch.bfloat16)
         assert torch.equal(yb.view(torch.int16), want.view(torch.int16)), f"{NAME[t]} both m={m}"
+
+
+@pytest.mark.parametrize("t", [R.Q4_K, R.Q8_0, R.Q6_K], ids=NAME.get)
+def test_tile_gemv_long_rows(t, cuda):
+    """one row of 28672 values (x staged in LDS in two batches; the 16-wave blocks of a 5120-row weight) and a 70-row
+    weight whose single block holds a partial tile: every output against the float64 product of the oracle's
+    dequantization, in float32 and bfloat16 (the bfloat16 output is the float32 one rounded)"""
+    rng = np.random.default_rng([t, 131])
+    for n, k in ((5120, 28672), (70, 28672)):
+        assert LIB.gemm_plan(KQ.TILED[t], 1, n, k)[0] == LIB.KERNEL_GEMV
+        raw = G.RAW[t](rng, n, k)
+        xb, x = _x(rng, 1, k, cuda)
+        p = KQ.repack(t, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
+        print(f"{NAME[t]} tile GEMV {n}x{k}", flush=True)
+        y = KQ.matmul(x, p)
+        w64 = torch.from_numpy(R.dequant(raw, t, k)).to(cuda).to(torch.float64)
+        assert_product_dev(y, x.to(torch.float64) @ w64.T, f"{NAME[t]} tile GEMV {n}x{k}")
+        yb = KQ.matmul(x, p, out_dtype=torch.bfloat16)
+        assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y.cpu().numpy()))
+        del w64
+        torch.cuda.empty_cache()

@@ -2,7 +2,8 @@
 the benchmark configs: the specialized-wave GEMM (producer waves dequantize weights into LDS for the consumer waves;
 Q4_K with the even split of that work, Q6_K with the uneven one) and the K-group kernel (x staged by DMA, the K groups'
 sums reduced through LDS, and, for the down projection, split-K partials exchanged through memory). Every one of these
-sums in a fixed order, so repeated calls give the same bits; a writer that passes a barrier before its writes land
+sums in a fixed order, so repeated calls give the same bits; and the tile GEMV at one row (x staged in LDS, each
+tile's rows summed over the waves through LDS), in its 8-wave and 16-wave blocks; a writer that passes a barrier before its writes land
 shows as calls that differ (seen on MI355X as stale dequantized weights once the producers were sped up, until the
 producers waited for their LDS writes before each barrier)."""
 import pytest
@@ -15,8 +16,10 @@ from mashbox_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(12, 2048, 6144, 5120), (14, 2048, 5120, 6144), ("int8", 64, 17408, 5120), ("int8", 64, 5120, 17408)]
-IDS = ["Q4_K-2048x6144x5120", "Q6_K-2048x5120x6144", "int8-64x17408x5120", "int8-64x5120x17408"]
+CASES = [(12, 2048, 6144, 5120), (14, 2048, 5120, 6144), ("int8", 64, 17408, 5120), ("int8", 64, 5120, 17408),
+         ("tiles", 1, 17408, 5120), ("tiles", 1, 5120, 17408)]
+IDS = ["Q4_K-2048x6144x5120", "Q6_K-2048x5120x6144", "int8-64x17408x5120", "int8-64x5120x17408",
+       "Q4_K-tiles-1x17408x5120", "Q4_K-tiles-1x5120x17408"]
 CALLS = 8
 
 
@@ -28,6 +31,10 @@ def test_batched_kernels_repeat_bit_for_bit(t, m, n, k, cuda):
         planes = I8.repack(q, s)
         run = lambda: I8.linear(x, planes)
         plan = LIB.plan_str(LIB.I8T, m, n, k)
+    elif t == "tiles":
+        planes = KQ.repack(12, synth.q4_k_raw(n, k, seed=12, device=cuda), (n, k), tiled=True)
+        run = lambda: KQ.matmul(x, planes, out_dtype=torch.bfloat16)
+        plan = LIB.plan_str(planes.t, m, n, k)
     else:
         raw = {12: synth.q4_k_raw, 14: synth.q6_k_raw}[t](n, k, seed=12, device=cuda)
         planes = KQ.repack(t, raw, (n, k))
