@@ -418,8 +418,8 @@ def summarize_pmc(fetch_dir, write_dir, out, configs=(1, 2, 3, 4, 5), launches=4
 
     fm, fc = _probe_dispatches(_counter_rows(fetch_dir), "FETCH_SIZE")
     wm, wc = _probe_dispatches(_counter_rows(write_dir), "WRITE_SIZE")
-    plan = [(idx, name, n, k, synth.CONFIGS[idx][0], synth.CONFIGS[idx][1])
-            for idx in configs for name, n, k in synth.CONFIGS[idx][2]]
+    cfg = lambda idx: synth.CONFIGS[idx] if idx in synth.CONFIGS else synth.EXTRA[idx]
+    plan = [(idx, name, n, k, cfg(idx)[0], cfg(idx)[1]) for idx in configs for name, n, k in cfg(idx)[2]]
     per = launches + 1                                      # setup_projection's eager check, then the probe's launches
     if len(fm) != len(plan) * per or len(wm) != len(plan) * per:
         raise SystemExit(f"expected {len(plan) * per} matmul dispatches, got fetch {len(fm)} write {len(wm)}")
@@ -442,7 +442,7 @@ def summarize_pmc(fetch_dir, write_dir, out, configs=(1, 2, 3, 4, 5), launches=4
             write_b += stt.median(wk) * fw * 1024.0
             alg += algorithmic_bytes(t, m, n, k)
             kernels.add(fm[p * per]["Kernel_Name"].split("(")[0])
-        rec[f"c{idx}"] = {"hbm_bytes_per_launch": round(fetch_b + write_b), "fetch_bytes": round(fetch_b),
+        rec[_key(idx)] = {"hbm_bytes_per_launch": round(fetch_b + write_b), "fetch_bytes": round(fetch_b),
                           "write_bytes": round(write_b), "algorithmic_bytes": round(alg),
                           "traffic_over_algorithmic": round((fetch_b + write_b) / alg, 4), "kernels": sorted(kernels)}
     with open(out, "w") as f:
@@ -530,12 +530,14 @@ def main():
                     help="only the configs' matmul launches + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write --traffic from the two --pmc runs of --pmc-probe")
+    ap.add_argument("--pmc-configs", default="1,2,3,4,5", metavar="CONFIGS",
+                    help="--summarize-pmc: the configs the --pmc-probe runs launched, in order")
     ap.add_argument("--summarize-counters", nargs="+", metavar=("DIR", "KERNEL"),
                     help="markdown of a --pmc run of --pmc-probe: counter means per matmul kernel")
     ap.add_argument("--summarize-stats", metavar="KERNEL_STATS_CSV", help="print a rocprofv3 --stats CSV as markdown")
     a = ap.parse_args()
     if a.summarize_pmc:
-        return summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.traffic)
+        return summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.traffic, _configs(a.pmc_configs))
     if a.summarize_stats:
         return summarize_stats(a.summarize_stats)
     if a.summarize_counters:
@@ -550,7 +552,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     if a.pmc_probe:
-        return pmc_probe(tuple(int(c) if c.isdigit() else c for c in a.pmc_probe.split(",") if c), rotate_mb=a.rotate_mb)
+        return pmc_probe(_configs(a.pmc_probe), rotate_mb=a.rotate_mb)
     configs = [int(c) if c.isdigit() else c for c in a.configs.split(",") if c]
     if HEADLINE not in configs:
         configs.insert(0, HEADLINE)
@@ -577,6 +579,11 @@ def main():
 
 def _key(c):
     return f"c{c}" if isinstance(c, int) else str(c)
+
+
+def _configs(text):
+    """"1,2,m1_q4k_tiles" -> (1, 2, "m1_q4k_tiles")"""
+    return tuple(int(c) if c.isdigit() else c for c in text.split(",") if c)
 
 
 def summary(r):
