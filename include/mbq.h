@@ -183,16 +183,18 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  * rows, mbq_gemm_plan reports how mbq_matmul / mbq_int8_linear would run a (N, K) weight of type t (MBQ_INT8 for the
  * int8 linear): the kernel (MBQ_KERNEL_*), *bm x *bn output tiles and *splits K ranges (1 = no split; a split K uses
  * the per-device workspace below).
- *   MBQ_KERNEL_GEMV    M <= 4 on rows the GEMV's registers hold, bm = bn = splits = 0.
+ *   MBQ_KERNEL_GEMV    M <= 4 on row-major planes whose rows the GEMV's registers hold; M = 1 on tiled planes (the
+ *                      tile GEMV: x staged in LDS, K up to about 58,000 values); bm = bn = splits = 0.
  *   MBQ_KERNEL_STREAM  weight-stream kernel, M <= 64 (M <= 4 when the GEMV has no plan: e.g. K = 17408 at 3-4 rows,
  *                      Q8_0 / int8 rows over 24576 values): bm = 16, bn = weight rows per block (64 or 128); from 17
  *                      rows on, a weight of at least 64 rows per CU runs MBQ_KERNEL_TILES instead (automatic plan).
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
  *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T and the tiled GGUF types) at M <= 64:
  *                      bm = 16, bn = weight rows per block (any count: N is cut into equal ranges that fill the
- *                      CUs), splits = K ranges. The automatic plan of tiled planes up to 64 rows (they have no
- *                      GEMV or weight-stream plan).
- * mbq_force_gemm_plan makes every later GEMM call of M > 4 rows in the process use that kernel, tile and K ranges
+ *                      CUs), splits = K ranges. The automatic plan of tiled planes from 2 to 64 rows (and at one row
+ *                      when the tile GEMV has no plan); they have no weight-stream plan.
+ * mbq_force_gemm_plan makes every later GEMM call in the process use that kernel, tile and K ranges (row-major planes
+ * at M <= 4 with a GEMV plan keep the GEMV; tiled planes at one row take the forced kernel)
  * (kernel MBQ_KERNEL_AUTO: automatic again; bm = bn = 0 with MBQ_KERNEL_TILES: that kernel with its own tile choice;
  * MBQ_KERNEL_KGROUP takes bm = bn = 0 and chooses its rows per block for the forced splits, 0 = its own choice).
  * Workspace: a GEMM that splits K adds float32 partial tiles in a 64 MiB workspace (plus 256 KiB of counters) of
