@@ -31,10 +31,11 @@ on the host's CPU; without libmbq.so every call raises. The forced-failure switc
 
 Weight layout (no counterpart in the reference, whose kernel package has one): weights of the types the kernel package
 can tile (its TILED map: every GGUF type it serves) load as its 16-row tiles, the layout its K-group kernel runs at
-2-64 activation rows and its prefill GEMM runs fastest on (MI355X, a 27B-class Q4_K layer: 4 rows 87 us against 122 us
-on row-major planes, 16 rows 98 against 137, 2048 rows 1339 against 1398); at one row the row-major planes' decode
-GEMV is faster (64 against 84 us). Env MBQ_LAYOUT picks another: "rowmajor", or "both" (the tiles plus the row-major
-planes of the same weights, twice the bytes: every batch size gets its faster kernel).
+2-64 activation rows, its tile GEMV at one row, and its prefill GEMM runs fastest on (MI355X, a 27B-class Q4_K layer:
+4 rows 87 us against 122 us on row-major planes, 16 rows 98 against 137, 2048 rows 1339 against 1398); at one row the
+row-major planes' decode GEMV is still a little faster (64-67 against 68-74 us). Env MBQ_LAYOUT picks another:
+"rowmajor", or "both" (the tiles plus the row-major planes of the same weights, twice the bytes: every batch size gets
+its faster kernel).
 """
 from __future__ import annotations
 
