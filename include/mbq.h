@@ -191,7 +191,8 @@ int mbq_int8_embed(const int8_t* q_dev, const float* s_dev, int64_t N, int64_t D
  *   MBQ_KERNEL_TILES   LDS-tile kernel: 256x{256,192,128}, 128x{256,192,128,64}, 64x{256,192,128,64}.
  *   MBQ_KERNEL_KGROUP  K-group kernel of tiled planes (MBQ_I8T and the tiled GGUF types) at M <= 64:
  *                      bm = 16, bn = weight rows per block (any count: N is cut into equal ranges that fill the
- *                      CUs), splits = K ranges. The automatic plan of tiled planes from 2 to 64 rows (and at one row
+ *                      CUs, or several rounds of them for a weight of more than about 96 rows per CU), splits = K
+ *                      ranges. The automatic plan of tiled planes from 2 to 64 rows (and at one row
  *                      when the tile GEMV has no plan); they have no weight-stream plan.
  * mbq_force_gemm_plan makes every later GEMM call in the process use that kernel, tile and K ranges (row-major planes
  * at M <= 4 with a GEMV plan keep the GEMV; tiled planes at one row take the forced kernel)

@@ -818,8 +818,6 @@ int workspace(Workspace* out, hipStream_t s) {
 // of 16 KiB at 64 activation rows), the LDS tiles while tiles x splits stay within two blocks per CU (at most 512
 // partial tiles of 64 x 128 floats, 32 KiB each); a plan that needs more is refused. In host code the name `scratch`
 // is not a device address: the address is taken once per device with hipGetSymbolAddress and used from then on.
-constexpr size_t SCRATCH_BYTES = (size_t)16 << 20;
-constexpr int SCRATCH_TILES = 4096;
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES + SCRATCH_TILES * sizeof(int)];
 
 // the scratch's device address on the current device, set up once per device: the address from hipGetSymbolAddress

@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <type_traits>
 #include <utility>
 
@@ -773,8 +774,8 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 }
 
 // ------------------------------------------------------------------------------------------------------ planner
-// A plan: K splits S, rows per block R, row groups RG and tiles per wave NTW.
-struct KgmPlan { int S, R, RG, NTW; };
+// A plan: K splits S, rows per block R, row groups RG, tiles per wave NTW and the kernel's x-tile parameter MT (kgm_mt).
+struct KgmPlan { int S, R, RG, NTW, MT; };
 constexpr int KGM_MAX_NTW = 6;
 // most tiles per wave of a type, x-tile parameter (kgm_mt) and row-group count whose units and scales fit the registers
 // without spilling at 256 per lane (two row groups keep three stages of weights in flight, one group two); from the
@@ -816,33 +817,47 @@ static int kgm_ntw(int64_t N, int64_t R, int RG) {
     return (int)most;
 }
 
-// The plan of least estimated cost per block, in bytes a CU moves (its weights, the x of its K range, and for S > 1
+// The plan of least estimated cost, in bytes a CU moves per block (its weights, the x of its K range, and for S > 1
 // its partial tile written plus, for the last arriver, S partials read) plus the MFMA rows spent on rows outside the
-// block's range and the K groups left idle in a block's last step; the weights reflect MI355X timings of the 7
-// projections of a 27B-class layer at 64 rows against forced split counts, over S in {1, 2, 3, 4, 6, 8} (only `force_s` when
-// it is set) and RG in {1, 2} (those whose x rings fit the LDS), with rows per block chosen so that the ranges fill
-// the CUs once. Q4_K tiles: a row's chunk is 64 bytes of quants and half a 16-byte header, and a tile row outside the
-// range costs its dequantization (the vector work of the whole row), not only its MFMA row.
-static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int force_s) {
+// block's range and the K groups left idle in a block's last step, times the rounds of blocks the CUs run; the weights
+// reflect MI355X timings of the 7 projections of a 27B-class layer at 64 rows against forced split counts, over S in
+// {1, 2, 3, 4, 6, 8} (only `force_s` when it is set) and RG in {1, 2} (those whose x rings fit the LDS). Rows per block
+// are chosen so that the ranges fill the CUs once, or, for a weight whose ranges would then hold more tiles than a
+// wave's registers take (more than about 96 rows per CU), the CUs' share times the fewest rounds whose ranges fit;
+// split plans keep their partials within the static scratch of mbq_matmul_noalloc. Q4_K tiles: a row's chunk is 64
+// bytes of quants and half a 16-byte header, and a tile row outside the range costs its dequantization (the vector
+// work of the whole row), not only its MFMA row.
+static KgmPlan kgm_choose_mt(int t, int MTS, int64_t M, int64_t N, int64_t K, int cus, int force_s) {
     const int CW = kgm_cw(t);
     const int64_t KC = (K + CW - 1) / CW;
-    const int MTS = kgm_mt(t, M), MT = kgm_abs(MTS);
+    const int MT = kgm_abs(MTS);
     const double wpc = t == T_Q4KT ? 72.0 : t == T_Q40T ? 72.0 : t == T_Q5KT ? 88.0 : t == T_Q6KT ? 105.0 : t == T_Q8T ? 68.0 : 64.0;
     const double waste_w = (t == T_Q4KT || t == T_Q5KT || t == T_Q6KT || t == T_Q40T) ? 1.5 : t == T_Q8T ? 1.0 : 0.5;
-    KgmPlan best{0, 0, 0, 0};
+    KgmPlan best{0, 0, 0, 0, MTS};
     double best_cost = 0;
     for (int S : {1, 2, 3, 4, 6, 8}) {
         if (force_s > 0) S = force_s;
         if (KC >= S) {
-            const int64_t ranges = std::max<int64_t>(1, cus / S);
-            const int64_t R = (N + ranges - 1) / ranges;
+            const int64_t share = std::max<int64_t>(1, cus / S);
+            const int64_t kcs = (KC + S - 1) / S;
             for (int RG : {1, 2}) {
                 const int KG = 8 / RG;
                 if (kgm_ring(t, MT, RG) > KGM_LDS_MAX) continue;
-                const int ntw = kgm_ntw(N, R, RG);
-                if (ntw > kgm_max_ntw(t, MTS, RG)) continue;
-                const int64_t kcs = (KC + S - 1) / S;
+                const int maxn = kgm_max_ntw(t, MTS, RG);
+                if (maxn == 0) continue;
                 if (MTS == -1 && (kcs + KG - 1) / KG > kgm_rx_chunks()) continue;       // the chunks x registers hold
+                // the fewest rounds of `share` ranges whose row groups fit a wave's tiles (16 rows always do)
+                int64_t rounds = 1, R = 0;
+                int ntw = 0;
+                for (;; ++rounds) {
+                    R = (N + share * rounds - 1) / (share * rounds);
+                    ntw = kgm_ntw(N, R, RG);
+                    if (ntw <= maxn || R <= 16) break;
+                }
+                if (ntw > maxn) continue;
+                const int64_t ranges = (N + R - 1) / R;
+                if (S > 1 && (ranges > SCRATCH_TILES ||
+                              (size_t)ranges * S * RG * MT * ntw * 1024 > SCRATCH_BYTES)) continue;
                 const double w = (double)R * kcs * wpc;                         // weight bytes
                 // x bytes (L2 hits: half weight); diagonal x tiles move only the batch's rows
                 const double x = 0.5 * (MTS < 0 ? (double)M : 16.0 * MT) * 2 * CW * kcs;
@@ -852,9 +867,10 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
                 const double part = S > 1 ? (double)RG * MT * ntw * 1024 * (1 + 2 * S) + (M <= 16 ? 96e3 : 0.0) : 0.0;
                 const double waste = waste_w * (double)std::max<int64_t>(0, RG * ntw * 16 - R) * kcs * wpc;
                 const double idle = (double)((kcs + KG - 1) / KG * KG - kcs) / (double)kcs;
-                const double cost = (w + x + part + waste) * (1.0 + idle);
+                const double blocks_per_cu = std::ceil((double)(ranges * S) / (double)cus);
+                const double cost = (w + x + part + waste) * (1.0 + idle) * blocks_per_cu;
                 if (best.S == 0 || cost < best_cost) {
-                    best = KgmPlan{S, (int)R, RG, ntw};
+                    best = KgmPlan{S, (int)R, RG, ntw, MTS};
                     best_cost = cost;
                 }
             }
@@ -862,6 +878,15 @@ static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int f
         if (force_s > 0) break;
     }
     return best;
+}
+
+// The plan for M activation rows: x tiles kgm_mt(t, M), or, where x in registers (1-4 rows of the nibble tiles) holds
+// too few chunks for any split (K above 40960), the two diagonal x tiles staged in LDS
+static KgmPlan kgm_choose(int t, int64_t M, int64_t N, int64_t K, int cus, int force_s) {
+    const int MTS = kgm_mt(t, M);
+    KgmPlan p = kgm_choose_mt(t, MTS, M, N, K, cus, force_s);
+    if (p.S == 0 && MTS == -1) p = kgm_choose_mt(t, -2, M, N, K, cus, force_s);
+    return p;
 }
 
 // ------------------------------------------------------------------------------------------------------ launchers
@@ -910,22 +935,22 @@ static int kgm_launch_rg(const Args& a, const KgmPlan& p, const Workspace& w, hi
 template <int T, bool KFULL>
 static int kgm_launch_mt(const Args& a, const KgmPlan& p, const Workspace& w, hipStream_t s) {
     if constexpr (T == T_Q4KT || T == T_Q5KT || T == T_Q40T) {
-        if (a.M <= 4) return kgm_launch_rg<T, -1, KFULL>(a, p, w, s);
-        if (a.M <= 8) return kgm_launch_rg<T, -2, KFULL>(a, p, w, s);
+        if (p.MT == -1) return kgm_launch_rg<T, -1, KFULL>(a, p, w, s);
+        if (p.MT == -2) return kgm_launch_rg<T, -2, KFULL>(a, p, w, s);
     }
-    switch ((a.M + 15) / 16) {
+    switch (p.MT) {
         case 1: return kgm_launch_rg<T, 1, KFULL>(a, p, w, s);
         case 2: return kgm_launch_rg<T, 2, KFULL>(a, p, w, s);
         case 3: return kgm_launch_rg<T, 3, KFULL>(a, p, w, s);
-        default: return kgm_launch_rg<T, 4, KFULL>(a, p, w, s);
+        case 4: return kgm_launch_rg<T, 4, KFULL>(a, p, w, s);
     }
+    return set_error(MBQ_BAD_ARG, "K-group GEMM: x-tile parameter %d for type %d", p.MT, T);
 }
 
 // bytes of the partial tiles of a plan
-static size_t kgm_ws_bytes(int t, int64_t M, int64_t N, const KgmPlan& p) {
-    const int MT = kgm_abs(kgm_mt(t, M));
+static size_t kgm_ws_bytes(int64_t N, const KgmPlan& p) {
     const int64_t ranges = (N + p.R - 1) / p.R;
-    return (size_t)ranges * p.S * p.RG * MT * p.NTW * 256 * 4;
+    return (size_t)ranges * p.S * p.RG * kgm_abs(p.MT) * p.NTW * 256 * 4;
 }
 
 int kgemm_plan(int t, const Args& a, int force_s, int* rows_per_block, int* splits) {
@@ -949,7 +974,7 @@ int launch_kgemm(int t, const Args& a, int force_s, hipStream_t s) {
     Workspace w;
     if (p.S > 1) {
         const int64_t ranges = (a.N + p.R - 1) / p.R;
-        if (int rc = split_workspace(a, ranges, kgm_ws_bytes(t, a.M, a.N, p), s, &w)) return rc;
+        if (int rc = split_workspace(a, ranges, kgm_ws_bytes(a.N, p), s, &w)) return rc;
     }
     if (t == T_Q4KT) return kgm_launch_mt<T_Q4KT, true>(a, p, w, s);                  // K % 128 == 0
     if (t == T_Q6KT) return kgm_launch_mt<T_Q6KT, true>(a, p, w, s);

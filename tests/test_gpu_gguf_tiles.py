@@ -316,3 +316,61 @@ def test_tile_gemv_long_rows(t, cuda):
         assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y.cpu().numpy()))
         del w64
         torch.cuda.empty_cache()
+
+
+def test_every_covered_shape_has_a_plan(cuda):
+    """every weight that mbq_covers accepts has a plan at every batch size, on row-major planes, tiled planes and int8
+    (a plan query launches nothing): tall weights (more rows per CU than a wave's tiles hold) take several rounds of
+    K-group blocks, and 1-4 rows of K beyond what x in registers holds take x through LDS"""
+    types = [R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K] + [KQ.TILED[t] for t in TYPES] + [LIB.INT8, LIB.I8T]
+    quant_k = {R.Q4_K, R.Q5_K, R.Q6_K, KQ.TILED[R.Q4_K], KQ.TILED[R.Q5_K], KQ.TILED[R.Q6_K]}
+    ns = (1, 16, 70, 1024, 5120, 17408, 24576, 28672, 34816, 53248, 151936)
+    ks = (256, 2560, 5120, 8192, 17408, 28672, 41216, 53248)
+    ms = (1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 48, 64, 65, 2048)
+    checked = 0
+    for t in types:
+        for n in ns:
+            for k in ks:
+                if t in quant_k and k % 256:
+                    continue
+                if not LIB.lib().mbq_covers(int(t), n, k):
+                    continue
+                for m in ms:
+                    try:
+                        LIB.gemm_plan(t, m, n, k)
+                    except LIB.MbqError as e:
+                        pytest.fail(f"type {t} m={m} n={n} k={k}: {e}")
+                    checked += 1
+    print(f"{checked} covered (type, m, n, k) have a plan", flush=True)
+    assert checked > 10000
+
+
+@pytest.mark.parametrize("t,n,k,ms", [
+    (R.Q4_K, 34816, 512, (2, 4, 8, 16, 64)),       # gate|up stacked: two rounds of K-group blocks at 2-8 rows
+    (R.Q5_K, 34816, 512, (4,)),
+    (R.Q8_0, 34816, 512, (4, 64)),
+    (R.Q6_K, 151936, 256, (4, 16, 64)),            # a vocabulary head's rows: four to seven rounds
+    (R.Q4_K, 12416, 5376, (4,)),                   # two K splits over two rounds
+    (R.Q4_K, 300, 41216, (2, 4)),                  # K past x in registers: the diagonal x tiles through LDS
+    (R.Q4_0, 300, 41216, (3,)),
+], ids=lambda v: NAME.get(v) if isinstance(v, int) and v in NAME else str(v))
+def test_tall_and_long_weights(t, n, k, ms, cuda):
+    """weights the K-group kernel runs in several rounds of blocks, or with x staged in LDS at 1-4 rows: every output
+    against the float64 product (on the GPU) of the oracle's dequantization, in float32 and bfloat16 (the float32
+    result rounded), and a second call repeats bit for bit"""
+    rng = np.random.default_rng([t, n, k, 132])
+    raw = G.RAW[t](rng, n, k)
+    p = KQ.repack(t, torch.from_numpy(raw).to(cuda), (n, k), tiled=True)
+    w64 = torch.from_numpy(R.dequant(raw, t, k)).to(cuda).to(torch.float64)
+    for m in ms:
+        plan = LIB.gemm_plan(KQ.TILED[t], m, n, k)
+        assert plan[0] == LIB.KERNEL_KGROUP, plan
+        print(f"{NAME[t]} tiles m={m} {n}x{k} ({LIB.plan_str(KQ.TILED[t], m, n, k)})", flush=True)
+        xb, x = _x(rng, m, k, cuda)
+        y = KQ.matmul(x, p)
+        assert_product_dev(y, x.to(torch.float64) @ w64.T, f"{NAME[t]} tiles m={m} {n}x{k}")
+        yb = KQ.matmul(x, p, out_dtype=torch.bfloat16)
+        assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y.cpu().numpy()))
+        assert torch.equal(KQ.matmul(x, p).view(torch.int32), y.view(torch.int32))
+    del w64
+    torch.cuda.empty_cache()
