@@ -12,7 +12,10 @@ int8, 5 Q4_K) into 16-row tiles, the layout ops.prepare loads by default. `q6k_h
 the shape of the reference's largest published per-call number (a 151936 x 2560 Q6_K output head at one activation
 row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the configs, as are one 27B-class layer at 1,
 4 and 16 activation rows (`m1_q4k` row-major, `m1_q4k_tiles`, `m4_*`, `m16_*`: the reference engine's row buckets;
-Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, tiles from 2 rows on) and config 5 on row-major planes (`c5_rm`).
+Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, tiles from 2 rows on) and config 5 on row-major planes (`c5_rm`). Rows
+`m1_q4k_stacked`, `m4_q4k_stacked`, `m16_q4k_stacked` and `c4_stacked` time the same layer with the projections that
+share an input stacked by rows at load (ops.stack_rows: q|k|v 8192 x 5120, gate|up 34816 x 5120), four launches per
+layer instead of seven; the BASELINE configs 4 and 5 stay the seven launches they name.
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) of K launches that cycles through
 >= 1 GiB of distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for warmup, then R
@@ -65,6 +68,11 @@ def algorithmic_bytes(t, m, n, k):
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
+
+# the configs a run without --configs times, in order
+DEFAULT_CONFIGS = ("1,2,3,4,5,q6k_head,m1_q4k,m1_q4k_tiles,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,"
+                   "m4_int8,m16_int8,c5_rm,c2_ops,m1_q4k_ops,m4_q4k_ops,c5_ops,m1_q4k_stacked,m4_q4k_stacked,"
+                   "m16_q4k_stacked,c4_stacked")
 
 # rows timed through mashbox_amd.ops.qmatmul (the caller's path) instead of the C ABI: row -> the config it repeats
 OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k", "m1_q4k_ops": "m1_q4k"}
@@ -147,7 +155,7 @@ def setup_projection(idx, pi, rotate_bytes):
         raw = {8: synth.q8_0_raw, 12: synth.q4_k_raw, 13: synth.q5_k_raw, 14: synth.q6_k_raw}[t](N, K, seed=seed + 7, device=dev)
         # batched GGUF configs (2 rows and more) load the blocks as 16-row tiles, ops.prepare's default layout;
         # single-row configs keep the row-major planes of the decode GEMV; "_rm" / "_tiles" rows force one
-        tiles = (M > 1 and not str(idx).endswith("_rm")) or str(idx).endswith("_tiles")
+        tiles = (M > 1 and not str(idx).endswith("_rm")) or str(idx).endswith(("_tiles", "_stacked"))
         pt = {12: LIB.Q4KT, 8: LIB.Q8T, 13: LIB.Q5KT, 14: LIB.Q6KT}.get(t, t) if tiles else t
         pb = check(L.mbq_plane_bytes(pt, N, K), "plane_bytes")
         planes = torch.empty(pb, dtype=torch.uint8, device=dev)
@@ -517,8 +525,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5,q6k_head,m1_q4k,m1_q4k_tiles,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,"
-                                          "m16_q5k,m4_q6k,m16_q6k,m4_int8,m16_int8,c5_rm,c2_ops,m1_q4k_ops,m4_q4k_ops,c5_ops")
+    ap.add_argument("--configs", default=DEFAULT_CONFIGS)
     ap.add_argument("--rotate-mb", type=int, default=1024, help="distinct weight bytes cycled per projection")
     ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU baseline time per config (at least 5 calls)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -11,6 +11,8 @@ loaders and tests drive this module unchanged:
     prepare(raw, t, shape, use_kernel=True)          Packed (kernel planes) | Raw (the file's blocks) (:412-467)
     stack_mixed(layers, shape)                       one role whose block types differ by layer -> Mixed (the callers'
                                                       construction, reference gguf/archs/dense.py:206-218)
+    stack_rows(parts) -> (raw, t, sizes)             weights that share an input stacked by rows into one weight (one
+                                                      launch per call; reference model.py:374 keeps q, k, v this way)
     qmatmul(x, h) -> x @ W.T in x's dtype            float32 accumulation (:594-632)
     dequant(h), take_rows(h, ids)                    float32 weights / rows, exact (:513-548)
     contract_check(t, raw, shape) -> (ok, bad)       dequant(repack(raw)) == reference dequant(raw) (:691-705)
@@ -376,6 +378,32 @@ def stack_mixed(layers, shape, use_kernel: bool = True):
     dev = _device()
     return Mixed(stacks, torch.tensor(which, dtype=torch.int32, device=dev), torch.tensor(sub, dtype=torch.int32, device=dev),
                  order, shape)
+
+
+def stack_rows(parts):
+    """weights that multiply one input (a layer's q, k and v; its gate and up) as one weight: `parts` =
+    [(raw blocks (rows_i, row_bytes), ggml type)], all of one type and row length, host (NumPy) or device (torch) ->
+    (raw (sum rows_i, row_bytes), type, sizes). prepare(raw, type, (sum(sizes), cols)) loads it as one weight, so a
+    call runs the parts in one kernel launch, and torch.split(qmatmul(x, h), sizes, -1) gives each part's output as a
+    view of the result. No output row mixes weight rows: each part's output is its own product, within the float32
+    rounding of another plan. The reference keeps its linear-attention layers' q, k and v stacked by rows the same way
+    (one weight w["qkv"], reference src/mashbox/models/qwen3_8_27b/model.py:374)."""
+    if not parts:
+        raise ValueError("stack_rows: no parts")
+    types = {int(t) for _, t in parts}
+    if len(types) != 1:
+        raise ValueError(f"stack_rows: the parts' types differ ({sorted(type_name(t) for t in types)}); only weights of "
+                         f"one type stack")
+    t = types.pop()
+    raws = [r for r, _ in parts]
+    widths = {int(r.shape[-1]) for r in raws}
+    if len(widths) != 1 or any(len(tuple(r.shape)) != 2 for r in raws):
+        raise ValueError(f"stack_rows: every part must be (rows, row_bytes) of one row length, got "
+                         f"{[tuple(r.shape) for r in raws]}")
+    sizes = [int(r.shape[0]) for r in raws]
+    if all(isinstance(r, torch.Tensor) for r in raws):
+        return torch.cat([r.to(raws[0].device) for r in raws], 0), t, sizes
+    return np.concatenate([r.cpu().numpy() if isinstance(r, torch.Tensor) else np.asarray(r, np.uint8) for r in raws], 0), t, sizes
 
 
 # ------------------------------------------------------------------------------------------------- the exact path

@@ -102,6 +102,8 @@ def int8_weights(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2)
 # (ggml type or "int8", activation rows M, [(name, N, K), ...])
 LAYER_27B = [("q", 6144, 5120), ("k", 1024, 5120), ("v", 1024, 5120), ("o", 5120, 6144),
              ("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
+# the layer with q, k, v stacked by rows into one weight and gate, up into another (they share their input)
+LAYER_27B_STACKED = [("qkv", 8192, 5120), ("o", 5120, 6144), ("gate_up", 34816, 5120), ("down", 5120, 17408)]
 CONFIGS = {
     1: ("int8", 1, [("w", 4096, 4096)]),
     2: (8, 1, [("w", 17408, 5120)]),
@@ -121,5 +123,9 @@ EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          # single-row decode of the same layer: row-major planes (decode GEMV) and the same weights as 16-row tiles
          "m1_q4k": (12, 1, LAYER_27B), "m1_q4k_tiles": (12, 1, LAYER_27B),
          # config 5's prefill on the row-major planes (config 5 itself loads the weights as 16-row tiles)
-         "c5_rm": (12, 2048, LAYER_27B)}
+         "c5_rm": (12, 2048, LAYER_27B),
+         # the same layer with the projections that share an input stacked by rows at load (ops.stack_rows): q|k|v and
+         # gate|up, four launches instead of seven (Q4_K as 16-row tiles, ops.prepare's default; int8 as config 4)
+         "m1_q4k_stacked": (12, 1, LAYER_27B_STACKED), "m4_q4k_stacked": (12, 4, LAYER_27B_STACKED),
+         "m16_q4k_stacked": (12, 16, LAYER_27B_STACKED), "c4_stacked": ("int8", 64, LAYER_27B_STACKED)}
 REF_TPU_US = {"q6k_head": 369.8}

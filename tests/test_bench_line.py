@@ -5,8 +5,7 @@ import json
 
 import bench
 
-CONFIGS = [1, 2, 3, 4, 5, "q6k_head", "m4_q4k", "m16_q4k", "m4_q8", "m16_q8", "m4_q5k", "m16_q5k", "m4_q6k",
-           "m16_q6k", "m4_int8", "m16_int8", "c2_ops", "c5_ops", "m4_q4k_ops"]
+CONFIGS = list(bench._configs(bench.DEFAULT_CONFIGS))       # every config a default run times
 PROJ = ["q", "k", "v", "o", "gate", "up", "down"]
 
 
