@@ -578,13 +578,18 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
             for (int ci = 0; ci < CHX; ++ci) {
                 const bool live = lv && ci < mine && (KFULL || CW * chunk_of(ci) + 32 * lg < K);
                 const uint32_t off = live ? (uint32_t)(((int64_t)xrow * K + CW * chunk_of(ci) + 32 * lg) * 2) : OOB_VOFF;
+                // the scalar offset stays uniform (a per-lane choice there makes the compiler loop over its values):
+                // a lane that loads nothing has OOB_VOFF + 16 u, still past the range
 #pragma unroll
                 for (int u = 0; u < NS; ++u)
-                    AX[ci][u] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, live ? 16u * u : 0u, 0));
+                    AX[ci][u] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 16u * u, 0));
             }
         }
 #pragma unroll
         for (int p = 0; p < D; ++p) load_w(W[p], H[p], Hb[Q5 ? p : 0], p);
+        // every weight load issues before the first wait for x (else the compiler hoists the x sums' MFMAs, and their
+        // waits for x, above the weight loads, and the stream starts a round trip late)
+        __builtin_amdgcn_sched_barrier(0);
         wait_vm<D * NWL>();                                               // the x loads (issued first) have landed
         const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{BF16_ONES, BF16_ONES, BF16_ONES, BF16_ONES});
         f32x4_t DX[CHX];
