@@ -372,5 +372,11 @@ def test_tall_and_long_weights(t, n, k, ms, cuda):
         yb = KQ.matmul(x, p, out_dtype=torch.bfloat16)
         assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y.cpu().numpy()))
         assert torch.equal(KQ.matmul(x, p).view(torch.int32), y.view(torch.int32))
+        # the allocation-free entry point runs the same plan (split partials in its static scratch): the same bits
+        got = torch.empty_like(y)
+        assert LIB.lib().mbq_matmul_noalloc(KQ.TILED[t], ctypes.c_void_p(p.buf.data_ptr()), 0, None, 1,
+                                            ctypes.c_void_p(x.data_ptr()), m, n, k, ctypes.c_void_p(got.data_ptr()),
+                                            LIB.OUT_F32, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+        assert torch.equal(got.view(torch.int32), y.view(torch.int32))
     del w64
     torch.cuda.empty_cache()
