@@ -809,16 +809,20 @@ constexpr int kgm_mt(int t, int64_t M) {
 constexpr int kgm_abs(int v) { return v < 0 ? -v : v; }
 
 // the most 16-row tiles a wave touches: over the blocks' row ranges [rr R, min(N, rr R + R)) and their RG row groups
+// (every range but the last is full, and a full range's row groups span tiles by their starts modulo 16, which repeat
+// every 16 ranges: the first 16 ranges and the last cover every case)
 static int kgm_ntw(int64_t N, int64_t R, int RG) {
     const int64_t ranges = (N + R - 1) / R, RQ = (R + RG - 1) / RG;
     int64_t most = 0;
-    for (int64_t rr = 0; rr < ranges; ++rr) {
+    auto range = [&](int64_t rr) {
         const int64_t r0 = rr * R, r1 = std::min(N, r0 + R);
         for (int q = 0; q < RG; ++q) {
             const int64_t a = std::min(r1, r0 + q * RQ), b = std::min(r1, a + RQ);
             if (b > a) most = std::max(most, (b - 1) / 16 - a / 16 + 1);
         }
-    }
+    };
+    for (int64_t rr = 0; rr < std::min<int64_t>(ranges, 16); ++rr) range(rr);
+    if (ranges > 16) range(ranges - 1);
     return (int)most;
 }
 
@@ -851,8 +855,9 @@ static KgmPlan kgm_choose_mt(int t, int MTS, int64_t M, int64_t N, int64_t K, in
                 const int maxn = kgm_max_ntw(t, MTS, RG);
                 if (maxn == 0) continue;
                 if (MTS == -1 && (kcs + KG - 1) / KG > kgm_rx_chunks()) continue;       // the chunks x registers hold
-                // the fewest rounds of `share` ranges whose row groups fit a wave's tiles (16 rows always do)
-                int64_t rounds = 1, R = 0;
+                // the fewest rounds of `share` ranges whose row groups fit a wave's tiles (16 rows always do), from a
+                // bound below it: a row group of RQ rows spans at least RQ / 16 tiles
+                int64_t rounds = std::max<int64_t>(1, N / (share * RG * 16 * maxn)), R = 0;
                 int ntw = 0;
                 for (;; ++rounds) {
                     R = (N + share * rounds - 1) / (share * rounds);
