@@ -389,20 +389,18 @@ __global__ __launch_bounds__(GV_THREADS, 2) void gemv_kernel(const GvArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------------------ launchers
-// blocks of a GEMV kernel the GPU holds at once (cached per kernel and LDS size)
+// blocks of a GEMV kernel the current GPU holds at once: its CUs (cached per device) times the kernel's blocks per CU
+// (cached per kernel and LDS size)
 template <class Kern>
 static int resident_blocks(Kern kernel, size_t lds) {
-    static thread_local struct { const void* k; size_t lds; int n; } cache[64];
+    static thread_local struct { const void* k; size_t lds; int per; } cache[64];
     static thread_local int used = 0;
     for (int i = 0; i < used; ++i)
-        if (cache[i].k == (const void*)kernel && cache[i].lds == lds) return cache[i].n;
-    int dev = 0, cus = 0, per = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GV_THREADS, lds) != hipSuccess || per < 1)
-        return -1;
-    const int n = cus * per;
-    if (used < 64) cache[used++] = {(const void*)kernel, lds, n};
-    return n;
+        if (cache[i].k == (const void*)kernel && cache[i].lds == lds) return cus_of_device() * cache[i].per;
+    int per = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GV_THREADS, lds) != hipSuccess || per < 1) return -1;
+    if (used < 64) cache[used++] = {(const void*)kernel, lds, per};
+    return cus_of_device() * per;
 }
 
 // Parts per row: the fewest S in {1, 2, 4, 8} whose parts take at most GV_ITEM_CHUNKS chunks and fit the registers
@@ -435,8 +433,7 @@ static int gv_parts(int64_t U, int* S, int* PU) {
 template <int T, int M, int CH, int R = 1>
 static int launch_gemv_ch(const Args& a, int S, int PU, hipStream_t s) {
     auto kern = gemv_kernel<T, M, CH, 2, R>;
-    int cus = 256, dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    const int cus = cus_of_device();
     int P = resident_blocks(kern, 4096);
     if (P < 1) return set_error(MBQ_LAUNCH_FAIL, "GEMV occupancy query failed");
     const int bpc = gv_two_blocks(a.N, S, M, cus) ? 2 : 1;
