@@ -126,7 +126,7 @@ int mbq_matmul(int t, const uint8_t* planes_dev, int64_t layer, const int32_t* l
 /* mbq_matmul for callers that cannot allocate: code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. No counterpart in the reference. It runs the same plans and kernels as mbq_matmul, with identical results,
  * and calls no hipMalloc, hipFree or allocating library routine: a batch that splits K keeps its float32 partial tiles
- * and arrival counters in the library's static scratch array (16 MiB of partials and 4096 counters; every GPU the
+ * and arrival counters in the library's static scratch array (64 MiB of partials, the allocated workspace's size, and 4096 counters; every GPU the
  * library runs on holds its own copy until the process ends), instead of mbq_matmul's allocated workspace. A plan whose
  * partials exceed the scratch (none of the automatic plans on up to 256 CUs; a forced plan can) returns MBQ_E_ARG and
  * launches nothing. Every call on one GPU shares that GPU's scratch: calls that overlap in time on one GPU (two streams)

@@ -813,11 +813,11 @@ int workspace(Workspace* out, hipStream_t s) {
 // --------------------------------------------------------------------------------------------------- scratch
 // The split-K partials and arrival counters of mbq_matmul_noalloc, for callers that cannot allocate (code under HIP
 // graph capture, serving loops, harnesses that forbid hipMalloc): one static device array, which every GPU the library
-// runs on holds at its own address until the process ends. Its SCRATCH_BYTES of partial tiles cover every automatic
-// split plan on up to 256 CUs: the weight stream splits only while its tiles x splits fit the CUs (at most 256 blocks
-// of 16 KiB at 64 activation rows), the LDS tiles while tiles x splits stay within two blocks per CU (at most 512
-// partial tiles of 64 x 128 floats, 32 KiB each); a plan that needs more is refused. In host code the name `scratch`
-// is not a device address: the address is taken once per device with hipGetSymbolAddress and used from then on.
+// runs on holds at its own address until the process ends. Its SCRATCH_BYTES of partial tiles (the allocated
+// workspace's size) cover every automatic split plan: the planners keep each plan's partials within it, so both entry
+// points run the same plan and give the same bits; a forced plan that needs more is refused. In host code the name
+// `scratch` is not a device address: the address is taken once per device with hipGetSymbolAddress and used from then
+// on.
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES + SCRATCH_TILES * sizeof(int)];
 
 // the scratch's device address on the current device, set up once per device: the address from hipGetSymbolAddress
@@ -936,28 +936,65 @@ static const Cand<T> CANDS[] = {cand<T, 256, 256, 1>(), cand<T, 256, 192, 1>(), 
                                 cand<T, 128, 64, 3>(),  cand<T, 64, 256, 3>(),  cand<T, 64, 192, 3>(),
                                 cand<T, 64, 128, 3>(),  cand<T, 64, 64, 3>()};
 
-// K-step time (us) of one block of each candidate when it runs alone on its CU (the order of CANDS)
+// K-step time (us) of one block of each candidate when it runs alone on its CU (the order of CANDS; 256 x 192 without a
+// split is the specialized-wave kernel)
 static constexpr double T1_US[] = {1.56, 1.20, 1.14, 1.10, 1.04, 0.83, 0.57, 0.84, 0.80, 0.58, 0.43};
+// Batches of more than 64 rows: the busiest CU's time. It runs ceil(blocks / CUs) blocks, `occ` at a time, each K step
+// taking T1_US when a block has its CU alone and PG_G2 / PG_G3 times that when 2 / 3 blocks share it; 256 x 192 tiles
+// with a split K run the plain LDS-tile kernel, PG_SGX times slower per step than the specialized one; a split adds
+// PG_SA us and PG_SB us per MB of one block's partials (S bm bn float32 tiles: its own store and the last arriver's
+// loads). The constants are a least-squares fit (of log time) to 1,320 timings of every candidate at 1, 2 and 4 splits
+// on MI355X: Q4_K and int8 tiles, 128-2048 rows, the 17408 x 5120, 5120 x 17408, 6144 x 5120 and 1024 x 5120 weights of a
+// 27B-class layer. Its choices run within 5 % of the fastest candidate on 38 of those 40 shapes (all 40 together 0.3 %
+// over the fastest), where the model below (fitted to loaded CUs of one tile shape) lost 15 % (512 rows: 1.6-1.9x).
+constexpr double PG_G2 = 1.44, PG_G3 = 2.11, PG_SGX = 1.18, PG_SA = 8.4, PG_SB = 22.5;
 
-// Tile shape and K split for an (M, N, K) problem: the candidate with the least modelled time. A block's K step costs
-// about 0.1 us + 3.5e-5 us per output of its tile (fitted to MI355X timings of these kernels at 2048 and 64 activation
-// rows); blocks run in rounds over the CUs x the blocks of that shape a CU holds (LDS, registers). K is split only for
-// batches of at most 64 rows (then the weight stream, not the matrix work, bounds the time): into at most 4 ranges of
-// at least 4 steps, until the tiles x splits reach 128 blocks; larger batches fill the GPU with tiles, and a split's
-// partial tiles would cost more than the rounds they save.
 template <int T>
-static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
+static Plan plan_wide(int64_t M, int64_t N, int64_t K, int cus) {
     const int64_t KT = (K + GK - 1) / GK;
     Plan best{(int)(sizeof CANDS<T> / sizeof CANDS<T>[0]) - 1, 1, (int)KT};
     double best_t = 1e300;
     for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i) {
         const int bm = CANDS<T>[i].bm, bn = CANDS<T>[i].bn;
         if (bm > 64 && M <= bm / 2) continue;                // more than half the tile's rows would be padding
-        if (M <= 64 && bn != 128) continue;
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        const int occ = std::max(1, std::min(3, CANDS<T>[i].occ()));
+        for (int64_t S0 : {1, 2, 3, 4}) {
+            const int64_t kts = (KT + S0 - 1) / S0, S = (KT + kts - 1) / kts;     // no empty split
+            if (S != S0 || (S > 1 && kts < 4)) continue;
+            if (S > 1 && (tiles > std::min<int64_t>(WS_TILES, SCRATCH_TILES) ||
+                          (size_t)tiles * S * bm * bn * 4 > std::min(WS_BYTES, SCRATCH_BYTES))) continue;
+            const int64_t nb = (tiles * S + cus - 1) / cus;
+            const double g = occ == 1 ? 1.0 : occ == 2 ? PG_G2 : PG_G3;
+            const int64_t part = nb % occ;
+            const double steps = (double)(nb / occ) * g + (part == 0 ? 0.0 : part == 1 ? 1.0 : PG_G2);
+            double t = (double)kts * T1_US[i] * (bm == SG_BM && bn == SG_BN && S > 1 ? PG_SGX : 1.0) * steps;
+            if (S > 1) t += PG_SA + PG_SB * (double)(S * bm * bn * 4) / 1e6;
+            if (t < best_t) best_t = t, best = Plan{i, (int)S, (int)kts};
+        }
+    }
+    return best;
+}
+
+// Tile shape and K split for an (M, N, K) problem: the candidate with the least modelled time. More than 64 rows:
+// plan_wide. Up to 64 rows (row-major planes the weight stream does not take): a block's K step costs about 0.1 us +
+// 3.5e-5 us per output of its tile (fitted to MI355X timings of these kernels at 64 activation rows); blocks run in
+// rounds over the CUs x the blocks of that shape a CU holds (LDS, registers); K is split into at most 4 ranges of at
+// least 4 steps, until the tiles x splits reach 128 blocks (the weight stream, not the matrix work, bounds the time).
+template <int T>
+static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
+    if (M > 64) return plan_wide<T>(M, N, K, cus);
+    const int64_t KT = (K + GK - 1) / GK;
+    Plan best{(int)(sizeof CANDS<T> / sizeof CANDS<T>[0]) - 1, 1, (int)KT};
+    double best_t = 1e300;
+    for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i) {
+        const int bm = CANDS<T>[i].bm, bn = CANDS<T>[i].bn;
+        if (bm > 64 && M <= bm / 2) continue;                // more than half the tile's rows would be padding
+        if (bn != 128) continue;
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         const int occ = CANDS<T>[i].occ();
         int64_t S = 1;
-        if (M <= 64 && tiles < 128 && tiles <= WS_TILES) {
+        if (tiles < 128 && tiles <= WS_TILES) {
             S = std::min<int64_t>({(128 + tiles - 1) / tiles, 4, std::max<int64_t>(1, KT / 4)});
             S = std::max<int64_t>(1, std::min<int64_t>(S, (int64_t)(WS_BYTES / ((size_t)tiles * bm * bn * 4))));
         }
@@ -967,32 +1004,8 @@ static Plan plan_gemm(int64_t M, int64_t N, int64_t K, int cus) {
         const double t = (double)rounds * occ * (0.1 + 3.46e-5 * bm * bn) * kts;
         if (t < best_t) best_t = t, best = Plan{i, (int)S, (int)kts};
     }
-    // A batch whose chosen tiles leave more than a fifth of the CUs idle (a small N, or M < 256): the model above, fitted
-    // to loaded CUs, misjudges it. Then every CU runs at most one block, and the tile with the least K-step time of a
-    // lone block (T1_US, measured on MI355X, Q4_K, one block per CU) times the steps wins among those whose tiles fit
-    // in one round: e.g. 2048 x 1024 x 5120 runs 128 x 64 tiles in 47 us instead of 64 x 192 in 66 us, 96 x 5120 x 17408
-    // 64 x 64 tiles in 112 us instead of 213 us; shapes whose tiles fill the CUs keep the model's choice.
-    static_assert(sizeof T1_US / sizeof T1_US[0] == sizeof CANDS<T> / sizeof CANDS<T>[0], "one lone-block time per candidate");
-    if (M > 64) {
-        const int bm = CANDS<T>[best.idx].bm, bn = CANDS<T>[best.idx].bn;
-        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * best.S;
-        if (tiles * 5 < (int64_t)cus * 4) {
-            double bt = 1e300;
-            for (int i = 0; i < (int)(sizeof CANDS<T> / sizeof CANDS<T>[0]); ++i) {
-                const int cbm = CANDS<T>[i].bm, cbn = CANDS<T>[i].bn;
-                if (cbm > 64 && M <= cbm / 2) continue;
-                const int64_t ct = ((M + cbm - 1) / cbm) * ((N + cbn - 1) / cbn);
-                if (ct > cus) continue;
-                const double t = T1_US[i] * KT;
-                if (t < bt) bt = t, best = Plan{i, 1, (int)KT};
-            }
-        }
-    }
     // Small tiles (at most 8192 outputs) that leave CUs idle split K until about two blocks run per CU, at most 4
-    // ranges of at least 4 steps (MI355X, Q4_K: 96 x 5120 x 17408 64 x 64 tiles 107 -> 64 us with 3 ranges; 512 x 1024
-    // x 5120 33 -> 20 us with 4; 64 x 17408 x 5120 64 x 128 tiles 51 -> 38 us with 3; 2048 x 1024 x 5120 128 x 64 tiles
-    // -6 % with 2). Larger tiles keep one range: their partial tiles cost more than the split saves (64 x 192 and
-    // 128 x 192 tiles 15-20 % slower with 2 ranges).
+    // ranges of at least 4 steps (MI355X, Q4_K: 64 x 17408 x 5120 64 x 128 tiles 51 -> 38 us with 3 ranges).
     {
         const int bm = CANDS<T>[best.idx].bm, bn = CANDS<T>[best.idx].bn;
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);

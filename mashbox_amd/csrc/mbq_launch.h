@@ -34,7 +34,7 @@ struct Args {
 constexpr size_t WS_BYTES = (size_t)64 << 20;
 constexpr int WS_TILES = 1 << 16;
 // the static scratch of mbq_matmul_noalloc: partial-tile bytes and arrival counters (automatic plans stay within it)
-constexpr size_t SCRATCH_BYTES = (size_t)16 << 20;
+constexpr size_t SCRATCH_BYTES = (size_t)64 << 20;
 constexpr int SCRATCH_TILES = 4096;
 // fenced: the memory is ordinary cached memory (the static scratch of mbq_matmul_noalloc), so the blocks that exchange
 // partials through it release and acquire at agent scope (split_release / split_acquire); the allocated workspace is

@@ -67,22 +67,30 @@ def test_noalloc_equals_matmul_on_consecutive_calls():
 
 
 def test_noalloc_refuses_a_plan_beyond_its_scratch():
+    """the scratch holds as many partials as the allocated workspace (every automatic plan fits both), so a forced plan
+    beyond it is refused by both entry points with nothing launched; the automatic plan then runs in both, bit for bit
+    alike"""
     dev = torch.device("cuda", 0)
     L = LIB.lib()
-    t, m, n, k = R.Q8_0, 64, 17408, 1024
+    t, m, n, k = R.Q8_0, 512, 17408, 1024
     planes, x, ref = _case(t, m, n, k, 7, dev)
-    LIB.force_gemm_plan(LIB.KERNEL_TILES, 64, 64, 4)        # 272 tiles x 4 ranges x 16 KiB = 17.8 MB of partials
+    LIB.force_gemm_plan(LIB.KERNEL_TILES, 64, 64, 4)        # 2176 tiles x 4 ranges x 16 KiB = 142.6 MB of partials
     try:
-        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
-        rc = _call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y)
-        assert rc == -1 and b"scratch" in L.mbq_last_error()
-        torch.cuda.synchronize()
-        assert bool(torch.isnan(y).all()), "a refused call must launch nothing"
-        LIB.check(_call(L.mbq_matmul, t, planes, x, m, n, k, y), "mbq_matmul")
-        torch.cuda.synchronize()
-        assert_product_dev(y, ref, "forced 64x64/4")
+        for fn in (L.mbq_matmul_noalloc, L.mbq_matmul):
+            y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+            rc = _call(fn, t, planes, x, m, n, k, y)
+            assert rc == -1 and b"does not fit" in L.mbq_last_error(), L.mbq_last_error()
+            torch.cuda.synchronize()
+            assert bool(torch.isnan(y).all()), "a refused call must launch nothing"
     finally:
         LIB.force_gemm_plan()
+    y_ref = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    LIB.check(_call(L.mbq_matmul, t, planes, x, m, n, k, y_ref), "mbq_matmul")
+    LIB.check(_call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y), "mbq_matmul_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32))
+    assert_product_dev(y, ref, f"automatic plan ({LIB.plan_str(t, m, n, k)})")
 
 
 def test_noalloc_int8_planes_split_k():
@@ -172,3 +180,23 @@ def test_noalloc_first_call_under_graph_capture():
     sys.stdout.write(r.stdout)
     sys.stderr.write(r.stderr[-4000:])
     assert r.returncode == 0 and "noalloc capture ok" in r.stdout
+
+
+def test_noalloc_wide_batch_split():
+    """batches of more than 64 rows whose automatic plan splits K (LDS tiles, partials of up to 64 MiB in the scratch):
+    two calls in a row, the second smaller, bit for bit equal to mbq_matmul and within the product bars"""
+    dev = torch.device("cuda", 0)
+    L = LIB.lib()
+    t, n, k = R.Q4_K, 6144, 5120
+    for m in (256, 200):
+        planes, x, ref = _case(t, m, n, k, 8, dev)
+        plan = LIB.gemm_plan(t, m, n, k)
+        print(f"Q4_K m={m} {n}x{k} ({LIB.plan_str(t, m, n, k)})", flush=True)
+        assert plan[0] == LIB.KERNEL_TILES and plan[3] > 1, plan
+        y_ref = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+        LIB.check(_call(L.mbq_matmul, t, planes, x, m, n, k, y_ref), "mbq_matmul")
+        LIB.check(_call(L.mbq_matmul_noalloc, t, planes, x, m, n, k, y), "mbq_matmul_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), f"m={m}: noalloc differs from mbq_matmul"
+        assert_product_dev(y, ref, f"m={m}")
