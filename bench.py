@@ -15,7 +15,8 @@ row, 369.8 us on TPU v6e-1, reference CORE-CHANGES.md:73), reported beside the c
 Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, tiles from 2 rows on) and config 5 on row-major planes (`c5_rm`). Rows
 `m1_q4k_stacked`, `m4_q4k_stacked`, `m16_q4k_stacked` and `c4_stacked` time the same layer with the projections that
 share an input stacked by rows at load (ops.stack_rows: q|k|v 8192 x 5120, gate|up 34816 x 5120), four launches per
-layer instead of seven; the BASELINE configs 4 and 5 stay the seven launches they name.
+layer instead of seven; the BASELINE configs 4 and 5 stay the seven launches they name. `p512_q4k` is the same Q4_K
+layer at 512 rows, the reference engine's default prefill chunk (runtime/engine.py:168).
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) of K launches that cycles through
 >= 1 GiB of distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for warmup, then R
@@ -72,7 +73,7 @@ def log(*a):
 # the configs a run without --configs times, in order
 DEFAULT_CONFIGS = ("1,2,3,4,5,q6k_head,m1_q4k,m1_q4k_tiles,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,"
                    "m4_int8,m16_int8,c5_rm,c2_ops,m1_q4k_ops,m4_q4k_ops,c5_ops,m1_q4k_stacked,m4_q4k_stacked,"
-                   "m16_q4k_stacked,c4_stacked")
+                   "m16_q4k_stacked,c4_stacked,p512_q4k")
 
 # rows timed through mashbox_amd.ops.qmatmul (the caller's path) instead of the C ABI: row -> the config it repeats
 OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k", "m1_q4k_ops": "m1_q4k"}

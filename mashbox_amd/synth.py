@@ -127,5 +127,7 @@ EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          # the same layer with the projections that share an input stacked by rows at load (ops.stack_rows): q|k|v and
          # gate|up, four launches instead of seven (Q4_K as 16-row tiles, ops.prepare's default; int8 as config 4)
          "m1_q4k_stacked": (12, 1, LAYER_27B_STACKED), "m4_q4k_stacked": (12, 4, LAYER_27B_STACKED),
-         "m16_q4k_stacked": (12, 16, LAYER_27B_STACKED), "c4_stacked": ("int8", 64, LAYER_27B_STACKED)}
+         "m16_q4k_stacked": (12, 16, LAYER_27B_STACKED), "c4_stacked": ("int8", 64, LAYER_27B_STACKED),
+         # a prefill chunk of the reference engine's default size (runtime/engine.py:168: chunk=512), Q4_K tiles
+         "p512_q4k": (12, 512, LAYER_27B)}
 REF_TPU_US = {"q6k_head": 369.8}
