@@ -5,8 +5,8 @@ exercised too. The named tests cover the BASELINE configs and the 27B-class laye
   tiles;
 * rows N from 1 to 4000 (mostly not a multiple of 16);
 * K any multiple of the type's block up to 12288;
-* activation rows M over the kernels' boundaries (1-4 the GEMVs, 5-64 the weight stream and K-group kernels, 65 and
-  more the LDS-tile GEMMs).
+* activation rows M over the kernels' boundaries (1-4 the GEMVs, 5-64 the weight stream and K-group kernels, 65-2048
+  the LDS-tile and specialized-wave GEMMs with the wide-batch planner's tile shapes and K splits).
 
 Each case uses automatic plans.
 
@@ -30,10 +30,10 @@ pytestmark = pytest.mark.gpu
 BLOCK = {R.Q4_0: 32, R.Q8_0: 32, R.Q4_K: 256, R.Q5_K: 256, R.Q6_K: 256, "int8": 16}
 NAME = {R.Q4_0: "Q4_0", R.Q8_0: "Q8_0", R.Q4_K: "Q4_K", R.Q5_K: "Q5_K", R.Q6_K: "Q6_K", "int8": "int8"}
 KINDS = [(t, lay) for t in (R.Q4_0, R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K, "int8") for lay in ("rowmajor", "tiles")]
-MS = (1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 33, 47, 63, 64, 65, 100, 129, 257, 300)
+MS = (1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 33, 47, 63, 64, 65, 100, 129, 257, 300, 384, 512, 700, 1024, 2048)
 
 
-def _cases(count=96, seed=2026):
+def _cases(count=192, seed=2026):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
@@ -44,6 +44,8 @@ def _cases(count=96, seed=2026):
         while n * k > 6_000_000:                        # the oracle's dequantization stays a fraction of a second
             n = max(1, n // 2)
         m = int(MS[int(rng.integers(0, len(MS)))])
+        while m * (n + k) > 12_000_000:                  # and the float64 reference product small
+            m = max(1, m // 2)
         out.append((t, lay, m, n, k, i))
     return out
 
