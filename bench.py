@@ -32,7 +32,7 @@ baseline is the oracle's restatement of mashbox's exact path
 full size (a few seconds each); `cpu_baseline` is config 2's.
 
 The one JSON line on stdout carries the contract's fields and one short summary per config (well under the 8,000
-characters a driver keeps); the per-projection detail goes to --detail (default gpurun_out/bench_detail.json).
+characters a driver keeps); the per-projection detail goes to the --detail file (its default: --help).
 
 Profiling modes (rocprofv3 runs of committed files; summaries in profiles/): --pmc-probe [CONFIGS] launches each
 config's projections a few times plus a calibration copy; --summarize-pmc turns a FETCH_SIZE and a WRITE_SIZE run of
