@@ -85,8 +85,16 @@ const char* mbq_last_error(void);
  * Replaces the membership test `t in mod.TYPES` (reference src/mashbox/ops/__init__.py:21,303). */
 int mbq_has_type(int t);
 
-/* Bytes one packed row of `cols` values takes in the file (ggml row bytes), or a negative code if cols is not a
- * multiple of the type's block. Restates reference src/mashbox/ops/reference.py:390-395. */
+/* 1 if mbq_dequant_raw reads the file blocks of ggml type t, else 0: the five types above and F32, F16, BF16, Q4_1,
+ * Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, IQ4_XS, TQ1_0, TQ2_0, MXFP4 and NVFP4 (every ggml type but the seven that decode
+ * through gguf-py's code books: IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M). Replaces the membership test
+ * `t in BLOCKS` of the reference's dequant (src/mashbox/ops/reference.py:383-387,400-401), whose exact path takes every
+ * type. */
+int mbq_has_raw_type(int t);
+
+/* Bytes one packed row of `cols` values takes in the file (ggml row bytes) for any ggml type id, or a negative code if
+ * t is not one or cols is not a multiple of the type's block. Restates reference src/mashbox/ops/reference.py:22-29,
+ * 390-395. */
 int64_t mbq_row_bytes(int t, int64_t cols);
 
 /* 1 if the kernels run a (rows, cols) weight of type t at every batch size, else 0: cols must be a whole number of
@@ -147,8 +155,9 @@ int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int3
                      int64_t N, int64_t K, const int32_t* rows_dev, int64_t count, float* w_dev, void* stream);
 
 /* W (rows, cols) float32 straight from the file's blocks raw_dev (rows, row_bytes) in HBM, no planes: the exact path's
- * rebuild, bit for bit the reference dequantization (NaN where it has NaN). Replaces dequant(raw, t, cols) of
- * reference src/mashbox/ops/reference.py:398-409 as the exact path calls it (src/mashbox/ops/__init__.py:574-576). */
+ * rebuild, bit for bit the reference dequantization (NaN where it has NaN), for every type mbq_has_raw_type names
+ * (the float types take any cols; a block type whole blocks). Replaces dequant(raw, t, cols) of reference
+ * src/mashbox/ops/reference.py:398-409 as the exact path calls it (src/mashbox/ops/__init__.py:574-576). */
 int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream);
 
 /* int8 per-output-channel linear: y (M, N) = (x (M, K) @ bf16(q).T accumulated in float32) * s, then out_dtype.

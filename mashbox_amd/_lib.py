@@ -18,6 +18,7 @@ _SIGS = {
     "mbq_version": (_c.c_int, []),
     "mbq_last_error": (_c.c_char_p, []),
     "mbq_has_type": (_c.c_int, [_c.c_int]),
+    "mbq_has_raw_type": (_c.c_int, [_c.c_int]),
     "mbq_row_bytes": (_c.c_int64, [_c.c_int, _c.c_int64]),
     "mbq_covers": (_c.c_int, [_c.c_int, _c.c_int64, _c.c_int64]),
     "mbq_plane_bytes": (_c.c_int64, [_c.c_int, _c.c_int64, _c.c_int64]),

@@ -122,12 +122,15 @@ const char* mbq_last_error(void) { return g_error.c_str(); }
 
 int mbq_has_type(int t) { return is_type(t) ? 1 : 0; }
 
+int mbq_has_raw_type(int t) { return raw_type(t) ? 1 : 0; }
+
 int64_t mbq_row_bytes(int t, int64_t cols) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "ggml type %d has no kernel planes", t);
-    if (cols < 0 || cols % block_values(t))
+    const GgmlBlock b = ggml_block(t);
+    if (b.values == 0) return set_error(MBQ_BAD_ARG, "%d is not a ggml type id", t);
+    if (cols < 0 || cols % b.values)
         return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols,
-                         block_values(t));
-    return cols / block_values(t) * block_bytes(t);
+                         b.values);
+    return cols / b.values * b.bytes;
 }
 
 // Every kernel addresses one weight's planes through a buffer resource (32-bit offsets): weights whose planes exceed
@@ -256,8 +259,17 @@ int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int3
 }
 
 int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream) {
-    if (!is_type(t)) return set_error(MBQ_BAD_ARG, "dequant_raw takes a ggml type's blocks, not type %d", t);
-    if (int rc = check_shape(t, rows, cols)) return rc;
+    if (!raw_type(t)) {
+        if (ggml_block(t).values == 0) return set_error(MBQ_BAD_ARG, "dequant_raw takes a ggml type's blocks, not type %d", t);
+        return set_error(MBQ_BAD_ARG, "dequant_raw: ggml type %d decodes through gguf-py's code books, which this library "
+                                      "does not carry", t);
+    }
+    const int bv = ggml_block(t).values;
+    if (rows <= 0 || cols <= 0) return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) is empty", (long long)rows, (long long)cols);
+    if (cols % bv)
+        return set_error(MBQ_BAD_ARG, "a row of %lld values is not a multiple of the block size %d", (long long)cols, bv);
+    if (rows > INT32_MAX || cols > INT32_MAX || rows * cols > ((int64_t)1 << 40))
+        return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) too large", (long long)rows, (long long)cols);
     if (!raw_dev || !w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "raw is NULL or w is NULL / not 16-byte aligned");
     return launch_dequant_raw(t, raw_dev, rows, cols, w_dev, reinterpret_cast<hipStream_t>(stream));
 }

@@ -213,19 +213,188 @@ __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t* __restr
     }
 }
 
+// ---------------------------------------------------------------------------- raw dequant, the other ggml types
+// The exact path's rebuild for the ggml types that have no kernel planes here (reference src/mashbox/ops/reference.py,
+// the line ranges at each type below). Every value is exact or rounded once, as in the reference: a product of an fp16
+// scale and a small integer is exact in float32, so d * q + m (Q4_1, Q5_1) and dl * q - ml (Q2_K) round once whether
+// or not the compiler fuses them; IQ4_XS's (d * s) * k rounds once in the second product, in that order.
+__device__ __forceinline__ uint32_t le16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+__device__ __forceinline__ uint32_t le32(const uint8_t* p) { return le16(p) | (le16(p + 2) << 16); }
+// value i (0..31) of a 32-value block's 16 nibble bytes: low nibbles first, then the high ones
+__device__ __forceinline__ uint32_t nib32(const uint8_t* qs, int i) { return (qs[i & 15] >> (4 * (i >> 4))) & 15u; }
+// ggml's kvalues_iq4nl (reference :348) and the FP4 (E2M1) values doubled, kvalues_mxfp4 (reference :195)
+__constant__ float kIQ4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+__constant__ float kFP4[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+// MXFP4 (reference :198-219): k * 2^(e - 128) with the float32 bits built from integers, so results below the normal
+// range are exact subnormals, results past it inf, and zero codes +0
+__device__ __forceinline__ float mxfp4_value(uint32_t e, uint32_t q) {
+    const uint32_t c = q & 7u;
+    const int odd = (int)((0x31313110u >> (4 * c)) & 15u);     // |k| = odd * 2^p for c = 0..7: odd 0 1 1 3 1 3 1 3,
+    const int p = (int)((0x23120100u >> (4 * c)) & 15u);       //                                 p   0 0 1 0 2 1 3 2
+    if (odd == 0) return 0.f;
+    const int x = p + (int)e - 128, E = odd == 3 ? x + 1 : x;
+    uint32_t bits;
+    if (E > 127) bits = 0x7F800000u;
+    else if (E < -126) bits = (uint32_t)odd << (x + 149);                                // x >= -128: a shift of 21-22
+    else bits = ((uint32_t)(E + 127) << 23) | (odd == 3 ? 1u << 22 : 0u);
+    return __uint_as_float(bits | (q >= 8 ? 0x80000000u : 0u));
+}
+
+// NVFP4's block scale (reference :222-227): unsigned E4M3 of bits 0-6 (bias 7), halved; the bytes 0x00 and 0x7F give 0
+__device__ __forceinline__ float ue4m3_half(uint32_t x) {
+    if (x == 0u || x == 0x7Fu) return 0.f;
+    const uint32_t e = (x >> 3) & 15u;
+    const float man = (float)(x & 7u);
+    const float raw = e == 0 ? man * 0x1p-9f : (1.f + man * 0.125f) * __uint_as_float((e + 120u) << 23);
+    return raw * 0.5f;
+}
+
+// TQ1_0's code of value v (reference :176-185): the base-3 digit k of a byte, ((byte * 3^k mod 256) * 3) >> 8, over
+// bytes 0-31 (values 0-159, k = v / 32), 32-47 (values 160-239) and 48-51 (values 240-255)
+__device__ __forceinline__ int tq1_code(const uint8_t* b, int v) {
+    int k, byte;
+    if (v < 160) k = v >> 5, byte = b[v & 31];
+    else if (v < 240) k = (v - 160) >> 4, byte = b[32 + ((v - 160) & 15)];
+    else k = (v - 240) >> 2, byte = b[48 + ((v - 240) & 3)];
+    const int pw = k == 0 ? 1 : k == 1 ? 3 : k == 2 ? 9 : k == 3 ? 27 : 81;
+    return ((((byte * pw) & 255) * 3) >> 8) - 1;
+}
+
+// One thread per 32 values (a block of the 32-value types, half an NVFP4 block, a 32-value group of a 256-value
+// super-block), as dequant_raw_kernel
+template <int T>
+__global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
+                                                               float* __restrict__ w) {
+    const int64_t units = rows * (K / 32);
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= units) return;
+    const int64_t n = g / (K / 32), u = g % (K / 32);
+    float* out = w + n * K + u * 32;
+    float v[32];
+    if constexpr (T == T_Q4_1) {                                         // reference :73-77
+        const uint8_t* b = raw + (n * (K / 32) + u) * 20;
+        const float d = f16f(le16(b)), m = f16f(le16(b + 2));
+        for (int i = 0; i < 32; ++i) v[i] = d * (float)nib32(b + 4, i) + m;
+    } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {                   // reference :85-98
+        constexpr bool ONE = T == T_Q5_1;
+        const uint8_t* b = raw + (n * (K / 32) + u) * (ONE ? 24 : 22);
+        const float d = f16f(le16(b)), m = ONE ? f16f(le16(b + 2)) : 0.f;
+        const uint32_t qh = le32(b + (ONE ? 4 : 2));
+        const uint8_t* qs = b + (ONE ? 8 : 6);
+        for (int i = 0; i < 32; ++i) {
+            const int q = (int)(nib32(qs, i) | (((qh >> i) & 1u) << 4));
+            v[i] = ONE ? d * (float)q + m : d * (float)(q - 16);
+        }
+    } else if constexpr (T == T_IQ4_NL) {                                // reference :351-356
+        const uint8_t* b = raw + (n * (K / 32) + u) * 18;
+        const float d = f16f(le16(b));
+        for (int i = 0; i < 32; ++i) v[i] = d * kIQ4[nib32(b + 2, i)];
+    } else if constexpr (T == T_MXFP4) {                                 // reference :198-219
+        const uint8_t* b = raw + (n * (K / 32) + u) * 17;
+        for (int i = 0; i < 32; ++i) v[i] = mxfp4_value(b[0], nib32(b + 1, i));
+    } else if constexpr (T == T_NVFP4) {                                 // reference :230-236
+        // half h of the 64-value block: sub-blocks 2h, 2h + 1 of 16 (scale byte s; codes: the low nibbles of bytes
+        // 4 + 8s .. 11 + 8s, then their high nibbles)
+        const uint8_t* b = raw + (n * (K / 64) + (u >> 1)) * 36;
+        const int h = (int)(u & 1);
+        for (int i = 0; i < 32; ++i) {
+            const int s = 2 * h + (i >> 4), ii = i & 15;
+            const uint32_t byte = b[4 + 8 * s + (ii & 7)];
+            v[i] = ue4m3_half(b[s]) * kFP4[ii < 8 ? byte & 15u : byte >> 4];
+        }
+    } else {
+        // 256-value super-blocks: group j (values 32j .. 32j + 31) of super-block u / 8
+        const int j = (int)(u & 7), hh = j >> 2, si = j & 3;
+        if constexpr (T == T_Q2_K) {                                     // reference :106-114
+            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 84;
+            const float d = f16f(le16(b + 80)), dmin = f16f(le16(b + 82));
+            for (int half = 0; half < 2; ++half) {                       // sub-block 2j + half of 16 values
+                const uint32_t s = b[2 * j + half];
+                const float dl = d * (float)(s & 15u), ml = dmin * (float)(s >> 4);
+                for (int l = 0; l < 16; ++l) {
+                    const int i = 16 * half + l;
+                    v[i] = dl * (float)((b[16 + 32 * hh + i] >> (2 * si)) & 3u) - ml;
+                }
+            }
+        } else if constexpr (T == T_Q3_K) {                              // reference :117-129
+            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 110;
+            const float d = f16f(le16(b + 108));
+            for (int half = 0; half < 2; ++half) {
+                const int sb = 2 * j + half;                             // scale: low 4 bits from bytes 96-103, high 2 from 104-107
+                const uint32_t lo = sb < 8 ? (b[96 + sb] & 15u) : (b[96 + sb - 8] >> 4);
+                const uint32_t hi = (b[104 + (sb & 3)] >> (2 * (sb >> 2))) & 3u;
+                const float dl = d * (float)((int)(lo | (hi << 4)) - 32);
+                for (int l = 0; l < 16; ++l) {
+                    const int i = 16 * half + l;
+                    const int q = (int)((b[32 + 32 * hh + i] >> (2 * si)) & 3u) - (((b[i] >> j) & 1u) ? 0 : 4);
+                    v[i] = dl * (float)q;
+                }
+            }
+        } else if constexpr (T == T_IQ4_XS) {                            // reference :359-369
+            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 136;
+            const uint32_t lo = (b[4 + (j >> 1)] >> (4 * (j & 1))) & 15u, hi = (le16(b + 2) >> (2 * j)) & 3u;
+            const float dl = f16f(le16(b)) * (float)((int)(lo | (hi << 4)) - 32);
+            for (int i = 0; i < 32; ++i) v[i] = dl * kIQ4[nib32(b + 8 + 16 * j, i)];
+        } else if constexpr (T == T_TQ1_0) {                             // reference :176-185
+            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 54;
+            const float d = f16f(le16(b + 52));
+            for (int i = 0; i < 32; ++i) v[i] = d * (float)tq1_code(b, 32 * j + i);
+        } else {                                                         // TQ2_0, reference :188-192
+            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 66;
+            const float d = f16f(le16(b + 64));
+            for (int i = 0; i < 32; ++i) v[i] = d * (float)((int)((b[32 * hh + i] >> (2 * si)) & 3u) - 1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i += 4)
+        st16(out + i, u32x4{__float_as_uint(v[i]), __float_as_uint(v[i + 1]), __float_as_uint(v[i + 2]), __float_as_uint(v[i + 3])});
+}
+
+// F32, F16, BF16 (reference :372-381): one value per block, any row length; the rows are contiguous in the file and
+// in w, so one thread takes 4 consecutive values of the whole (rows x K) array
+template <int T>
+__global__ __launch_bounds__(256) void dequant_raw_float_kernel(const uint8_t* __restrict__ raw, int64_t total,
+                                                                float* __restrict__ w) {
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    const int64_t i1 = i0 + 4 < total ? i0 + 4 : total;
+    for (int64_t i = i0; i < i1; ++i) {
+        if constexpr (T == T_F32) w[i] = __uint_as_float(le32(raw + 4 * i));
+        else if constexpr (T == T_F16) w[i] = f16f(le16(raw + 2 * i));
+        else w[i] = __uint_as_float(le16(raw + 2 * i) << 16);
+    }
+}
+
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s) {
+    if (t == T_F32 || t == T_F16 || t == T_BF16) {
+        const int64_t total = rows * K;
+        const dim3 grid((unsigned)((total + 1023) / 1024));
+        if (t == T_F32) dequant_raw_float_kernel<T_F32><<<grid, 256, 0, s>>>(raw, total, w);
+        else if (t == T_F16) dequant_raw_float_kernel<T_F16><<<grid, 256, 0, s>>>(raw, total, w);
+        else dequant_raw_float_kernel<T_BF16><<<grid, 256, 0, s>>>(raw, total, w);
+        return check_launch("dequant_raw");
+    }
     const int64_t units = rows * (K / 32);
     const dim3 grid((unsigned)((units + 255) / 256));
-    if (t == T_Q4_0)
-        dequant_raw_kernel<T_Q4_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
-    else if (t == T_Q4_K)
-        dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
-    else if (t == T_Q5_K)
-        dequant_raw_kernel<T_Q5_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
-    else if (t == T_Q6_K)
-        dequant_raw_kernel<T_Q6_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
-    else
-        dequant_raw_kernel<T_Q8_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w);
+    switch (t) {
+        case T_Q4_0: dequant_raw_kernel<T_Q4_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q4_K: dequant_raw_kernel<T_Q4_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q5_K: dequant_raw_kernel<T_Q5_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q6_K: dequant_raw_kernel<T_Q6_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q8_0: dequant_raw_kernel<T_Q8_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q4_1: dequant_raw_more_kernel<T_Q4_1><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q5_0: dequant_raw_more_kernel<T_Q5_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q5_1: dequant_raw_more_kernel<T_Q5_1><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q2_K: dequant_raw_more_kernel<T_Q2_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_Q3_K: dequant_raw_more_kernel<T_Q3_K><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_IQ4_NL: dequant_raw_more_kernel<T_IQ4_NL><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_IQ4_XS: dequant_raw_more_kernel<T_IQ4_XS><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_TQ1_0: dequant_raw_more_kernel<T_TQ1_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_TQ2_0: dequant_raw_more_kernel<T_TQ2_0><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_MXFP4: dequant_raw_more_kernel<T_MXFP4><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        case T_NVFP4: dequant_raw_more_kernel<T_NVFP4><<<grid, 256, 0, s>>>(raw, rows, (int)K, w); break;
+        default: return set_error(MBQ_BAD_ARG, "dequant_raw: no kernel for ggml type %d", t);
+    }
     return check_launch("dequant_raw");
 }
 

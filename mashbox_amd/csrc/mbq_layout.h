@@ -87,6 +87,35 @@ namespace mbq {
 // 16-row tiles (MBQ_Q40T, MBQ_Q4KT, MBQ_Q5KT, MBQ_Q6KT and MBQ_Q8T planes)
 enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_INT8 = -8, T_I8T = -9, T_Q8T = -10,
              T_Q40T = -11, T_Q4KT = -12, T_Q5KT = -13, T_Q6KT = -14 };
+// the other ggml types whose file blocks the exact path dequantizes (mbq_dequant_raw, no planes)
+enum : int { T_F32 = 0, T_F16 = 1, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q2_K = 10, T_Q3_K = 11, T_IQ4_NL = 20,
+             T_IQ4_XS = 23, T_BF16 = 30, T_TQ1_0 = 34, T_TQ2_0 = 35, T_MXFP4 = 39, T_NVFP4 = 40 };
+
+// values and bytes of one block of ggml type t ({0, 0} for an id that is not a ggml type): the table of reference
+// src/mashbox/ops/reference.py:22-29 (gguf-py's GGML_QUANT_SIZES), which fixes every GGUF file's row bytes
+struct GgmlBlock { int values, bytes; };
+inline GgmlBlock ggml_block(int t) {
+    switch (t) {
+        case 0: return {1, 4};     case 1: return {1, 2};     case 2: return {32, 18};   case 3: return {32, 20};
+        case 6: return {32, 22};   case 7: return {32, 24};   case 8: return {32, 34};   case 10: return {256, 84};
+        case 11: return {256, 110}; case 12: return {256, 144}; case 13: return {256, 176}; case 14: return {256, 210};
+        case 16: return {256, 66}; case 17: return {256, 74}; case 18: return {256, 98}; case 19: return {256, 50};
+        case 20: return {32, 18};  case 21: return {256, 110}; case 22: return {256, 82}; case 23: return {256, 136};
+        case 29: return {256, 56}; case 30: return {1, 2};    case 34: return {256, 54}; case 35: return {256, 66};
+        case 39: return {32, 17};  case 40: return {64, 36};
+    }
+    return {0, 0};
+}
+// the ggml types mbq_dequant_raw reads: every one but the seven whose values come from gguf-py's code books (IQ2_XXS,
+// IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M: reference src/mashbox/ops/reference.py:243-252)
+inline bool raw_type(int t) {
+    switch (t) {
+        case T_F32: case T_F16: case T_BF16: case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: case T_Q8_0:
+        case T_Q2_K: case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_NL: case T_IQ4_XS: case T_TQ1_0:
+        case T_TQ2_0: case T_MXFP4: case T_NVFP4: return true;
+    }
+    return false;
+}
 // int8 types: 16-byte units of 16 values, a per-row float32 scale applied to the sum
 constexpr bool int8_type(int t) { return t == T_INT8 || t == T_I8T; }
 // T_I8T: bytes between consecutive 16-row tiles of the quant plane, and the byte offset of (row, K offset k0) (k0 a

@@ -57,8 +57,16 @@ EXACT_CHUNK = 1 << 24                 # float32 values the exact path rebuilds p
 PREFLIGHT_DTYPE = torch.bfloat16      # the preflight's input dtype: the forward's activation dtype
 FORCE = ("kernels-package", "quant-kernel")
 
-# the ggml types this path reads: id -> (name, values per block, bytes per block) (reference ops/reference.py:22-29)
-TYPES = {2: ("Q4_0", 32, 18), 8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210)}
+# the ggml types this path reads: id -> (name, values per block, bytes per block) (reference ops/reference.py:22-29).
+# The kernel package gives planes to the first five; every type here runs on the exact path (mbq_dequant_raw). The
+# reference's seven other types (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M) decode through code books that
+# gguf-py ships (reference ops/reference.py:243-252); this build does not carry them.
+TYPES = {2: ("Q4_0", 32, 18), 8: ("Q8_0", 32, 34), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176), 14: ("Q6_K", 256, 210),
+         0: ("F32", 1, 4), 1: ("F16", 1, 2), 30: ("BF16", 1, 2), 3: ("Q4_1", 32, 20), 6: ("Q5_0", 32, 22),
+         7: ("Q5_1", 32, 24), 10: ("Q2_K", 256, 84), 11: ("Q3_K", 256, 110), 20: ("IQ4_NL", 32, 18),
+         23: ("IQ4_XS", 256, 136), 34: ("TQ1_0", 256, 54), 35: ("TQ2_0", 256, 66), 39: ("MXFP4", 32, 17),
+         40: ("NVFP4", 64, 36)}
+CODEBOOK_TYPES = {16: "IQ2_XXS", 17: "IQ2_XS", 18: "IQ3_XXS", 19: "IQ1_S", 21: "IQ3_S", 22: "IQ2_S", 29: "IQ1_M"}
 
 
 def warn(msg: str) -> None:
@@ -343,6 +351,9 @@ def prepare(raw, t: int, shape, use_kernel: bool = True):
     """raw: host (NumPy) or device (torch) uint8 (rows, row_bytes), or a stack of them along leading axes; shape is one
     tensor's (rows, cols) -> Packed or Raw on the GPU"""
     t = int(t)
+    if t in CODEBOOK_TYPES:
+        raise NotImplementedError(f"ggml type {CODEBOOK_TYPES[t]} decodes through gguf-py's code books, which this build "
+                                  f"does not carry")
     if t not in TYPES:
         raise NotImplementedError(f"ggml type {t} has no reader on this path (types {sorted(TYPES)})")
     key = (t, tuple(int(s) for s in shape))
@@ -522,6 +533,8 @@ def take_rows(h, ids) -> torch.Tensor:
         return (dequant(h))[ids]
     blocks = _blocks(h).reshape(rows, -1)
     picked = blocks[ids.reshape(-1)].contiguous()
+    if picked.shape[0] == 0:
+        return torch.empty(tuple(ids.shape) + (cols,), dtype=torch.float32, device=blocks.device)
     return _raw_dequant(picked, h.t, picked.shape[0], cols).reshape(tuple(ids.shape) + (cols,))
 
 

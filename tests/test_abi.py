@@ -251,6 +251,38 @@ def test_q4_k_tiled_repack_is_lossless(n, kb):
         KQ.repack_host(99, np.zeros((1, 18), np.uint8), (1, 32), tiled=True)
 
 
+def test_raw_type_table():
+    """mbq_row_bytes knows every ggml type (the file's row bytes, reference ops/reference.py:22-29, 390-395) and
+    mbq_has_raw_type names the exact path's types: all but the seven code-book types, which mbq_dequant_raw refuses
+    before touching the GPU"""
+    from mashbox_amd import gguf
+    lib = L.lib()
+    for t, (name, bs, ts) in gguf.GGML_TYPES.items():
+        cols = bs * 6
+        assert lib.mbq_row_bytes(t, cols) == 6 * ts, name
+        if bs > 1:
+            assert lib.mbq_row_bytes(t, cols + 1) < 0, name
+        assert lib.mbq_has_raw_type(t) == (1 if t in R.TYPES else 0), name
+        if t in R.TYPES:
+            assert R.row_bytes(t, cols) == 6 * ts
+    assert set(R.TYPES) == set(R.KERNEL_TYPES) | set(R.EXACT_ONLY)
+    assert len(set(gguf.GGML_TYPES) - set(R.TYPES)) == 7
+    for t in set(gguf.GGML_TYPES) - set(R.TYPES):
+        assert lib.mbq_dequant_raw(t, None, 1, 256, None, None) < 0
+        assert "code book" in L.lib().mbq_last_error().decode()
+    for t in (-12, 4, 5, 41, 99):
+        assert lib.mbq_has_raw_type(t) == 0 and lib.mbq_row_bytes(t, 256) < 0
+    for t in R.KERNEL_TYPES:
+        assert lib.mbq_has_type(t) == 1 and lib.mbq_has_raw_type(t) == 1
+    for t in R.EXACT_ONLY:
+        assert lib.mbq_has_type(t) == 0                                   # no kernel planes: the exact path only
+    # argument checks before any launch: empty shapes, partial blocks, the float types' any row length
+    assert lib.mbq_dequant_raw(R.Q3_K, None, 0, 256, None, None) < 0
+    assert lib.mbq_dequant_raw(R.Q3_K, None, 4, 200, None, None) < 0
+    assert lib.mbq_dequant_raw(R.NVFP4, None, 4, 96, None, None) < 0
+    assert lib.mbq_row_bytes(R.BF16, 37) == 74 and lib.mbq_row_bytes(R.F32, 3) == 12
+
+
 @pytest.mark.parametrize("n,kb", [(1, 1), (17, 2), (130, 3)])
 def test_q6_k_tiled_repack_is_lossless(n, kb):
     """Q6_K blocks into 16-row tiles (MBQ_Q6KT) and back, exactly; the low-nibble tiles hold the row-major planes' bytes

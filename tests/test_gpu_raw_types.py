@@ -1,0 +1,160 @@
+"""The exact path's other ggml types on the GPU: F32, F16, BF16, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, IQ4_XS, TQ1_0,
+TQ2_0, MXFP4 and NVFP4 have no kernel planes; the reference runs them on its exact path (dequant + float32 product:
+src/mashbox/ops/__init__.py:574-576, 624-632, with src/mashbox/ops/reference.py's per-type rebuilds), and so does this
+build through mbq_dequant_raw.
+
+Bars, as the kernel types' (tests/test_gpu_parity.py):
+  dequant: bit for bit against the oracle (oracle/ref.py, pinned by tests/test_oracle_types.py), NaN where it has NaN,
+           on random bytes with all-zero and all-0xFF blocks (reference tests/cpu/test_gguf_dequant.py:17-45) and on
+           the real llama-quantize blocks of tests/golden;
+  product: ops.qmatmul on the prepared weight within the float32 bars of tests/_check.py against the float64 product
+           of the oracle's weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref as R
+from tests._check import assert_product_dev, diff_bits
+from tests.test_oracle import GOLDEN
+
+import mashbox_amd.ops as OPS
+
+NAME = {t: R.TYPES[t][0] for t in R.TYPES}
+FLOATS = (R.F32, R.F16, R.BF16)
+
+
+def _cols(t, kb):
+    bs = R.TYPES[t][1]
+    return bs * kb if bs > 1 else 37 * kb
+
+
+def _raw(t, rows, kb, seed):
+    rng = np.random.default_rng(seed)
+    cols = _cols(t, kb)
+    raw = rng.integers(0, 256, size=(rows, R.row_bytes(t, cols)), dtype=np.uint8)
+    raw[0], raw[1] = 0, 0xFF
+    return raw, cols
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", R.EXACT_ONLY, ids=NAME.get)
+@pytest.mark.parametrize("kb", [1, 2, 16])
+def test_raw_dequant_bit_exact(t, kb, cuda):
+    raw, cols = _raw(t, 6, kb, 5000 + 10 * t + kb)
+    got = OPS._raw_dequant(torch.from_numpy(raw).to(cuda), t, 6, cols).cpu().numpy()
+    assert diff_bits(got, R.dequant(raw, t, cols)) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", FLOATS, ids=NAME.get)
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 37), (5, 1001), (2, 4)])
+def test_float_types_any_row_length(t, rows, cols, cuda):
+    """one value per block: rows x cols not a multiple of the kernel's 4-value step"""
+    rng = np.random.default_rng(rows * cols + t)
+    raw = rng.integers(0, 256, size=(rows, R.row_bytes(t, cols)), dtype=np.uint8)
+    got = OPS._raw_dequant(torch.from_numpy(raw).to(cuda), t, rows, cols).cpu().numpy()
+    assert diff_bits(got, R.dequant(raw, t, cols)) == 0
+
+
+@pytest.mark.gpu
+def test_mxfp4_and_nvfp4_every_scale(cuda):
+    """every E8M0 exponent (subnormal results, overflow to inf) and every E4M3 scale byte, each with all 16 codes"""
+    codes = np.array([0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE], np.uint8)
+    mx = np.zeros((256, 17), np.uint8)
+    mx[:, 0] = np.arange(256)
+    mx[:, 1:9] = codes
+    nv = np.zeros((64, 36), np.uint8)
+    nv[:, :4] = np.arange(256, dtype=np.uint8).reshape(64, 4)
+    nv[:, 4:] = np.tile(codes, 4)
+    for t, raw, cols in ((R.MXFP4, mx, 32), (R.NVFP4, nv, 64)):
+        got = OPS._raw_dequant(torch.from_numpy(raw).to(cuda), t, raw.shape[0], cols).cpu().numpy()
+        assert diff_bits(got, R.dequant(raw, t, cols)) == 0, NAME[t]
+
+
+def _golden_exact():
+    import os
+    out = []
+    if os.path.isdir(GOLDEN):
+        for f in sorted(os.listdir(GOLDEN)):
+            if f.endswith(".npz"):
+                z = np.load(os.path.join(GOLDEN, f), allow_pickle=False)
+                if int(z["t"]) in R.EXACT_ONLY:
+                    out.append(f)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", _golden_exact())
+def test_golden_blocks_dequant_and_product(name, cuda):
+    """the committed fixtures of the exact path's types: dequant bit for bit; for the real llama-quantize slices also
+    ops.prepare -> Raw -> ops.qmatmul against the float64 product the fixture holds"""
+    import os
+    z = np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+    t, cols, raw = int(z["t"]), int(z["cols"]), z["raw"]
+    rows = raw.shape[0]
+    got = OPS._raw_dequant(torch.from_numpy(raw).to(cuda), t, rows, cols).cpu().numpy()
+    assert diff_bits(got, z["w"]) == 0
+    if "x" in z.files:
+        h = OPS.prepare(raw, t, (rows, cols))
+        assert isinstance(h, OPS.Raw) and OPS.weight_path(t, (rows, cols)) == "exact"
+        x = torch.from_numpy(z["x"].astype(np.int16)).view(torch.bfloat16).to(cuda)
+        y = OPS.qmatmul(x, h)
+        assert y.dtype == torch.bfloat16 and tuple(y.shape) == (x.shape[0], rows)
+        assert_product_dev(y.float(), torch.from_numpy(z["y64"]).to(cuda), name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", R.EXACT_ONLY, ids=NAME.get)
+def test_qmatmul_exact_path(t, cuda):
+    """a (rows, cols) weight of every exact-only type through ops.prepare / ops.qmatmul, leading activation axes kept,
+    against the float64 product of the oracle's weights; finite scales so that the product is finite"""
+    from tests.test_oracle_types import random_blocks
+    bs, ts = R.TYPES[t][1], R.TYPES[t][2]
+    rows = 45
+    if t in FLOATS:
+        cols = 300
+        rng = np.random.default_rng(t)
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        raw = (w.view(np.uint8) if t == R.F32 else
+               w.astype(np.float16).view(np.uint8) if t == R.F16 else
+               (R.bf16_round(w)).view(np.uint8)).reshape(rows, -1)
+    else:
+        kb = max(1, 512 // bs)
+        cols = bs * kb
+        blocks = random_blocks(t, rows * kb, 6000 + t)
+        if t == R.MXFP4:
+            blocks[:, 0] = np.random.default_rng(t).integers(110, 130, blocks.shape[0])      # exponents of weights
+        raw = blocks.reshape(rows, kb * ts)
+    h = OPS.prepare(raw, t, (rows, cols))
+    assert isinstance(h, OPS.Raw)
+    w64 = torch.from_numpy(R.dequant(raw, t, cols)).to(cuda).double()
+    rng = np.random.default_rng(7 + t)
+    x = torch.from_numpy(rng.standard_normal((2, 3, cols)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+    y = OPS.qmatmul(x, h)
+    assert tuple(y.shape) == (2, 3, rows) and y.dtype == torch.bfloat16
+    assert_product_dev(y.float(), x.double() @ w64.T, NAME[t])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [R.Q3_K, R.IQ4_XS, R.BF16, R.NVFP4], ids=NAME.get)
+def test_take_rows_exact_path(t, cuda):
+    """an embedding lookup on a Raw weight rebuilds only the looked-up rows, bit for bit the rows of the whole
+    dequantization (negative ids count from the end); no ids give an empty result"""
+    raw, cols = _raw(t, 20, 2, 7000 + t)
+    h = OPS.prepare(raw, t, (20, cols))
+    want = R.dequant(raw, t, cols)
+    ids = torch.tensor([[3, -1], [0, 19]], device=cuda)
+    got = OPS.take_rows(h, ids).cpu().numpy()
+    assert diff_bits(got, want[[[3, 19], [0, 19]]]) == 0
+    assert tuple(OPS.take_rows(h, torch.zeros(0, dtype=torch.long, device=cuda)).shape) == (0, cols)
+
+
+def test_prepare_refuses_code_book_types():
+    """the seven types whose values come from gguf-py's code books are refused at load, with the reason"""
+    for t in OPS.CODEBOOK_TYPES:
+        with pytest.raises(NotImplementedError, match="code books"):
+            OPS.prepare(np.zeros((1, 66), np.uint8), t, (1, 256))
+    assert set(OPS.TYPES) == set(R.TYPES)
+    for t in R.EXACT_ONLY:
+        assert OPS.row_bytes(t, _cols(t, 3)) == R.row_bytes(t, _cols(t, 3))

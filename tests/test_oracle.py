@@ -485,6 +485,8 @@ def test_real_llama_quantize_blocks_match_the_scalar_forms():
             continue
         z = np.load(os.path.join(GOLDEN, name), allow_pickle=False)
         t, cols, raw = int(z["t"]), int(z["cols"]), z["raw"]
+        if t not in (R.Q8_0, R.Q4_K, R.Q5_K, R.Q6_K):
+            continue                                  # the exact path's other types: tests/test_oracle_types.py
         got = R.dequant(raw, t, cols)
         _, bs, ts = R.TYPES[t]
         blocks = raw.reshape(-1, ts)
