@@ -158,3 +158,37 @@ def test_prepare_refuses_code_book_types():
     assert set(OPS.TYPES) == set(R.TYPES)
     for t in R.EXACT_ONLY:
         assert OPS.row_bytes(t, _cols(t, 3)) == R.row_bytes(t, _cols(t, 3))
+
+
+@pytest.mark.gpu
+def test_mixed_role_of_a_kernel_type_and_an_exact_type(cuda):
+    """a role whose layers mix a kernel type and an exact-only type (as Q3_K_M files mix Q3_K and Q4_K per layer,
+    reference src/mashbox/ops/__init__.py:216-270): stack_mixed, scan_split / scan_join and qmatmul give each layer's
+    product, the Q3_K stack dequantizes with its leading axis, against the oracle"""
+    from oracle import gen as G
+    from tests.test_oracle_types import random_blocks
+    rows, cols = 48, 512
+    layers = []
+    for l, t in enumerate([R.Q4_K, R.Q3_K, R.Q4_K, R.Q3_K]):
+        raw = (G.RAW[t](np.random.default_rng(l), rows, cols) if t == R.Q4_K else
+               random_blocks(t, rows * (cols // 256), 900 + l).reshape(rows, -1))
+        layers.append((raw, t))
+    OPS.load_kernels()
+    try:
+        h = OPS.stack_mixed(layers, (rows, cols))
+        assert isinstance(h, OPS.Mixed) and tuple(h.types) == (R.Q4_K, R.Q3_K)
+        assert isinstance(h.stacks[1], OPS.Raw)
+        st = OPS.dequant(h.stacks[1]).cpu().numpy()
+        assert st.shape == (2, rows, cols)
+        for s, l in enumerate((1, 3)):
+            assert diff_bits(st[s], R.dequant(layers[l][0], R.Q3_K, cols)) == 0
+        held, xs = OPS.scan_split({"w": h})
+        rng = np.random.default_rng(11)
+        x = torch.from_numpy(rng.standard_normal((3, cols)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+        for l, (raw, t) in enumerate(layers):
+            w = OPS.scan_join(held, xs, torch.tensor(l, dtype=torch.int32, device=cuda))["w"]
+            y = OPS.qmatmul(x, w)
+            ref = x.double() @ torch.from_numpy(R.dequant(raw, t, cols)).to(cuda).double().T
+            assert_product_dev(y.float(), ref, f"layer {l} {NAME[t]}")
+    finally:
+        OPS.load_kernels(module="off")
