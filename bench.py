@@ -16,7 +16,10 @@ Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, tiles from 2 rows on) and config 5 on r
 `m1_q4k_stacked`, `m4_q4k_stacked`, `m16_q4k_stacked` and `c4_stacked` time the same layer with the projections that
 share an input stacked by rows at load (ops.stack_rows: q|k|v 8192 x 5120, gate|up 34816 x 5120), four launches per
 layer instead of seven; the BASELINE configs 4 and 5 stay the seven launches they name. `p512_q4k` is the same Q4_K
-layer at 512 rows, the reference engine's default prefill chunk (runtime/engine.py:168).
+layer at 512 rows, the reference engine's default prefill chunk (runtime/engine.py:168). `q4k_9728` and `q2k_9728` are
+the shapes of the reference's other published per-call numbers (a 9728 x 2560 weight at one row: Q4_K 22.6 us, Q2_K
+25.5 us on TPU v6e-1, CORE-CHANGES.md:84): Q4_K on the decode GEMV, Q2_K (no kernel planes here) on the exact path's
+fused product over the file's blocks (mbq_matmul_raw).
 
 Timing: each projection's launches are captured in a HIP graph (torch.cuda.CUDAGraph) of K launches that cycles through
 >= 1 GiB of distinct weight copies (the 256 MB Infinity Cache cannot serve repeats), replayed once for warmup, then R
@@ -61,7 +64,7 @@ def algorithmic_bytes(t, m, n, k):
     if t == "int8":
         w = n * k + 4 * n
     else:
-        bs, ts = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}[t]
+        bs, ts = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 10: (256, 84)}[t]
         w = n * (k // bs) * ts
     return w + 2 * m * k + 2 * m * n
 
@@ -73,7 +76,7 @@ def log(*a):
 # the configs a run without --configs times, in order
 DEFAULT_CONFIGS = ("1,2,3,4,5,q6k_head,m1_q4k,m1_q4k_tiles,m4_q4k,m16_q4k,m4_q8,m16_q8,m4_q5k,m16_q5k,m4_q6k,m16_q6k,"
                    "m4_int8,m16_int8,c5_rm,c2_ops,m1_q4k_ops,m4_q4k_ops,c5_ops,m1_q4k_stacked,m4_q4k_stacked,"
-                   "m16_q4k_stacked,c4_stacked,p512_q4k")
+                   "m16_q4k_stacked,c4_stacked,p512_q4k,q4k_9728,q2k_9728")
 
 # rows timed through mashbox_amd.ops.qmatmul (the caller's path) instead of the C ABI: row -> the config it repeats
 OPS_ROWS = {"c2_ops": 2, "c5_ops": 5, "m4_q4k_ops": "m4_q4k", "m1_q4k_ops": "m1_q4k"}
@@ -123,6 +126,17 @@ def setup_projection(idx, pi, rotate_bytes):
             ops.qmatmul(x, hs[c])
             return 0
         plan = "ops.qmatmul " + LIB.plan_str(p.t, M, N, K)
+    elif t == 10:
+        # Q2_K has no kernel planes: the exact path's fused product reads the file's blocks (mbq_matmul_raw)
+        raw = synth.q2_k_raw(N, K, seed=seed + 7, device=dev)
+        wbytes = raw.numel()
+        copies = max(1, math.ceil(rotate_bytes / wbytes))
+        bufs = [raw] + [raw.clone() for _ in range(copies - 1)]
+
+        def launch(c):
+            return L.mbq_matmul_raw(t, ctypes.c_void_p(bufs[c].data_ptr()), ctypes.c_void_p(x.data_ptr()), M, N, K,
+                                    ctypes.c_void_p(y.data_ptr()), OUT_BF16, st())
+        plan = "raw GEMV (exact path, file blocks)"
     elif t == "int8" and M > 1:
         # batched int8: the weights repacked once at load into 16-row tiles (MBQ_I8T planes; from 2 rows on they run
         # faster than row-major weights: MI355X, 17408 x 5120 at 4 rows 19 vs 36 us)
@@ -251,7 +265,7 @@ def run_config(idx, steps, warmup, rotate_bytes):
         torch.cuda.empty_cache()
     gbs = total_bytes / total_us / 1e3
     tfl = total_flops / total_us / 1e6
-    out.update({"type": {8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}.get(t, t), "M": M,
+    out.update({"type": {8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 10: "Q2_K"}.get(t, t), "M": M,
                 "us_per_step": round(total_us, 3), "mean_us_per_step": round(total_mean_us, 3),
                 "launches_timed": replays * steps, "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
                 "TFLOPs": round(tfl, 2), "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4),
@@ -602,6 +616,8 @@ def summary(r):
     o.update(GBps=round(r["GBps"]), hbm=round(r["hbm_frac"], 3))
     if "traffic_over_algorithmic" in r:
         o["traffic_x"] = round(r["traffic_over_algorithmic"], 3)
+    if "speedup_vs_reference_tpu_v6e" in r:        # the shapes of the reference's published per-call numbers
+        o["x_ref_tpu"] = r["speedup_vs_reference_tpu_v6e"]
     return o
 
 

@@ -160,6 +160,17 @@ int mbq_dequant_rows(int t, const uint8_t* planes_dev, int64_t layer, const int3
  * src/mashbox/ops/reference.py:398-409 as the exact path calls it (src/mashbox/ops/__init__.py:574-576). */
 int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, float* w_dev, void* stream);
 
+/* y (M, N) = x (M, K) bf16 @ W.T for 1-8 activation rows, W (N, K) the file's blocks raw_dev (N, row_bytes) of a type
+ * mbq_has_raw_type names that has no kernel planes (F32, F16, BF16, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, IQ4_NL, IQ4_XS,
+ * TQ1_0, TQ2_0, MXFP4, NVFP4): each weight row rebuilt in registers, bit for bit the values of mbq_dequant_raw, and
+ * multiplied in float32 (float32 products summed in float32), without writing W. K must be a multiple of 32; M = 0
+ * launches nothing; more than 8 rows is refused (mbq_dequant_raw and a GEMM serve those). The exact path's product of
+ * reference src/mashbox/ops/__init__.py:574-576,624-632 (dequant, then a float32 dot) for decode-sized batches.
+ * raw_dev starts at a multiple of the type's block alignment (4 bytes for Q2_K, Q4_1, Q5_1, IQ4_XS, NVFP4 and F32; 2
+ * for Q3_K, Q5_0, IQ4_NL, TQ1_0, TQ2_0, F16 and BF16; any for MXFP4), as mbq_dequant_raw's does for these types. */
+int mbq_matmul_raw(int t, const uint8_t* raw_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev,
+                   int out_dtype, void* stream);
+
 /* int8 per-output-channel linear: y (M, N) = (x (M, K) @ bf16(q).T accumulated in float32) * s, then out_dtype.
  * q_dev int8 (N, K) row-major, s_dev float32 (N,). Replaces linear(x, {"q", "s"}) (reference
  * src/mashbox/models/qwen3_8_27b/model.py:72-82); with out_dtype MBQ_OUT_F32 it returns the float32 y*s that the

@@ -34,6 +34,8 @@ _SIGS = {
     "mbq_dequant_rows": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64,
                                     _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_void_p]),
     "mbq_dequant_raw": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_void_p]),
+    "mbq_matmul_raw": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_int,
+                                  _c.c_void_p]),
     "mbq_int8_embed": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_int64, _c.c_void_p,
                                   _c.c_int, _c.c_void_p]),
     "mbq_int8_repack_host": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64, _c.c_void_p, _c.c_size_t,

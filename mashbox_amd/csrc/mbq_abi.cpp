@@ -271,7 +271,30 @@ int mbq_dequant_raw(int t, const uint8_t* raw_dev, int64_t rows, int64_t cols, f
     if (rows > INT32_MAX || cols > INT32_MAX || rows * cols > ((int64_t)1 << 40))
         return set_error(MBQ_BAD_ARG, "shape (%lld, %lld) too large", (long long)rows, (long long)cols);
     if (!raw_dev || !w_dev || !aligned16(w_dev)) return set_error(MBQ_BAD_ARG, "raw is NULL or w is NULL / not 16-byte aligned");
+    if (!is_type(t) && reinterpret_cast<uintptr_t>(raw_dev) % raw_block_align(t))
+        return set_error(MBQ_BAD_ARG, "dequant_raw: the blocks must start at a multiple of %d bytes", raw_block_align(t));
     return launch_dequant_raw(t, raw_dev, rows, cols, w_dev, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mbq_matmul_raw(int t, const uint8_t* raw_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K, void* y_dev,
+                   int out_dtype, void* stream) {
+    if (!raw_type(t) || is_type(t))
+        return set_error(MBQ_BAD_ARG, "matmul_raw takes the file blocks of an exact-path type without kernel planes, not type %d", t);
+    if (out_dtype != MBQ_OUT_F32 && out_dtype != MBQ_OUT_BF16) return set_error(MBQ_BAD_ARG, "out_dtype %d", out_dtype);
+    if (M == 0) return MBQ_OK;
+    if (M < 0 || M > 8)
+        return set_error(MBQ_BAD_ARG, "matmul_raw: M = %lld (1-8 rows; more rows: mbq_dequant_raw and a GEMM)", (long long)M);
+    if (N <= 0 || K <= 0 || N > INT32_MAX || K > INT32_MAX || M * K > INT32_MAX || M * N > INT32_MAX)
+        return set_error(MBQ_BAD_ARG, "matmul_raw: shape (%lld, %lld, %lld)", (long long)M, (long long)N, (long long)K);
+    if (K % 32 || K % ggml_block(t).values)
+        return set_error(MBQ_BAD_ARG, "matmul_raw: K = %lld must be a multiple of 32 and of the block size %d", (long long)K,
+                         ggml_block(t).values);
+    if (!raw_dev || !x_dev || !y_dev || !aligned16(x_dev) || (reinterpret_cast<uintptr_t>(y_dev) & 3u))
+        return set_error(MBQ_BAD_ARG, "matmul_raw: raw, x or y is NULL, x not 16-byte or y not 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(raw_dev) % raw_block_align(t))
+        return set_error(MBQ_BAD_ARG, "matmul_raw: the blocks must start at a multiple of %d bytes", raw_block_align(t));
+    return launch_raw_gemv(t, raw_dev, x_dev, M, N, K, y_dev, out_dtype == MBQ_OUT_BF16 ? 1 : 0,
+                           reinterpret_cast<hipStream_t>(stream));
 }
 
 int mbq_int8_linear(const int8_t* q_dev, const float* s_dev, const uint16_t* x_dev, int64_t M, int64_t N, int64_t K,

@@ -261,24 +261,37 @@ __device__ __forceinline__ int tq1_code(const uint8_t* b, int v) {
     return ((((byte * pw) & 255) * 3) >> 8) - 1;
 }
 
-// One thread per 32 values (a block of the 32-value types, half an NVFP4 block, a 32-value group of a 256-value
-// super-block), as dequant_raw_kernel
+// the alignment every block start of type T has when the blocks start at an address of that alignment: the largest
+// power of two (at most 4) dividing the block bytes (Q2_K 84, Q4_1 20, Q5_1 24, IQ4_XS 136, NVFP4 36, F32: 4; Q3_K
+// 110, Q5_0 22, IQ4_NL 18, TQ1_0 54, TQ2_0 66, F16, BF16: 2; MXFP4 17: 1). Told to the compiler, it lets it merge the
+// byte reads of a block into wider loads.
 template <int T>
-__global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
-                                                               float* __restrict__ w) {
-    const int64_t units = rows * (K / 32);
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= units) return;
-    const int64_t n = g / (K / 32), u = g % (K / 32);
-    float* out = w + n * K + u * 32;
-    float v[32];
-    if constexpr (T == T_Q4_1) {                                         // reference :73-77
-        const uint8_t* b = raw + (n * (K / 32) + u) * 20;
+__host__ __device__ constexpr int raw_align() { return raw_block_align(T); }
+static_assert(raw_block_align(T_Q2_K) == 4 && raw_block_align(T_Q3_K) == 2 && raw_block_align(T_MXFP4) == 1 &&
+              raw_block_align(T_F32) == 4 && raw_block_align(T_BF16) == 2, "block alignments");
+template <int T>
+__device__ __forceinline__ const uint8_t* blk(const uint8_t* p) {
+    return static_cast<const uint8_t*>(__builtin_assume_aligned(p, raw_align<T>()));
+}
+
+// Values 32u .. 32u + 31 of one weight row in the file's blocks of type T (row: the row's first byte, aligned to
+// raw_align<T>()): a block of the 32-value types, half an NVFP4 block, a 32-value group of a 256-value super-block; for
+// the float types (one value per block) 32 consecutive values
+template <int T>
+__device__ __forceinline__ void raw_unit(const uint8_t* __restrict__ row, int u, float v[32]) {
+    if constexpr (T == T_F32 || T == T_F16 || T == T_BF16) {            // reference :372-381
+        constexpr int ES = T == T_F32 ? 4 : 2;
+        const uint8_t* p = blk<T>(row + (int64_t)ES * 32 * u);
+        for (int i = 0; i < 32; ++i)
+            v[i] = T == T_F32 ? __uint_as_float(le32(p + 4 * i)) : T == T_F16 ? f16f(le16(p + 2 * i))
+                                                                       : __uint_as_float(le16(p + 2 * i) << 16);
+    } else if constexpr (T == T_Q4_1) {                                  // reference :73-77
+        const uint8_t* b = blk<T>(row + (int64_t)u * 20);
         const float d = f16f(le16(b)), m = f16f(le16(b + 2));
         for (int i = 0; i < 32; ++i) v[i] = d * (float)nib32(b + 4, i) + m;
     } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {                   // reference :85-98
         constexpr bool ONE = T == T_Q5_1;
-        const uint8_t* b = raw + (n * (K / 32) + u) * (ONE ? 24 : 22);
+        const uint8_t* b = blk<T>(row + (int64_t)u * (ONE ? 24 : 22));
         const float d = f16f(le16(b)), m = ONE ? f16f(le16(b + 2)) : 0.f;
         const uint32_t qh = le32(b + (ONE ? 4 : 2));
         const uint8_t* qs = b + (ONE ? 8 : 6);
@@ -287,17 +300,17 @@ __global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __
             v[i] = ONE ? d * (float)q + m : d * (float)(q - 16);
         }
     } else if constexpr (T == T_IQ4_NL) {                                // reference :351-356
-        const uint8_t* b = raw + (n * (K / 32) + u) * 18;
+        const uint8_t* b = blk<T>(row + (int64_t)u * 18);
         const float d = f16f(le16(b));
         for (int i = 0; i < 32; ++i) v[i] = d * kIQ4[nib32(b + 2, i)];
     } else if constexpr (T == T_MXFP4) {                                 // reference :198-219
-        const uint8_t* b = raw + (n * (K / 32) + u) * 17;
+        const uint8_t* b = blk<T>(row + (int64_t)u * 17);
         for (int i = 0; i < 32; ++i) v[i] = mxfp4_value(b[0], nib32(b + 1, i));
     } else if constexpr (T == T_NVFP4) {                                 // reference :230-236
         // half h of the 64-value block: sub-blocks 2h, 2h + 1 of 16 (scale byte s; codes: the low nibbles of bytes
         // 4 + 8s .. 11 + 8s, then their high nibbles)
-        const uint8_t* b = raw + (n * (K / 64) + (u >> 1)) * 36;
-        const int h = (int)(u & 1);
+        const uint8_t* b = blk<T>(row + (int64_t)(u >> 1) * 36);
+        const int h = u & 1;
         for (int i = 0; i < 32; ++i) {
             const int s = 2 * h + (i >> 4), ii = i & 15;
             const uint32_t byte = b[4 + 8 * s + (ii & 7)];
@@ -305,9 +318,9 @@ __global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __
         }
     } else {
         // 256-value super-blocks: group j (values 32j .. 32j + 31) of super-block u / 8
-        const int j = (int)(u & 7), hh = j >> 2, si = j & 3;
+        const int j = u & 7, hh = j >> 2, si = j & 3;
         if constexpr (T == T_Q2_K) {                                     // reference :106-114
-            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 84;
+            const uint8_t* b = blk<T>(row + (int64_t)(u >> 3) * 84);
             const float d = f16f(le16(b + 80)), dmin = f16f(le16(b + 82));
             for (int half = 0; half < 2; ++half) {                       // sub-block 2j + half of 16 values
                 const uint32_t s = b[2 * j + half];
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __
                 }
             }
         } else if constexpr (T == T_Q3_K) {                              // reference :117-129
-            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 110;
+            const uint8_t* b = blk<T>(row + (int64_t)(u >> 3) * 110);
             const float d = f16f(le16(b + 108));
             for (int half = 0; half < 2; ++half) {
                 const int sb = 2 * j + half;                             // scale: low 4 bits from bytes 96-103, high 2 from 104-107
@@ -332,23 +345,105 @@ __global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __
                 }
             }
         } else if constexpr (T == T_IQ4_XS) {                            // reference :359-369
-            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 136;
+            const uint8_t* b = blk<T>(row + (int64_t)(u >> 3) * 136);
             const uint32_t lo = (b[4 + (j >> 1)] >> (4 * (j & 1))) & 15u, hi = (le16(b + 2) >> (2 * j)) & 3u;
             const float dl = f16f(le16(b)) * (float)((int)(lo | (hi << 4)) - 32);
             for (int i = 0; i < 32; ++i) v[i] = dl * kIQ4[nib32(b + 8 + 16 * j, i)];
         } else if constexpr (T == T_TQ1_0) {                             // reference :176-185
-            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 54;
+            const uint8_t* b = blk<T>(row + (int64_t)(u >> 3) * 54);
             const float d = f16f(le16(b + 52));
             for (int i = 0; i < 32; ++i) v[i] = d * (float)tq1_code(b, 32 * j + i);
         } else {                                                         // TQ2_0, reference :188-192
-            const uint8_t* b = raw + (n * (K / 256) + (u >> 3)) * 66;
+            static_assert(T == T_TQ2_0, "a raw type");
+            const uint8_t* b = blk<T>(row + (int64_t)(u >> 3) * 66);
             const float d = f16f(le16(b + 64));
             for (int i = 0; i < 32; ++i) v[i] = d * (float)((int)((b[32 * hh + i] >> (2 * si)) & 3u) - 1);
         }
     }
+}
+
+// bytes of one row of K values in the file's blocks of type T
+template <int T>
+__host__ __device__ constexpr int64_t raw_row_bytes(int64_t K) {
+    return T == T_F32 ? 4 * K : (T == T_F16 || T == T_BF16) ? 2 * K : T == T_Q4_1 ? K / 32 * 20 : T == T_Q5_0 ? K / 32 * 22
+         : T == T_Q5_1 ? K / 32 * 24 : T == T_IQ4_NL ? K / 32 * 18 : T == T_MXFP4 ? K / 32 * 17 : T == T_NVFP4 ? K / 64 * 36
+         : T == T_Q2_K ? K / 256 * 84 : T == T_Q3_K ? K / 256 * 110 : T == T_IQ4_XS ? K / 256 * 136
+         : T == T_TQ1_0 ? K / 256 * 54 : K / 256 * 66;
+}
+
+// One thread per 32 values, as dequant_raw_kernel
+template <int T>
+__global__ __launch_bounds__(256) void dequant_raw_more_kernel(const uint8_t* __restrict__ raw, int64_t rows, int K,
+                                                               float* __restrict__ w) {
+    const int64_t units = rows * (K / 32);
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= units) return;
+    const int64_t n = g / (K / 32), u = g % (K / 32);
+    float v[32];
+    raw_unit<T>(raw + n * raw_row_bytes<T>(K), (int)u, v);
+    float* out = w + n * K + u * 32;
 #pragma unroll
     for (int i = 0; i < 32; i += 4)
         st16(out + i, u32x4{__float_as_uint(v[i]), __float_as_uint(v[i + 1]), __float_as_uint(v[i + 2]), __float_as_uint(v[i + 3])});
+}
+
+// The exact path's product for one to eight activation rows, fused: y (M, N) = x (M, K) @ W.T with W's rows rebuilt
+// from the file's blocks in registers (raw_unit, bit for bit the values mbq_dequant_raw writes), float32 products and
+// sums, each row read once from HBM instead of written as float32 and read back (reference src/mashbox/ops/__init__.py
+// :574-576, 624-632: dequant, then a float32 dot). Lanes in groups of LPR take one weight row each (4 waves x 64 / LPR
+// rows per block, rows over the grid), a lane the row's 32-value units u = lane % LPR, + LPR, ...; the group's sums
+// meet by shuffles; with U2 a lane has two units' loads in flight. Up to RGV_MAX_M activation rows, one float32 sum
+// each in registers.
+constexpr int RGV_MAX_M = 8;
+template <int T, int LPR, bool U2>
+__global__ __launch_bounds__(256) void raw_gemv_kernel(const uint8_t* __restrict__ raw, const uint16_t* __restrict__ x,
+                                                       int M, int N, int K, void* __restrict__ y, int out_bf16) {
+    constexpr int RPB = 256 / LPR;                                       // rows per block
+    const int lane = threadIdx.x & (LPR - 1);
+    const int U = K >> 5;
+    const int64_t rb = raw_row_bytes<T>(K);
+    for (int64_t n = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; n < N; n += (int64_t)gridDim.x * RPB) {
+        float acc[RGV_MAX_M];
+#pragma unroll
+        for (int m = 0; m < RGV_MAX_M; ++m) acc[m] = 0.f;
+        const uint8_t* row = raw + n * rb;
+        for (int u0 = lane; u0 < U; u0 += (U2 ? 2 : 1) * LPR)
+#pragma unroll
+        for (int uu = 0; uu < (U2 ? 2 : 1); ++uu) {
+            const int u = u0 + uu * LPR;
+            if (u >= U) break;
+            float v[32];
+            raw_unit<T>(row, u, v);
+#pragma unroll
+            for (int m = 0; m < RGV_MAX_M; ++m) {
+                if (m < M) {
+                    const u32x4* xp = reinterpret_cast<const u32x4*>(x + (int64_t)m * K + 32 * u);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const u32x4 q = xp[c];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            acc[m] = __builtin_fmaf(__uint_as_float(q[e] << 16), v[8 * c + 2 * e], acc[m]);
+                            acc[m] = __builtin_fmaf(__uint_as_float(q[e] & 0xFFFF0000u), v[8 * c + 2 * e + 1], acc[m]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < RGV_MAX_M; ++m)
+#pragma unroll
+            for (int off = LPR / 2; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off, LPR);
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < RGV_MAX_M; ++m) {
+                if (m < M) {
+                    if (out_bf16) reinterpret_cast<uint16_t*>(y)[(int64_t)m * N + n] = (uint16_t)bf16_bits(acc[m]);
+                    else reinterpret_cast<float*>(y)[(int64_t)m * N + n] = acc[m];
+                }
+            }
+        }
+    }
 }
 
 // F32, F16, BF16 (reference :372-381): one value per block, any row length; the rows are contiguous in the file and
@@ -396,6 +491,48 @@ int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float
         default: return set_error(MBQ_BAD_ARG, "dequant_raw: no kernel for ggml type %d", t);
     }
     return check_launch("dequant_raw");
+}
+
+// Lanes per row by the row's 32-value units U (MI355X, interleaved timings of 16, 32 and 64 lanes, with and without two
+// units in flight, on Q2_K 9728 x 2560, Q3_K 17408 x 5120, IQ4_XS 5120 x 17408, Q5_0 6144 x 5120 at 4 rows and F16
+// 4096 x 4096): short rows (U < 128) 16 lanes, so that a wave holds 4 rows (Q2_K 14.5 -> 10.8 us); the 256-value types,
+// whose units cost the most vector work, 32 lanes up to U = 256 (Q3_K 51.3 -> 46.5 us); else 64, with two units in
+// flight from U = 256 on (IQ4_XS 66.1 -> 60.8 us). Each choice was the fastest or within 2 % of it on those cases.
+template <int T>
+static void raw_gemv_t(const uint8_t* raw, const uint16_t* x, int64_t M, int64_t N, int64_t K, void* y, int out_bf16,
+                       hipStream_t s) {
+    const int64_t U = K / 32;
+    constexpr bool HEAVY = ggml_block(T).values == 256;
+    if (U < 128)
+        raw_gemv_kernel<T, 16, false><<<dim3((unsigned)((N + 15) / 16)), 256, 0, s>>>(raw, x, (int)M, (int)N, (int)K, y, out_bf16);
+    else if (HEAVY && U < 256)
+        raw_gemv_kernel<T, 32, false><<<dim3((unsigned)((N + 7) / 8)), 256, 0, s>>>(raw, x, (int)M, (int)N, (int)K, y, out_bf16);
+    else if (U < 256)
+        raw_gemv_kernel<T, 64, false><<<dim3((unsigned)((N + 3) / 4)), 256, 0, s>>>(raw, x, (int)M, (int)N, (int)K, y, out_bf16);
+    else
+        raw_gemv_kernel<T, 64, true><<<dim3((unsigned)((N + 3) / 4)), 256, 0, s>>>(raw, x, (int)M, (int)N, (int)K, y, out_bf16);
+}
+
+int launch_raw_gemv(int t, const uint8_t* raw, const uint16_t* x, int64_t M, int64_t N, int64_t K, void* y, int out_bf16,
+                    hipStream_t s) {
+    switch (t) {
+        case T_F32: raw_gemv_t<T_F32>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_F16: raw_gemv_t<T_F16>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_BF16: raw_gemv_t<T_BF16>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_Q4_1: raw_gemv_t<T_Q4_1>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_Q5_0: raw_gemv_t<T_Q5_0>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_Q5_1: raw_gemv_t<T_Q5_1>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_Q2_K: raw_gemv_t<T_Q2_K>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_Q3_K: raw_gemv_t<T_Q3_K>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_IQ4_NL: raw_gemv_t<T_IQ4_NL>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_IQ4_XS: raw_gemv_t<T_IQ4_XS>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_TQ1_0: raw_gemv_t<T_TQ1_0>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_TQ2_0: raw_gemv_t<T_TQ2_0>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_MXFP4: raw_gemv_t<T_MXFP4>(raw, x, M, N, K, y, out_bf16, s); break;
+        case T_NVFP4: raw_gemv_t<T_NVFP4>(raw, x, M, N, K, y, out_bf16, s); break;
+        default: return set_error(MBQ_BAD_ARG, "raw GEMV: no kernel for ggml type %d (kernel types run on their planes)", t);
+    }
+    return check_launch("raw GEMV");
 }
 
 // -------------------------------------------------------------------------------------------------- zero fill

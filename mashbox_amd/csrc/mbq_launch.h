@@ -95,6 +95,9 @@ int launch_dequant(int t, const Args& a, float* w, const int32_t* rows, int64_t 
 int launch_int8_embed(const int8_t* q, const float* s, int64_t N, int64_t D, const int32_t* toks, int64_t T, void* y,
                       int out_bf16, hipStream_t st);
 int launch_dequant_raw(int t, const uint8_t* raw, int64_t rows, int64_t K, float* w, hipStream_t s);
+// the exact path's fused product for 1-8 activation rows on the file's blocks of an exact-only type (mbq_kernels.hip)
+int launch_raw_gemv(int t, const uint8_t* raw, const uint16_t* x, int64_t M, int64_t N, int64_t K, void* y, int out_bf16,
+                    hipStream_t s);
 int launch_zero(uint8_t* p, int64_t n, hipStream_t s);   // n bytes at device address p set to zero
 // measurement probes (mbq_probe.hip)
 int launch_probe_read(const uint8_t* p, int64_t bytes, uint32_t* sink, hipStream_t s);

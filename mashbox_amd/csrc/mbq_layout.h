@@ -94,7 +94,7 @@ enum : int { T_F32 = 0, T_F16 = 1, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q2_K = 
 // values and bytes of one block of ggml type t ({0, 0} for an id that is not a ggml type): the table of reference
 // src/mashbox/ops/reference.py:22-29 (gguf-py's GGML_QUANT_SIZES), which fixes every GGUF file's row bytes
 struct GgmlBlock { int values, bytes; };
-inline GgmlBlock ggml_block(int t) {
+constexpr GgmlBlock ggml_block(int t) {
     switch (t) {
         case 0: return {1, 4};     case 1: return {1, 2};     case 2: return {32, 18};   case 3: return {32, 20};
         case 6: return {32, 22};   case 7: return {32, 24};   case 8: return {32, 34};   case 10: return {256, 84};
@@ -105,6 +105,12 @@ inline GgmlBlock ggml_block(int t) {
         case 39: return {32, 17};  case 40: return {64, 36};
     }
     return {0, 0};
+}
+// the alignment (bytes) every block start of ggml type t keeps when its blocks start there: the largest power of two, at
+// most 4, that divides the block bytes (the raw kernels read the blocks with loads that assume it)
+constexpr int raw_block_align(int t) {
+    const int b = ggml_block(t).bytes;
+    return b % 4 == 0 ? 4 : b % 2 == 0 ? 2 : 1;
 }
 // the ggml types mbq_dequant_raw reads: every one but the seven whose values come from gguf-py's code books (IQ2_XXS,
 // IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M: reference src/mashbox/ops/reference.py:243-252)

@@ -436,6 +436,27 @@ def _blocks(h: Raw) -> torch.Tensor:
     return h.raw.reshape(tuple(h.raw.shape[:-2]) + (rows, row_bytes(h.t, cols)))
 
 
+RAW_GEMV_MAX_M = 8                    # activation rows mbq_matmul_raw takes
+
+
+def _raw_gemv(x: torch.Tensor, h: "Raw") -> torch.Tensor | None:
+    """the fused exact-path product for a bfloat16 x of 1-8 rows on a type without kernel planes (mbq_matmul_raw: each
+    weight row rebuilt in registers and multiplied in float32, result rounded to bfloat16); None where it does not apply
+    (other dtypes: the reference multiplies float32 x, not its bfloat16 rounding)"""
+    rows, cols = h.shape[-2:]
+    lead = tuple(x.shape[:-1])
+    m = int(np.prod(lead, dtype=np.int64)) if lead else 1
+    if (x.dtype != torch.bfloat16 or not 1 <= m <= RAW_GEMV_MAX_M or h.t in (2, 8, 12, 13, 14)
+            or cols % max(32, TYPES[h.t][1])):
+        return None                                  # (the kernel types' blocks, off the kernels: rebuild and GEMM)
+    blocks = _blocks(h).reshape(rows, -1).contiguous()
+    x2 = x.reshape(m, cols).to(blocks.device).contiguous()
+    y = torch.empty((m, rows), dtype=torch.bfloat16, device=blocks.device)
+    _lib.check(_lib.lib().mbq_matmul_raw(int(h.t), ctypes.c_void_p(blocks.data_ptr()), ctypes.c_void_p(x2.data_ptr()), m,
+                                         rows, cols, ctypes.c_void_p(y.data_ptr()), 1, _stream()), "matmul_raw")
+    return y.reshape(lead + (rows,))
+
+
 def _exact_matmul(x: torch.Tensor, h: Raw) -> torch.Tensor:
     """x (..., cols) @ W.T in float32, the weight rebuilt exact_chunk_rows rows at a time (reference
     ops/__init__.py:574-576, 624-632: a float32 product of float32 x and the float32 weights)"""
@@ -499,7 +520,8 @@ def qmatmul(x: torch.Tensor, h) -> torch.Tensor:
     if isinstance(h, Raw):
         if h.raw.dim() > 2:
             raise ValueError(f"{h}: a stack is multiplied one layer at a time (index the stack)")
-        return _exact_matmul(x, h).to(x.dtype)
+        y = _raw_gemv(x, h)
+        return y if y is not None else _exact_matmul(x, h).to(x.dtype)
     raise TypeError(f"qmatmul: not a weight handle: {h!r}")
 
 

@@ -92,6 +92,17 @@ def q6_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> 
                      dim=-1).reshape(n, nb * 210)
 
 
+def q2_k_raw(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2) -> torch.Tensor:
+    """(n, k/256*84) uint8 Q2_K super-blocks: 16 scale bytes (4-bit scale, 4-bit min, each uniform in [0, 15]), 64 bytes
+    of 2-bit quants (uniform bytes), fp16 d and dmin ~ U(lo, hi) (reference src/mashbox/ops/reference.py:106-114)"""
+    g = _gen(seed, device)
+    nb = k // 256
+    body = torch.randint(0, 256, (n, nb, 80), generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+    d = _uniform_f16_bytes(g, (n, nb, 1), lo, hi, device)
+    dmin = _uniform_f16_bytes(g, (n, nb, 1), lo, hi, device)
+    return torch.cat([body, d, dmin], dim=-1).reshape(n, nb * 84)
+
+
 def int8_weights(n: int, k: int, seed: int = 0, device="cuda", lo=1e-3, hi=1e-2):
     g = _gen(seed, device)
     q = torch.randint(-127, 128, (n, k), generator=g, device=device, dtype=torch.int8)
@@ -112,7 +123,7 @@ CONFIGS = {
     5: (12, 2048, LAYER_27B),
 }
 # the reference's largest published per-call number: a Q6_K output head, 151936 x 2560, one activation row
-# (reference CORE-CHANGES.md:73, 369.8 us on TPU v6e-1)
+# (reference CORE-CHANGES.md:73, 369.8 us on TPU v6e-1); the 9728 x 2560 rows below: CORE-CHANGES.md:84
 # batched decode over one 27B-class layer at the reference engine's row buckets 4 and 16 (runtime/engine.py:424-428):
 # Q4_K, Q8_0, Q5_K, Q6_K and int8 weights, each repacked into 16-row tiles (as config 4 takes int8)
 EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
@@ -129,5 +140,9 @@ EXTRA = {"q6k_head": (14, 1, [("w", 151936, 2560)]),
          "m1_q4k_stacked": (12, 1, LAYER_27B_STACKED), "m4_q4k_stacked": (12, 4, LAYER_27B_STACKED),
          "m16_q4k_stacked": (12, 16, LAYER_27B_STACKED), "c4_stacked": ("int8", 64, LAYER_27B_STACKED),
          # a prefill chunk of the reference engine's default size (runtime/engine.py:168: chunk=512), Q4_K tiles
-         "p512_q4k": (12, 512, LAYER_27B)}
-REF_TPU_US = {"q6k_head": 369.8}
+         "p512_q4k": (12, 512, LAYER_27B),
+         # the reference's other published per-call numbers (CORE-CHANGES.md:84, kernel package 0.1.13, one row):
+         # Q4_K 9728 x 2560 on the kernels (row-major planes, the decode GEMV) and Q2_K 9728 x 2560, a type without
+         # kernel planes here, on the exact path's fused product (mbq_matmul_raw over the file's blocks)
+         "q4k_9728": (12, 1, [("w", 9728, 2560)]), "q2k_9728": (10, 1, [("w", 9728, 2560)])}
+REF_TPU_US = {"q6k_head": 369.8, "q4k_9728": 22.6, "q2k_9728": 25.5}

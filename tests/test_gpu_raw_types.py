@@ -192,3 +192,86 @@ def test_mixed_role_of_a_kernel_type_and_an_exact_type(cuda):
             assert_product_dev(y.float(), ref, f"layer {l} {NAME[t]}")
     finally:
         OPS.load_kernels(module="off")
+
+
+# ---------------------------------------------------------------------------------------- fused raw GEMV (1-8 rows)
+def _weights(t, n, k, seed):
+    """(n, k) weights of type t as file blocks with finite values: random blocks with finite fp16 scales (MXFP4: the
+    exponents of weights), or normal values for the float types"""
+    from tests.test_oracle_types import random_blocks
+    bs, ts = R.TYPES[t][1], R.TYPES[t][2]
+    if t in FLOATS:
+        w = (np.random.default_rng(seed).standard_normal((n, k)) * 0.05).astype(np.float32)
+        return (w.view(np.uint8) if t == R.F32 else w.astype(np.float16).view(np.uint8) if t == R.F16 else
+                R.bf16_round(w).view(np.uint8)).reshape(n, -1)
+    blocks = random_blocks(t, n * (k // bs), seed)
+    if t == R.MXFP4:
+        blocks[:, 0] = np.random.default_rng(seed).integers(110, 130, blocks.shape[0])
+    return blocks.reshape(n, (k // bs) * ts)
+
+
+def _matmul_raw(t, raw_dev, x, n, k, out_bf16):
+    import ctypes
+    from mashbox_amd import _lib as LIB
+    m = x.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+    LIB.check(LIB.lib().mbq_matmul_raw(t, ctypes.c_void_p(raw_dev.data_ptr()), ctypes.c_void_p(x.data_ptr()), m, n, k,
+                                       ctypes.c_void_p(y.data_ptr()), 1 if out_bf16 else 0,
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "matmul_raw")
+    return y
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", R.EXACT_ONLY, ids=NAME.get)
+@pytest.mark.parametrize("m,n,k", [(1, 77, 256), (3, 200, 4096), (8, 33, 512), (5, 130, 2304), (2, 65, 8448)])
+def test_matmul_raw_against_the_exact_product(t, m, n, k, cuda):
+    """mbq_matmul_raw against the float64 product of the oracle's weights (16, 32 and 64 lanes per row, two units in
+    flight at K = 8448, rows past a block and partial lane rounds); its bfloat16 output is its float32 output rounded to
+    nearest even, bit for bit; a second call repeats the bits"""
+    raw = _weights(t, n, k, 8000 + 7 * t + m)
+    raw_dev = torch.from_numpy(raw).to(cuda)
+    rng = np.random.default_rng(m * n + k)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+    y32 = _matmul_raw(t, raw_dev, x, n, k, False)
+    ref = x.double() @ torch.from_numpy(R.dequant(raw, t, k)).to(cuda).double().T
+    assert_product_dev(y32, ref, f"{NAME[t]} m={m} {n}x{k}")
+    yb = _matmul_raw(t, raw_dev, x, n, k, True)
+    assert np.array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), R.bf16_round(y32.cpu().numpy()))
+    assert torch.equal(_matmul_raw(t, raw_dev, x, n, k, False).view(torch.int32), y32.view(torch.int32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [R.Q2_K, R.IQ4_XS, R.F16], ids=NAME.get)
+def test_qmatmul_routes_decode_rows_to_the_fused_product(t, cuda):
+    """ops.qmatmul on a Raw weight: a bfloat16 x of 1-8 rows takes mbq_matmul_raw (the same bits as a direct call),
+    9 rows and float32 x the rebuild and a GEMM; all within the bars"""
+    n, k = 96, 1024
+    raw = _weights(t, n, k, 9100 + t)
+    h = OPS.prepare(raw, t, (n, k))
+    w64 = torch.from_numpy(R.dequant(raw, t, k)).to(cuda).double()
+    rng = np.random.default_rng(t)
+    for m in (1, 8, 9):
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(cuda).to(torch.bfloat16)
+        y = OPS.qmatmul(x, h)
+        assert_product_dev(y.float(), x.double() @ w64.T, f"{NAME[t]} m={m}")
+        if m <= OPS.RAW_GEMV_MAX_M:
+            direct = _matmul_raw(t, h.raw.reshape(n, -1).contiguous(), x, n, k, True)
+            assert torch.equal(y.view(torch.int16), direct.view(torch.int16))
+    x32 = torch.from_numpy(rng.standard_normal((2, k)).astype(np.float32)).to(cuda)
+    y32 = OPS.qmatmul(x32, h)
+    assert y32.dtype == torch.float32
+    assert_product_dev(y32, x32.double() @ w64.T, f"{NAME[t]} float32 x")
+
+
+def test_matmul_raw_argument_checks():
+    """refused before any launch: the kernel types (they have planes), more than 8 rows, K not a multiple of 32 or of
+    the block, a non-ggml type; M = 0 launches nothing"""
+    from mashbox_amd import _lib as LIB
+    lib = LIB.lib()
+    assert lib.mbq_matmul_raw(R.Q4_K, None, None, 1, 8, 256, None, 0, None) < 0
+    assert lib.mbq_matmul_raw(R.Q2_K, None, None, 9, 8, 256, None, 0, None) < 0
+    assert lib.mbq_matmul_raw(R.F16, None, None, 1, 8, 48, None, 0, None) < 0
+    assert lib.mbq_matmul_raw(R.NVFP4, None, None, 1, 8, 96, None, 0, None) < 0
+    assert lib.mbq_matmul_raw(16, None, None, 1, 8, 256, None, 0, None) < 0
+    assert lib.mbq_matmul_raw(R.Q2_K, None, None, 1, 8, 256, None, 5, None) < 0
+    assert lib.mbq_matmul_raw(R.Q2_K, None, None, 0, 8, 256, None, 0, None) == 0
