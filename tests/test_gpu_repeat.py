@@ -46,4 +46,17 @@ def test_batched_kernels_repeat_bit_for_bit(t, m, n, k, cuda):
     for i in range(1, CALLS):
         y = run().view(torch.int16)
         diff = int((y != first).sum())
-        assert diff == 0, f"call {i}: {diff} outputs differ from the first call ({plan})"
+        assert diff == 0, f"call {i}: {diff} outputs differ from the first call ({plan}); {_where(y, first, run)}"
+
+
+def _where(y, first, run):
+    """where two calls' outputs differ (rows, columns, 256 x 192 tiles), and which of them one more call agrees with"""
+    d = (y != first)
+    rows = torch.nonzero(d.any(1)).flatten()
+    cols = torch.nonzero(d.any(0)).flatten()
+    tiles = torch.nonzero(d.reshape(-1, 1) if d.dim() < 2 else d).cpu()
+    tset = sorted({(int(r) // 256, int(c) // 192) for r, c in tiles[:: max(1, len(tiles) // 4096)].tolist()})
+    again = run().view(torch.int16)
+    return (f"rows {int(rows.min())}-{int(rows.max())} ({len(rows)} distinct), columns {int(cols.min())}-"
+            f"{int(cols.max())} ({len(cols)} distinct), tiles (row, column) {tset[:24]}; one more call differs from the "
+            f"first in {int((again != first).sum())} outputs and from the failing call in {int((again != y).sum())}")
