@@ -56,5 +56,23 @@ def assert_product_dev(y, ref, what=""):
         return 0.0, 0.0
     nmse = float(((y - ref) ** 2).sum()) / den
     mr = float((y - ref).abs().max() / ref.abs().max())
-    assert nmse <= NMSE_BF16 and mr <= MAX_REL, f"{what}: NMSE {nmse:.3e} (bar {NMSE_BF16}), max rel {mr:.3e} (bar {MAX_REL})"
+    assert nmse <= NMSE_BF16 and mr <= MAX_REL, (f"{what}: NMSE {nmse:.3e} (bar {NMSE_BF16}), max rel {mr:.3e} "
+                                                 f"(bar {MAX_REL}); {_where_off(y, ref)}")
     return nmse, mr
+
+
+def _where_off(y, ref):
+    """where a 2-D product misses its bar: the outputs off by more than 1e-2 of max |ref|, their row and column ranges,
+    and the 256 x 192 tiles (the specialized GEMM's) and 16-row blocks they fall in"""
+    import torch
+    if y.dim() != 2:
+        y, ref = y.reshape(-1, y.shape[-1]), ref.reshape(-1, ref.shape[-1])
+    bad = (y - ref).abs() > MAX_REL * ref.abs().max()
+    idx = torch.nonzero(bad).cpu()
+    if len(idx) == 0:
+        return "no single output past 1e-2 of max |ref| (the NMSE bar failed on many small errors)"
+    r, c = idx[:, 0], idx[:, 1]
+    tiles = sorted({(int(a) // 256, int(b) // 192) for a, b in idx[:: max(1, len(idx) // 4096)].tolist()})
+    return (f"{len(idx)} outputs past 1e-2 of max |ref| in rows {int(r.min())}-{int(r.max())} ({len(torch.unique(r))} "
+            f"distinct), columns {int(c.min())}-{int(c.max())} ({len(torch.unique(c))} distinct), 256x192 tiles "
+            f"{tiles[:24]}")
