@@ -337,12 +337,17 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
 
     // local step l (l % NA == U): MFMAs on A stage U and B stage U & 1; x of step l + P streams into A stage
     // (U + P) % NA, the unit of step l + 1 (register buffer U + 1) is dequantized into B stage (U + 1) & 1 between the
-    // MFMAs, and buffer U (dequantized a step ago) is refilled with the unit of step l + P + 1
-    auto step = [&](auto U_, int l) {
+    // MFMAs, and buffer U (dequantized a step ago) is refilled with the unit of step l + P + 1. J < 0: a step of the
+    // unrolled loop. J >= 0: step J of the last n % NA, whose x and weights would be for steps past n, so it issues no
+    // DMA and no loads (loads nobody reads are dropped by the compiler, and the wait must count what is issued).
+    auto step = [&](auto U_, auto J_, int l) {
         constexpr int U = decltype(U_)::value;
-        dma_x((U + P) % NA, k0(l + P));
-        __builtin_amdgcn_sched_barrier(0);             // the DMA stays ahead of the weight loads (vmcnt order below)
-        b_load<T, KFULL>(R[U], wr, bo, K, k0(l + P + 1), bu);
+        constexpr int J = decltype(J_)::value;
+        if constexpr (J < 0) {
+            dma_x((U + P) % NA, k0(l + P));
+            __builtin_amdgcn_sched_barrier(0);         // the DMA stays ahead of the weight loads (vmcnt order below)
+            b_load<T, KFULL>(R[U], wr, bo, K, k0(l + P + 1), bu);
+        }
         const BUnit<T>& dq = R[(U + 1) % NA];
         const uint16_t* Ac = gemm_lds + U * BM * GK;
         const uint16_t* Bc = B0 + (U & 1) * BROWS * GK;
@@ -366,8 +371,10 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
             }
         }
         // the x DMA of step l + 1 (issued P steps ago) has landed once at most the loads issued after it are in flight:
-        // its own step's NB weight loads and P - 1 later steps' XD + NB
-        wait_vm<NB + (P - 1) * (XD + NB)>();
+        // its own step's NB weight loads and P - 1 later steps' XD + NB. In tail step J those later steps are the
+        // P - 2 - J loop steps before the tail (the tail issues nothing); in the last one no later step reads x.
+        constexpr int VM = J < 0 ? NB + (P - 1) * (XD + NB) : J <= P - 2 ? NB + (P - 2 - J) * (XD + NB) : 0;
+        wait_vm<VM>();
         __syncthreads();
     };
 
@@ -388,19 +395,20 @@ __global__ __launch_bounds__(GT, (BM == 64 && BN <= 192) ? 4 : 2) void gemm_kern
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
+    using LOOP = std::integral_constant<int, -1>;
     int l = 0;
     for (; l + NA <= n; l += NA) {
-        step(I0{}, l);
-        step(I1{}, l + 1);
+        step(I0{}, LOOP{}, l);
+        step(I1{}, LOOP{}, l + 1);
         if constexpr (NA == 4) {
-            step(I2{}, l + 2);
-            step(I3{}, l + 3);
+            step(I2{}, LOOP{}, l + 2);
+            step(I3{}, LOOP{}, l + 3);
         }
     }
-    if (l < n) step(I0{}, l);
+    if (l < n) step(I0{}, I0{}, l);
     if constexpr (NA == 4) {
-        if (l + 1 < n) step(I1{}, l + 1);
-        if (l + 2 < n) step(I2{}, l + 2);
+        if (l + 1 < n) step(I1{}, I1{}, l + 1);
+        if (l + 2 < n) step(I2{}, I2{}, l + 2);
     }
 
     // epilogue: lane holds column n = lane & 15 and rows 4 * (lane >> 4) + r of each 16 x 16 tile
@@ -687,13 +695,20 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
         load_w(R[1], 1);
         load_w(R[2], 2);
         dequant(R[0], 0);
-        wait_vm<NDW + 3 * NWL>();                                     // x(0) has landed
+        // x(0) has landed: only x(1)'s DMA is certain to follow it, since the three weight sets may share loads the
+        // compiler merges (a K-quant's scale block is the same for the steps of one 256-value superblock)
+        wait_vm<NDW>();
         wait_lgkm0();                                                 // and the dequantized weights of step 0
         barrier_nofence();                                            // barrier 0
         // step l (l = 0 .. n - 2): x(l + 2), weights (l + 3), dequantize (l + 1), wait x(l + 1), barrier l + 1. The x
         // DMA's 8 instructions are spread between the dequantized chunks (a burst of them slows the consumers' reads).
-        auto pstep = [&](auto U_, int l) {
+        // The wait counts the vector-memory instructions the step itself issues, so it must match them exactly: the
+        // last one or two steps (after the unrolled loop) load no weights, because no later step dequantizes them. They
+        // say so (W false) rather than leave the loads for the compiler to drop, which would leave the wait 4 too high
+        // and let the consumers read the tail of x(l + 1) before its DMA landed.
+        auto pstep = [&](auto U_, auto W_, int l) {
             constexpr int U = decltype(U_)::value;                    // l % 3
+            constexpr bool W = decltype(W_)::value;                   // the step loads the weights of step l + 3
             const int kk = k0(l + 2);
             uint16_t* ast = A0 + ((l + 2) % 3) * SG_BM * GK;
             auto dma_i = [&](int i) {
@@ -707,7 +722,7 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < UPT; ++v) sc[v] = b_scale<T>(Rr[v], ((k0(l + 1) >> 5) + bu[v]) & 7);
             dma_i(0);
-            load_w(R[U], l + 3);                                      // the set of step l, dequantized a step ago
+            if constexpr (W) load_w(R[U], l + 3);                     // the set of step l, dequantized a step ago
 #pragma unroll
             for (int i = 0; i < XD; ++i) {
                 if (i > 0) dma_i(i);
@@ -716,21 +731,23 @@ __global__ __launch_bounds__(GT, 1) void sgemm_kernel(const GemmArgs g) {
                     if (v == 0 || two) st16(bst + sg_off(brow[v], 4 * bu[v] + c), b_chunk<T>(Rr[v], sc[v], c));
                 }
             }
-            wait_vm<NDW + NWL>();                                     // x(l + 1) has landed (loads complete in order)
+            wait_vm<NDW + (W ? NWL : 0)>();                           // x(l + 1) has landed (loads complete in order)
             wait_lgkm0();                                             // and the dequantized weights of step l + 1
             barrier_nofence();
         };
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
         using I2 = std::integral_constant<int, 2>;
+        using LOAD = std::true_type;
+        using TAIL = std::false_type;
         int l = 0;
         for (; l + 3 <= n - 1; l += 3) {
-            pstep(I0{}, l);
-            pstep(I1{}, l + 1);
-            pstep(I2{}, l + 2);
+            pstep(I0{}, LOAD{}, l);
+            pstep(I1{}, LOAD{}, l + 1);
+            pstep(I2{}, LOAD{}, l + 2);
         }
-        if (l < n - 1) pstep(I0{}, l);
-        if (l + 1 < n - 1) pstep(I1{}, l + 1);
+        if (l < n - 1) pstep(I0{}, TAIL{}, l);                        // steps l + 2 and l + 3 do not exist
+        if (l + 1 < n - 1) pstep(I1{}, TAIL{}, l + 1);
         wait_vm<0>();                                                 // no DMA may land after the block ends
     }
     if (vec) barrier_nofence();                                       // the consumers may now write the output tile into LDS

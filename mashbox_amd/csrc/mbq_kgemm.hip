@@ -346,14 +346,18 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
 
     // Issue order: x0 w0 x1 w1 .. x(D-2) w(D-2) w(D-1), then step l issues x(l+D-1) and w(l+D). At step l's wait the
     // loads issued after x(l) (steady state) or w(l) (first steps) number VMT, so vmcnt <= VMT means both landed.
-    auto step = [&](auto U_, int l) __attribute__((always_inline)) {
+    // J < 0: a step of the unrolled loop. J >= 0: step J of the last steps % D, whose x and weights would be for steps
+    // past the last, so it issues no DMA and no loads (loads nobody reads are dropped by the compiler, and the wait
+    // must count what is issued): after x(l) come only the loads of the D - 1 - J loop steps before the tail.
+    auto step = [&](auto U_, auto J_, int l) __attribute__((always_inline)) {
         constexpr int U = decltype(U_)::value;                            // l % D
-        wait_vm<VMT>();
+        constexpr int J = decltype(J_)::value;
+        wait_vm<J < 0 ? VMT : (D - 1 - J) * NWL + (D - 2 - J) * NX>();
         // stage U landed for every wave; stage (l - 1) % D is no longer read. With one row group a wave reads only the
         // stages it fills, but the block-wide barrier still measured faster (it keeps the waves' x reads together)
         barrier_nofence();
         __builtin_amdgcn_sched_barrier(0);
-        dma_x((U + D - 1) % D, l + D - 1);
+        if constexpr (J < 0) dma_x((U + D - 1) % D, l + D - 1);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (DIAG) {
             // the chunk's four K steps chain into one product per tile: output row 4 u + e of x tile i is x row 4 i + e
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                         acc[i][j][r] = __builtin_fmaf(on, DX[i][r], __builtin_fmaf(a, P[i][j][r], acc[i][j][r]));
             }
             __builtin_amdgcn_sched_barrier(0);
-            load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
+            if constexpr (J < 0) load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
             return;
         }
         if constexpr (FACT) {
@@ -478,7 +482,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
                 for (int i = 0; i < MX; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[i], on, acc[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
+            if constexpr (J < 0) load_w(W[U], H[U], Hb[Q5 ? U : 0], l + D);
             return;
         }
         // Q4_K: the lane's 16 bytes are one 32-value unit of its row, sub-block 4 (chunk % 2) + lg of the super-block;
@@ -563,7 +567,7 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_w(W[U], H[QK || Q8 ? U : 0], Hb[Q5 ? U : 0], l + D);
+        if constexpr (J < 0) load_w(W[U], H[QK || Q8 ? U : 0], Hb[Q5 ? U : 0], l + D);
     };
 
     if constexpr (RX) {
@@ -648,9 +652,11 @@ __global__ __launch_bounds__(KGM_THREADS, 1) void kgemm_kernel(const KgmArgs g) 
         }
         int l = 0;
         for (; l + D <= steps; l += D)
-            kgm_each([&](auto P) __attribute__((always_inline)) { step(P, l + decltype(P)::value); }, std::make_integer_sequence<int, D>{});
+            kgm_each([&](auto P) __attribute__((always_inline)) {
+                step(P, std::integral_constant<int, -1>{}, l + decltype(P)::value);
+            }, std::make_integer_sequence<int, D>{});
         kgm_each([&](auto P) __attribute__((always_inline)) {
-            if (l + decltype(P)::value < steps) step(P, l + decltype(P)::value);
+            if (l + decltype(P)::value < steps) step(P, P, l + decltype(P)::value);
         }, std::make_integer_sequence<int, D - 1>{});
         wait_vm<0>();                                                     // no DMA may land after the rings are reused
     }

@@ -134,16 +134,17 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
         for (int j = 0; j < NT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     WsRaw<T> W[D][NT];
-    // the DMA of iteration l has landed once at most the loads issued after it are in flight: the weight loads of
-    // its own step and both groups of the D - 2 steps after
-    constexpr int XWAIT = NWL + (D - 2) * (NDW + NWL);
-
-    auto step = [&](auto U_, int l) {
+    // The DMA of iteration l has landed once at most the loads issued after it are in flight: the weight loads of
+    // its own step and both groups of the D - 2 steps after. J < 0: a step of the unrolled loop. J >= 0: step J of the
+    // last n % D, whose x and weights would be for iterations past n, so it issues no DMA and no loads (loads nobody
+    // reads are dropped by the compiler, and the wait must count what is issued): only the loop steps before it count.
+    auto step = [&](auto U_, auto J_, int l) {
         constexpr int U = decltype(U_)::value;                       // l % D
-        wait_vm<XWAIT>();
+        constexpr int J = decltype(J_)::value;
+        wait_vm<NWL + (D - 2 - (J < 0 ? 0 : J)) * (NDW + NWL)>();
         barrier_nofence();
         __builtin_amdgcn_sched_barrier(0);
-        dma_x((U + D - 1) % D, k0(l + D - 1));
+        if constexpr (J < 0) dma_x((U + D - 1) % D, k0(l + D - 1));
         __builtin_amdgcn_sched_barrier(0);
         // the step's A operands are all read first, the weights converted while the reads are in flight, then the
         // MFMAs run: one LDS latency per step instead of one per MFMA
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
                 for (int i = 0; i < MT; ++i)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i][s], B[j][s], acc[i][j], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(W[U], k0(l + D));
+        if constexpr (J < 0) load_w(W[U], k0(l + D));
     };
 
     using I0 = std::integral_constant<int, 0>;
@@ -181,33 +182,37 @@ __global__ __launch_bounds__(WS_THREADS, 2) void wsgemm_kernel(const WsArgs g) {
     using I6 = std::integral_constant<int, 6>;
     using I7 = std::integral_constant<int, 7>;
     if (n > 0) {                                                      // block-uniform
-        // prologue: x of iterations 0 .. D-2 into stages 0 .. D-2, weights of iterations 0 .. D-1
+        // prologue: x of iterations 0 .. D-2 into stages 0 .. D-2, weights of iterations 0 .. D-1. The empty asm keeps
+        // the compiler from merging loads of two iterations at one address (a K-quant's scale block is shared by the
+        // iterations of a 256-value superblock), which would leave fewer loads in flight than the waits count.
 #pragma unroll
         for (int p = 0; p < D; ++p) {
             if (p < D - 1) dma_x(p, k0(p));
             load_w(W[p], k0(p));
+            asm volatile("" ::: "memory");
         }
+        using LOOP = std::integral_constant<int, -1>;
         int l = 0;
         for (; l + D <= n; l += D) {
-            step(I0{}, l);
-            step(I1{}, l + 1);
-            step(I2{}, l + 2);
-            step(I3{}, l + 3);
+            step(I0{}, LOOP{}, l);
+            step(I1{}, LOOP{}, l + 1);
+            step(I2{}, LOOP{}, l + 2);
+            step(I3{}, LOOP{}, l + 3);
             if constexpr (D == 8) {
-                step(I4{}, l + 4);
-                step(I5{}, l + 5);
-                step(I6{}, l + 6);
-                step(I7{}, l + 7);
+                step(I4{}, LOOP{}, l + 4);
+                step(I5{}, LOOP{}, l + 5);
+                step(I6{}, LOOP{}, l + 6);
+                step(I7{}, LOOP{}, l + 7);
             }
         }
-        if (l < n) step(I0{}, l);
-        if (l + 1 < n) step(I1{}, l + 1);
-        if (l + 2 < n) step(I2{}, l + 2);
+        if (l < n) step(I0{}, I0{}, l);
+        if (l + 1 < n) step(I1{}, I1{}, l + 1);
+        if (l + 2 < n) step(I2{}, I2{}, l + 2);
         if constexpr (D == 8) {
-            if (l + 3 < n) step(I3{}, l + 3);
-            if (l + 4 < n) step(I4{}, l + 4);
-            if (l + 5 < n) step(I5{}, l + 5);
-            if (l + 6 < n) step(I6{}, l + 6);
+            if (l + 3 < n) step(I3{}, I3{}, l + 3);
+            if (l + 4 < n) step(I4{}, I4{}, l + 4);
+            if (l + 5 < n) step(I5{}, I5{}, l + 5);
+            if (l + 6 < n) step(I6{}, I6{}, l + 6);
         }
         wait_vm<0>();                                                 // no DMA may land after the block ends
     }
