@@ -5,7 +5,9 @@ sums reduced through LDS, and, for the down projection, split-K partials exchang
 sums in a fixed order, so repeated calls give the same bits; and the tile GEMV at one row (x staged in LDS, each
 tile's rows summed over the waves through LDS), in its 8-wave and 16-wave blocks; a writer that passes a barrier before its writes land
 shows as calls that differ (seen on MI355X as stale dequantized weights once the producers were sped up, until the
-producers waited for their LDS writes before each barrier)."""
+producers waited for their LDS writes before each barrier; and as stale x rows in a tile's final K step, from a
+producer wait that counted weight loads the compiler had dropped, until the last steps issued only what they wait
+for: tests/test_vmcnt.py checks those waits in the built code)."""
 import pytest
 import torch
 
