@@ -19,6 +19,12 @@ barrier b is issued before barrier b - G):
   kgemm_kernel   D - 2   (D = kgm_depth(T, MT, RG) stages)
 and no path may reach s_endpgm with a DMA outstanding. An exec-masked if / else (s_and_saveexec ... s_cbranch_execz,
 then s_andn2_saveexec ... s_cbranch_execz) runs at least one arm, so the path that skips both is not followed.
+
+The same walk checks a wave's own LDS writes in every kernel that has a barrier: no `ds_write` may be outstanding at
+an s_barrier (the barrier does not wait for them, and the other waves read after it), counting `s_waitcnt lgkmcnt(N)`
+as keeping the newest N LDS / scalar-memory operations (none retired while a scalar load, which returns out of order,
+is among them). sgemm_kernel once had that race (producers passing the barrier before their dequantized weights
+landed in LDS), and the check flags every sgemm_kernel instantiation of that build.
 """
 import os
 import re
@@ -88,6 +94,9 @@ def code_objects(path):
 
 
 VMEM = re.compile(r"^(buffer_|global_|flat_|scratch_)")
+LGKM = re.compile(r"^(ds_|s_load|s_buffer_load|s_memtime|s_memrealtime|s_sendmsg|flat_)")
+LDS_WRITE = re.compile(r"^ds_(write|store|add|sub|max|min|and|or|xor|inc|dec|cmpst|wrxchg|append|consume)")
+LGKMCNT = re.compile(r"lgkmcnt\((\d+)\)")
 VMCNT = re.compile(r"vmcnt\((\d+)\)")
 BRANCH = re.compile(r"^s_(c?branch\w*)\s+(L\d+)")
 
@@ -133,8 +142,10 @@ def blocks(ins):
 
 
 def check(args):
-    """[(function, problem)] for one function: barriers a DMA may pass, or an end with a DMA outstanding"""
+    """[(function, problem)] for one function: barriers a DMA may pass, or an end with a DMA outstanding (G >= 0); or,
+    with G = None, barriers an LDS write of the wave may pass"""
     fname, ins, G = args
+    lds = G is None
     bmap, entry = blocks(ins)
     seen = defaultdict(set)
     work = [(entry, (), False)]
@@ -150,6 +161,19 @@ def check(args):
         body = bmap[lab][1]
         for k, s in enumerate(body):
             op = s.split()[0]
+            if lds:
+                if LGKM.match(op):
+                    q.append("W" if LDS_WRITE.match(op) else "S" if op.startswith("s_") else "R")
+                    q = q[-32:]
+                elif op == "s_waitcnt" and LGKMCNT.search(s):
+                    keep = int(LGKMCNT.search(s).group(1))
+                    if keep == 0:
+                        q = []
+                    elif "S" not in q:
+                        q = q[-keep:]
+                elif op == "s_barrier" and "W" in q:
+                    bad.add(f"barrier at {lab}+{k}: an LDS write of the wave may be outstanding")
+                continue
             if VMEM.match(op):
                 dma = op.startswith(("buffer_load", "global_load")) and re.search(r"\blds\b", s) is not None
                 q.append(("D" if dma else "L", 0))
@@ -178,25 +202,33 @@ def check(args):
     return [(fname, b) for b in sorted(bad)]
 
 
-def _dma_kernels():
+_FUNCS = []
+
+
+def _library_functions():
+    """every kernel of the library's gfx950 code objects, disassembled once per session"""
     if OBJDUMP is None or not os.path.exists(LIB):
         pytest.skip("needs the built libmbq.so and llvm-objdump")
+    if not _FUNCS:
+        for k, co in enumerate(code_objects(LIB)):
+            path = os.path.join(os.environ.get("TMPDIR", "/tmp"), f"mbq_vmcnt_{os.getpid()}_{k}.co")
+            with open(path, "wb") as f:
+                f.write(co)
+            try:
+                dis = subprocess.run([OBJDUMP, "-d", "--symbolize-operands", "--no-show-raw-insn", "--mcpu=gfx950", path],
+                                     capture_output=True, text=True, check=True).stdout
+            finally:
+                os.remove(path)
+            _FUNCS.extend(functions(dis).items())
+    return _FUNCS
+
+
+def _dma_kernels():
     found = []
-    for k, co in enumerate(code_objects(LIB)):
-        if b"gemm_kernel" not in co:
-            continue
-        path = os.path.join(os.environ.get("TMPDIR", "/tmp"), f"mbq_vmcnt_{os.getpid()}_{k}.co")
-        with open(path, "wb") as f:
-            f.write(co)
-        try:
-            dis = subprocess.run([OBJDUMP, "-d", "--symbolize-operands", "--no-show-raw-insn", "--mcpu=gfx950", path],
-                                 capture_output=True, text=True, check=True).stdout
-        finally:
-            os.remove(path)
-        for fname, ins in functions(dis).items():
-            G = guard(fname)
-            if G is not None and any(kind == "ins" and re.search(r"\blds\b", s) for kind, s in ins):
-                found.append((fname, ins, G))
+    for fname, ins in _library_functions():
+        G = guard(fname)
+        if G is not None and any(kind == "ins" and re.search(r"\blds\b", s) for kind, s in ins):
+            found.append((fname, ins, G))
     return found
 
 
@@ -208,6 +240,26 @@ def test_every_lds_dma_lands_before_the_barrier_that_publishes_it():
     with ProcessPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
         problems = [p for r in ex.map(check, kernels, chunksize=4) for p in r]
     assert not problems, f"{len(problems)} problems in {len({f for f, _ in problems})} kernels, e.g. {problems[:4]}"
+
+
+def test_every_lds_write_lands_before_the_barrier_that_publishes_it():
+    kernels = [(f, ins, None) for f, ins in _library_functions() if any(k == "ins" and s.startswith("s_barrier") for k, s in ins)]
+    assert any("12sgemm_kernel" in f for f, _, _ in kernels) and len(kernels) > 100, len(kernels)
+    with ProcessPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        problems = [p for r in ex.map(check, kernels, chunksize=8) for p in r]
+    assert not problems, f"{len(problems)} problems in {len({f for f, _ in problems})} kernels, e.g. {problems[:4]}"
+
+
+def test_the_checker_finds_an_uncovered_lds_write():
+    w = ("ins", "ds_write_b128 v1, v[2:5]")
+    assert check(("waited", [w, ("ins", "s_waitcnt lgkmcnt(0)"), ("ins", "s_barrier"), ("ins", "s_endpgm")], None)) == []
+    assert check(("unwaited", [w, ("ins", "s_barrier"), ("ins", "s_endpgm")], None))
+    # lgkmcnt(1) after the write and a later LDS read retires the write; with a scalar load in flight it does not
+    rd = ("ins", "ds_read_b128 v[6:9], v1")
+    assert check(("older", [w, rd, ("ins", "s_waitcnt lgkmcnt(1)"), ("ins", "s_barrier"), ("ins", "s_endpgm")], None)) == []
+    assert check(("newest", [rd, w, ("ins", "s_waitcnt lgkmcnt(1)"), ("ins", "s_barrier"), ("ins", "s_endpgm")], None))
+    sl = ("ins", "s_load_dwordx2 s[0:1], s[4:5], 0x0")
+    assert check(("scalar", [w, sl, ("ins", "s_waitcnt lgkmcnt(1)"), ("ins", "s_barrier"), ("ins", "s_endpgm")], None))
 
 
 def test_the_checker_finds_an_uncovered_dma():
