@@ -19,6 +19,11 @@ barrier b is issued before barrier b - G):
   kgemm_kernel   D - 2   (D = kgm_depth(T, MT, RG) stages)
 and no path may reach s_endpgm with a DMA outstanding. An exec-masked if / else (s_and_saveexec ... s_cbranch_execz,
 then s_andn2_saveexec ... s_cbranch_execz) runs at least one arm, so the path that skips both is not followed.
+What the walk cannot tell apart: two stages issued within one barrier interval (a prologue's first stage, read after
+the first barrier, and the next). The first is covered by each prologue's own wait: gemm_kernel waits for every load
+(vmcnt(0)), sgemm_kernel for all but the next stage's 8 DMA instructions, wsgemm_kernel and kgemm_kernel by their
+first step's count, which the prologue's issue order (and, in wsgemm_kernel, a compiler barrier between its
+iterations' loads) keeps exact.
 
 The same walk checks a wave's own LDS writes in every kernel that has a barrier: no `ds_write` may be outstanding at
 an s_barrier (the barrier does not wait for them, and the other waves read after it), counting `s_waitcnt lgkmcnt(N)`
